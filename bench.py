@@ -1,0 +1,191 @@
+#!/usr/bin/env python3
+"""Gemma-2B Int8Blocks decode throughput on one MI355X.
+
+Workload (the headline decode configuration): the full Gemma-2B shape (18
+layers, width 2048, 8 query heads / 1 KV head of 256, FFN 16384, vocabulary
+256000 with the tied embedding), seeded N(0, 0.02) weights (norms N(0, 0.1))
+quantized to Int8Blocks, a 512-token seeded uniform prompt, greedy decode with
+an fp16 KV cache.  A step is one decode token: embed, 18 layers, final norm,
+the tied lm_head over 256000 rows and the on-device argmax that feeds the next
+step.  The prefill is untimed; W warmup decode steps run in a separate
+sequence; then exactly K decode steps are timed after a fresh 512-token
+prefill, bracketed by device synchronisation.
+
+Prints one JSON line on stdout (everything else goes to stderr).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "Gemma-2B Q8_0 decode tok/s (b=1, ctx 512) + % of HBM roofline"
+STAGE_LABELS = {
+    "gate_up": "q8_product_kernel<1,4> (gate|up, 2048 -> 32768)",
+    "lm_head": "q8_product_kernel<1,8> (tied lm_head, 2048 -> 256000)",
+    "down": "q8_product_kernel<1,1> (down, 16384 -> 2048)",
+}
+
+
+def log(*args):
+    print(*args, file=sys.stderr, flush=True)
+
+
+def stage_bytes(shape, stage: str) -> int:
+    """Algorithmic bytes of one launch of a product stage: the Int8Blocks
+    weight bytes, the Q8 activation row read and the fp32 output row written."""
+    w, f, v = shape.width, shape.intermediate, shape.vocab
+    dims = {"gate_up": (w, 2 * f), "lm_head": (w, v), "down": (f, w),
+            "qkv": (w, shape.query_width + 2 * shape.kv_width), "o_proj": (shape.query_width, w)}
+    inner, outputs = dims[stage]
+    weights = inner * outputs * 17 // 16
+    extra_read = outputs * 4 if stage in ("down", "o_proj") else 0  # residual read
+    return weights + inner * 17 // 16 + outputs * 4 + extra_read
+
+
+def cpu_baseline(layers: int, sample_steps: int, threads: int) -> dict:
+    """The oracle's Q8 decoder (C, OpenMP) on the host cores, bounded sample."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    O.lib()
+    shape = O.gemma_2b_shape(layers=layers, max_positions=64)
+    model = O.Model(shape, O.MODE_Q8)
+    t0 = time.perf_counter()
+    assert model.fill_synthetic() == 0
+    load = time.perf_counter() - t0
+    prompt = O.prompt_ids(0xC0FFEE + 2, shape.vocab, 4)
+    status, logits, _ = model.step(prompt)
+    assert status == 0
+    token = O.argmax(logits[-1])
+    t0 = time.perf_counter()
+    for _ in range(sample_steps):
+        status, logits, _ = model.step(np.array([token], dtype=np.int32))
+        token = O.argmax(logits[0])
+    seconds = time.perf_counter() - t0
+    model.close()
+    log(f"cpu baseline: weights {load:.1f} s, {sample_steps} steps in {seconds:.2f} s")
+    return {"value": round(sample_steps / seconds, 3), "unit": "tok/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle C Q8 decoder (OpenMP, {threads} threads), {layers} layers at full "
+                      f"Gemma-2B shape, 4-token seeded prompt, {sample_steps} greedy decode steps "
+                      f"timed (positions 4..{4 + sample_steps - 1}); host "
+                      f"'{platform.processor() or platform.machine()}'"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--layers", type=int, default=18)
+    ap.add_argument("--threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "0") or 0))
+    ap.add_argument("--cpu-steps", type=int, default=8, help="decode steps of the CPU sample")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-graph", action="store_true", help="launch steps without hipGraph replay")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported "
+              "(batch-1 decode is not sharded across GPUs here)", file=sys.stderr)
+        return 2
+
+    import torch
+    from huggingfaceeacp_amd import gemma_q8 as G
+
+    if not torch.cuda.is_available():
+        log("no GPU visible")
+        return 1
+    threads = args.threads if args.threads > 0 else (os.cpu_count() or 1)
+    max_positions = 8192
+    shape = G.DecoderShape.gemma_2b(layers=args.layers, max_positions=max_positions,
+                                    max_step_rows=512)
+    decoder = G.Decoder(shape)
+    t0 = time.perf_counter()
+    decoder.fill_synthetic(threads)
+    log(f"weights generated + quantized on device: {time.perf_counter() - t0:.1f} s")
+    prompt = G.prompt_ids(0xC0FFEE + 2, shape.vocab, args.prompt)
+    use_graph = not args.no_graph
+
+    # warmup: its own sequence (graph instantiation, first launches)
+    decoder.generate(prompt, args.warmup + 1, eos=-1, use_graph=use_graph)
+
+    # timed: prefill + first token untimed, then exactly K decode steps
+    _, stats = decoder.generate(prompt, 1, eos=-1, use_graph=use_graph)
+    log(f"prefill of {args.prompt} tokens: {stats.prefill_seconds * 1e3:.1f} ms")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    decoder.decode(args.steps, use_graph=use_graph)
+    torch.cuda.synchronize()
+    seconds = time.perf_counter() - t0
+    tok_s = args.steps / seconds
+    first_l = args.prompt + 1
+    lengths = range(first_l, first_l + args.steps)
+    step_bytes = sum(G.algorithmic_decode_bytes(shape, L) for L in lengths) / args.steps
+    step_gbs = step_bytes * tok_s / 1e9
+    tokens = decoder.tokens(args.prompt, args.steps + 1)
+    log(f"decode: {tok_s:.1f} tok/s, {seconds / args.steps * 1e3:.3f} ms/step, "
+        f"{step_gbs:.0f} GB/s of {step_bytes / 1e9:.4f} GB/token; first ids {list(tokens[:6])}")
+
+    # stage timing with HIP events on the decoder's stream over the same K steps
+    decoder.generate(prompt, 1, eos=-1, use_graph=False)
+    decoder.set_timing(True)
+    decoder.decode(args.steps, use_graph=False)
+    timing = decoder.timing()
+    decoder.set_timing(False)
+    total_ms = sum(ms for ms, _ in timing.values())
+    for name, (ms, n) in sorted(timing.items(), key=lambda kv: -kv[1][0]):
+        if n:
+            log(f"  {name:10s} {ms / args.steps * 1e3:8.1f} us/step  {n // args.steps:3d} launches/step"
+                f"  {100 * ms / total_ms:5.1f} %")
+    dominant = max(("gate_up", "lm_head", "down"), key=lambda k: timing[k][0])
+    ms, launches = timing[dominant]
+    per_launch_s = ms / launches / 1e3
+    launch_bytes = stage_bytes(shape, dominant)
+    achieved = launch_bytes / per_launch_s / 1e9
+    roofline = {"bound": "hbm", "kernel": STAGE_LABELS[dominant], "achieved": round(achieved, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": None, "bytes_per_launch": launch_bytes,
+                "avg_launch_us": round(per_launch_s * 1e6, 2)}
+
+    result = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(seconds / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: seeded N(0,0.02) weights / N(0,0.1) norms quantized to Int8Blocks, "
+                "seeded uniform prompt ids",
+        "config": {"workload": f"Gemma-2B Int8Blocks greedy decode, {args.layers} layers, "
+                               f"{args.prompt}-token prompt, {args.steps} timed decode steps, "
+                               "fp16 KV cache, batch 1",
+                   "layers": args.layers, "prompt_tokens": args.prompt,
+                   "decode_steps": args.steps, "graph": use_graph},
+        "step_hbm": {"bytes_per_token": int(step_bytes), "achieved_gbs": round(step_gbs, 1),
+                     "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
+        "roofline": roofline,
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(args.layers, args.cpu_steps, threads)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,82 @@
+// gq8_kernels.hpp -- launch functions for the gfx950 kernels of the Gemma
+// Int8Blocks token loop.  Every launcher checks its grid against its buffers
+// on the host; positions can come from a device int (pos_ptr, so a captured
+// decode step replays at every position) plus a host offset.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace gq8 {
+
+// Q8 row buffer helpers: rows x inner elements in the Int8Blocks layout.
+inline int64_t q8_bytes(int64_t rows, int64_t inner)
+{
+    return rows * inner + rows * inner / 16;
+}
+
+// elements fp32 values -> q[elements] bytes and scales[elements / 32] fp16
+// bits (the two regions of an Int8Blocks buffer, given separately so a piece
+// of a larger tensor can be quantized in place).
+hipError_t launch_quantize(const float *x, int64_t elements, uint8_t *q, uint16_t *scales,
+                           hipStream_t stream);
+
+hipError_t launch_embed(const uint32_t *tokens, const int *pos_ptr, int rows,
+                        const uint8_t *table, int vocab, int width, float scale, float *out,
+                        hipStream_t stream);
+
+// y (optional) fp32 and q8 (optional) Q8 row buffer of rows x width.
+hipError_t launch_rmsnorm(const float *x, const float *weight, int rows, int width,
+                          float epsilon, float *y, uint8_t *q8, hipStream_t stream);
+
+hipError_t launch_rope(float *x, int row_stride, int heads, int head_dim, const int *pos_ptr,
+                       int pos_value, int rows, const float *cosines, const float *sines,
+                       hipStream_t stream);
+
+// The fused-qkv epilogue of a step: rotate q (in place, heads) and k (kv
+// heads), store k and v as fp16 into the caches at the step's positions.
+hipError_t launch_rope_kv(float *qkv, int qkv_stride, int heads, int kv_heads, int head_dim,
+                          const int *pos_ptr, int pos_value, int rows, const float *cosines,
+                          const float *sines, uint16_t *key_cache, uint16_t *value_cache,
+                          hipStream_t stream);
+
+hipError_t launch_kv_store(const float *k, const float *v, int src_stride, int rows,
+                           int kv_width, uint16_t *key_cache, uint16_t *value_cache,
+                           const int *pos_ptr, int pos_value, hipStream_t stream);
+
+// x8: Q8 row buffer of x_rows_total rows; rows [x_row0, x_row0 + rows) are used.
+hipError_t launch_q8_product(const uint8_t *x8, int x_rows_total, int x_row0, int rows,
+                             const uint8_t *w8, int inner, int outputs, float *y, int y_stride,
+                             int residual, hipStream_t stream);
+
+constexpr int kAttentionChunk = 64;
+constexpr int kMaxHeads = 16;
+constexpr int kMaxHeadDim = 256;
+
+size_t mqa_workspace_bytes(int rows, int heads, int head_dim, int max_keys);
+
+// Rows of queries (row stride q_stride) at positions base + r where
+// base = (*pos_ptr if pos_ptr) + pos_value; row r attends keys [0, base + r].
+// max_keys bounds base + rows (sizes the grid so a captured step fits every
+// position).  out: fp32 [rows, heads * head_dim] (optional), q8: Q8 row buffer
+// of the same (optional).
+hipError_t launch_mqa(const float *queries, int q_stride, const uint16_t *key_cache,
+                      const uint16_t *value_cache, int heads, int kv_heads, int head_dim,
+                      int rows, const int *pos_ptr, int pos_value, int max_keys, float scale,
+                      float *out, uint8_t *q8, void *workspace, size_t workspace_bytes,
+                      hipStream_t stream);
+
+hipError_t launch_geglu(const float *fused, int rows, int intermediate, float *out,
+                        uint8_t *q8, hipStream_t stream);
+
+size_t argmax_workspace_bytes(int rows, int length);
+// indices[(pos_ptr ? *pos_ptr : 0) + index_offset + row] for each row.
+hipError_t launch_argmax(const float *logits, const float *mask, int rows, int length,
+                         uint32_t *indices, const int *pos_ptr, int index_offset,
+                         void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+hipError_t launch_advance(int *pos_ptr, int amount, hipStream_t stream);
+
+} // namespace gq8

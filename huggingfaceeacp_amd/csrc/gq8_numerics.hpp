@@ -1,0 +1,113 @@
+// gq8_numerics.hpp -- the scalar arithmetic every gq8 kernel shares, written
+// once for the device and the host (the host side is what the CPU unit tests
+// exercise against the oracle without a GPU).
+//
+// Rule of the path: each operation is evaluated in IEEE double and rounded to
+// fp32 at the points where the reference's decoder stores an fp32 buffer;
+// int8 dot products are exact.  Floating-point contraction is switched off in
+// these helpers so an expression is evaluated exactly as it is written.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#define GQ8_HD __host__ __device__ inline
+
+namespace gq8 {
+
+constexpr int kBlock = 32;          // Int8Blocks.h:56
+constexpr float kLargestQuantized = 127.0f;
+
+// IEEE binary16 round-to-nearest-even, via the compiler's _Float16 conversion
+// (v_cvt_f16_f32 on gfx950, the libgcc soft conversion on the host).
+GQ8_HD uint16_t half_bits(float value)
+{
+    _Float16 h = (_Float16) value;
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+GQ8_HD float half_value(uint16_t bits)
+{
+    return (float) __builtin_bit_cast(_Float16, bits);
+}
+
+// blockScaleBits (Lib/HuggingFaceEACP/Kernels/Int8Blocks.cpp:114-125) from a
+// block's largest magnitude: amax / 127 as a float division, narrowed to fp16;
+// a scale that is zero, infinite or NaN is stored as zero.
+GQ8_HD uint16_t scale_bits_from_amax(float amax)
+{
+#pragma clang fp contract(off)
+    const uint16_t bits = half_bits(amax / kLargestQuantized);
+    const float scale = half_value(bits);
+    return (scale > 0.f && scale <= 65504.f) ? bits : (uint16_t) 0;
+}
+
+// quantizedByte (Int8Blocks.cpp:130-136): nearbyint((double) x / (double) s)
+// clamped to [-127, 127], with s the fp16 scale (positive, finite).  The double
+// quotient of two such numbers never lands on or across a half-integer the
+// exact quotient is not on (the exact distance from a tie is at least 2^-25,
+// its rounding error at most 2^-45), so this is round-half-even of the exact
+// quotient; it is found here without a division: a candidate from the fp32
+// product x * (1 / s) is within one of it, and the exact fp32 products
+// (k +- 0.5) * s (at most 10 + 11 significant bits) say which side of each
+// boundary x lies on.  A NaN element is stored as zero.
+GQ8_HD int quantize_value(float x, float scale, float inverse)
+{
+#pragma clang fp contract(off)
+    if (!(x == x))
+        return 0;
+    float k = rintf(x * inverse);
+    k = fminf(fmaxf(k, -256.f), 256.f);
+    const float hi = (k + 0.5f) * scale;
+    const float lo = (k - 0.5f) * scale;
+    const bool kOdd = ((int) k & 1) != 0;
+    if (x > hi || (x == hi && kOdd))
+        k += 1.f;
+    else if (x < lo || (x == lo && kOdd))
+        k -= 1.f;
+    k = fminf(fmaxf(k, -127.f), 127.f);
+    return (int) k;
+}
+
+// tanh GELU (Lib/HuggingFaceEACP/Kernels/Gelu.h:27-46, double constants of
+// Tests/Kernels/Common.h:170-175), the tanh argument saturating at |z| >= 10.
+GQ8_HD double tanh_gelu(double x)
+{
+#pragma clang fp contract(off)
+    const double rootTwoOverPi = 0.7978845608028654;
+    const double inner = rootTwoOverPi * (x + 0.044715 * x * x * x);
+    const double t = inner >= 10.0 ? 1.0 : (inner <= -10.0 ? -1.0 : tanh(inner));
+    return 0.5 * x * (1.0 + t);
+}
+
+GQ8_HD float geglu(float gate, float up)
+{
+#pragma clang fp contract(off)
+    return (float) (tanh_gelu((double) gate) * (double) up);
+}
+
+// One rotate-half pair (RoPE.h:7-20, 59-81) in double, rounded once.
+GQ8_HD void rotate_pair(float lo, float hi, float c, float s, float *outLo, float *outHi)
+{
+#pragma clang fp contract(off)
+    const double dl = (double) lo, dh = (double) hi, dc = (double) c, ds = (double) s;
+    *outLo = (float) (dl * dc - dh * ds);
+    *outHi = (float) (dh * dc + dl * ds);
+}
+
+// x * scale * (1 + w) of RMSNorm (RMSNorm.h:44-56), scale = 1/sqrt(mean+eps).
+GQ8_HD float norm_value(float x, double scale, float weight)
+{
+#pragma clang fp contract(off)
+    return (float) (((double) x * scale) * (1.0 + (double) weight));
+}
+
+GQ8_HD double norm_scale(double squares, int n, float epsilon)
+{
+#pragma clang fp contract(off)
+    return 1.0 / sqrt(squares / (double) n + (double) epsilon);
+}
+
+} // namespace gq8

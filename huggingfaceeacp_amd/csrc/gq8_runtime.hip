@@ -1,0 +1,1358 @@
+// gq8_runtime.hip -- the C ABI of include/gemma_q8.h: the op-level entry
+// points, the decoder (HF::Decoder, Lib/HuggingFaceEACP/Decoder/Decoder.cpp)
+// and the greedy token loop (HF::Gemma, Lib/HuggingFaceEACP/Generation/
+// Gemma.cpp).  Host C++ over the HIP runtime; every device buffer is owned
+// here and every refusal is checked before anything is launched.
+#include "gemma_q8.h"
+#include "gq8_kernels.hpp"
+#include "gq8_numerics.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <random>
+#include <string>
+#include <thread>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_lastError;
+
+int fail(int status, const std::string &message)
+{
+    g_lastError = message;
+    return status;
+}
+
+#define GQ8_HIP(expr)                                                                    \
+    do {                                                                                 \
+        hipError_t status_ = (expr);                                                     \
+        if (status_ != hipSuccess)                                                       \
+            return fail(GQ8_ERR_DEVICE, std::string(#expr) + ": " + hipGetErrorString(status_)); \
+    } while (0)
+
+#define GQ8_LAUNCH(expr)                                                                 \
+    do {                                                                                 \
+        hipError_t status_ = (expr);                                                     \
+        if (status_ == hipErrorInvalidValue)                                             \
+            return fail(GQ8_ERR_ARGUMENT, std::string(#expr) + ": arguments refused");   \
+        if (status_ != hipSuccess)                                                       \
+            return fail(GQ8_ERR_DEVICE, std::string(#expr) + ": " + hipGetErrorString(status_)); \
+    } while (0)
+
+hipStream_t as_stream(void *stream)
+{
+    return reinterpret_cast<hipStream_t>(stream);
+}
+
+int hardware_threads(int requested)
+{
+    if (requested > 0)
+        return requested;
+    const unsigned n = std::thread::hardware_concurrency();
+    return n == 0 ? 1 : (int) n;
+}
+
+template <typename F>
+void parallel_for(int64_t count, int threads, F body)
+{
+    threads = (int) std::max<int64_t>(1, std::min<int64_t>(threads, count));
+    if (threads == 1) {
+        for (int64_t i = 0; i < count; ++i)
+            body(i);
+        return;
+    }
+    std::vector<std::thread> pool;
+    std::atomic<int64_t> next{0};
+    for (int t = 0; t < threads; ++t)
+        pool.emplace_back([&] {
+            for (int64_t i = next++; i < count; i = next++)
+                body(i);
+        });
+    for (auto &thread : pool)
+        thread.join();
+}
+
+// ---- host Int8Blocks (Int8Blocks.cpp:114-213), the same numerics as the GPU
+void quantize_block_host(const float *block, uint8_t *bytes, uint16_t *scale)
+{
+    float largest = 0.f;
+    for (int i = 0; i < gq8::kBlock; ++i) {
+        const float m = std::fabs(block[i]);
+        if (largest < m)
+            largest = m;
+    }
+    const uint16_t bits = gq8::scale_bits_from_amax(largest);
+    *scale = bits;
+    if (bits == 0) {
+        std::memset(bytes, 0, gq8::kBlock);
+        return;
+    }
+    const float s = gq8::half_value(bits);
+    const float inverse = 1.0f / s;
+    for (int i = 0; i < gq8::kBlock; ++i)
+        bytes[i] = (uint8_t) (int8_t) gq8::quantize_value(block[i], s, inverse);
+}
+
+// ---- seeded synthetic weights -------------------------------------------
+// Box-Muller in double over std::mt19937_64: one engine per 2^20-element
+// chunk, seeded (tensor_seed << 32) | chunk; (r cos t, r sin t) fill two
+// consecutive elements, r = sqrt(-2 ln(1 - u1)), t = 2 pi u2, u = next() >> 11
+// scaled by 2^-53; each value sigma * z narrowed to fp32.
+constexpr int64_t kChunk = int64_t(1) << 20;
+
+void normal_chunk(uint64_t tensorSeed, double sigma, int64_t chunk, int64_t count, float *out)
+{
+    std::mt19937_64 engine((tensorSeed << 32) | (uint64_t) chunk);
+    const int64_t begin = chunk * kChunk;
+    const int64_t end = std::min(begin + kChunk, count);
+    const double twoPi = 6.283185307179586476925286766559;
+    for (int64_t at = begin; at < end; at += 2) {
+        const double u1 = (double) (engine() >> 11) * (1.0 / 9007199254740992.0);
+        const double u2 = (double) (engine() >> 11) * (1.0 / 9007199254740992.0);
+        const double radius = std::sqrt(-2.0 * std::log(1.0 - u1));
+        const double angle = twoPi * u2;
+        out[at - begin] = (float) (sigma * (radius * std::cos(angle)));
+        if (at + 1 < end)
+            out[at + 1 - begin] = (float) (sigma * (radius * std::sin(angle)));
+    }
+}
+
+} // namespace
+
+// ============================================================================
+// Status and format helpers
+// ============================================================================
+extern "C" const char *gq8_status_string(int status)
+{
+    switch (status) {
+    case GQ8_OK: return "ok";
+    case GQ8_ERR_ARGUMENT: return "invalid argument";
+    case GQ8_ERR_SHAPE: return "decoder shape refused";
+    case GQ8_ERR_CAPACITY: return "rows past the step capacity";
+    case GQ8_ERR_WINDOW: return "position past the window";
+    case GQ8_ERR_TOKEN: return "token id outside the vocabulary";
+    case GQ8_ERR_UNQUANTIZABLE: return "tensor shape not storable as Int8Blocks";
+    case GQ8_ERR_NOT_PREPARED: return "weights not loaded";
+    case GQ8_ERR_EMPTY: return "no tokens";
+    case GQ8_ERR_DEVICE: return "HIP error";
+    case GQ8_ERR_MEMORY: return "device allocation failed";
+    default: return "unknown status";
+    }
+}
+
+extern "C" const char *gq8_last_error(void)
+{
+    return g_lastError.c_str();
+}
+
+extern "C" const char *gq8_version(void)
+{
+    return "gemma_q8 0.1.0 gfx950";
+}
+
+extern "C" int64_t gq8_int8_block_count(int64_t element_count)
+{
+    return element_count / gq8::kBlock;
+}
+
+extern "C" int64_t gq8_int8_blocks_byte_count(int64_t element_count)
+{
+    return element_count + 2 * gq8_int8_block_count(element_count);
+}
+
+extern "C" int gq8_quantizes_as_int8_blocks(int64_t contiguous_extent, int64_t element_count)
+{
+    return contiguous_extent > 0 && element_count > 0 && contiguous_extent % gq8::kBlock == 0
+           && element_count % (2 * gq8::kBlock) == 0;
+}
+
+extern "C" int gq8_quantize_int8_blocks_host(const float *values, int64_t value_count,
+                                             int64_t first, int64_t element_count,
+                                             uint8_t *destination)
+{
+    if (!values || !destination || value_count < 0 || first < 0 || first % gq8::kBlock != 0
+        || value_count % gq8::kBlock != 0 || first + value_count > element_count)
+        return fail(GQ8_ERR_ARGUMENT, "quantize: pieces must be whole blocks inside the tensor");
+    uint16_t *scales = reinterpret_cast<uint16_t *>(destination + element_count);
+    const int64_t blocks = value_count / gq8::kBlock;
+    const int64_t perTask = 4096;
+    parallel_for((blocks + perTask - 1) / perTask, hardware_threads(0), [&](int64_t task) {
+        const int64_t b0 = task * perTask, b1 = std::min(blocks, b0 + perTask);
+        for (int64_t b = b0; b < b1; ++b) {
+            const int64_t element = first + b * gq8::kBlock;
+            uint16_t bits;
+            quantize_block_host(values + b * gq8::kBlock, destination + element, &bits);
+            std::memcpy(reinterpret_cast<uint8_t *>(scales) + 2 * (element / gq8::kBlock), &bits, 2);
+        }
+    });
+    return GQ8_OK;
+}
+
+extern "C" int gq8_dequantize_int8_blocks_host(const uint8_t *stored, int64_t element_count,
+                                               float *values)
+{
+    if (!stored || !values || element_count < 0)
+        return fail(GQ8_ERR_ARGUMENT, "dequantize: null buffer");
+    for (int64_t i = 0; i < element_count; ++i) {
+        uint16_t bits;
+        std::memcpy(&bits, stored + element_count + 2 * (i / gq8::kBlock), 2);
+        values[i] = gq8::half_value(bits) * (float) ((int) (stored[i] ^ 0x80u) - 128);
+    }
+    return GQ8_OK;
+}
+
+extern "C" int gq8_rotary_table_host(int max_positions, int head_dim, double theta,
+                                     float *cosines, float *sines)
+{
+    if (max_positions <= 0 || head_dim <= 0 || head_dim % 2 != 0 || !cosines || !sines)
+        return fail(GQ8_ERR_ARGUMENT, "rotary table: bad shape");
+    // makeRotaryTable (RoPE.cpp:7-34): double inverse frequency and angle,
+    // cos/sin narrowed to fp32.
+    const int half = head_dim / 2;
+    for (int channel = 0; channel < half; ++channel) {
+        const double exponent = 2.0 * channel / (double) head_dim;
+        const double inverseFrequency = 1.0 / std::pow(theta, exponent);
+        for (int position = 0; position < max_positions; ++position) {
+            const double angle = (double) position * inverseFrequency;
+            cosines[(int64_t) position * half + channel] = (float) std::cos(angle);
+            sines[(int64_t) position * half + channel] = (float) std::sin(angle);
+        }
+    }
+    return GQ8_OK;
+}
+
+// ============================================================================
+// Op-level entry points
+// ============================================================================
+extern "C" int gq8_quantize_rows(const float *x, int64_t rows, int64_t inner, uint8_t *q8,
+                                 void *stream)
+{
+    if (!x || !q8 || rows <= 0 || inner <= 0 || inner % gq8::kBlock != 0)
+        return fail(GQ8_ERR_UNQUANTIZABLE, "quantize_rows: inner must be a positive multiple of 32");
+    const int64_t elements = rows * inner;
+    GQ8_LAUNCH(gq8::launch_quantize(x, elements, q8,
+                                    reinterpret_cast<uint16_t *>(q8 + elements), as_stream(stream)));
+    return GQ8_OK;
+}
+
+extern "C" int gq8_embed(const uint32_t *tokens, int rows, const uint8_t *table, int vocab,
+                         int width, float scale, float *out, void *stream)
+{
+    if (!tokens || !table || !out || rows <= 0 || vocab <= 0 || width <= 0
+        || width % gq8::kBlock != 0)
+        return fail(GQ8_ERR_ARGUMENT, "embed: bad arguments");
+    GQ8_LAUNCH(gq8::launch_embed(tokens, nullptr, rows, table, vocab, width, scale, out,
+                                 as_stream(stream)));
+    return GQ8_OK;
+}
+
+extern "C" int gq8_rmsnorm(const float *x, const float *weight, int rows, int width,
+                           float epsilon, float *y, uint8_t *q8, void *stream)
+{
+    if (!x || !weight || (!y && !q8) || rows <= 0 || width <= 0 || width % gq8::kBlock != 0)
+        return fail(GQ8_ERR_ARGUMENT, "rmsnorm: bad arguments");
+    GQ8_LAUNCH(gq8::launch_rmsnorm(x, weight, rows, width, epsilon, y, q8, as_stream(stream)));
+    return GQ8_OK;
+}
+
+extern "C" int gq8_rope(float *x, int row_stride, int heads, int head_dim, int first_position,
+                        int rows, const float *cosines, const float *sines, void *stream)
+{
+    if (!x || !cosines || !sines || rows <= 0 || heads <= 0 || head_dim <= 0
+        || head_dim % 4 != 0 || row_stride < heads * head_dim || first_position < 0)
+        return fail(GQ8_ERR_ARGUMENT, "rope: bad arguments");
+    GQ8_LAUNCH(gq8::launch_rope(x, row_stride, heads, head_dim, nullptr, first_position, rows,
+                                cosines, sines, as_stream(stream)));
+    return GQ8_OK;
+}
+
+extern "C" int gq8_q8_product(const uint8_t *x8, const uint8_t *w8, int rows, int inner,
+                              int outputs, float *y, int y_stride, int residual, void *stream)
+{
+    if (!x8 || !w8 || !y || rows <= 0 || outputs <= 0 || y_stride < outputs)
+        return fail(GQ8_ERR_ARGUMENT, "q8_product: bad arguments");
+    if (!gq8_quantizes_as_int8_blocks(inner, (int64_t) inner * outputs)
+        || inner % gq8::kBlock != 0 || inner > 16384)
+        return fail(GQ8_ERR_UNQUANTIZABLE, "q8_product: inner must be a multiple of 32, <= 16384");
+    GQ8_LAUNCH(gq8::launch_q8_product(x8, rows, 0, rows, w8, inner, outputs, y, y_stride, residual,
+                                      as_stream(stream)));
+    return GQ8_OK;
+}
+
+extern "C" int gq8_kv_store_f16(const float *k, const float *v, int src_stride, int rows,
+                                int kv_width, uint16_t *key_cache, uint16_t *value_cache,
+                                int position, void *stream)
+{
+    if (!k || !v || !key_cache || !value_cache || rows <= 0 || kv_width <= 0
+        || src_stride < kv_width || position < 0)
+        return fail(GQ8_ERR_ARGUMENT, "kv_store: bad arguments");
+    GQ8_LAUNCH(gq8::launch_kv_store(k, v, src_stride, rows, kv_width, key_cache, value_cache,
+                                    nullptr, position, as_stream(stream)));
+    return GQ8_OK;
+}
+
+static int check_attention_shape(int heads, int kv_heads, int head_dim)
+{
+    // MultiQueryAttention.cpp:19-39 plus this kernel's own limits
+    if (heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0 || head_dim <= 0
+        || head_dim % 4 != 0 || head_dim > gq8::kMaxHeadDim || heads > gq8::kMaxHeads
+        || heads * head_dim > 2048 || kv_heads * head_dim > 256)
+        return fail(GQ8_ERR_SHAPE, "attention: heads a multiple of kv heads, head width a "
+                                   "multiple of 4 up to 256, at most 16 heads, query row <= 2048, "
+                                   "kv row <= 256");
+    return GQ8_OK;
+}
+
+extern "C" size_t gq8_mqa_workspace_bytes(int rows, int heads, int head_dim, int max_keys)
+{
+    return gq8::mqa_workspace_bytes(rows, heads, head_dim, max_keys);
+}
+
+extern "C" int gq8_mqa_decode(const float *query, const uint16_t *key_cache,
+                              const uint16_t *value_cache, int heads, int kv_heads, int head_dim,
+                              int key_count, float scale, float *out, void *workspace,
+                              size_t workspace_bytes, void *stream)
+{
+    if (int s = check_attention_shape(heads, kv_heads, head_dim))
+        return s;
+    if (!query || !key_cache || !value_cache || !out || !workspace || key_count < 1)
+        return fail(GQ8_ERR_ARGUMENT, "mqa_decode: bad arguments");
+    if (workspace_bytes < gq8::mqa_workspace_bytes(1, heads, head_dim, key_count))
+        return fail(GQ8_ERR_ARGUMENT, "mqa_decode: workspace too small");
+    GQ8_LAUNCH(gq8::launch_mqa(query, heads * head_dim, key_cache, value_cache, heads, kv_heads,
+                               head_dim, 1, nullptr, key_count - 1, key_count, scale, out, nullptr,
+                               workspace, workspace_bytes, as_stream(stream)));
+    return GQ8_OK;
+}
+
+extern "C" int gq8_mqa_prefill(const float *queries, const uint16_t *key_cache,
+                               const uint16_t *value_cache, int heads, int kv_heads,
+                               int head_dim, int rows, int position_offset, float scale,
+                               float *out, void *workspace, size_t workspace_bytes, void *stream)
+{
+    if (int s = check_attention_shape(heads, kv_heads, head_dim))
+        return s;
+    if (!queries || !key_cache || !value_cache || !out || !workspace || rows < 1
+        || position_offset < 0)
+        return fail(GQ8_ERR_ARGUMENT, "mqa_prefill: bad arguments");
+    const int maxKeys = position_offset + rows;
+    if (workspace_bytes < gq8::mqa_workspace_bytes(rows, heads, head_dim, maxKeys))
+        return fail(GQ8_ERR_ARGUMENT, "mqa_prefill: workspace too small");
+    GQ8_LAUNCH(gq8::launch_mqa(queries, heads * head_dim, key_cache, value_cache, heads, kv_heads,
+                               head_dim, rows, nullptr, position_offset, maxKeys, scale, out,
+                               nullptr, workspace, workspace_bytes, as_stream(stream)));
+    return GQ8_OK;
+}
+
+extern "C" int gq8_geglu(const float *fused, int rows, int intermediate, float *out, uint8_t *q8,
+                         void *stream)
+{
+    if (!fused || (!out && !q8) || rows <= 0 || intermediate <= 0
+        || intermediate % gq8::kBlock != 0)
+        return fail(GQ8_ERR_ARGUMENT, "geglu: bad arguments");
+    GQ8_LAUNCH(gq8::launch_geglu(fused, rows, intermediate, out, q8, as_stream(stream)));
+    return GQ8_OK;
+}
+
+extern "C" size_t gq8_argmax_workspace_bytes(int rows, int length)
+{
+    return gq8::argmax_workspace_bytes(rows, length);
+}
+
+extern "C" int gq8_argmax_rows(const float *logits, const float *mask, int rows, int length,
+                               uint32_t *indices, void *workspace, size_t workspace_bytes,
+                               void *stream)
+{
+    if (!logits || !indices || !workspace || rows <= 0 || length <= 0)
+        return fail(GQ8_ERR_ARGUMENT, "argmax: bad arguments");
+    if (workspace_bytes < gq8::argmax_workspace_bytes(rows, length))
+        return fail(GQ8_ERR_ARGUMENT, "argmax: workspace too small");
+    GQ8_LAUNCH(gq8::launch_argmax(logits, mask, rows, length, indices, nullptr, 0, workspace,
+                                  workspace_bytes, as_stream(stream)));
+    return GQ8_OK;
+}
+
+// ============================================================================
+// Decoder
+// ============================================================================
+namespace {
+enum Role { kQ = 0, kK, kV, kO, kGate, kUp, kDown, kInputNorm, kPostNorm, kPerLayer };
+}
+
+struct gq8_decoder {
+    gq8_shape shape{};
+    int capacity = 0; // step rows
+    int qWidth = 0, kvWidth = 0, qkvWidth = 0, maxInner = 0;
+    hipStream_t stream = nullptr;
+
+    uint8_t *embedding = nullptr;
+    std::vector<uint8_t *> qkv, out, gateUp, down;
+    std::vector<float *> inputNorm, postNorm;
+    float *finalNorm = nullptr;
+    std::vector<char> present;
+
+    uint16_t *keyCache = nullptr, *valueCache = nullptr;
+    float *cosines = nullptr, *sines = nullptr;
+
+    float *hidden = nullptr, *normalisedRows = nullptr, *qkvRows = nullptr, *fused = nullptr;
+    uint8_t *x8 = nullptr;
+    void *attentionWorkspace = nullptr;
+    size_t attentionWorkspaceBytes = 0;
+    void *argmaxWorkspace = nullptr;
+    size_t argmaxWorkspaceBytes = 0;
+    float *logits = nullptr; // one vocabulary row, for the greedy loop
+    uint32_t *sequence = nullptr;
+    int *position = nullptr; // device copy of the position
+    int hostPosition = 0;
+    uint32_t *pinnedToken = nullptr;
+
+    bool debug = false;
+    float *debugValues = nullptr; // (layers + 1) x 4 x maxInner
+    uint8_t *debugQ8 = nullptr;   // (layers + 1) x 4 x q8_bytes(1, maxInner)
+    float *debugAttended = nullptr, *debugActivated = nullptr, *debugNormalised = nullptr;
+
+    hipGraphExec_t graph = nullptr;
+    bool capturing = false;
+
+    bool timing = false;
+    struct Mark {
+        int stage;
+        hipEvent_t start, stop;
+    };
+    std::vector<Mark> marks;
+    std::vector<hipEvent_t> spareEvents;
+
+    std::vector<void *> allocations;
+};
+
+namespace {
+
+int64_t fused_rows_offset(const gq8_decoder *d, int role)
+{
+    switch (role) {
+    case kK: return d->qWidth;
+    case kV: return d->qWidth + d->kvWidth;
+    case kUp: return d->shape.intermediate;
+    default: return 0;
+    }
+}
+
+int device_alloc(gq8_decoder *d, void **out, size_t bytes)
+{
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+        (void) hipGetLastError();
+        return fail(GQ8_ERR_MEMORY, "hipMalloc of " + std::to_string(bytes) + " bytes failed");
+    }
+    d->allocations.push_back(p);
+    *out = p;
+    return GQ8_OK;
+}
+
+template <typename T>
+int alloc_as(gq8_decoder *d, T **out, size_t bytes)
+{
+    void *p = nullptr;
+    int s = device_alloc(d, &p, bytes);
+    *out = reinterpret_cast<T *>(p);
+    return s;
+}
+
+bool is_final_norm(const gq8_shape *s, int index)
+{
+    return index == 1 + kPerLayer * s->layers;
+}
+
+} // namespace
+
+extern "C" int gq8_tensor_count(const gq8_shape *shape)
+{
+    return shape ? 2 + kPerLayer * shape->layers : 0;
+}
+
+extern "C" int gq8_tensor_is_norm(const gq8_shape *s, int index)
+{
+    if (!s || index <= 0)
+        return 0;
+    if (is_final_norm(s, index))
+        return 1;
+    const int role = (index - 1) % kPerLayer;
+    return role == kInputNorm || role == kPostNorm;
+}
+
+extern "C" int64_t gq8_tensor_elements(const gq8_shape *s, int index)
+{
+    if (!s || index < 0 || index >= gq8_tensor_count(s))
+        return -1;
+    const int64_t w = s->width, q = (int64_t) s->heads * s->head_dim,
+                  kv = (int64_t) s->kv_heads * s->head_dim, f = s->intermediate;
+    if (index == 0)
+        return (int64_t) s->vocab * w;
+    if (is_final_norm(s, index))
+        return w;
+    switch ((index - 1) % kPerLayer) {
+    case kQ: return q * w;
+    case kK: case kV: return kv * w;
+    case kO: return w * q;
+    case kGate: case kUp: return f * w;
+    case kDown: return w * f;
+    default: return w;
+    }
+}
+
+static int64_t tensor_inner(const gq8_shape *s, int index)
+{
+    if (index == 0)
+        return s->width;
+    switch ((index - 1) % kPerLayer) {
+    case kO: return (int64_t) s->heads * s->head_dim;
+    case kDown: return s->intermediate;
+    default: return s->width;
+    }
+}
+
+extern "C" int gq8_shape_validate(const gq8_shape *s)
+{
+    if (!s)
+        return fail(GQ8_ERR_ARGUMENT, "null shape");
+    const int fields[] = {s->width, s->heads, s->kv_heads, s->head_dim, s->layers,
+                          s->intermediate, s->vocab, s->max_positions};
+    const char *names[] = {"width", "heads", "kvHeads", "headWidth", "layers",
+                           "intermediate", "vocabularySize", "maxPositions"};
+    for (int i = 0; i < 8; ++i)
+        if (fields[i] <= 0)
+            return fail(GQ8_ERR_SHAPE, std::string("a decoder shape's '") + names[i]
+                                           + "' must be positive");
+    if (s->max_step_rows < 0 || s->max_step_rows > s->max_positions)
+        return fail(GQ8_ERR_SHAPE, "step capacity must be 0..maxPositions");
+    if (s->head_dim % 4 != 0 || s->head_dim > gq8::kMaxHeadDim)
+        return fail(GQ8_ERR_SHAPE, "head width must be a multiple of four and at most 256");
+    if (s->heads % s->kv_heads != 0)
+        return fail(GQ8_ERR_SHAPE, "kv heads must divide the query heads");
+    if (int st = check_attention_shape(s->heads, s->kv_heads, s->head_dim))
+        return st;
+    for (int i = 0; i < gq8_tensor_count(s); ++i)
+        if (!gq8_tensor_is_norm(s, i)
+            && !gq8_quantizes_as_int8_blocks(tensor_inner(s, i), gq8_tensor_elements(s, i)))
+            return fail(GQ8_ERR_UNQUANTIZABLE, "tensor " + std::to_string(i)
+                                                   + " cannot be stored as Int8Blocks");
+    if (s->width > 16384 || s->intermediate > 16384 || s->heads * s->head_dim > 16384)
+        return fail(GQ8_ERR_SHAPE, "product inner extents are limited to 16384");
+    return GQ8_OK;
+}
+
+extern "C" gq8_shape gq8_gemma_2b_shape(int layers, int max_positions, int max_step_rows)
+{
+    gq8_shape s{};
+    s.width = 2048;
+    s.heads = 8;
+    s.kv_heads = 1;
+    s.head_dim = 256;
+    s.layers = layers;
+    s.intermediate = 16384;
+    s.vocab = 256000;
+    s.max_positions = max_positions;
+    s.max_step_rows = max_step_rows;
+    s.rms_epsilon = 1e-6f;
+    s.rope_theta = 10000.0;
+    s.embedding_scale = std::sqrt((float) s.width); // GemmaConfig.cpp:123-126
+    return s;
+}
+
+extern "C" void gq8_decoder_destroy(gq8_decoder *d)
+{
+    if (!d)
+        return;
+    if (d->graph)
+        (void) hipGraphExecDestroy(d->graph);
+    if (d->stream)
+        (void) hipStreamSynchronize(d->stream);
+    for (auto &m : d->marks) {
+        (void) hipEventDestroy(m.start);
+        (void) hipEventDestroy(m.stop);
+    }
+    for (auto e : d->spareEvents)
+        (void) hipEventDestroy(e);
+    for (void *p : d->allocations)
+        (void) hipFree(p);
+    if (d->pinnedToken)
+        (void) hipHostFree(d->pinnedToken);
+    if (d->stream)
+        (void) hipStreamDestroy(d->stream);
+    delete d;
+}
+
+extern "C" int gq8_decoder_create(const gq8_shape *shape, gq8_decoder **out)
+{
+    if (!out)
+        return fail(GQ8_ERR_ARGUMENT, "null output");
+    *out = nullptr;
+    if (int s = gq8_shape_validate(shape))
+        return s;
+
+    gq8_decoder *d = new gq8_decoder();
+    d->shape = *shape;
+    const gq8_shape &s = d->shape;
+    d->capacity = s.max_step_rows > 0 ? s.max_step_rows : s.max_positions;
+    d->qWidth = s.heads * s.head_dim;
+    d->kvWidth = s.kv_heads * s.head_dim;
+    d->qkvWidth = d->qWidth + 2 * d->kvWidth;
+    d->maxInner = std::max({s.width, d->qWidth, s.intermediate});
+
+    auto cleanup = [&](int status) {
+        gq8_decoder_destroy(d);
+        return status;
+    };
+    if (hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking) != hipSuccess)
+        return cleanup(fail(GQ8_ERR_DEVICE, "hipStreamCreate failed"));
+
+    const int64_t W = s.width, R = d->capacity, L = s.layers;
+    int st = GQ8_OK;
+#define GQ8_ALLOC(ptr, bytes)                                \
+    if ((st = alloc_as(d, &(ptr), (size_t) (bytes))) != 0) \
+        return cleanup(st)
+
+    GQ8_ALLOC(d->embedding, gq8_int8_blocks_byte_count((int64_t) s.vocab * W));
+    d->qkv.resize(L);
+    d->out.resize(L);
+    d->gateUp.resize(L);
+    d->down.resize(L);
+    d->inputNorm.resize(L);
+    d->postNorm.resize(L);
+    for (int l = 0; l < L; ++l) {
+        GQ8_ALLOC(d->qkv[l], gq8_int8_blocks_byte_count((int64_t) d->qkvWidth * W));
+        GQ8_ALLOC(d->out[l], gq8_int8_blocks_byte_count(W * d->qWidth));
+        GQ8_ALLOC(d->gateUp[l], gq8_int8_blocks_byte_count(2 * (int64_t) s.intermediate * W));
+        GQ8_ALLOC(d->down[l], gq8_int8_blocks_byte_count(W * s.intermediate));
+        GQ8_ALLOC(d->inputNorm[l], W * sizeof(float));
+        GQ8_ALLOC(d->postNorm[l], W * sizeof(float));
+    }
+    GQ8_ALLOC(d->finalNorm, W * sizeof(float));
+    d->present.assign(gq8_tensor_count(&s), 0);
+
+    const int64_t cacheElements = L * (int64_t) s.max_positions * d->kvWidth;
+    GQ8_ALLOC(d->keyCache, cacheElements * sizeof(uint16_t));
+    GQ8_ALLOC(d->valueCache, cacheElements * sizeof(uint16_t));
+
+    const int64_t tableElements = (int64_t) s.max_positions * (s.head_dim / 2);
+    GQ8_ALLOC(d->cosines, tableElements * sizeof(float));
+    GQ8_ALLOC(d->sines, tableElements * sizeof(float));
+    {
+        std::vector<float> c(tableElements), sn(tableElements);
+        gq8_rotary_table_host(s.max_positions, s.head_dim, s.rope_theta, c.data(), sn.data());
+        if (hipMemcpy(d->cosines, c.data(), tableElements * sizeof(float), hipMemcpyHostToDevice)
+                != hipSuccess
+            || hipMemcpy(d->sines, sn.data(), tableElements * sizeof(float), hipMemcpyHostToDevice)
+                   != hipSuccess)
+            return cleanup(fail(GQ8_ERR_DEVICE, "rotary table upload failed"));
+    }
+
+    GQ8_ALLOC(d->hidden, R * W * sizeof(float));
+    GQ8_ALLOC(d->normalisedRows, R * W * sizeof(float));
+    GQ8_ALLOC(d->qkvRows, R * d->qkvWidth * sizeof(float));
+    GQ8_ALLOC(d->fused, R * 2 * (int64_t) s.intermediate * sizeof(float));
+    GQ8_ALLOC(d->x8, gq8::q8_bytes(R, d->maxInner));
+    d->attentionWorkspaceBytes = gq8::mqa_workspace_bytes((int) R, s.heads, s.head_dim,
+                                                          s.max_positions);
+    GQ8_ALLOC(d->attentionWorkspace, d->attentionWorkspaceBytes);
+    d->argmaxWorkspaceBytes = gq8::argmax_workspace_bytes(1, s.vocab);
+    GQ8_ALLOC(d->argmaxWorkspace, d->argmaxWorkspaceBytes);
+    GQ8_ALLOC(d->logits, (size_t) s.vocab * sizeof(float));
+    GQ8_ALLOC(d->sequence, ((size_t) s.max_positions + 1) * sizeof(uint32_t));
+    GQ8_ALLOC(d->position, sizeof(int));
+    GQ8_ALLOC(d->debugValues, (size_t) (L + 1) * 4 * d->maxInner * sizeof(float));
+    GQ8_ALLOC(d->debugQ8, (size_t) (L + 1) * 4 * gq8::q8_bytes(1, d->maxInner));
+    GQ8_ALLOC(d->debugNormalised, R * W * sizeof(float));
+    GQ8_ALLOC(d->debugAttended, R * d->qWidth * sizeof(float));
+    GQ8_ALLOC(d->debugActivated, R * (int64_t) s.intermediate * sizeof(float));
+#undef GQ8_ALLOC
+    if (hipHostMalloc((void **) &d->pinnedToken, sizeof(uint32_t) * 4) != hipSuccess)
+        return cleanup(fail(GQ8_ERR_MEMORY, "pinned allocation failed"));
+    if (hipMemset(d->sequence, 0, ((size_t) s.max_positions + 1) * sizeof(uint32_t)) != hipSuccess
+        || hipMemset(d->position, 0, sizeof(int)) != hipSuccess
+        || hipMemset(d->keyCache, 0, cacheElements * sizeof(uint16_t)) != hipSuccess
+        || hipMemset(d->valueCache, 0, cacheElements * sizeof(uint16_t)) != hipSuccess
+        || hipDeviceSynchronize() != hipSuccess)
+        return cleanup(fail(GQ8_ERR_DEVICE, "initialisation failed"));
+    *out = d;
+    return GQ8_OK;
+}
+
+// Where tensor `index` lives: the device bytes of its own region inside the
+// fused q|k|v or gate|up tensor (quantized) or its fp32 norm buffer.
+namespace {
+struct Placement {
+    uint8_t *q = nullptr;        // first quantized byte
+    uint16_t *scales = nullptr;  // first scale
+    float *values = nullptr;     // norms
+    int64_t elements = 0;
+};
+
+Placement placement(gq8_decoder *d, int index)
+{
+    const gq8_shape &s = d->shape;
+    Placement p;
+    p.elements = gq8_tensor_elements(&s, index);
+    if (index == 0) {
+        p.q = d->embedding;
+        p.scales = reinterpret_cast<uint16_t *>(d->embedding + p.elements);
+        return p;
+    }
+    if (is_final_norm(&s, index)) {
+        p.values = d->finalNorm;
+        return p;
+    }
+    const int layer = (index - 1) / kPerLayer, role = (index - 1) % kPerLayer;
+    const int64_t W = s.width;
+    uint8_t *base = nullptr;
+    int64_t total = 0, rowOffset = fused_rows_offset(d, role), inner = W;
+    switch (role) {
+    case kQ: case kK: case kV:
+        base = d->qkv[layer];
+        total = (int64_t) d->qkvWidth * W;
+        break;
+    case kGate: case kUp:
+        base = d->gateUp[layer];
+        total = 2 * (int64_t) s.intermediate * W;
+        break;
+    case kO:
+        base = d->out[layer];
+        total = W * d->qWidth;
+        inner = d->qWidth;
+        break;
+    case kDown:
+        base = d->down[layer];
+        total = W * s.intermediate;
+        inner = s.intermediate;
+        break;
+    case kInputNorm: p.values = d->inputNorm[layer]; return p;
+    default: p.values = d->postNorm[layer]; return p;
+    }
+    p.q = base + rowOffset * inner;
+    p.scales = reinterpret_cast<uint16_t *>(base + total) + rowOffset * inner / gq8::kBlock;
+    return p;
+}
+
+int mark_present(gq8_decoder *d, int index)
+{
+    d->present[index] = 1;
+    return GQ8_OK;
+}
+} // namespace
+
+// fp32 values (host) -> device, quantized on the device in pieces.
+static int upload_values(gq8_decoder *d, int index, const float *host, int64_t first,
+                         int64_t count, float *staging)
+{
+    Placement p = placement(d, index);
+    if (p.values) {
+        GQ8_HIP(hipMemcpyAsync(p.values + first, host, count * sizeof(float), hipMemcpyHostToDevice,
+                               d->stream));
+        return GQ8_OK;
+    }
+    GQ8_HIP(hipMemcpyAsync(staging, host, count * sizeof(float), hipMemcpyHostToDevice, d->stream));
+    GQ8_LAUNCH(gq8::launch_quantize(staging, count, p.q + first, p.scales + first / gq8::kBlock,
+                                    d->stream));
+    return GQ8_OK;
+}
+
+extern "C" int gq8_decoder_load_tensor(gq8_decoder *d, int index, const float *host_values)
+{
+    if (!d || !host_values || index < 0 || index >= gq8_tensor_count(&d->shape))
+        return fail(GQ8_ERR_ARGUMENT, "load_tensor: bad arguments");
+    const int64_t elements = gq8_tensor_elements(&d->shape, index);
+    const int64_t piece = int64_t(64) << 20;
+    float *staging = nullptr;
+    if (!gq8_tensor_is_norm(&d->shape, index))
+        GQ8_HIP(hipMalloc(&staging, std::min(piece, elements) * sizeof(float)));
+    int status = GQ8_OK;
+    for (int64_t first = 0; first < elements && status == GQ8_OK; first += piece) {
+        const int64_t count = std::min(piece, elements - first);
+        status = upload_values(d, index, host_values + first, first, count, staging);
+        if (status == GQ8_OK && hipStreamSynchronize(d->stream) != hipSuccess)
+            status = fail(GQ8_ERR_DEVICE, "load_tensor: synchronize failed");
+    }
+    if (staging)
+        (void) hipFree(staging);
+    return status == GQ8_OK ? mark_present(d, index) : status;
+}
+
+extern "C" int gq8_decoder_load_tensor_q8(gq8_decoder *d, int index, const uint8_t *host_bytes)
+{
+    if (!d || !host_bytes || index < 0 || index >= gq8_tensor_count(&d->shape))
+        return fail(GQ8_ERR_ARGUMENT, "load_tensor_q8: bad arguments");
+    if (gq8_tensor_is_norm(&d->shape, index))
+        return fail(GQ8_ERR_ARGUMENT, "load_tensor_q8: norms are fp32 tensors");
+    Placement p = placement(d, index);
+    GQ8_HIP(hipMemcpy(p.q, host_bytes, p.elements, hipMemcpyHostToDevice));
+    GQ8_HIP(hipMemcpy(p.scales, host_bytes + p.elements, p.elements / 16, hipMemcpyHostToDevice));
+    return mark_present(d, index);
+}
+
+extern "C" int gq8_decoder_fill_synthetic(gq8_decoder *d, int threads)
+{
+    if (!d)
+        return fail(GQ8_ERR_ARGUMENT, "fill_synthetic: null decoder");
+    threads = hardware_threads(threads);
+    const int64_t piece = int64_t(64) << 20; // a whole number of 2^20 chunks
+    float *host = nullptr;
+    float *staging = nullptr;
+    GQ8_HIP(hipHostMalloc((void **) &host, piece * sizeof(float)));
+    if (hipMalloc(&staging, piece * sizeof(float)) != hipSuccess) {
+        (void) hipHostFree(host);
+        return fail(GQ8_ERR_MEMORY, "fill_synthetic: staging allocation failed");
+    }
+    int status = GQ8_OK;
+    for (int index = 0; index < gq8_tensor_count(&d->shape) && status == GQ8_OK; ++index) {
+        const int64_t elements = gq8_tensor_elements(&d->shape, index);
+        const uint64_t seed = 0x5EED0000ULL + (uint64_t) index;
+        const double sigma = gq8_tensor_is_norm(&d->shape, index) ? 0.1 : 0.02;
+        for (int64_t first = 0; first < elements && status == GQ8_OK; first += piece) {
+            const int64_t count = std::min(piece, elements - first);
+            const int64_t chunk0 = first / kChunk;
+            const int64_t chunks = (count + kChunk - 1) / kChunk;
+            // the previous piece's copy reads `host`: finish it before refilling
+            if (hipStreamSynchronize(d->stream) != hipSuccess) {
+                status = fail(GQ8_ERR_DEVICE, "fill_synthetic: synchronize failed");
+                break;
+            }
+            parallel_for(chunks, threads, [&](int64_t c) {
+                normal_chunk(seed, sigma, chunk0 + c, elements, host + c * kChunk);
+            });
+            status = upload_values(d, index, host, first, count, staging);
+        }
+        if (status == GQ8_OK)
+            mark_present(d, index);
+    }
+    if (hipStreamSynchronize(d->stream) != hipSuccess && status == GQ8_OK)
+        status = fail(GQ8_ERR_DEVICE, "fill_synthetic: synchronize failed");
+    (void) hipFree(staging);
+    (void) hipHostFree(host);
+    return status;
+}
+
+extern "C" int gq8_normal_fill_host(uint64_t tensor_seed, double sigma, float *out, int64_t count)
+{
+    if (count < 0 || (count > 0 && !out))
+        return fail(GQ8_ERR_ARGUMENT, "normal_fill_host: bad arguments");
+    const int64_t chunks = (count + kChunk - 1) / kChunk;
+    parallel_for(chunks, hardware_threads(0), [&](int64_t c) {
+        normal_chunk(tensor_seed, sigma, c, count, out + c * kChunk);
+    });
+    return GQ8_OK;
+}
+
+extern "C" int gq8_prompt_ids(uint64_t seed, int vocab, int count, int32_t *out)
+{
+    if (vocab <= 0 || count < 0 || (count > 0 && !out))
+        return fail(GQ8_ERR_ARGUMENT, "prompt_ids: bad arguments");
+    std::mt19937_64 engine(seed);
+    for (int i = 0; i < count; ++i)
+        out[i] = (int32_t) (engine() % (uint64_t) vocab);
+    return GQ8_OK;
+}
+
+extern "C" int gq8_decoder_read_tensor(gq8_decoder *d, int index, void *host_out, size_t bytes)
+{
+    if (!d || !host_out || index < 0 || index >= gq8_tensor_count(&d->shape))
+        return fail(GQ8_ERR_ARGUMENT, "read_tensor: bad arguments");
+    Placement p = placement(d, index);
+    if (p.values) {
+        if (bytes < (size_t) p.elements * sizeof(float))
+            return fail(GQ8_ERR_ARGUMENT, "read_tensor: buffer too small");
+        GQ8_HIP(hipMemcpy(host_out, p.values, p.elements * sizeof(float), hipMemcpyDeviceToHost));
+        return GQ8_OK;
+    }
+    if (bytes < (size_t) gq8_int8_blocks_byte_count(p.elements))
+        return fail(GQ8_ERR_ARGUMENT, "read_tensor: buffer too small");
+    uint8_t *h = reinterpret_cast<uint8_t *>(host_out);
+    GQ8_HIP(hipMemcpy(h, p.q, p.elements, hipMemcpyDeviceToHost));
+    GQ8_HIP(hipMemcpy(h + p.elements, p.scales, p.elements / 16, hipMemcpyDeviceToHost));
+    return GQ8_OK;
+}
+
+extern "C" int gq8_decoder_begin_sequence(gq8_decoder *d)
+{
+    if (!d)
+        return fail(GQ8_ERR_ARGUMENT, "null decoder");
+    GQ8_HIP(hipStreamSynchronize(d->stream));
+    d->hostPosition = 0;
+    const int zero = 0;
+    GQ8_HIP(hipMemcpy(d->position, &zero, sizeof(int), hipMemcpyHostToDevice));
+    return GQ8_OK;
+}
+
+extern "C" int gq8_decoder_position(const gq8_decoder *d)
+{
+    return d ? d->hostPosition : -1;
+}
+
+extern "C" int gq8_decoder_set_debug(gq8_decoder *d, int enabled)
+{
+    if (!d)
+        return fail(GQ8_ERR_ARGUMENT, "null decoder");
+    d->debug = enabled != 0;
+    return GQ8_OK;
+}
+
+namespace {
+
+// The last row of a Q8 row buffer of `rows` x `inner` into a one-row buffer.
+int copy_last_q8_row(gq8_decoder *d, const uint8_t *x8, int rows, int inner, uint8_t *dst)
+{
+    const int64_t elements = (int64_t) rows * inner;
+    GQ8_HIP(hipMemcpyAsync(dst, x8 + (int64_t) (rows - 1) * inner, inner, hipMemcpyDeviceToDevice,
+                           d->stream));
+    GQ8_HIP(hipMemcpyAsync(dst + inner, x8 + elements + 2 * (int64_t) (rows - 1) * (inner / 32),
+                           inner / 16, hipMemcpyDeviceToDevice, d->stream));
+    return GQ8_OK;
+}
+
+int capture_debug(gq8_decoder *d, int which, int layer, const float *rowsValues, int rows,
+                  int inner, const uint8_t *x8)
+{
+    const int64_t slot = (int64_t) layer * 4 + which;
+    float *dst = d->debugValues + slot * d->maxInner;
+    GQ8_HIP(hipMemcpyAsync(dst, rowsValues + (int64_t) (rows - 1) * inner, inner * sizeof(float),
+                           hipMemcpyDeviceToDevice, d->stream));
+    if (x8)
+        return copy_last_q8_row(d, x8, rows, inner,
+                                d->debugQ8 + slot * gq8::q8_bytes(1, d->maxInner));
+    return GQ8_OK;
+}
+
+enum Stage {
+    kStageEmbed = 0, kStageNorm, kStageQkv, kStageRope, kStageAttention, kStageO, kStageGateUp,
+    kStageGeglu, kStageDown, kStageLogits, kStageArgmax
+};
+
+hipEvent_t take_event(gq8_decoder *d)
+{
+    if (!d->spareEvents.empty()) {
+        hipEvent_t e = d->spareEvents.back();
+        d->spareEvents.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess)
+        return nullptr;
+    return e;
+}
+
+// Brackets one launch group with events on the decoder's stream while
+// stage timing is on and the step is not being captured.
+struct StageTimer {
+    gq8_decoder *d;
+    int stage;
+    hipEvent_t start = nullptr;
+    StageTimer(gq8_decoder *decoder, int s) : d(decoder), stage(s)
+    {
+        if (d->timing && !d->capturing) {
+            start = take_event(d);
+            if (start)
+                (void) hipEventRecord(start, d->stream);
+        }
+    }
+    ~StageTimer()
+    {
+        if (!start)
+            return;
+        hipEvent_t stop = take_event(d);
+        if (!stop) {
+            d->spareEvents.push_back(start);
+            return;
+        }
+        (void) hipEventRecord(stop, d->stream);
+        d->marks.push_back({stage, start, stop});
+    }
+};
+
+#define GQ8_STAGE(stage, expr)                    \
+    do {                                          \
+        StageTimer timer_(d, stage);              \
+        GQ8_LAUNCH(expr);                         \
+    } while (0)
+
+// Decoder::step's recording (Decoder.cpp:579-706) for `rows` tokens read
+// from the sequence slots at the device position; logits of the last
+// logitsRows rows; with sample, the argmax of the last row is written to the
+// slot after the step; the device position advances by rows.
+int encode_step(gq8_decoder *d, int rows, float *logits, int logitsRows, bool sample)
+{
+    const gq8_shape &s = d->shape;
+    const int W = s.width, F = s.intermediate;
+    hipStream_t st = d->stream;
+    const float attentionScale = 1.f / std::sqrt((float) s.head_dim);
+    const bool dbg = d->debug;
+
+    GQ8_STAGE(kStageEmbed, gq8::launch_embed(d->sequence, d->position, rows, d->embedding, s.vocab, W,
+                                 s.embedding_scale, d->hidden, st));
+
+    for (int l = 0; l < s.layers; ++l) {
+        const size_t layerCache = (size_t) l * s.max_positions * d->kvWidth;
+        uint16_t *keys = d->keyCache + layerCache;
+        uint16_t *values = d->valueCache + layerCache;
+
+        GQ8_STAGE(kStageNorm, gq8::launch_rmsnorm(d->hidden, d->inputNorm[l], rows, W, s.rms_epsilon,
+                                       dbg ? d->debugNormalised : nullptr, d->x8, st));
+        if (dbg && capture_debug(d, 0, l, d->debugNormalised, rows, W, d->x8))
+            return GQ8_ERR_DEVICE;
+        GQ8_STAGE(kStageQkv, gq8::launch_q8_product(d->x8, rows, 0, rows, d->qkv[l], W, d->qkvWidth,
+                                          d->qkvRows, d->qkvWidth, 0, st));
+        GQ8_STAGE(kStageRope, gq8::launch_rope_kv(d->qkvRows, d->qkvWidth, s.heads, s.kv_heads, s.head_dim,
+                                       d->position, 0, rows, d->cosines, d->sines, keys, values,
+                                       st));
+        GQ8_STAGE(kStageAttention, gq8::launch_mqa(d->qkvRows, d->qkvWidth, keys, values, s.heads, s.kv_heads,
+                                   s.head_dim, rows, d->position, 0, s.max_positions,
+                                   attentionScale, dbg ? d->debugAttended : nullptr, d->x8,
+                                   d->attentionWorkspace, d->attentionWorkspaceBytes, st));
+        if (dbg && capture_debug(d, 1, l, d->debugAttended, rows, d->qWidth, d->x8))
+            return GQ8_ERR_DEVICE;
+        GQ8_STAGE(kStageO, gq8::launch_q8_product(d->x8, rows, 0, rows, d->out[l], d->qWidth, W,
+                                          d->hidden, W, 1, st));
+        GQ8_STAGE(kStageNorm, gq8::launch_rmsnorm(d->hidden, d->postNorm[l], rows, W, s.rms_epsilon,
+                                       nullptr, d->x8, st));
+        GQ8_STAGE(kStageGateUp, gq8::launch_q8_product(d->x8, rows, 0, rows, d->gateUp[l], W, 2 * F, d->fused,
+                                          2 * F, 0, st));
+        GQ8_STAGE(kStageGeglu, gq8::launch_geglu(d->fused, rows, F, dbg ? d->debugActivated : nullptr, d->x8,
+                                     st));
+        if (dbg && capture_debug(d, 2, l, d->debugActivated, rows, F, d->x8))
+            return GQ8_ERR_DEVICE;
+        GQ8_STAGE(kStageDown, gq8::launch_q8_product(d->x8, rows, 0, rows, d->down[l], F, W, d->hidden, W,
+                                          1, st));
+        if (dbg && capture_debug(d, 3, l, d->hidden, rows, W, nullptr))
+            return GQ8_ERR_DEVICE;
+    }
+
+    GQ8_STAGE(kStageNorm, gq8::launch_rmsnorm(d->hidden, d->finalNorm, rows, W, s.rms_epsilon,
+                                   d->normalisedRows, d->x8, st));
+    if (dbg && capture_debug(d, 0, s.layers, d->normalisedRows, rows, W, d->x8))
+        return GQ8_ERR_DEVICE;
+    if (logits && logitsRows > 0)
+        GQ8_STAGE(kStageLogits, gq8::launch_q8_product(d->x8, rows, rows - logitsRows, logitsRows,
+                                          d->embedding, W, s.vocab, logits, s.vocab, 0, st));
+    if (sample)
+        GQ8_STAGE(kStageArgmax, gq8::launch_argmax(logits + (int64_t) (logitsRows - 1) * s.vocab, nullptr, 1,
+                                      s.vocab, d->sequence, d->position, rows,
+                                      d->argmaxWorkspace, d->argmaxWorkspaceBytes, st));
+    GQ8_LAUNCH(gq8::launch_advance(d->position, rows, st));
+    return GQ8_OK;
+}
+
+int check_step(gq8_decoder *d, int rows)
+{
+    for (size_t i = 0; i < d->present.size(); ++i)
+        if (!d->present[i])
+            return fail(GQ8_ERR_NOT_PREPARED, "tensor " + std::to_string(i) + " was never loaded");
+    if (rows <= 0)
+        return fail(GQ8_ERR_EMPTY, "a decoder step needs at least one token");
+    if (rows > d->capacity)
+        return fail(GQ8_ERR_CAPACITY, "this step carries " + std::to_string(rows)
+                                          + " rows and the step capacity is "
+                                          + std::to_string(d->capacity));
+    if (d->hostPosition + rows > d->shape.max_positions)
+        return fail(GQ8_ERR_WINDOW, "this step would carry the sequence to "
+                                        + std::to_string(d->hostPosition + rows)
+                                        + " tokens, past the window of "
+                                        + std::to_string(d->shape.max_positions));
+    return GQ8_OK;
+}
+
+} // namespace
+
+extern "C" int gq8_decoder_step(gq8_decoder *d, const uint32_t *tokens, int n, float *logits,
+                                int logits_rows)
+{
+    if (!d || !tokens)
+        return fail(GQ8_ERR_ARGUMENT, "decoder_step: null argument");
+    if (int s = check_step(d, n))
+        return s;
+    if (logits && logits_rows != 1 && logits_rows != n)
+        return fail(GQ8_ERR_ARGUMENT, "decoder_step: logits_rows is 1 or n");
+    // token ids are validated here: the reference validates the prompt
+    // (Gemma.cpp:418-424); a step's ids are checked the same way.
+    std::vector<uint32_t> ids(n);
+    GQ8_HIP(hipMemcpy(ids.data(), tokens, n * sizeof(uint32_t), hipMemcpyDeviceToHost));
+    for (uint32_t id : ids)
+        if (id >= (uint32_t) d->shape.vocab)
+            return fail(GQ8_ERR_TOKEN, "token " + std::to_string(id) + " is outside a vocabulary of "
+                                           + std::to_string(d->shape.vocab));
+    GQ8_HIP(hipMemcpyAsync(d->sequence + d->hostPosition, ids.data(), n * sizeof(uint32_t),
+                           hipMemcpyHostToDevice, d->stream));
+    if (int s = encode_step(d, n, logits, logits ? logits_rows : 0, false))
+        return s;
+    GQ8_HIP(hipStreamSynchronize(d->stream));
+    d->hostPosition += n;
+    return GQ8_OK;
+}
+
+extern "C" int gq8_decoder_hidden(gq8_decoder *d, float *host_out, int rows)
+{
+    if (!d || !host_out || rows <= 0 || rows > d->capacity)
+        return fail(GQ8_ERR_ARGUMENT, "decoder_hidden: bad arguments");
+    GQ8_HIP(hipMemcpy(host_out, d->normalisedRows, (size_t) rows * d->shape.width * sizeof(float),
+                      hipMemcpyDeviceToHost));
+    return GQ8_OK;
+}
+
+extern "C" int gq8_decoder_debug(gq8_decoder *d, int which, int layer, float *host_values,
+                                 uint8_t *host_q8)
+{
+    if (!d || which < 0 || which > 3 || layer < 0 || layer > d->shape.layers)
+        return fail(GQ8_ERR_ARGUMENT, "decoder_debug: bad arguments");
+    const int inner = which == 1 ? d->qWidth : (which == 2 ? d->shape.intermediate : d->shape.width);
+    const int64_t slot = (int64_t) layer * 4 + which;
+    if (host_values)
+        GQ8_HIP(hipMemcpy(host_values, d->debugValues + slot * d->maxInner, inner * sizeof(float),
+                          hipMemcpyDeviceToHost));
+    if (host_q8)
+        GQ8_HIP(hipMemcpy(host_q8, d->debugQ8 + slot * gq8::q8_bytes(1, d->maxInner),
+                          gq8::q8_bytes(1, inner), hipMemcpyDeviceToHost));
+    return GQ8_OK;
+}
+
+// ============================================================================
+// Greedy loop (Gemma::generate at temperature 0, Gemma.cpp:395-543)
+// ============================================================================
+namespace {
+
+int ensure_graph(gq8_decoder *d)
+{
+    if (d->graph)
+        return GQ8_OK;
+    // One decode step reads its token and position from device memory and
+    // advances the position itself, so the same graph replays at every step.
+    hipGraph_t graph = nullptr;
+    GQ8_HIP(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
+    const bool debug = d->debug;
+    d->debug = false;
+    d->capturing = true;
+    const int status = encode_step(d, 1, d->logits, 1, true);
+    d->capturing = false;
+    d->debug = debug;
+    hipError_t end = hipStreamEndCapture(d->stream, &graph);
+    if (status != GQ8_OK) {
+        if (graph)
+            (void) hipGraphDestroy(graph);
+        return status;
+    }
+    if (end != hipSuccess)
+        return fail(GQ8_ERR_DEVICE, std::string("hipStreamEndCapture: ") + hipGetErrorString(end));
+    hipError_t inst = hipGraphInstantiate(&d->graph, graph, nullptr, nullptr, 0);
+    (void) hipGraphDestroy(graph);
+    if (inst != hipSuccess) {
+        d->graph = nullptr;
+        return fail(GQ8_ERR_DEVICE, std::string("hipGraphInstantiate: ") + hipGetErrorString(inst));
+    }
+    return GQ8_OK;
+}
+
+int decode_one(gq8_decoder *d, bool useGraph)
+{
+    if (int s = check_step(d, 1))
+        return s;
+    if (useGraph) {
+        GQ8_HIP(hipGraphLaunch(d->graph, d->stream));
+    } else if (int s = encode_step(d, 1, d->logits, 1, true)) {
+        return s;
+    }
+    d->hostPosition += 1;
+    return GQ8_OK;
+}
+
+int read_slot(gq8_decoder *d, int slot, uint32_t *value)
+{
+    GQ8_HIP(hipMemcpyAsync(d->pinnedToken, d->sequence + slot, sizeof(uint32_t),
+                           hipMemcpyDeviceToHost, d->stream));
+    GQ8_HIP(hipStreamSynchronize(d->stream));
+    *value = d->pinnedToken[0];
+    return GQ8_OK;
+}
+
+} // namespace
+
+extern "C" int gq8_generate(gq8_decoder *d, const int32_t *prompt, int prompt_length,
+                            int max_tokens, int eos, int use_graph, int32_t *out,
+                            gq8_run_stats *stats)
+{
+    using Clock = std::chrono::steady_clock;
+    if (!d || !prompt || !out)
+        return fail(GQ8_ERR_ARGUMENT, "generate: null argument");
+    const gq8_shape &s = d->shape;
+    if (prompt_length <= 0)
+        return fail(GQ8_ERR_EMPTY, "a run needs at least one prompt token");
+    if (prompt_length > s.max_positions)
+        return fail(GQ8_ERR_WINDOW, "the prompt is longer than the window");
+    for (int i = 0; i < prompt_length; ++i)
+        if (prompt[i] < 0 || prompt[i] >= s.vocab)
+            return fail(GQ8_ERR_TOKEN, "prompt token " + std::to_string(prompt[i])
+                                           + " is outside a vocabulary of "
+                                           + std::to_string(s.vocab));
+    for (size_t i = 0; i < d->present.size(); ++i)
+        if (!d->present[i])
+            return fail(GQ8_ERR_NOT_PREPARED, "tensor " + std::to_string(i) + " was never loaded");
+
+    if (int st = gq8_decoder_begin_sequence(d))
+        return st;
+    GQ8_HIP(hipMemcpy(d->sequence, prompt, prompt_length * sizeof(uint32_t), hipMemcpyHostToDevice));
+    if (use_graph)
+        if (int st = ensure_graph(d))
+            return st;
+
+    const int window = s.max_positions - prompt_length;
+    const int limit = max_tokens > 0 ? std::min(max_tokens, window) : window;
+    gq8_run_stats local{};
+    int steps = 0;
+
+    // the prefill, in blocks of the step capacity (Gemma.cpp:350-380)
+    const auto prefillStart = Clock::now();
+    for (int first = 0; first < prompt_length; first += d->capacity) {
+        const int rows = std::min(d->capacity, prompt_length - first);
+        const bool last = first + rows >= prompt_length;
+        if (int st = check_step(d, rows))
+            return st;
+        if (int st = encode_step(d, rows, last ? d->logits : nullptr, last ? 1 : 0,
+                                 last && limit > 0))
+            return st;
+        d->hostPosition += rows;
+        ++steps;
+    }
+    GQ8_HIP(hipStreamSynchronize(d->stream));
+    local.prefill_seconds = std::chrono::duration<double>(Clock::now() - prefillStart).count();
+
+    int count = 0;
+    const auto decodeStart = Clock::now();
+    if (limit > 0 && eos < 0) {
+        // nothing can stop the run early: every step is enqueued back to back
+        for (int step = 1; step < limit; ++step) {
+            if (int st = decode_one(d, use_graph != 0))
+                return st;
+            ++steps;
+        }
+        GQ8_HIP(hipStreamSynchronize(d->stream));
+        std::vector<uint32_t> ids(limit);
+        GQ8_HIP(hipMemcpy(ids.data(), d->sequence + prompt_length, limit * sizeof(uint32_t),
+                          hipMemcpyDeviceToHost));
+        for (int i = 0; i < limit; ++i)
+            out[i] = (int32_t) ids[i];
+        count = limit;
+    } else if (limit > 0) {
+        // Gemma::generateGreedily (Gemma.cpp:459-543): two steps in flight;
+        // step k's token is copied to a pinned slot behind an event of its
+        // own, so reading it waits for step k alone while step k + 1 runs.
+        hipEvent_t ready[2] = {nullptr, nullptr};
+        for (auto &e : ready)
+            GQ8_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        auto finish = [&](int status) {
+            (void) hipStreamSynchronize(d->stream);
+            for (auto &e : ready)
+                (void) hipEventDestroy(e);
+            return status;
+        };
+        auto startStep = [&](int step) -> int {
+            if (int st = decode_one(d, use_graph != 0))
+                return st;
+            GQ8_HIP(hipMemcpyAsync(d->pinnedToken + (step & 1), d->sequence + prompt_length + step,
+                                   sizeof(uint32_t), hipMemcpyDeviceToHost, d->stream));
+            GQ8_HIP(hipEventRecord(ready[step & 1], d->stream));
+            ++steps;
+            return GQ8_OK;
+        };
+        int nextStep = 1;
+        if (nextStep < limit) {
+            if (int st = startStep(nextStep))
+                return finish(st);
+            ++nextStep;
+        }
+        for (int step = 0; step < nextStep; ++step) {
+            uint32_t token = 0;
+            if (step == 0) {
+                // the prefill's argmax, already complete
+                GQ8_HIP(hipMemcpy(&token, d->sequence + prompt_length, sizeof(uint32_t),
+                                  hipMemcpyDeviceToHost));
+            } else {
+                if (hipEventSynchronize(ready[step & 1]) != hipSuccess)
+                    return finish(fail(GQ8_ERR_DEVICE, "generate: event wait failed"));
+                token = d->pinnedToken[step & 1];
+            }
+            if ((int) token == eos)
+                break;
+            out[count++] = (int32_t) token;
+            if (nextStep < limit) {
+                if (int st = startStep(nextStep))
+                    return finish(st);
+                ++nextStep;
+            }
+        }
+        finish(GQ8_OK);
+    }
+    local.decode_seconds = std::chrono::duration<double>(Clock::now() - decodeStart).count();
+    local.step_count = steps;
+    local.generated = count;
+    if (stats)
+        *stats = local;
+    return count;
+}
+
+extern "C" int gq8_decoder_decode(gq8_decoder *d, int steps, int use_graph)
+{
+    if (!d || steps < 0)
+        return fail(GQ8_ERR_ARGUMENT, "decoder_decode: bad arguments");
+    if (d->hostPosition + steps > d->shape.max_positions)
+        return fail(GQ8_ERR_WINDOW, "decoder_decode: the steps would pass the window");
+    if (use_graph)
+        if (int st = ensure_graph(d))
+            return st;
+    for (int i = 0; i < steps; ++i)
+        if (int st = decode_one(d, use_graph != 0))
+            return st;
+    GQ8_HIP(hipStreamSynchronize(d->stream));
+    return GQ8_OK;
+}
+
+extern "C" int gq8_decoder_tokens(gq8_decoder *d, int first, int count, int32_t *host_out)
+{
+    if (!d || !host_out || first < 0 || count < 0 || first + count > d->shape.max_positions + 1)
+        return fail(GQ8_ERR_ARGUMENT, "decoder_tokens: bad range");
+    GQ8_HIP(hipStreamSynchronize(d->stream));
+    GQ8_HIP(hipMemcpy(host_out, d->sequence + first, count * sizeof(uint32_t),
+                      hipMemcpyDeviceToHost));
+    return GQ8_OK;
+}
+
+extern "C" int gq8_decoder_set_timing(gq8_decoder *d, int enabled)
+{
+    if (!d)
+        return fail(GQ8_ERR_ARGUMENT, "null decoder");
+    d->timing = enabled != 0;
+    return GQ8_OK;
+}
+
+extern "C" int gq8_decoder_timing(gq8_decoder *d, double *milliseconds, int *launches)
+{
+    if (!d || !milliseconds || !launches)
+        return fail(GQ8_ERR_ARGUMENT, "decoder_timing: null argument");
+    GQ8_HIP(hipStreamSynchronize(d->stream));
+    for (int i = 0; i < GQ8_STAGE_COUNT; ++i) {
+        milliseconds[i] = 0.0;
+        launches[i] = 0;
+    }
+    for (auto &m : d->marks) {
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, m.start, m.stop) == hipSuccess && m.stage >= 0
+            && m.stage < GQ8_STAGE_COUNT) {
+            milliseconds[m.stage] += ms;
+            launches[m.stage] += 1;
+        }
+        d->spareEvents.push_back(m.start);
+        d->spareEvents.push_back(m.stop);
+    }
+    d->marks.clear();
+    return GQ8_OK;
+}

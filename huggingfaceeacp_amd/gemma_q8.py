@@ -1,0 +1,446 @@
+"""Python mirror of the reference's decoder interface over libgemma_q8.so.
+
+The shipped compute path is the C ABI in include/gemma_q8.h (gfx950 HIP
+kernels plus the C++ decoder runtime).  This module only binds it with ctypes,
+with the reference's names: ``DecoderShape`` (Lib/HuggingFaceEACP/Decoder/
+DecoderShape.h:42-110), ``Decoder`` (Decoder.h:69-319: prepare, beginSequence,
+step, position, hiddenStates) and ``Gemma.generate`` (Generation/Gemma.h:
+65-342, greedy).  Device buffers passed to the op-level functions are raw
+pointers (torch tensors' ``data_ptr()`` in the tests).
+
+There is no fallback: if the library is missing, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY_PATH = os.path.join(HERE, "libgemma_q8.so")
+
+OK = 0
+ERR_ARGUMENT, ERR_SHAPE, ERR_CAPACITY, ERR_WINDOW, ERR_TOKEN = -1, -2, -3, -4, -5
+ERR_UNQUANTIZABLE, ERR_NOT_PREPARED, ERR_EMPTY, ERR_DEVICE, ERR_MEMORY = -6, -7, -8, -9, -10
+
+# GemmaTensors::all order (GemmaTensors.cpp:30-57)
+T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN, T_INPUT_NORM, T_POST_NORM = range(9)
+PER_LAYER = 9
+
+
+# stage indices of gq8_decoder_timing
+STAGES = ["embed", "norm", "qkv", "rope_kv", "attention", "o_proj", "gate_up", "geglu",
+          "down", "lm_head", "argmax"]
+
+
+class Gq8Error(RuntimeError):
+    """A refusal or failure reported by libgemma_q8 (the reference's ModelError)."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[{status}] {message}")
+        self.status = status
+
+
+class _Shape(ctypes.Structure):
+    _fields_ = [
+        ("width", ctypes.c_int), ("heads", ctypes.c_int), ("kv_heads", ctypes.c_int),
+        ("head_dim", ctypes.c_int), ("layers", ctypes.c_int), ("intermediate", ctypes.c_int),
+        ("vocab", ctypes.c_int), ("max_positions", ctypes.c_int),
+        ("max_step_rows", ctypes.c_int), ("rms_epsilon", ctypes.c_float),
+        ("rope_theta", ctypes.c_double), ("embedding_scale", ctypes.c_float),
+    ]
+
+
+class _RunStats(ctypes.Structure):
+    _fields_ = [("prefill_seconds", ctypes.c_double), ("decode_seconds", ctypes.c_double),
+                ("step_count", ctypes.c_int), ("generated", ctypes.c_int)]
+
+
+_lib = None
+
+
+def library() -> ctypes.CDLL:
+    """Load libgemma_q8.so (built in-tree); raise if it is not there."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIBRARY_PATH):
+        raise RuntimeError(f"{LIBRARY_PATH} is not built: run `python -m huggingfaceeacp_amd.build`"
+                           " (the HIP path has no fallback)")
+    L = ctypes.CDLL(LIBRARY_PATH)
+    P, i32, i64, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
+    f32, f64 = ctypes.c_float, ctypes.c_double
+    sig = {
+        "gq8_status_string": (ctypes.c_char_p, [i32]),
+        "gq8_last_error": (ctypes.c_char_p, []),
+        "gq8_version": (ctypes.c_char_p, []),
+        "gq8_int8_block_count": (i64, [i64]),
+        "gq8_int8_blocks_byte_count": (i64, [i64]),
+        "gq8_quantizes_as_int8_blocks": (i32, [i64, i64]),
+        "gq8_quantize_int8_blocks_host": (i32, [P, i64, i64, i64, P]),
+        "gq8_dequantize_int8_blocks_host": (i32, [P, i64, P]),
+        "gq8_rotary_table_host": (i32, [i32, i32, f64, P, P]),
+        "gq8_quantize_rows": (i32, [P, i64, i64, P, P]),
+        "gq8_embed": (i32, [P, i32, P, i32, i32, f32, P, P]),
+        "gq8_rmsnorm": (i32, [P, P, i32, i32, f32, P, P, P]),
+        "gq8_rope": (i32, [P, i32, i32, i32, i32, i32, P, P, P]),
+        "gq8_q8_product": (i32, [P, P, i32, i32, i32, P, i32, i32, P]),
+        "gq8_kv_store_f16": (i32, [P, P, i32, i32, i32, P, P, i32, P]),
+        "gq8_mqa_workspace_bytes": (sz, [i32, i32, i32, i32]),
+        "gq8_mqa_decode": (i32, [P, P, P, i32, i32, i32, i32, f32, P, P, sz, P]),
+        "gq8_mqa_prefill": (i32, [P, P, P, i32, i32, i32, i32, i32, f32, P, P, sz, P]),
+        "gq8_geglu": (i32, [P, i32, i32, P, P, P]),
+        "gq8_argmax_workspace_bytes": (sz, [i32, i32]),
+        "gq8_argmax_rows": (i32, [P, P, i32, i32, P, P, sz, P]),
+        "gq8_shape_validate": (i32, [P]),
+        "gq8_gemma_2b_shape": (_Shape, [i32, i32, i32]),
+        "gq8_decoder_create": (i32, [P, ctypes.POINTER(P)]),
+        "gq8_decoder_destroy": (None, [P]),
+        "gq8_tensor_count": (i32, [P]),
+        "gq8_tensor_elements": (i64, [P, i32]),
+        "gq8_tensor_is_norm": (i32, [P, i32]),
+        "gq8_decoder_load_tensor": (i32, [P, i32, P]),
+        "gq8_decoder_load_tensor_q8": (i32, [P, i32, P]),
+        "gq8_decoder_fill_synthetic": (i32, [P, i32]),
+        "gq8_decoder_read_tensor": (i32, [P, i32, P, sz]),
+        "gq8_decoder_begin_sequence": (i32, [P]),
+        "gq8_decoder_position": (i32, [P]),
+        "gq8_decoder_step": (i32, [P, P, i32, P, i32]),
+        "gq8_decoder_hidden": (i32, [P, P, i32]),
+        "gq8_decoder_set_debug": (i32, [P, i32]),
+        "gq8_decoder_debug": (i32, [P, i32, i32, P, P]),
+        "gq8_generate": (i32, [P, P, i32, i32, i32, i32, P, ctypes.POINTER(_RunStats)]),
+        "gq8_decoder_decode": (i32, [P, i32, i32]),
+        "gq8_prompt_ids": (i32, [ctypes.c_uint64, i32, i32, P]),
+        "gq8_normal_fill_host": (i32, [ctypes.c_uint64, f64, P, i64]),
+        "gq8_decoder_tokens": (i32, [P, i32, i32, P]),
+        "gq8_decoder_set_timing": (i32, [P, i32]),
+        "gq8_decoder_timing": (i32, [P, P, P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def check(status: int) -> int:
+    """Raise Gq8Error for a negative status, return it otherwise."""
+    if status < 0:
+        msg = library().gq8_last_error().decode(errors="replace")
+        raise Gq8Error(status, msg or library().gq8_status_string(status).decode())
+    return status
+
+
+def _host(a: np.ndarray):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+# ---- op-level entry points (device pointers as ints) --------------------------
+def quantize_rows(x, rows, inner, q8, stream=0):
+    return check(library().gq8_quantize_rows(x, rows, inner, q8, stream))
+
+
+def embed(tokens, rows, table, vocab, width, scale, out, stream=0):
+    return check(library().gq8_embed(tokens, rows, table, vocab, width, scale, out, stream))
+
+
+def rmsnorm(x, weight, rows, width, epsilon, y, q8, stream=0):
+    return check(library().gq8_rmsnorm(x, weight, rows, width, epsilon, y, q8, stream))
+
+
+def rope(x, row_stride, heads, head_dim, first_position, rows, cosines, sines, stream=0):
+    return check(library().gq8_rope(x, row_stride, heads, head_dim, first_position, rows,
+                                    cosines, sines, stream))
+
+
+def q8_product(x8, w8, rows, inner, outputs, y, y_stride, residual=False, stream=0):
+    return check(library().gq8_q8_product(x8, w8, rows, inner, outputs, y, y_stride,
+                                          int(residual), stream))
+
+
+def kv_store_f16(k, v, src_stride, rows, kv_width, key_cache, value_cache, position, stream=0):
+    return check(library().gq8_kv_store_f16(k, v, src_stride, rows, kv_width, key_cache,
+                                            value_cache, position, stream))
+
+
+def mqa_workspace_bytes(rows, heads, head_dim, max_keys):
+    return int(library().gq8_mqa_workspace_bytes(rows, heads, head_dim, max_keys))
+
+
+def mqa_decode(query, keys, values, heads, kv_heads, head_dim, key_count, scale, out,
+               workspace, workspace_bytes, stream=0):
+    return check(library().gq8_mqa_decode(query, keys, values, heads, kv_heads, head_dim,
+                                          key_count, scale, out, workspace, workspace_bytes,
+                                          stream))
+
+
+def mqa_prefill(queries, keys, values, heads, kv_heads, head_dim, rows, position_offset, scale,
+                out, workspace, workspace_bytes, stream=0):
+    return check(library().gq8_mqa_prefill(queries, keys, values, heads, kv_heads, head_dim,
+                                           rows, position_offset, scale, out, workspace,
+                                           workspace_bytes, stream))
+
+
+def geglu(fused, rows, intermediate, out, q8, stream=0):
+    return check(library().gq8_geglu(fused, rows, intermediate, out, q8, stream))
+
+
+def argmax_workspace_bytes(rows, length):
+    return int(library().gq8_argmax_workspace_bytes(rows, length))
+
+
+def argmax_rows(logits, mask, rows, length, indices, workspace, workspace_bytes, stream=0):
+    return check(library().gq8_argmax_rows(logits, mask, rows, length, indices, workspace,
+                                           workspace_bytes, stream))
+
+
+# ---- host format helpers ---------------------------------------------------------
+def quantize_int8_blocks_host(values: np.ndarray) -> np.ndarray:
+    values = np.ascontiguousarray(values, dtype=np.float32).ravel()
+    n = values.size
+    out = np.zeros(int(library().gq8_int8_blocks_byte_count(n)), dtype=np.uint8)
+    check(library().gq8_quantize_int8_blocks_host(_host(values), n, 0, n, _host(out)))
+    return out
+
+
+def dequantize_int8_blocks_host(stored: np.ndarray, element_count: int) -> np.ndarray:
+    stored = np.ascontiguousarray(stored, dtype=np.uint8)
+    out = np.zeros(element_count, dtype=np.float32)
+    check(library().gq8_dequantize_int8_blocks_host(_host(stored), element_count, _host(out)))
+    return out
+
+
+def rotary_table_host(max_positions: int, head_dim: int, theta: float = 10000.0):
+    half = head_dim // 2
+    c = np.empty(max_positions * half, dtype=np.float32)
+    s = np.empty(max_positions * half, dtype=np.float32)
+    check(library().gq8_rotary_table_host(max_positions, head_dim, theta, _host(c), _host(s)))
+    return c.reshape(max_positions, half), s.reshape(max_positions, half)
+
+
+# ---- the decoder ----------------------------------------------------------------------
+@dataclass
+class DecoderShape:
+    """DecoderShape (DecoderShape.h:42-110)."""
+    width: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    layers: int
+    intermediate: int
+    vocab: int
+    max_positions: int
+    max_step_rows: int = 0
+    rms_epsilon: float = 1e-6
+    rope_theta: float = 10000.0
+    embedding_scale: float | None = None
+
+    def __post_init__(self):
+        if self.embedding_scale is None:  # sqrtf(hidden_size), GemmaConfig.cpp:123-126
+            self.embedding_scale = float(np.sqrt(np.float32(self.width), dtype=np.float32))
+
+    @staticmethod
+    def gemma_2b(layers: int = 18, max_positions: int = 8192, max_step_rows: int = 512):
+        return DecoderShape(2048, 8, 1, 256, layers, 16384, 256000, max_positions, max_step_rows)
+
+    @property
+    def query_width(self) -> int:
+        return self.heads * self.head_dim
+
+    @property
+    def kv_width(self) -> int:
+        return self.kv_heads * self.head_dim
+
+    def step_capacity(self) -> int:
+        return self.max_step_rows if self.max_step_rows > 0 else self.max_positions
+
+    def attention_scale(self) -> float:
+        return float(np.float32(1.0) / np.sqrt(np.float32(self.head_dim), dtype=np.float32))
+
+    def as_c(self) -> _Shape:
+        return _Shape(self.width, self.heads, self.kv_heads, self.head_dim, self.layers,
+                      self.intermediate, self.vocab, self.max_positions, self.max_step_rows,
+                      self.rms_epsilon, self.rope_theta, self.embedding_scale)
+
+    def validate(self) -> None:
+        c = self.as_c()
+        check(library().gq8_shape_validate(ctypes.byref(c)))
+
+    def tensor_count(self) -> int:
+        c = self.as_c()
+        return int(library().gq8_tensor_count(ctypes.byref(c)))
+
+    def tensor_elements(self, index: int) -> int:
+        c = self.as_c()
+        return int(library().gq8_tensor_elements(ctypes.byref(c), index))
+
+    def tensor_is_norm(self, index: int) -> bool:
+        c = self.as_c()
+        return bool(library().gq8_tensor_is_norm(ctypes.byref(c), index))
+
+
+@dataclass
+class RunStats:
+    prefill_seconds: float
+    decode_seconds: float
+    step_count: int
+    generated: int
+
+
+class Decoder:
+    """HF::Decoder over libgemma_q8: one sequence, fp16 KV caches on the device."""
+
+    def __init__(self, shape: DecoderShape):
+        self.shape = shape
+        self._c_shape = shape.as_c()
+        handle = ctypes.c_void_p()
+        check(library().gq8_decoder_create(ctypes.byref(self._c_shape), ctypes.byref(handle)))
+        self.handle = handle
+
+    def close(self) -> None:
+        if self.handle:
+            library().gq8_decoder_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # TensorLoader counterparts
+    def load_tensor(self, index: int, values: np.ndarray) -> None:
+        values = np.ascontiguousarray(values, dtype=np.float32).ravel()
+        if values.size != self.shape.tensor_elements(index):
+            raise ValueError("tensor size does not match the shape")
+        check(library().gq8_decoder_load_tensor(self.handle, index, _host(values)))
+
+    def load_tensor_q8(self, index: int, stored: np.ndarray) -> None:
+        stored = np.ascontiguousarray(stored, dtype=np.uint8).ravel()
+        check(library().gq8_decoder_load_tensor_q8(self.handle, index, _host(stored)))
+
+    def fill_synthetic(self, threads: int = 0) -> None:
+        check(library().gq8_decoder_fill_synthetic(self.handle, threads))
+
+    def read_tensor(self, index: int) -> np.ndarray:
+        n = self.shape.tensor_elements(index)
+        if self.shape.tensor_is_norm(index):
+            out = np.empty(n, dtype=np.float32)
+        else:
+            out = np.empty(int(library().gq8_int8_blocks_byte_count(n)), dtype=np.uint8)
+        check(library().gq8_decoder_read_tensor(self.handle, index, _host(out), out.nbytes))
+        return out
+
+    # Decoder API
+    def begin_sequence(self) -> None:
+        check(library().gq8_decoder_begin_sequence(self.handle))
+
+    @property
+    def position(self) -> int:
+        return int(library().gq8_decoder_position(self.handle))
+
+    def step(self, tokens_ptr: int, n: int, logits_ptr: int | None, logits_rows: int | None = None):
+        rows = n if logits_rows is None else logits_rows
+        check(library().gq8_decoder_step(self.handle, tokens_ptr, n, logits_ptr or None,
+                                         rows if logits_ptr else 0))
+
+    def hidden_states(self, rows: int) -> np.ndarray:
+        out = np.empty((rows, self.shape.width), dtype=np.float32)
+        check(library().gq8_decoder_hidden(self.handle, _host(out), rows))
+        return out
+
+    def set_debug(self, enabled: bool) -> None:
+        check(library().gq8_decoder_set_debug(self.handle, int(enabled)))
+
+    def debug(self, which: int, layer: int):
+        inner = {0: self.shape.width, 1: self.shape.query_width, 2: self.shape.intermediate,
+                 3: self.shape.width}[which]
+        values = np.empty(inner, dtype=np.float32)
+        q8 = np.empty(inner + inner // 16, dtype=np.uint8)
+        check(library().gq8_decoder_debug(self.handle, which, layer, _host(values), _host(q8)))
+        return values, q8
+
+    def decode(self, steps: int, use_graph: bool = True) -> None:
+        """Continue the greedy loop `steps` tokens (on-device token feedback)."""
+        check(library().gq8_decoder_decode(self.handle, steps, int(use_graph)))
+
+    def tokens(self, first: int, count: int) -> np.ndarray:
+        """The sequence slots [first, first + count) (prompt ids, then chosen ids)."""
+        out = np.empty(count, dtype=np.int32)
+        check(library().gq8_decoder_tokens(self.handle, first, count, _host(out)))
+        return out
+
+    def set_timing(self, enabled: bool) -> None:
+        check(library().gq8_decoder_set_timing(self.handle, int(enabled)))
+
+    def timing(self) -> dict:
+        """{stage: (total milliseconds, launches)} since the last call."""
+        ms = np.zeros(len(STAGES), dtype=np.float64)
+        launches = np.zeros(len(STAGES), dtype=np.int32)
+        check(library().gq8_decoder_timing(self.handle, _host(ms), _host(launches)))
+        return {name: (float(ms[i]), int(launches[i])) for i, name in enumerate(STAGES)}
+
+    # Gemma::generate, greedy
+    def generate(self, prompt, max_tokens: int, eos: int = 1, use_graph: bool = True):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        window = self.shape.max_positions - prompt.size
+        cap = max(1, min(max_tokens, window) if max_tokens > 0 else window)
+        out = np.zeros(cap, dtype=np.int32)
+        stats = _RunStats()
+        count = check(library().gq8_generate(self.handle, _host(prompt), prompt.size, max_tokens,
+                                             eos, int(use_graph), _host(out),
+                                             ctypes.byref(stats)))
+        return out[:count].copy(), RunStats(stats.prefill_seconds, stats.decode_seconds,
+                                            stats.step_count, stats.generated)
+
+
+def normal_fill_host(seed: int, sigma: float, count: int) -> np.ndarray:
+    """The synthetic-weight generator for one tensor (host threads)."""
+    out = np.empty(count, dtype=np.float32)
+    check(library().gq8_normal_fill_host(seed, sigma, _host(out), count))
+    return out
+
+
+def prompt_ids(seed: int, vocab: int, count: int) -> np.ndarray:
+    """Seeded uniform prompt ids (std::mt19937_64(seed), next() % vocab)."""
+    out = np.empty(count, dtype=np.int32)
+    check(library().gq8_prompt_ids(seed, vocab, count, _host(out)))
+    return out
+
+
+def version() -> str:
+    return library().gq8_version().decode()
+
+
+def exported_symbols() -> list[str]:
+    """Every function include/gemma_q8.h declares (parsed from the header)."""
+    import re
+    header = os.path.join(os.path.dirname(HERE), "include", "gemma_q8.h")
+    text = open(header).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gq8_[a-z0-9_]+)\s*\(", text)))
+
+
+def algorithmic_decode_bytes(shape: DecoderShape, attended_length: int) -> int:
+    """Bytes one decode token must move: the Q8 weights (tied lm_head once),
+    the fp32 norm vectors, one embedding row, the fp16 K+V read over
+    attended_length positions and the token's own K+V write."""
+    w = shape.width
+    weights = shape.tensor_elements(0)
+    for i in range(1, shape.tensor_count()):
+        if not shape.tensor_is_norm(i):
+            weights += shape.tensor_elements(i)
+    q8 = weights + weights // 16
+    norms = (2 * shape.layers + 1) * w * 4
+    embed_row = w + w // 16
+    kv_row = shape.layers * 2 * shape.kv_width * 2
+    return q8 + norms + embed_row + kv_row * attended_length + kv_row
+
+
+def log2ceil(n: int) -> int:
+    return int(math.ceil(math.log2(n))) if n > 1 else 0

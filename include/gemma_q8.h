@@ -1,0 +1,258 @@
+/*
+ * gemma_q8.h -- C ABI of the MI355X (gfx950) Gemma-2B Int8Blocks token loop.
+ *
+ * One shared library, huggingfaceeacp_amd/libgemma_q8.so, with two layers:
+ *
+ *   1. op-level entry points, one per kernel of the reference's decoder
+ *      (the headers under Lib/HuggingFaceEACP/Kernels), taking device pointers, sizes and a
+ *      HIP stream (passed as void *);
+ *   2. the decoder runtime: the counterparts of HF::Decoder
+ *      (Lib/HuggingFaceEACP/Decoder/Decoder.h:69-319) and of the greedy loop
+ *      of HF::Gemma (Lib/HuggingFaceEACP/Generation/Gemma.h:65-342).
+ *
+ * Conventions.  Every function returns an int status (GQ8_OK = 0, a negative
+ * gq8_status otherwise) and never throws; gq8_last_error() names the last
+ * failure.  Refusals are checked on the host before anything is launched, so a
+ * refused call leaves every output untouched (the reference throws before it
+ * records: Decoder.cpp:644-675).  Device pointers belong to the caller unless
+ * a function says otherwise.
+ *
+ * Int8Blocks layout (Lib/HuggingFaceEACP/Kernels/Int8Blocks.h:19-31): a tensor
+ * of E elements is one buffer of E + E / 16 bytes: E signed bytes, then E / 32
+ * little-endian fp16 scales, the scale of block b at half index E / 2 + b.  An
+ * activation "Q8 row buffer" of R rows of K is the same layout over R * K
+ * elements.
+ */
+#ifndef GEMMA_Q8_H
+#define GEMMA_Q8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum gq8_status {
+    GQ8_OK = 0,
+    GQ8_ERR_ARGUMENT = -1,      /* null pointer, negative or inconsistent size */
+    GQ8_ERR_SHAPE = -2,         /* DecoderShape::validate refusals (DecoderShape.cpp:41-92) */
+    GQ8_ERR_CAPACITY = -3,      /* rows past the step capacity (Decoder.cpp:655-664) */
+    GQ8_ERR_WINDOW = -4,        /* position + rows past maxPositions (Decoder.cpp:666-675) */
+    GQ8_ERR_TOKEN = -5,         /* token id outside the vocabulary (Gemma.cpp:418-424) */
+    GQ8_ERR_UNQUANTIZABLE = -6, /* quantizesAsInt8Blocks refusal (Int8Blocks.cpp:169-174) */
+    GQ8_ERR_NOT_PREPARED = -7,  /* weights missing (Decoder.cpp:286-300) */
+    GQ8_ERR_EMPTY = -8,         /* a step or prompt of zero tokens (Decoder.cpp:650-651) */
+    GQ8_ERR_DEVICE = -9,        /* a HIP call failed */
+    GQ8_ERR_MEMORY = -10        /* device allocation failed */
+} gq8_status;
+
+const char *gq8_status_string(int status);
+/* The message of the last failure on this thread ("" if none). */
+const char *gq8_last_error(void);
+/* Library identity: "gemma_q8 <version> gfx950". */
+const char *gq8_version(void);
+
+/* ======================================================================= */
+/* Int8Blocks format on the host (Int8Blocks.h:58-88).                     */
+/* ======================================================================= */
+int64_t gq8_int8_block_count(int64_t element_count);       /* Int8Blocks.h:60 */
+int64_t gq8_int8_blocks_byte_count(int64_t element_count); /* Int8Blocks.h:61 */
+/* 1 if a tensor of this shape is storable (Int8Blocks.h:69), else 0. */
+int gq8_quantizes_as_int8_blocks(int64_t contiguous_extent, int64_t element_count);
+/* quantizeInt8Blocks, both overloads (Int8Blocks.h:72-82): values holds
+ * value_count elements starting at element `first` of a tensor of
+ * element_count, destination is that whole tensor's bytes.  Runs on all host
+ * cores (TensorLoader.cpp:190-228). */
+int gq8_quantize_int8_blocks_host(const float *values, int64_t value_count, int64_t first,
+                                  int64_t element_count, uint8_t *destination);
+/* dequantizeInt8Blocks (Int8Blocks.h:88). */
+int gq8_dequantize_int8_blocks_host(const uint8_t *stored, int64_t element_count,
+                                    float *values);
+/* makeRotaryTable (RoPE.h:116-117): cos/sin [max_positions, head_dim / 2]. */
+int gq8_rotary_table_host(int max_positions, int head_dim, double theta, float *cosines,
+                          float *sines);
+
+/* ======================================================================= */
+/* Op-level entry points (device pointers, stream = hipStream_t or NULL).  */
+/* ======================================================================= */
+
+/* Int8Blocks quantization of rows x inner fp32 values into one Q8 row
+ * buffer; bit-exact with quantizeInt8Blocks (Int8Blocks.cpp:181-199).  Used
+ * for activations and for quantize-on-upload of weights. */
+int gq8_quantize_rows(const float *x, int64_t rows, int64_t inner, uint8_t *q8, void *stream);
+
+/* EmbedProgram<Int8Blocks> (Embed.h:45-82): out[t, c] = scale * W[token[t], c]
+ * for a [vocab, width] Int8Blocks table. */
+int gq8_embed(const uint32_t *tokens, int rows, const uint8_t *table, int vocab, int width,
+              float scale, float *out, void *stream);
+
+/* RMSNorm (RMSNorm.h:37-90): y = x / sqrt(mean(x^2) + eps) * (1 + w), per row.
+ * y may be NULL when q8 is given; q8 (optional) receives the Q8 row buffer of
+ * y (the fused norm + activation quantization of the Q8 path). */
+int gq8_rmsnorm(const float *x, const float *weight, int rows, int width, float epsilon,
+                float *y, uint8_t *q8, void *stream);
+
+/* RoPE (RoPE.h:50-94): rotate-half in place over rows x heads heads of
+ * head_dim at row_stride, row r at position first_position + r, from the
+ * [max_positions, head_dim / 2] tables. */
+int gq8_rope(float *x, int row_stride, int heads, int head_dim, int first_position, int rows,
+             const float *cosines, const float *sines, void *stream);
+
+/* The Int8Blocks product of SplitLinearProgram / TiledMatMulProgram
+ * (Linear.h:128-357, TiledMatMul.h:167-650) with Q8 activations:
+ *   y[r, o] = sum_b scale_w[o, b] * scale_x[r, b] * dot8(w[o, b], x[r, b])  (+ y[r, o])
+ * x8: Q8 row buffer [rows, inner]; w8: Int8Blocks [outputs, inner];
+ * y: fp32 [rows, y_stride] (y_stride >= outputs); residual != 0 adds the
+ * existing y (Linear.h:284-298).  Exact int8 dots, double accumulation. */
+int gq8_q8_product(const uint8_t *x8, const uint8_t *w8, int rows, int inner, int outputs,
+                   float *y, int y_stride, int residual, void *stream);
+
+/* fp16 KV-cache append (the ranged bind of Decoder.cpp:450-466, with fp16
+ * storage): rows of k and v (fp32, row stride src_stride) written at cache
+ * rows position .. position + rows - 1 of [max_positions, kv_width] caches. */
+int gq8_kv_store_f16(const float *k, const float *v, int src_stride, int rows, int kv_width,
+                     uint16_t *key_cache, uint16_t *value_cache, int position, void *stream);
+
+/* MultiQueryDecodeAttention (MultiQueryAttention.h:317-341): one query row of
+ * heads x head_dim over key_count fp16 cached rows, split over key chunks with
+ * an exact online-softmax merge.  workspace >= gq8_mqa_workspace_bytes(). */
+size_t gq8_mqa_workspace_bytes(int rows, int heads, int head_dim, int max_keys);
+int gq8_mqa_decode(const float *query, const uint16_t *key_cache, const uint16_t *value_cache,
+                   int heads, int kv_heads, int head_dim, int key_count, float scale, float *out,
+                   void *workspace, size_t workspace_bytes, void *stream);
+
+/* MultiQueryPrefillAttention (MultiQueryAttention.h:275-308): rows query rows
+ * at positions position_offset + r, row r over keys [0, position_offset + r]. */
+int gq8_mqa_prefill(const float *queries, const uint16_t *key_cache,
+                    const uint16_t *value_cache, int heads, int kv_heads, int head_dim,
+                    int rows, int position_offset, float scale, float *out, void *workspace,
+                    size_t workspace_bytes, void *stream);
+
+/* GeGLU (GeGLU.h:50-73): out[r, c] = gelu_tanh(f[r, c]) * f[r, inter + c]
+ * over fused [rows, 2 * inter]; out (fp32) and/or q8 (Q8 row buffer). */
+int gq8_geglu(const float *fused, int rows, int intermediate, float *out, uint8_t *q8,
+              void *stream);
+
+/* ArgmaxPartial + ArgmaxFinal (Argmax.h:47-257): per row the first maximum
+ * over unmasked entries (mask may be NULL; nonzero = suppressed), 0 if none. */
+size_t gq8_argmax_workspace_bytes(int rows, int length);
+int gq8_argmax_rows(const float *logits, const float *mask, int rows, int length,
+                    uint32_t *indices, void *workspace, size_t workspace_bytes, void *stream);
+
+/* ======================================================================= */
+/* Decoder runtime (HF::Decoder, Decoder.h:69-319).                        */
+/* ======================================================================= */
+typedef struct gq8_shape {
+    int width, heads, kv_heads, head_dim, layers, intermediate, vocab, max_positions;
+    int max_step_rows; /* 0 = max_positions (DecoderShape.h:85-89) */
+    float rms_epsilon;
+    double rope_theta;
+    float embedding_scale;
+} gq8_shape;
+
+/* DecoderShape::validate (DecoderShape.cpp:41-92) plus the Int8Blocks shape
+ * rule for every product weight. */
+int gq8_shape_validate(const gq8_shape *shape);
+/* DecoderShape::fromConfig for google/gemma-2b (GemmaConfig.h:41-92). */
+gq8_shape gq8_gemma_2b_shape(int layers, int max_positions, int max_step_rows);
+
+typedef struct gq8_decoder gq8_decoder;
+
+/* Decoder::prepare (Decoder.cpp:172-218): validates, allocates the step
+ * buffers, the per-layer fp16 KV caches and the rotary tables on the current
+ * device.  Weights are loaded separately. */
+int gq8_decoder_create(const gq8_shape *shape, gq8_decoder **out);
+void gq8_decoder_destroy(gq8_decoder *decoder);
+
+/* Tensor catalogue in GemmaTensors::all order (GemmaTensors.cpp:30-57):
+ * 0 embedding; layer l at 1 + 9 l + {q, k, v, o, gate, up, down,
+ * input_layernorm, post_attention_layernorm}; the final norm last. */
+int gq8_tensor_count(const gq8_shape *shape);
+int64_t gq8_tensor_elements(const gq8_shape *shape, int index);
+int gq8_tensor_is_norm(const gq8_shape *shape, int index);
+
+/* TensorLoader::loadProjectionWeight / loadStackedProjectionWeights /
+ * loadFloatTensor (TensorLoader.cpp:186-347): fp32 host values, quantized on
+ * the device (bit-exact with quantizeInt8Blocks) and placed in the layer's
+ * fused q|k|v or gate|up tensor; norms stay fp32. */
+int gq8_decoder_load_tensor(gq8_decoder *decoder, int index, const float *host_values);
+/* The same tensor already quantized: Int8Blocks bytes from the host. */
+int gq8_decoder_load_tensor_q8(gq8_decoder *decoder, int index, const uint8_t *host_bytes);
+/* Seeded synthetic N(0, sigma) weights for every tensor (sigma 0.02 for the
+ * projections and embedding, 0.1 for norms): Box-Muller in double over
+ * std::mt19937_64, one engine per 2^20-element chunk seeded
+ * ((0x5EED0000 + index) << 32) | chunk; generated on host threads, quantized
+ * on the device.  threads <= 0 uses every hardware thread. */
+int gq8_decoder_fill_synthetic(gq8_decoder *decoder, int threads);
+/* The generator of gq8_decoder_fill_synthetic for one tensor, on the host:
+ * count N(0, sigma) fp32 values from tensor_seed (all host threads). */
+int gq8_normal_fill_host(uint64_t tensor_seed, double sigma, float *out, int64_t count);
+/* Seeded uniform prompt ids: std::mt19937_64(seed), id = next() % vocab. */
+int gq8_prompt_ids(uint64_t seed, int vocab, int count, int32_t *out);
+/* The tensor's Int8Blocks bytes (or fp32 norm values) read back to the host. */
+int gq8_decoder_read_tensor(gq8_decoder *decoder, int index, void *host_out, size_t bytes);
+
+/* Decoder::beginSequence / position (Decoder.h:93-104). */
+int gq8_decoder_begin_sequence(gq8_decoder *decoder);
+int gq8_decoder_position(const gq8_decoder *decoder);
+
+/* Decoder::step (Decoder.cpp:644-706): n token ids (device, uint32) at
+ * positions position .. position + n - 1; logits (device, fp32) receives
+ * [n, vocab] when logits_rows == n, or only the last row when logits_rows == 1,
+ * or nothing when logits == NULL.  Synchronous on the decoder's stream. */
+int gq8_decoder_step(gq8_decoder *decoder, const uint32_t *tokens, int n, float *logits,
+                     int logits_rows);
+/* Decoder::hiddenStates (Decoder.h:119-121): the last step's rows after the
+ * final norm, [rows, width] fp32, copied to the host. */
+int gq8_decoder_hidden(gq8_decoder *decoder, float *host_out, int rows);
+/* Intermediates of the last row of the last step, for bisecting against the
+ * oracle: which = 0 normalised (input norm output), 1 attended, 2 activated
+ * (GeGLU output), 3 hidden after the layer; fp32 values and their Q8 bytes
+ * (q8 may be NULL).  Only kept when debug capture is on. */
+int gq8_decoder_set_debug(gq8_decoder *decoder, int enabled);
+int gq8_decoder_debug(gq8_decoder *decoder, int which, int layer, float *host_values,
+                      uint8_t *host_q8);
+
+/* ======================================================================= */
+/* Greedy token loop (HF::Gemma::generate at temperature 0,                 */
+/* Gemma.cpp:395-543).                                                      */
+/* ======================================================================= */
+typedef struct gq8_run_stats {
+    double prefill_seconds;  /* Gemma::lastPrefillSeconds */
+    double decode_seconds;   /* Gemma::lastDecodeSeconds  */
+    int step_count;          /* Gemma::lastStepCount      */
+    int generated;           /* tokens written to out     */
+} gq8_run_stats;
+
+/* Prefill the prompt in blocks of max_step_rows, then one token per step with
+ * the id chosen on the device and fed back through the sequence slots; eos >=
+ * 0 stops the run and is excluded (Gemma.cpp:503-504), eos < 0 never stops.
+ * The run's limit is min(max_tokens, max_positions - prompt_length)
+ * (Gemma.cpp:395-400; max_tokens <= 0 means the window).  use_graph != 0
+ * replays each decode step as one captured hipGraph.  out receives up to the
+ * limit token ids; returns the count (>= 0) or a negative status. */
+int gq8_generate(gq8_decoder *decoder, const int32_t *prompt, int prompt_length,
+                 int max_tokens, int eos, int use_graph, int32_t *out, gq8_run_stats *stats);
+
+/* Continue the greedy loop `steps` tokens from the current position: each
+ * step embeds the id in the slot at the position, runs the decoder and writes
+ * its argmax into the next slot (Gemma.cpp:320-333, on-device feedback); no
+ * EOS check.  Synchronous.  gq8_decoder_tokens reads slots back. */
+int gq8_decoder_decode(gq8_decoder *decoder, int steps, int use_graph);
+int gq8_decoder_tokens(gq8_decoder *decoder, int first, int count, int32_t *host_out);
+
+/* Stage timing: while enabled, every launch group of a step recorded outside
+ * a graph is bracketed by HIP events on the decoder's stream.  Stages: 0 embed,
+ * 1 norm, 2 qkv product, 3 rope+kv, 4 attention, 5 o product, 6 gate|up
+ * product, 7 geglu, 8 down product, 9 lm_head product, 10 argmax.
+ * gq8_decoder_timing fills per-stage totals (milliseconds) and launch counts
+ * since the last reset, and resets. */
+enum { GQ8_STAGE_COUNT = 11 };
+int gq8_decoder_set_timing(gq8_decoder *decoder, int enabled);
+int gq8_decoder_timing(gq8_decoder *decoder, double *milliseconds, int *launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

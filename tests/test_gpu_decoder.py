@@ -1,0 +1,246 @@
+"""The GPU decoder and greedy loop against the oracle decoder (Q8 path).
+
+Mirrors Tests/Decoder/DecoderTests.cpp (prompt in one step, one token at a
+time, two blocks, refusals) and Tests/Generation/GenerationTests.cpp (the loop
+equals a reference loop over single steps + argmax), at the reference's small
+quantizable config, at Gemma-2B dims with 2 layers (the CPU-runnable
+workload), and at the full 18 layers with a short prompt.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_helpers import empty, exact_fraction, to_device, worst_error
+from huggingfaceeacp_amd import gemma_q8 as G
+
+pytestmark = pytest.mark.gpu
+
+PROMPT = [5, 41, 3, 17, 28, 9, 60]  # DecoderTests.cpp:51-54
+LOGIT_TOLERANCE = 1e-2              # |a - e| / (1 + |e|), relative to the oracle
+
+
+def small_shape(max_step_rows=0, max_positions=16):
+    # Tests/Decoder/Common.h:38-72, the quantizable variant (FFN 64)
+    return G.DecoderShape(32, 2, 1, 16, 2, 64, 64, max_positions, max_step_rows)
+
+
+def to_oracle_shape(shape: G.DecoderShape):
+    return O.make_shape(shape.width, shape.heads, shape.kv_heads, shape.head_dim, shape.layers,
+                        shape.intermediate, shape.vocab, shape.max_positions,
+                        embedding_scale=shape.embedding_scale)
+
+
+def small_weights(shape: G.DecoderShape):
+    """N(0, sigma) per tensor with the reference test's spreads: embedding 0.2,
+    norms 0.1, projections 1/sqrt(fan in) (Tests/Decoder/Common.h:164-237)."""
+    tensors = []
+    for i in range(shape.tensor_count()):
+        n = shape.tensor_elements(i)
+        if i == 0:
+            sigma = 0.2
+        elif shape.tensor_is_norm(i):
+            sigma = 0.1
+        else:
+            role = (i - 1) % G.PER_LAYER
+            fan_in = {G.T_O: shape.query_width, G.T_DOWN: shape.intermediate}.get(role, shape.width)
+            sigma = 1.0 / np.sqrt(fan_in)
+        tensors.append(O.normal_fill(0x7100 + i, sigma, n))
+    return tensors
+
+
+def build_pair(shape: G.DecoderShape, tensors):
+    decoder = G.Decoder(shape)
+    model = O.Model(to_oracle_shape(shape), O.MODE_Q8)
+    for i, values in enumerate(tensors):
+        decoder.load_tensor(i, values)
+        assert model.set_tensor(i, values) == 0
+    return decoder, model
+
+
+def gpu_step(torch, decoder, tokens, logits_rows=None):
+    tokens = np.asarray(tokens, dtype=np.uint32)
+    rows = tokens.size if logits_rows is None else logits_rows
+    logits = empty(torch, rows * decoder.shape.vocab, torch.float32)
+    decoder.step(to_device(torch, tokens).data_ptr(), tokens.size, logits.data_ptr(), rows)
+    torch.cuda.synchronize()
+    return logits.cpu().numpy().reshape(rows, decoder.shape.vocab)
+
+
+def test_quantize_on_upload_matches_the_oracle_bytes(torch_cuda):
+    shape = small_shape()
+    tensors = small_weights(shape)
+    decoder, model = build_pair(shape, tensors)
+    for i in range(shape.tensor_count()):
+        if shape.tensor_is_norm(i):
+            assert np.array_equal(decoder.read_tensor(i), tensors[i])
+        else:
+            assert np.array_equal(decoder.read_tensor(i), model.tensor_bytes(i))
+
+
+def test_small_model_prompt_in_one_step(torch_cuda):
+    torch = torch_cuda
+    shape = small_shape()
+    decoder, model = build_pair(shape, small_weights(shape))
+    got = gpu_step(torch, decoder, PROMPT)
+    status, ref, _ = model.step(np.array(PROMPT))
+    assert status == 0
+    err = worst_error(got, ref)
+    print(f"small model, prompt in one step: worst {err:.3g}, exact {exact_fraction(got, ref):.4f}")
+    assert err <= 1e-5
+    assert decoder.position == len(PROMPT)
+    hidden = decoder.hidden_states(len(PROMPT))
+    assert np.isfinite(hidden).all()
+
+
+def test_small_model_one_token_at_a_time_and_two_blocks(torch_cuda):
+    torch = torch_cuda
+    shape = small_shape()
+    tensors = small_weights(shape)
+    decoder, model = build_pair(shape, tensors)
+    _, ref, _ = model.step(np.array(PROMPT))
+    rows = [gpu_step(torch, decoder, [t])[0] for t in PROMPT]
+    assert worst_error(np.stack(rows), ref) <= 1e-5
+    decoder.begin_sequence()
+    assert decoder.position == 0
+    first = gpu_step(torch, decoder, PROMPT[:4])
+    second = gpu_step(torch, decoder, PROMPT[4:])
+    assert worst_error(np.concatenate([first, second]), ref) <= 1e-5
+    # the step that carries only the last row's logits
+    decoder.begin_sequence()
+    last = gpu_step(torch, decoder, PROMPT, logits_rows=1)
+    assert worst_error(last[0], ref[-1]) <= 1e-5
+
+
+def test_small_model_intermediates_bisect(torch_cuda):
+    """The Q8 bytes of each layer's product inputs equal the oracle's."""
+    torch = torch_cuda
+    shape = small_shape()
+    decoder, model = build_pair(shape, small_weights(shape))
+    decoder.set_debug(True)
+    gpu_step(torch, decoder, PROMPT)
+    model.step(np.array(PROMPT))
+    inner = {0: shape.width, 1: shape.query_width, 2: shape.intermediate}
+    mismatched = 0
+    for layer in range(shape.layers):
+        for which in (0, 1, 2):
+            values, q8 = decoder.debug(which, layer)
+            ref = model.debug(which, layer)
+            assert worst_error(values, ref) <= 1e-5
+            rq, rs = model.debug_q(which, layer)
+            n = inner[which]
+            mismatched += int(np.sum(q8[:n].view(np.int8) != rq))
+            mismatched += int(np.sum(q8[n:].view(np.uint16) != rs))
+    print(f"Q8 activation bytes differing from the oracle: {mismatched}")
+    assert mismatched == 0
+
+
+def poisoned(torch, n):
+    return torch.full((n,), -12345.0, dtype=torch.float32, device="cuda")
+
+
+def test_refusals_leave_state_untouched(torch_cuda):
+    """DecoderTests.cpp:227-284 and ReferenceDecoder.h:420-446."""
+    torch = torch_cuda
+    shape = small_shape(max_step_rows=4)
+    decoder, _ = build_pair(shape, small_weights(shape))
+    gpu_step(torch, decoder, [1, 2])
+    before = decoder.position
+
+    def refused(tokens, expected):
+        tokens = np.asarray(tokens, dtype=np.uint32)
+        logits = poisoned(torch, max(1, tokens.size) * shape.vocab)
+        with pytest.raises(G.Gq8Error) as info:
+            decoder.step(to_device(torch, tokens if tokens.size else np.zeros(1, np.uint32)).data_ptr(),
+                         tokens.size, logits.data_ptr(), max(1, tokens.size))
+        assert info.value.status == expected
+        torch.cuda.synchronize()
+        assert (logits.cpu().numpy() == -12345.0).all()
+        assert decoder.position == before
+
+    refused([1, 2, 3, 4, 5], G.ERR_CAPACITY)
+    refused([], G.ERR_EMPTY)
+    refused([64], G.ERR_TOKEN)
+    for _ in range(3):
+        gpu_step(torch, decoder, [7, 8, 9, 10])
+    before = decoder.position  # 14 of 16
+    refused([1, 2, 3], G.ERR_WINDOW)
+
+
+def test_shape_and_preparation_refusals(torch_cuda):
+    with pytest.raises(G.Gq8Error) as info:
+        G.DecoderShape(32, 2, 1, 6, 2, 64, 64, 16).validate()
+    assert info.value.status == G.ERR_SHAPE
+    with pytest.raises(G.Gq8Error) as info:
+        G.Decoder(G.DecoderShape(32, 2, 1, 16, 2, 48, 64, 16))
+    assert info.value.status == G.ERR_UNQUANTIZABLE
+    decoder = G.Decoder(small_shape())
+    with pytest.raises(G.Gq8Error) as info:
+        decoder.generate(PROMPT, 4)
+    assert info.value.status == G.ERR_NOT_PREPARED
+
+
+def test_greedy_loop_matches_reference_loop(torch_cuda):
+    """GenerationTests.cpp:192-224: the loop equals single steps + argmax."""
+    shape = small_shape(max_step_rows=3)
+    decoder, model = build_pair(shape, small_weights(shape))
+    for use_graph in (False, True):
+        tokens, stats = decoder.generate(PROMPT, 6, eos=-1, use_graph=use_graph)
+        count, ref, margins = model.generate(np.array(PROMPT), 6, eos=-1)
+        assert list(tokens) == list(ref), (use_graph, list(tokens), list(ref), list(margins))
+        assert stats.generated == len(tokens)
+    # the window: 16 - 7 leaves 9 tokens at most (Gemma.cpp:395-400)
+    tokens, _ = decoder.generate(PROMPT, 100, eos=-1)
+    assert len(tokens) == 9
+    count, ref, _ = model.generate(np.array(PROMPT), 100, eos=-1)
+    assert list(tokens) == list(ref)
+    # EOS stops the run and is not returned (Gemma.cpp:503-504)
+    eos = int(ref[3])
+    tokens, _ = decoder.generate(PROMPT, 100, eos=eos)
+    assert list(tokens) == list(ref[: list(ref).index(eos)])
+
+
+def gemma_pair(layers, max_positions, max_step_rows=16):
+    shape = G.DecoderShape.gemma_2b(layers=layers, max_positions=max_positions,
+                                    max_step_rows=max_step_rows)
+    decoder = G.Decoder(shape)
+    decoder.fill_synthetic(16)
+    model = O.Model(to_oracle_shape(shape), O.MODE_Q8)
+    assert model.fill_synthetic() == 0
+    return shape, decoder, model
+
+
+def test_two_layer_gemma_workload(torch_cuda):
+    """The CPU-runnable workload: Gemma-2B dims, 2 layers, seeded N(0, 0.02)
+    weights, 16 uniform prompt ids, 32 greedy tokens."""
+    torch = torch_cuda
+    shape, decoder, model = gemma_pair(2, 64)
+    for i in (0, 1, 2, 3, 7, 8):
+        got = decoder.read_tensor(i)
+        ref = model.tensor_bytes(i) if not shape.tensor_is_norm(i) else None
+        if ref is not None:
+            assert np.array_equal(got, ref), f"tensor {i} bytes differ"
+    prompt = O.prompt_ids(0xC0FFEE + 1, shape.vocab, 16)
+    tokens, stats = decoder.generate(prompt, 32, eos=1)
+    count, ref, margins = model.generate(prompt, 32, eos=1)
+    print(f"2-layer greedy: gpu {list(tokens)[:8]}..., oracle {list(ref)[:8]}..., "
+          f"smallest top-2 margin {margins.min():.3g}")
+    assert list(tokens) == list(ref)
+    # the prefill's last row of logits
+    decoder.begin_sequence()
+    model.begin()
+    got = gpu_step(torch, decoder, prompt, logits_rows=1)[0]
+    _, ref_logits, _ = model.step(prompt)
+    err = worst_error(got, ref_logits[-1])
+    print(f"2-layer last-row logits: worst {err:.3g}, exact {exact_fraction(got, ref_logits[-1]):.4f}")
+    assert err <= LOGIT_TOLERANCE
+
+
+@pytest.mark.slow
+def test_full_gemma_short_run(torch_cuda):
+    """All 18 layers at real shapes, an 8-token prompt and 4 greedy tokens."""
+    shape, decoder, model = gemma_pair(18, 64)
+    prompt = O.prompt_ids(0xC0FFEE + 2, shape.vocab, 8)
+    tokens, _ = decoder.generate(prompt, 4, eos=1, use_graph=True)
+    count, ref, margins = model.generate(prompt, 4, eos=1)
+    print(f"18-layer greedy: gpu {list(tokens)}, oracle {list(ref)}, margins {margins}")
+    assert list(tokens) == list(ref)
