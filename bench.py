@@ -30,9 +30,9 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 METRIC = "Gemma-2B Q8_0 decode tok/s (b=1, ctx 512) + % of HBM roofline"
 STAGE_LABELS = {
-    "gate_up": "q8_product_kernel<1,4> (gate|up, 2048 -> 32768)",
-    "lm_head": "q8_product_kernel<1,8> (tied lm_head, 2048 -> 256000)",
-    "down": "q8_product_kernel<1,1> (down, 16384 -> 2048)",
+    "gate_up": "q8_matvec_kernel<4,1,1> (gate|up, 2048 -> 32768)",
+    "lm_head": "q8_matvec_kernel<8,1,1> (tied lm_head, 2048 -> 256000)",
+    "down": "q8_matvec_kernel<1,4,2> (down, 16384 -> 2048)",
 }
 
 

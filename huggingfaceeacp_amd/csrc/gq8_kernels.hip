@@ -309,114 +309,300 @@ __global__ __launch_bounds__(kThreads) void q8_product_kernel(
     }
 }
 
-// ---- multi-query attention, split over 64-key chunks ----------------------
-// Partial: one workgroup per (chunk, query row) holds every head; scores in
-// double (sequential over channels, as the oracle sums them), the chunk's
-// maximum and exp-sum per head, and the chunk's unnormalised value sums.
-constexpr int kChunk = kAttentionChunk;
+// ---- the one-row product of a decode step --------------------------------
+// Same arithmetic as q8_product_kernel for a single activation row, without
+// LDS or barriers on the common shapes: the activation blocks a lane needs sit
+// in its registers, and every weight load of the wave is issued before any
+// arithmetic.  A row of `inner` elements is split into 64-block segments;
+// WPR waves share a row group (segments dealt round-robin), each wave owns U
+// consecutive rows and S segments of each.
+template <int U, int WPR, int S>
+__global__ __launch_bounds__(kThreads) void q8_matvec_kernel(
+    const uint8_t *__restrict__ x8, int64_t x_elements, int x_row, const uint8_t *__restrict__ w8,
+    int inner, int outputs, float *__restrict__ y, int residual)
+{
+    __shared__ double sPartial[kThreads / 64][U];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int group = wave / WPR, part = wave % WPR;
+    const int row0 = (blockIdx.x * (4 / WPR) + group) * U;
+    const int nb = inner / kBlock;
+    const int64_t wElements = (int64_t) outputs * inner;
+    const uint16_t *wScales = reinterpret_cast<const uint16_t *>(w8 + wElements);
+
+    int4 wa[U][S], wb[U][S];
+    uint16_t wsBits[U][S];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int o = row0 + u;
+#pragma unroll
+        for (int j = 0; j < S; ++j) {
+            const int b = lane + 64 * (part + WPR * j);
+            if (o < outputs && b < nb) {
+                const int4 *p = reinterpret_cast<const int4 *>(w8 + (int64_t) o * inner + (int64_t) b * kBlock);
+                wa[u][j] = p[0];
+                wb[u][j] = p[1];
+                wsBits[u][j] = wScales[(int64_t) o * nb + b];
+            } else {
+                wa[u][j] = make_int4(0, 0, 0, 0);
+                wb[u][j] = make_int4(0, 0, 0, 0);
+                wsBits[u][j] = 0;
+            }
+        }
+    }
+    int4 a0[S], a1[S];
+    double sa[S];
+    const uint16_t *xScales = reinterpret_cast<const uint16_t *>(x8 + x_elements);
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+        const int b = lane + 64 * (part + WPR * j);
+        if (b < nb) {
+            const int4 *p = reinterpret_cast<const int4 *>(x8 + (int64_t) x_row * inner + (int64_t) b * kBlock);
+            a0[j] = p[0];
+            a1[j] = p[1];
+            sa[j] = (double) half_value(xScales[(int64_t) x_row * nb + b]);
+        } else {
+            a0[j] = make_int4(0, 0, 0, 0);
+            a1[j] = make_int4(0, 0, 0, 0);
+            sa[j] = 0.0;
+        }
+    }
+
+    double acc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        acc[u] = 0.0;
+#pragma unroll
+        for (int j = 0; j < S; ++j) {
+            int d = 0;
+            d = __builtin_amdgcn_sdot4(wa[u][j].x, a0[j].x, d, false);
+            d = __builtin_amdgcn_sdot4(wa[u][j].y, a0[j].y, d, false);
+            d = __builtin_amdgcn_sdot4(wa[u][j].z, a0[j].z, d, false);
+            d = __builtin_amdgcn_sdot4(wa[u][j].w, a0[j].w, d, false);
+            d = __builtin_amdgcn_sdot4(wb[u][j].x, a1[j].x, d, false);
+            d = __builtin_amdgcn_sdot4(wb[u][j].y, a1[j].y, d, false);
+            d = __builtin_amdgcn_sdot4(wb[u][j].z, a1[j].z, d, false);
+            d = __builtin_amdgcn_sdot4(wb[u][j].w, a1[j].w, d, false);
+            acc[u] += (double) d * ((double) half_value(wsBits[u][j]) * sa[j]);
+        }
+        acc[u] = wave_sum(acc[u]);
+    }
+
+    if (WPR > 1) {
+        if (lane == 0)
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                sPartial[wave][u] = acc[u];
+        __syncthreads();
+        if (part != 0)
+            return;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            double total = 0.0;
+            for (int w = 0; w < WPR; ++w)
+                total += sPartial[wave + w][u];
+            acc[u] = total;
+        }
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int o = row0 + u;
+            if (o < outputs) {
+                const double old = residual ? (double) y[o] : 0.0;
+                y[o] = (float) (acc[u] + old);
+            }
+        }
+    }
+}
+
+// ---- multi-query attention, split over the keys ------------------------------
+// Partial: a workgroup per (split, query row) owns a contiguous range of keys
+// (a whole number of 32-key tiles, at most kMaxSplits splits per row) and all
+// heads; it walks its range a tile at a time through LDS with an online
+// softmax (running maximum and sum per head, the value sums rescaled when the
+// maximum moves: the exact streaming fold of MultiQueryAttention.h:43-49).
+// Scores and sums are in double; each score is its channel sum in four
+// interleaved partial sums.
+constexpr int kTile = 32;
+constexpr int kMaxSplits = kAttentionSplits;
 constexpr int kMaxQueryWidth = 2048;
 constexpr int kMaxKvWidth = 256;
+constexpr int kOutPerThread = kMaxQueryWidth / kThreads; // 8
+
+__device__ inline int keys_per_split(int keyCount)
+{
+    const int tiles = (keyCount + kTile - 1) / kTile;
+    return ((tiles + kMaxSplits - 1) / kMaxSplits) * kTile;
+}
 
 __global__ __launch_bounds__(kThreads) void mqa_partial_kernel(
     const float *__restrict__ queries, int q_stride, const uint16_t *__restrict__ key_cache,
     const uint16_t *__restrict__ value_cache, int heads, int kv_heads, int head_dim,
-    const int *pos_ptr, int pos_value, float scale, int chunks_cap, double *__restrict__ ws_o,
+    const int *pos_ptr, int pos_value, float scale, double *__restrict__ ws_o,
     double *__restrict__ ws_ml)
 {
     __shared__ double sQuery[kMaxQueryWidth];
-    __shared__ uint32_t sKeys[kChunk * (kMaxKvWidth / 2 + 1)];
-    __shared__ double sWeights[kMaxHeads * kChunk];
+    __shared__ uint32_t sKeys[kTile * (kMaxKvWidth / 2 + 1)];
+    __shared__ uint32_t sValues[kTile * (kMaxKvWidth / 2)];
+    __shared__ double sWeights[kMaxHeads * kTile];
+    __shared__ double sMax[kMaxHeads], sSum[kMaxHeads], sFactor[kMaxHeads];
 
-    const int chunk = blockIdx.x, row = blockIdx.y;
+    const int split = blockIdx.x, row = blockIdx.y;
     const int keyCount = (pos_ptr ? *pos_ptr : 0) + pos_value + row + 1;
-    const int k0 = chunk * kChunk;
+    const int perSplit = keys_per_split(keyCount);
+    const int k0 = split * perSplit;
     if (k0 >= keyCount)
         return;
-    const int nkeys = min(kChunk, keyCount - k0);
+    const int k1 = min(k0 + perSplit, keyCount);
     const int qWidth = heads * head_dim, kvWidth = kv_heads * head_dim;
     const int perKv = heads / kv_heads;
     const int keyWords = kvWidth / 2, keyStride = kMaxKvWidth / 2 + 1;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 
     for (int i = threadIdx.x; i < qWidth; i += kThreads)
         sQuery[i] = (double) queries[(int64_t) row * q_stride + i];
-    const uint32_t *keyRows = reinterpret_cast<const uint32_t *>(key_cache + (int64_t) k0 * kvWidth);
-    for (int i = threadIdx.x; i < nkeys * keyWords; i += kThreads) {
-        const int j = i / keyWords, w = i % keyWords;
-        sKeys[j * keyStride + w] = keyRows[(int64_t) j * keyWords + w];
+    if (threadIdx.x < heads) {
+        sMax[threadIdx.x] = -INFINITY;
+        sSum[threadIdx.x] = 0.0;
     }
-    __syncthreads();
+    double acc[kOutPerThread];
+#pragma unroll
+    for (int i = 0; i < kOutPerThread; ++i)
+        acc[i] = 0.0;
 
-    for (int idx = threadIdx.x; idx < heads * kChunk; idx += kThreads) {
-        const int head = idx / kChunk, j = idx % kChunk;
-        double score = -INFINITY;
-        if (j < nkeys) {
-            const double *q = sQuery + head * head_dim;
-            const uint32_t *k = sKeys + j * keyStride + ((head / perKv) * head_dim) / 2;
-            double total = 0.0;
-            for (int c = 0; c < head_dim; c += 2) {
-                const uint32_t pair = k[c / 2];
-                total += q[c] * (double) half_value((uint16_t) (pair & 0xFFFFu));
-                total += q[c + 1] * (double) half_value((uint16_t) (pair >> 16));
+    for (int t0 = k0; t0 < k1; t0 += kTile) {
+        const int nk = min(kTile, k1 - t0);
+        __syncthreads(); // the previous tile's reads are done
+        const uint32_t *keyRows = reinterpret_cast<const uint32_t *>(key_cache + (int64_t) t0 * kvWidth);
+        const uint32_t *valueRows = reinterpret_cast<const uint32_t *>(value_cache + (int64_t) t0 * kvWidth);
+        for (int i = threadIdx.x; i < nk * keyWords; i += kThreads) {
+            const int j = i / keyWords, w = i % keyWords;
+            sKeys[j * keyStride + w] = keyRows[i];
+            sValues[i] = valueRows[i];
+        }
+        __syncthreads();
+
+        for (int idx = threadIdx.x; idx < heads * kTile; idx += kThreads) {
+            const int head = idx / kTile, j = idx % kTile;
+            double score = -INFINITY;
+            if (j < nk) {
+                const double *q = sQuery + head * head_dim;
+                const uint32_t *k = sKeys + j * keyStride + ((head / perKv) * head_dim) / 2;
+                double p0 = 0.0, p1 = 0.0, p2 = 0.0, p3 = 0.0;
+                int c = 0;
+                for (; c + 4 <= head_dim; c += 4) {
+                    const uint32_t a = k[c / 2], b = k[c / 2 + 1];
+                    p0 += q[c] * (double) half_value((uint16_t) (a & 0xFFFFu));
+                    p1 += q[c + 1] * (double) half_value((uint16_t) (a >> 16));
+                    p2 += q[c + 2] * (double) half_value((uint16_t) (b & 0xFFFFu));
+                    p3 += q[c + 3] * (double) half_value((uint16_t) (b >> 16));
+                }
+                for (; c < head_dim; c += 2) {
+                    const uint32_t a = k[c / 2];
+                    p0 += q[c] * (double) half_value((uint16_t) (a & 0xFFFFu));
+                    p1 += q[c + 1] * (double) half_value((uint16_t) (a >> 16));
+                }
+                score = (double) scale * ((p0 + p1) + (p2 + p3));
             }
-            score = (double) scale * total;
+            sWeights[idx] = score;
         }
-        sWeights[idx] = score;
-    }
-    __syncthreads();
+        __syncthreads();
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int head = wave; head < heads; head += kThreads / 64) {
-        const double s = sWeights[head * kChunk + lane];
-        const double m = wave_max(s);
-        const double w = lane < nkeys ? exp(s - m) : 0.0;
-        const double l = wave_sum(w);
-        sWeights[head * kChunk + lane] = w;
-        if (lane == 0) {
-            double *ml = ws_ml + (((int64_t) row * chunks_cap + chunk) * heads + head) * 2;
-            ml[0] = m;
-            ml[1] = l;
+        // per head: the tile's weights against the running maximum
+        for (int head = wave; head < heads; head += kThreads / 64) {
+            const double s = lane < kTile ? sWeights[head * kTile + lane] : -INFINITY;
+            const double tileMax = wave_max(s);
+            const double previous = sMax[head];
+            const double largest = fmax(previous, tileMax);
+            const double w = (lane < nk) ? exp(s - largest) : 0.0;
+            const double total = wave_sum(w);
+            if (lane < kTile)
+                sWeights[head * kTile + lane] = w;
+            if (lane == 0) {
+                const double factor = previous == -INFINITY ? 0.0 : exp(previous - largest);
+                sFactor[head] = factor;
+                sSum[head] = sSum[head] * factor + total;
+                sMax[head] = largest;
+            }
+        }
+        __syncthreads();
+
+#pragma unroll
+        for (int i = 0; i < kOutPerThread; ++i) {
+            const int idx = threadIdx.x + i * kThreads;
+            if (idx < qWidth) {
+                const int head = idx / head_dim, c = idx % head_dim;
+                const int column = (head / perKv) * head_dim + c;
+                const uint16_t *v = reinterpret_cast<const uint16_t *>(sValues) + column;
+                const double *w = sWeights + head * kTile;
+                double sum = 0.0;
+                for (int j = 0; j < nk; ++j)
+                    sum += w[j] * (double) half_value(v[j * kvWidth]);
+                acc[i] = acc[i] * sFactor[head] + sum;
+            }
         }
     }
-    __syncthreads();
 
-    double *o = ws_o + ((int64_t) row * chunks_cap + chunk) * qWidth;
-    for (int idx = threadIdx.x; idx < qWidth; idx += kThreads) {
-        const int head = idx / head_dim, c = idx % head_dim;
-        const uint16_t *v = value_cache + (int64_t) k0 * kvWidth + (head / perKv) * head_dim + c;
-        double acc = 0.0;
-        for (int j = 0; j < nkeys; ++j)
-            acc += sWeights[head * kChunk + j] * (double) half_value(v[(int64_t) j * kvWidth]);
-        o[idx] = acc;
+    double *o = ws_o + ((int64_t) row * kMaxSplits + split) * qWidth;
+#pragma unroll
+    for (int i = 0; i < kOutPerThread; ++i) {
+        const int idx = threadIdx.x + i * kThreads;
+        if (idx < qWidth)
+            o[idx] = acc[i];
+    }
+    if (threadIdx.x < heads) {
+        double *ml = ws_ml + (((int64_t) row * kMaxSplits + split) * heads + threadIdx.x) * 2;
+        ml[0] = sMax[threadIdx.x];
+        ml[1] = sSum[threadIdx.x];
     }
 }
 
-// Merge: per query row, the chunks' maxima and sums rescaled to the row's
-// maximum (the exact online-softmax join, MultiQueryAttention.h:43-49), the
-// output divided by the total, rounded to fp32 and optionally quantized.
+// Merge: per query row, each split's maximum and sum rescaled to the row's
+// maximum, the factors computed once per (head, split) in LDS, the output
+// divided by the total, rounded to fp32 and optionally quantized.
 __global__ __launch_bounds__(kThreads) void mqa_merge_kernel(
-    int heads, int head_dim, const int *pos_ptr, int pos_value, int chunks_cap,
-    const double *__restrict__ ws_o, const double *__restrict__ ws_ml, float *__restrict__ out,
-    uint8_t *__restrict__ q8, int rows)
+    int heads, int head_dim, const int *pos_ptr, int pos_value, const double *__restrict__ ws_o,
+    const double *__restrict__ ws_ml, float *__restrict__ out, uint8_t *__restrict__ q8, int rows)
 {
+    __shared__ double sFactor[kMaxHeads * kMaxSplits];
+    __shared__ double sLargest[kMaxHeads], sTotal[kMaxHeads];
     const int row = blockIdx.x;
     const int keyCount = (pos_ptr ? *pos_ptr : 0) + pos_value + row + 1;
-    const int chunks = (keyCount + kChunk - 1) / kChunk;
+    const int perSplit = keys_per_split(keyCount);
+    const int splits = (keyCount + perSplit - 1) / perSplit;
     const int qWidth = heads * head_dim;
     const int64_t elements = (int64_t) rows * qWidth;
+    const double *ml = ws_ml + (int64_t) row * kMaxSplits * heads * 2;
 
+    if (threadIdx.x < heads) {
+        double largest = -INFINITY;
+        for (int s = 0; s < splits; ++s)
+            largest = fmax(largest, ml[((int64_t) s * heads + threadIdx.x) * 2]);
+        sLargest[threadIdx.x] = largest;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < heads * splits; idx += kThreads) {
+        const int head = idx / splits, s = idx % splits;
+        sFactor[head * kMaxSplits + s] = exp(ml[((int64_t) s * heads + head) * 2] - sLargest[head]);
+    }
+    __syncthreads();
+    if (threadIdx.x < heads) {
+        double total = 0.0;
+        for (int s = 0; s < splits; ++s)
+            total += ml[((int64_t) s * heads + threadIdx.x) * 2 + 1]
+                     * sFactor[threadIdx.x * kMaxSplits + s];
+        sTotal[threadIdx.x] = total;
+    }
+    __syncthreads();
+
+    const double *o = ws_o + (int64_t) row * kMaxSplits * qWidth;
     for (int idx = threadIdx.x; idx < qWidth; idx += kThreads) {
         const int head = idx / head_dim;
-        double largest = -INFINITY;
-        for (int c = 0; c < chunks; ++c)
-            largest = fmax(largest, ws_ml[(((int64_t) row * chunks_cap + c) * heads + head) * 2]);
-        double total = 0.0, weighted = 0.0;
-        for (int c = 0; c < chunks; ++c) {
-            const double *ml = ws_ml + (((int64_t) row * chunks_cap + c) * heads + head) * 2;
-            const double factor = exp(ml[0] - largest);
-            total += ml[1] * factor;
-            weighted += ws_o[((int64_t) row * chunks_cap + c) * qWidth + idx] * factor;
-        }
-        const float v = (float) (weighted / total);
+        const double *factor = sFactor + head * kMaxSplits;
+        double weighted = 0.0;
+        for (int s = 0; s < splits; ++s)
+            weighted += o[(int64_t) s * qWidth + idx] * factor[s];
+        const float v = (float) (weighted / sTotal[head]);
         const int64_t at = (int64_t) row * qWidth + idx;
         if (out)
             out[at] = v;
@@ -626,6 +812,38 @@ hipError_t product_with(const uint8_t *x8, int64_t xElements, int xRow0, int row
     return hipGetLastError();
 }
 
+template <int U, int WPR, int S>
+hipError_t matvec_with(const uint8_t *x8, int64_t xElements, int xRow, const uint8_t *w8,
+                       int inner, int outputs, float *y, int residual, hipStream_t stream)
+{
+    const unsigned grid = blocks_for(outputs, (4 / WPR) * U);
+    hipLaunchKernelGGL((q8_matvec_kernel<U, WPR, S>), dim3(grid), dim3(kThreads), 0, stream, x8,
+                       xElements, xRow, w8, inner, outputs, y, residual);
+    return hipGetLastError();
+}
+
+// The one-row product: rows per wave by the output count, waves per row by
+// the number of 64-block segments in a row.
+hipError_t launch_matvec(const uint8_t *x8, int64_t xElements, int xRow, const uint8_t *w8,
+                         int inner, int outputs, float *y, int residual, hipStream_t stream)
+{
+    const int segments = (inner / kBlock + 63) / 64;
+    if (segments <= 1) {
+        if (outputs >= 131072)
+            return matvec_with<8, 1, 1>(x8, xElements, xRow, w8, inner, outputs, y, residual, stream);
+        if (outputs >= 16384)
+            return matvec_with<4, 1, 1>(x8, xElements, xRow, w8, inner, outputs, y, residual, stream);
+        return matvec_with<1, 1, 1>(x8, xElements, xRow, w8, inner, outputs, y, residual, stream);
+    }
+    if (segments == 2)
+        return matvec_with<1, 2, 1>(x8, xElements, xRow, w8, inner, outputs, y, residual, stream);
+    if (segments <= 4)
+        return matvec_with<1, 4, 1>(x8, xElements, xRow, w8, inner, outputs, y, residual, stream);
+    if (segments <= 8)
+        return matvec_with<1, 4, 2>(x8, xElements, xRow, w8, inner, outputs, y, residual, stream);
+    return hipErrorInvalidValue;
+}
+
 constexpr size_t kProductLdsLimit = 64 * 1024;
 
 size_t product_lds(int b, int inner)
@@ -642,6 +860,8 @@ hipError_t launch_q8_product(const uint8_t *x8, int x_rows_total, int x_row0, in
         || x_row0 < 0 || x_row0 + rows > x_rows_total || product_lds(1, inner) > kProductLdsLimit)
         return hipErrorInvalidValue;
     const int64_t xElements = (int64_t) x_rows_total * inner;
+    if (rows == 1)
+        return launch_matvec(x8, xElements, x_row0, w8, inner, outputs, y, residual, stream);
     int b = 8;
     while (b > 1 && (b > rows || product_lds(b, inner) > kProductLdsLimit))
         b >>= 1;
@@ -668,9 +888,9 @@ hipError_t launch_q8_product(const uint8_t *x8, int x_rows_total, int x_row0, in
 
 size_t mqa_workspace_bytes(int rows, int heads, int head_dim, int max_keys)
 {
-    const int64_t chunks = (max_keys + kChunk - 1) / kChunk;
+    (void) max_keys; // the split count is fixed, so a captured step fits every length
     const int64_t qWidth = (int64_t) heads * head_dim;
-    return (size_t) (rows * chunks * qWidth + rows * chunks * heads * 2) * sizeof(double);
+    return (size_t) ((int64_t) rows * kMaxSplits * (qWidth + 2 * heads)) * sizeof(double);
 }
 
 hipError_t launch_mqa(const float *queries, int q_stride, const uint16_t *key_cache,
@@ -680,23 +900,22 @@ hipError_t launch_mqa(const float *queries, int q_stride, const uint16_t *key_ca
                       hipStream_t stream)
 {
     if (rows <= 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0 || heads > kMaxHeads
-        || head_dim % 2 != 0 || heads * head_dim > kMaxQueryWidth
+        || head_dim % 4 != 0 || heads * head_dim > kMaxQueryWidth
         || kv_heads * head_dim > kMaxKvWidth || max_keys <= 0
         || workspace_bytes < mqa_workspace_bytes(rows, heads, head_dim, max_keys))
         return hipErrorInvalidValue;
     if (q8 && (heads * head_dim) % kBlock != 0)
         return hipErrorInvalidValue;
-    const int chunksCap = (max_keys + kChunk - 1) / kChunk;
     double *wsO = reinterpret_cast<double *>(workspace);
-    double *wsMl = wsO + (int64_t) rows * chunksCap * heads * head_dim;
-    hipLaunchKernelGGL(mqa_partial_kernel, dim3(chunksCap, rows), dim3(kThreads), 0, stream,
+    double *wsMl = wsO + (int64_t) rows * kMaxSplits * heads * head_dim;
+    hipLaunchKernelGGL(mqa_partial_kernel, dim3(kMaxSplits, rows), dim3(kThreads), 0, stream,
                        queries, q_stride, key_cache, value_cache, heads, kv_heads, head_dim,
-                       pos_ptr, pos_value, scale, chunksCap, wsO, wsMl);
+                       pos_ptr, pos_value, scale, wsO, wsMl);
     hipError_t status = hipGetLastError();
     if (status != hipSuccess)
         return status;
     hipLaunchKernelGGL(mqa_merge_kernel, dim3(rows), dim3(kThreads), 0, stream, heads, head_dim,
-                       pos_ptr, pos_value, chunksCap, wsO, wsMl, out, q8, rows);
+                       pos_ptr, pos_value, wsO, wsMl, out, q8, rows);
     return hipGetLastError();
 }
 

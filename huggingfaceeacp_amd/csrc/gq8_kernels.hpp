@@ -51,7 +51,7 @@ hipError_t launch_q8_product(const uint8_t *x8, int x_rows_total, int x_row0, in
                              const uint8_t *w8, int inner, int outputs, float *y, int y_stride,
                              int residual, hipStream_t stream);
 
-constexpr int kAttentionChunk = 64;
+constexpr int kAttentionSplits = 64; // workgroups over one query row's keys
 constexpr int kMaxHeads = 16;
 constexpr int kMaxHeadDim = 256;
 

@@ -469,9 +469,21 @@ int gor_argmax(const float *logits, const float *mask, int n)
  * h / (heads / kv_heads); scores scale * q.k in double, softmax by the
  * maximum, the output the weighted value sum divided by the weight sum,
  * rounded to fp32 once.  Keys and values are fp16. */
-void gor_mqa_row_f16(const float *query, const uint16_t *keys, const uint16_t *values,
-                     int heads, int kv_heads, int head_dim, int key_count, float scale,
-                     float *out)
+typedef double (*cache_reader)(const void *cache, int64_t index);
+
+static double read_half_cache(const void *cache, int64_t index)
+{
+    return (double) g_half_table[((const uint16_t *) cache)[index]];
+}
+
+static double read_float_cache(const void *cache, int64_t index)
+{
+    return (double) ((const float *) cache)[index];
+}
+
+static void mqa_row(const float *query, const void *keys, const void *values,
+                    cache_reader read, int heads, int kv_heads, int head_dim, int key_count,
+                    float scale, float *out)
 {
     ensure_half_table();
 
@@ -486,10 +498,10 @@ void gor_mqa_row_f16(const float *query, const uint16_t *keys, const uint16_t *v
         double largest = -INFINITY;
 
         for (int key = 0; key < key_count; ++key) {
-            const uint16_t *k = keys + (int64_t) key * kvWidth + kvColumn;
+            const int64_t k = (int64_t) key * kvWidth + kvColumn;
             double total = 0.0;
             for (int c = 0; c < head_dim; ++c)
-                total += (double) q[c] * (double) g_half_table[k[c]];
+                total += (double) q[c] * read(keys, k + c);
             weights[key] = (double) scale * total;
             if (weights[key] > largest)
                 largest = weights[key];
@@ -504,9 +516,9 @@ void gor_mqa_row_f16(const float *query, const uint16_t *keys, const uint16_t *v
         for (int c = 0; c < head_dim; ++c)
             acc[c] = 0.0;
         for (int key = 0; key < key_count; ++key) {
-            const uint16_t *v = values + (int64_t) key * kvWidth + kvColumn;
+            const int64_t v = (int64_t) key * kvWidth + kvColumn;
             for (int c = 0; c < head_dim; ++c)
-                acc[c] += weights[key] * (double) g_half_table[v[c]];
+                acc[c] += weights[key] * read(values, v + c);
         }
         for (int c = 0; c < head_dim; ++c)
             out[head * head_dim + c] = (float) (acc[c] / denominator);
@@ -514,6 +526,20 @@ void gor_mqa_row_f16(const float *query, const uint16_t *keys, const uint16_t *v
 
     free(acc);
     free(weights);
+}
+
+/* Multi-query attention of one query row over key_count cached rows
+ * (Lib/HuggingFaceEACP/Kernels/MultiQueryAttention.h:138-260 and
+ * Tests/Decoder/ReferenceDecoder.h:208-272): query head h reads KV head
+ * h / (heads / kv_heads); scores scale * q.k in double, softmax by the
+ * maximum, the output the weighted value sum divided by the weight sum,
+ * rounded to fp32 once.  Keys and values are fp16. */
+void gor_mqa_row_f16(const float *query, const uint16_t *keys, const uint16_t *values,
+                     int heads, int kv_heads, int head_dim, int key_count, float scale,
+                     float *out)
+{
+    mqa_row(query, keys, values, read_half_cache, heads, kv_heads, head_dim, key_count, scale,
+            out);
 }
 
 /* ======================================================================== */
@@ -600,6 +626,7 @@ struct gor_model {
     int *present;
     float *cosines, *sines;
     uint16_t *keyCache, *valueCache; /* Q8 mode: [layers][maxPos][kvWidth] fp16 */
+    float *keyCacheF, *valueCacheF;  /* Q8-path-f32 mode */
     double *keyCacheD, *valueCacheD; /* reference mode */
     gor_layer_debug *debug;           /* layers + 1 entries (last: final norm) */
 };
@@ -625,6 +652,9 @@ gor_model *gor_model_create(const gor_shape *shape, int mode)
     if (mode == GOR_MODE_Q8) {
         model->keyCache = (uint16_t *) calloc(cacheElements, sizeof(uint16_t));
         model->valueCache = (uint16_t *) calloc(cacheElements, sizeof(uint16_t));
+    } else if (mode == GOR_MODE_Q8_PATH_F32) {
+        model->keyCacheF = (float *) calloc(cacheElements, sizeof(float));
+        model->valueCacheF = (float *) calloc(cacheElements, sizeof(float));
     } else {
         model->keyCacheD = (double *) calloc(cacheElements, sizeof(double));
         model->valueCacheD = (double *) calloc(cacheElements, sizeof(double));
@@ -672,6 +702,8 @@ void gor_model_destroy(gor_model *model)
     free(model->sines);
     free(model->keyCache);
     free(model->valueCache);
+    free(model->keyCacheF);
+    free(model->valueCacheF);
     free(model->keyCacheD);
     free(model->valueCacheD);
     free(model);
@@ -790,6 +822,39 @@ static const float *layer_norm(const gor_model *model, int layer, int role)
 }
 
 /* ---- Q8 path: one token ------------------------------------------------ */
+static double dequantized(const uint8_t *bytes, int64_t elements, int64_t index);
+
+/* A product input row: quantized in the Q8 mode (kept for the debug view),
+ * left as fp32 in the Q8-path-f32 mode. */
+static void product_input(const gor_model *model, const float *x, int n, int8_t *xq,
+                          uint16_t *xs)
+{
+    if (model->mode == GOR_MODE_Q8) {
+        gor_quantize_row(x, n, xq, xs);
+    } else {
+        memset(xq, 0, (size_t) n);
+        memset(xs, 0, sizeof(uint16_t) * (size_t) (n / GOR_BLOCK));
+    }
+}
+
+static void product(const gor_model *model, const float *x, const int8_t *xq,
+                    const uint16_t *xs, const uint8_t *weights, int64_t rows, int64_t inner,
+                    double *out)
+{
+    if (model->mode == GOR_MODE_Q8) {
+        q8_matvec_double(xq, xs, weights, rows, inner, out);
+        return;
+    }
+    const int64_t elements = rows * inner;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        double total = 0.0;
+        for (int64_t i = 0; i < inner; ++i)
+            total += (double) x[i] * dequantized(weights, elements, r * inner + i);
+        out[r] = total;
+    }
+}
+
 static void q8_token(gor_model *model, int32_t token, float *logits, float *hiddenOut)
 {
     const gor_shape *s = &model->shape;
@@ -838,58 +903,67 @@ static void q8_token(gor_model *model, int32_t token, float *logits, float *hidd
         /* Decoder.cpp:579-642, encodeLayer: pre-norm attention sublayer */
         gor_rmsnorm_row(h, layer_norm(model, layer, GOR_T_INPUT_NORM), width,
                         s->rms_epsilon, n);
-        gor_quantize_row(n, width, xq, xs);
+        product_input(model, n, width, xq, xs);
         memcpy(dbg->normalised, n, sizeof(float) * (size_t) width);
         memcpy(dbg->normalisedQ, xq, (size_t) width);
         memcpy(dbg->normalisedS, xs, sizeof(uint16_t) * (size_t) (width / GOR_BLOCK));
 
-        q8_matvec_double(xq, xs, layer_bytes(model, layer, GOR_T_Q), qw, width, y);
+        product(model, n, xq, xs, layer_bytes(model, layer, GOR_T_Q), qw, width, y);
         for (int i = 0; i < qw; ++i) q[i] = (float) y[i];
-        q8_matvec_double(xq, xs, layer_bytes(model, layer, GOR_T_K), kvw, width, y);
+        product(model, n, xq, xs, layer_bytes(model, layer, GOR_T_K), kvw, width, y);
         for (int i = 0; i < kvw; ++i) k[i] = (float) y[i];
-        q8_matvec_double(xq, xs, layer_bytes(model, layer, GOR_T_V), kvw, width, y);
+        product(model, n, xq, xs, layer_bytes(model, layer, GOR_T_V), kvw, width, y);
         for (int i = 0; i < kvw; ++i) v[i] = (float) y[i];
 
         /* Decoder.cpp:541-546: rotate the queries and this step's key row */
         gor_rope_row(q, qw, s->heads, s->head_dim, position, model->cosines, model->sines);
         gor_rope_row(k, kvw, s->kv_heads, s->head_dim, position, model->cosines, model->sines);
 
-        uint16_t *keyRows = model->keyCache + (int64_t) layer * maxCacheRow;
-        uint16_t *valueRows = model->valueCache + (int64_t) layer * maxCacheRow;
-        for (int i = 0; i < kvw; ++i) {
-            keyRows[(int64_t) position * kvw + i] = gor_half_from_float(k[i]);
-            valueRows[(int64_t) position * kvw + i] = gor_half_from_float(v[i]);
+        const float scale = 1.f / sqrtf((float) s->head_dim);
+        if (model->mode == GOR_MODE_Q8) {
+            uint16_t *keyRows = model->keyCache + (int64_t) layer * maxCacheRow;
+            uint16_t *valueRows = model->valueCache + (int64_t) layer * maxCacheRow;
+            for (int i = 0; i < kvw; ++i) {
+                keyRows[(int64_t) position * kvw + i] = gor_half_from_float(k[i]);
+                valueRows[(int64_t) position * kvw + i] = gor_half_from_float(v[i]);
+            }
+            /* Decoder.cpp:553-562: decode attention over position + 1 keys */
+            mqa_row(q, keyRows, valueRows, read_half_cache, s->heads, s->kv_heads, s->head_dim,
+                    position + 1, scale, att);
+        } else {
+            float *keyRows = model->keyCacheF + (int64_t) layer * maxCacheRow;
+            float *valueRows = model->valueCacheF + (int64_t) layer * maxCacheRow;
+            memcpy(keyRows + (int64_t) position * kvw, k, sizeof(float) * (size_t) kvw);
+            memcpy(valueRows + (int64_t) position * kvw, v, sizeof(float) * (size_t) kvw);
+            mqa_row(q, keyRows, valueRows, read_float_cache, s->heads, s->kv_heads,
+                    s->head_dim, position + 1, scale, att);
         }
-
-        /* Decoder.cpp:553-562: decode attention over position + 1 keys */
-        gor_mqa_row_f16(q, keyRows, valueRows, s->heads, s->kv_heads, s->head_dim,
-                        position + 1, 1.f / sqrtf((float) s->head_dim), att);
-        gor_quantize_row(att, qw, xq, xs);
+        product_input(model, att, qw, xq, xs);
         memcpy(dbg->attended, att, sizeof(float) * (size_t) qw);
         memcpy(dbg->attendedQ, xq, (size_t) qw);
         memcpy(dbg->attendedS, xs, sizeof(uint16_t) * (size_t) (qw / GOR_BLOCK));
 
         /* o_proj with the residual folded (Decoder.cpp:595-603) */
-        q8_matvec_double(xq, xs, layer_bytes(model, layer, GOR_T_O), width, qw, y);
+        product(model, att, xq, xs, layer_bytes(model, layer, GOR_T_O), width, qw, y);
         for (int i = 0; i < width; ++i)
             h[i] = (float) ((double) h[i] + y[i]);
 
         /* the feed-forward sublayer (Decoder.cpp:605-641) */
         gor_rmsnorm_row(h, layer_norm(model, layer, GOR_T_POST_NORM), width,
                         s->rms_epsilon, n);
-        gor_quantize_row(n, width, xq, xs);
-        q8_matvec_double(xq, xs, layer_bytes(model, layer, GOR_T_GATE), inter, width, y);
+        product_input(model, n, width, xq, xs);
+        product(model, n, xq, xs, layer_bytes(model, layer, GOR_T_GATE), inter, width, y);
         for (int i = 0; i < inter; ++i) gate[i] = (float) y[i];
-        q8_matvec_double(xq, xs, layer_bytes(model, layer, GOR_T_UP), inter, width, y);
+        product(model, n, xq, xs, layer_bytes(model, layer, GOR_T_UP), inter, width, y);
         for (int i = 0; i < inter; ++i) up[i] = (float) y[i];
         for (int i = 0; i < inter; ++i)
             act[i] = gor_geglu(gate[i], up[i]);
-        gor_quantize_row(act, inter, xq, xs);
+        product_input(model, act, inter, xq, xs);
         memcpy(dbg->activated, act, sizeof(float) * (size_t) inter);
         memcpy(dbg->activatedQ, xq, (size_t) inter);
         memcpy(dbg->activatedS, xs, sizeof(uint16_t) * (size_t) (inter / GOR_BLOCK));
 
-        q8_matvec_double(xq, xs, layer_bytes(model, layer, GOR_T_DOWN), width, inter, y);
+        product(model, act, xq, xs, layer_bytes(model, layer, GOR_T_DOWN), width, inter, y);
         for (int i = 0; i < width; ++i)
             h[i] = (float) ((double) h[i] + y[i]);
         memcpy(dbg->hidden, h, sizeof(float) * (size_t) width);
@@ -900,14 +974,14 @@ static void q8_token(gor_model *model, int32_t token, float *logits, float *hidd
         gor_layer_debug *dbg = &model->debug[s->layers];
         gor_rmsnorm_row(h, model->norms[1 + GOR_T_PER_LAYER * s->layers], width,
                         s->rms_epsilon, n);
-        gor_quantize_row(n, width, xq, xs);
+        product_input(model, n, width, xq, xs);
         memcpy(dbg->normalised, n, sizeof(float) * (size_t) width);
         memcpy(dbg->normalisedQ, xq, (size_t) width);
         memcpy(dbg->normalisedS, xs, sizeof(uint16_t) * (size_t) (width / GOR_BLOCK));
         if (hiddenOut)
             memcpy(hiddenOut, n, sizeof(float) * (size_t) width);
         if (logits) {
-            q8_matvec_double(xq, xs, model->bytes[0], s->vocab, width, y);
+            product(model, n, xq, xs, model->bytes[0], s->vocab, width, y);
             for (int64_t i = 0; i < s->vocab; ++i)
                 logits[i] = (float) y[i];
         }
@@ -1078,7 +1152,7 @@ int gor_model_step(gor_model *model, const int32_t *tokens, int n, float *logits
     for (int i = 0; i < n; ++i) {
         float *rowLogits = logits ? logits + (int64_t) i * model->shape.vocab : NULL;
         float *rowHidden = hidden ? hidden + (int64_t) i * model->shape.width : NULL;
-        if (model->mode == GOR_MODE_Q8)
+        if (model->mode != GOR_MODE_REFERENCE)
             q8_token(model, tokens[i], rowLogits, rowHidden);
         else
             reference_token(model, tokens[i], rowLogits, rowHidden);

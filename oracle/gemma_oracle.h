@@ -101,7 +101,10 @@ typedef struct gor_shape {
 
 enum {
     GOR_MODE_Q8 = 0,        /* activation Q8 + fp16 KV, double compute, fp32 storage */
-    GOR_MODE_REFERENCE = 1  /* ReferenceDecoder.h: double activations, no Q8, double KV */
+    GOR_MODE_REFERENCE = 1, /* ReferenceDecoder.h: double activations, no Q8, double KV */
+    GOR_MODE_Q8_PATH_F32 = 2 /* the Q8 path's code with the two new storage rules off:
+                                fp32 product inputs and an fp32 KV cache (a check of
+                                that code path's composition) */
 };
 
 /* Tensor indices in GemmaTensors::all order (GemmaTensors.cpp:30-57):

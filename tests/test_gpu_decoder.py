@@ -61,7 +61,8 @@ def gpu_step(torch, decoder, tokens, logits_rows=None):
     tokens = np.asarray(tokens, dtype=np.uint32)
     rows = tokens.size if logits_rows is None else logits_rows
     logits = empty(torch, rows * decoder.shape.vocab, torch.float32)
-    decoder.step(to_device(torch, tokens).data_ptr(), tokens.size, logits.data_ptr(), rows)
+    ids = to_device(torch, tokens)  # referenced until the step has read it
+    decoder.step(ids.data_ptr(), tokens.size, logits.data_ptr(), rows)
     torch.cuda.synchronize()
     return logits.cpu().numpy().reshape(rows, decoder.shape.vocab)
 
@@ -149,9 +150,9 @@ def test_refusals_leave_state_untouched(torch_cuda):
     def refused(tokens, expected):
         tokens = np.asarray(tokens, dtype=np.uint32)
         logits = poisoned(torch, max(1, tokens.size) * shape.vocab)
+        ids = to_device(torch, tokens if tokens.size else np.zeros(1, np.uint32))
         with pytest.raises(G.Gq8Error) as info:
-            decoder.step(to_device(torch, tokens if tokens.size else np.zeros(1, np.uint32)).data_ptr(),
-                         tokens.size, logits.data_ptr(), max(1, tokens.size))
+            decoder.step(ids.data_ptr(), tokens.size, logits.data_ptr(), max(1, tokens.size))
         assert info.value.status == expected
         torch.cuda.synchronize()
         assert (logits.cpu().numpy() == -12345.0).all()

@@ -16,6 +16,25 @@ from huggingfaceeacp_amd import gemma_q8 as G
 
 pytestmark = pytest.mark.gpu
 
+# Device copies of the inputs stay referenced until the test ends: a tensor
+# whose only use is an inline data_ptr() would go back to torch's caching
+# allocator before the kernel reads it.
+_alive = []
+
+
+@pytest.fixture(autouse=True)
+def _keep_device_inputs():
+    _alive.clear()
+    yield
+    _alive.clear()
+
+
+def dev(array) -> int:
+    import torch
+    tensor = to_device(torch, np.ascontiguousarray(array))
+    _alive.append(tensor)
+    return tensor.data_ptr()
+
 
 def special_blocks() -> np.ndarray:
     """Blocks chosen to exercise every branch of the Int8Blocks rule."""
@@ -63,7 +82,7 @@ def test_quantize_rows_bit_exact(torch_cuda):
     inner = 64
     rows = x.size // inner
     out = empty(torch, q8_bytes(rows, inner), torch.uint8)
-    G.quantize_rows(to_device(torch, x).data_ptr(), rows, inner, out.data_ptr())
+    G.quantize_rows(dev(x), rows, inner, out.data_ptr())
     torch.cuda.synchronize()
     q_gpu, s_gpu = split_q8(out.cpu().numpy(), rows, inner)
     q_ref, s_ref = O.quantize_row(x)
@@ -84,7 +103,7 @@ def test_scale_rule_over_amax_sweep(torch_cuda):
     x[:, 9] = -amax * np.float32(0.5)
     x = x.ravel()
     out = empty(torch, q8_bytes(amax.size, 32), torch.uint8)
-    G.quantize_rows(to_device(torch, x).data_ptr(), amax.size, 32, out.data_ptr())
+    G.quantize_rows(dev(x), amax.size, 32, out.data_ptr())
     torch.cuda.synchronize()
     q_gpu, s_gpu = split_q8(out.cpu().numpy(), amax.size, 32)
     q_ref, s_ref = O.quantize_row(x)
@@ -100,7 +119,7 @@ def test_embed_bit_exact(torch_cuda):
     tokens = np.array([0, 999, 17, 500, 17], dtype=np.uint32)
     out = empty(torch, tokens.size * width, torch.float32)
     scale = float(np.sqrt(np.float32(2048), dtype=np.float32))
-    G.embed(to_device(torch, tokens).data_ptr(), tokens.size, to_device(torch, table).data_ptr(),
+    G.embed(dev(tokens), tokens.size, dev(table),
             vocab, width, scale, out.data_ptr())
     torch.cuda.synchronize()
     deq = O.dequantize_int8_blocks(table, vocab * width).reshape(vocab, width)
@@ -115,7 +134,7 @@ def test_rmsnorm_and_q8(torch_cuda, width, rows):
     w = spread(width, 8, 0.1)
     y = empty(torch, rows * width, torch.float32)
     q8 = empty(torch, q8_bytes(rows, width), torch.uint8)
-    G.rmsnorm(to_device(torch, x).data_ptr(), to_device(torch, w).data_ptr(), rows, width, 1e-6,
+    G.rmsnorm(dev(x), dev(w), rows, width, 1e-6,
               y.data_ptr(), q8.data_ptr())
     torch.cuda.synchronize()
     got = y.cpu().numpy().reshape(rows, width)
@@ -136,7 +155,7 @@ def test_rope_matches_oracle(torch_cuda):
     x = spread(rows * heads * head_dim, 9, 2.0)
     xd = to_device(torch, x)
     G.rope(xd.data_ptr(), heads * head_dim, heads, head_dim, first, rows,
-           to_device(torch, cos).data_ptr(), to_device(torch, sin).data_ptr())
+           dev(cos), dev(sin))
     torch.cuda.synchronize()
     got = xd.cpu().numpy().reshape(rows, heads * head_dim)
     for r in range(rows):
@@ -157,7 +176,7 @@ def test_q8_product_real_shapes(torch_cuda, inner, outputs):
     xq, xs = O.quantize_row(x)
     x8 = np.concatenate([xq.view(np.uint8), xs.view(np.uint8)])
     y = empty(torch, outputs, torch.float32)
-    G.q8_product(to_device(torch, x8).data_ptr(), to_device(torch, w).data_ptr(), 1, inner,
+    G.q8_product(dev(x8), dev(w), 1, inner,
                  outputs, y.data_ptr(), outputs)
     torch.cuda.synchronize()
     got = y.cpu().numpy()
@@ -176,7 +195,7 @@ def test_q8_product_rows_and_residual(torch_cuda, rows):
     x8 = np.concatenate([q_all.view(np.uint8), s_all.view(np.uint8)])
     base = spread(rows * outputs, 79, 1.0)
     y = to_device(torch, base)
-    G.q8_product(to_device(torch, x8).data_ptr(), to_device(torch, w).data_ptr(), rows, inner,
+    G.q8_product(dev(x8), dev(w), rows, inner,
                  outputs, y.data_ptr(), outputs, residual=True)
     torch.cuda.synchronize()
     got = y.cpu().numpy().reshape(rows, outputs)
@@ -193,7 +212,7 @@ def test_kv_store_f16(torch_cuda):
     v = spread(rows * 512, 22, 3.0)
     kc = torch.zeros(maxpos * kv, dtype=torch.int16, device="cuda")
     vc = torch.zeros(maxpos * kv, dtype=torch.int16, device="cuda")
-    G.kv_store_f16(to_device(torch, k).data_ptr(), to_device(torch, v).data_ptr(), 512, rows, kv,
+    G.kv_store_f16(dev(k), dev(v), 512, rows, kv,
                    kc.data_ptr(), vc.data_ptr(), pos)
     torch.cuda.synchronize()
     kh = kc.cpu().numpy().view(np.uint16).reshape(maxpos, kv)
@@ -217,8 +236,8 @@ def test_mqa_decode(torch_cuda, keys):
     ws_bytes = G.mqa_workspace_bytes(1, heads, hd, keys)
     ws = empty(torch, ws_bytes, torch.uint8)
     out = empty(torch, heads * hd, torch.float32)
-    G.mqa_decode(to_device(torch, q).data_ptr(), to_device(torch, kc).data_ptr(),
-                 to_device(torch, vc).data_ptr(), heads, kvh, hd, keys, 0.0625, out.data_ptr(),
+    G.mqa_decode(dev(q), dev(kc),
+                 dev(vc), heads, kvh, hd, keys, 0.0625, out.data_ptr(),
                  ws.data_ptr(), ws_bytes)
     torch.cuda.synchronize()
     ref = O.mqa_row_f16(q, kc, vc, heads, kvh, hd, keys, 0.0625)
@@ -238,8 +257,8 @@ def test_mqa_prefill_equals_rows_of_decodes(torch_cuda):
     ws_bytes = G.mqa_workspace_bytes(rows, heads, hd, total)
     ws = empty(torch, ws_bytes, torch.uint8)
     out = empty(torch, rows * heads * hd, torch.float32)
-    G.mqa_prefill(to_device(torch, q).data_ptr(), to_device(torch, kc).data_ptr(),
-                  to_device(torch, vc).data_ptr(), heads, kvh, hd, rows, offset, 0.0625,
+    G.mqa_prefill(dev(q), dev(kc),
+                  dev(vc), heads, kvh, hd, rows, offset, 0.0625,
                   out.data_ptr(), ws.data_ptr(), ws_bytes)
     torch.cuda.synchronize()
     got = out.cpu().numpy().reshape(rows, heads * hd)
@@ -267,9 +286,9 @@ def test_mqa_causal_never_reads_later_keys(torch_cuda):
         if variant == 1:
             k[2:] = np.float16(1e4).view(np.uint16)
             v[2:] = np.float16(-1e4).view(np.uint16)
-        G.mqa_prefill(to_device(torch, q[heads * hd:2 * heads * hd]).data_ptr(),
-                      to_device(torch, np.ascontiguousarray(k)).data_ptr(),
-                      to_device(torch, np.ascontiguousarray(v)).data_ptr(), heads, kvh, hd, 1, 1,
+        G.mqa_prefill(dev(q[heads * hd:2 * heads * hd]),
+                      dev(np.ascontiguousarray(k)),
+                      dev(np.ascontiguousarray(v)), heads, kvh, hd, 1, 1,
                       0.25, out.data_ptr(), ws.data_ptr(), ws_bytes)
         torch.cuda.synchronize()
         outs.append(out.cpu().numpy())
@@ -284,7 +303,7 @@ def test_geglu_and_q8(torch_cuda, rows):
     fused[:8] = [30, -30, 1000, -1000, 0, 5, -5, 9]  # saturated tails (GeluTests.cpp:115-138)
     out = empty(torch, rows * inter, torch.float32)
     q8 = empty(torch, q8_bytes(rows, inter), torch.uint8)
-    G.geglu(to_device(torch, fused).data_ptr(), rows, inter, out.data_ptr(), q8.data_ptr())
+    G.geglu(dev(fused), rows, inter, out.data_ptr(), q8.data_ptr())
     torch.cuda.synchronize()
     got = out.cpu().numpy().reshape(rows, inter)
     q_gpu, s_gpu = split_q8(q8.cpu().numpy(), rows, inter)
@@ -304,8 +323,8 @@ def _argmax_gpu(torch, logits, mask=None, rows=1):
     ws_bytes = G.argmax_workspace_bytes(rows, length)
     ws = empty(torch, ws_bytes, torch.uint8)
     out = torch.zeros(rows, dtype=torch.int32, device="cuda")
-    G.argmax_rows(to_device(torch, logits).data_ptr(),
-                  to_device(torch, mask).data_ptr() if mask is not None else None, rows, length,
+    G.argmax_rows(dev(logits),
+                  dev(mask) if mask is not None else None, rows, length,
                   out.data_ptr(), ws.data_ptr(), ws_bytes)
     torch.cuda.synchronize()
     return out.cpu().numpy().astype(np.int64)
