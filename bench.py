@@ -30,9 +30,9 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 METRIC = "Gemma-2B Q8_0 decode tok/s (b=1, ctx 512) + % of HBM roofline"
 STAGE_LABELS = {
-    "gate_up": "q8_matvec_kernel<4,1,1> (gate|up, 2048 -> 32768)",
-    "lm_head": "q8_matvec_kernel<8,1,1> (tied lm_head, 2048 -> 256000)",
-    "down": "q8_matvec_kernel<1,4,2> (down, 16384 -> 2048)",
+    "gate_up": "gateup_geglu_kernel (post-attention norm + gate|up 2048 -> 2x16384 + GeGLU + Q8)",
+    "lm_head": "lmhead_argmax_kernel (tied lm_head 2048 -> 256000 + first-maximum fold)",
+    "down": "q8_matvec_kernel<1,4,2> (down 16384 -> 2048 + residual)",
 }
 
 
@@ -41,15 +41,18 @@ def log(*args):
 
 
 def stage_bytes(shape, stage: str) -> int:
-    """Algorithmic bytes of one launch of a product stage: the Int8Blocks
-    weight bytes, the Q8 activation row read and the fp32 output row written."""
+    """Algorithmic HBM bytes of one launch of a one-token product kernel: the
+    Int8Blocks weight bytes (17/16 byte per element) plus the activation rows
+    it must read and write once."""
     w, f, v = shape.width, shape.intermediate, shape.vocab
-    dims = {"gate_up": (w, 2 * f), "lm_head": (w, v), "down": (f, w),
-            "qkv": (w, shape.query_width + 2 * shape.kv_width), "o_proj": (shape.query_width, w)}
-    inner, outputs = dims[stage]
-    weights = inner * outputs * 17 // 16
-    extra_read = outputs * 4 if stage in ("down", "o_proj") else 0  # residual read
-    return weights + inner * 17 // 16 + outputs * 4 + extra_read
+    q8 = lambda n: n * 17 // 16  # noqa: E731 -- an Int8Blocks row of n elements
+    if stage == "gate_up":  # fp32 residual row + norm weights in, Q8 GeGLU row out
+        return q8(2 * f * w) + 2 * w * 4 + q8(f)
+    if stage == "lm_head":  # Q8 final-norm row in, fp32 logits out
+        return q8(v * w) + q8(w) + v * 4
+    if stage == "down":  # Q8 GeGLU row in, fp32 residual read and written
+        return q8(f * w) + q8(f) + 2 * w * 4
+    raise ValueError(stage)
 
 
 def cpu_baseline(layers: int, sample_steps: int, threads: int) -> dict:

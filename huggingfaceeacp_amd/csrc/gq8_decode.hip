@@ -1,0 +1,872 @@
+// gq8_decode.hip -- the fused kernels of a one-token decode step.
+//
+// A decode step is a chain of global dependencies (every product needs the
+// whole of its input row), so its cost on MI355X is the weight bytes plus a
+// fixed cost per kernel boundary.  These kernels cut the chain to five
+// kernels a layer and three for the head:
+//
+//   qkv_rope_kernel      norm + Q8 of the hidden row (per workgroup, in LDS),
+//                        the fused q|k|v product, RoPE on q and k, k and v
+//                        stored fp16 at the step's cache row (layer 0 also
+//                        gathers the embedding row);
+//   attention_kernel     split-key attention over the fp16 cache with an
+//                        online softmax; the last workgroup of a row merges
+//                        the splits and writes the Q8 row for o_proj;
+//   (o_proj, down)       q8_matvec_kernel with the residual add;
+//   gateup_geglu_kernel  norm + Q8 prologue, the gate|up product, GeGLU and
+//                        the Q8 row for down_proj;
+//   final_norm_kernel    the final norm and its Q8 row (one workgroup);
+//   lmhead_argmax_kernel the tied lm_head over the whole vocabulary, each
+//                        workgroup's first maximum merged into one packed
+//                        64-bit word by atomicMax;
+//   head_finalize_kernel the id into the next sequence slot and the position
+//                        advance.
+//
+// Reference counterparts: Decoder.cpp:579-706 (the layer), Embed.h, RMSNorm.h,
+// RoPE.h, Linear.h, MultiQueryAttention.h, GeGLU.h, Argmax.h.  The arithmetic
+// is gq8_numerics.hpp's, identical to the unfused kernels'.
+#include "gq8_decode.hpp"
+#include "gq8_numerics.hpp"
+
+#include <cfloat>
+
+namespace gq8 {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+
+__device__ inline double wave_sum_d(double v)
+{
+    for (int mask = 32; mask >= 1; mask >>= 1)
+        v += __shfl_xor(v, mask);
+    return v;
+}
+
+__device__ inline double wave_max_d(double v)
+{
+    for (int mask = 32; mask >= 1; mask >>= 1)
+        v = fmax(v, __shfl_xor(v, mask));
+    return v;
+}
+
+__device__ inline int dot32(const int4 &w0, const int4 &w1, const int4 &a0, const int4 &a1)
+{
+    int d = 0;
+    d = __builtin_amdgcn_sdot4(w0.x, a0.x, d, false);
+    d = __builtin_amdgcn_sdot4(w0.y, a0.y, d, false);
+    d = __builtin_amdgcn_sdot4(w0.z, a0.z, d, false);
+    d = __builtin_amdgcn_sdot4(w0.w, a0.w, d, false);
+    d = __builtin_amdgcn_sdot4(w1.x, a1.x, d, false);
+    d = __builtin_amdgcn_sdot4(w1.y, a1.y, d, false);
+    d = __builtin_amdgcn_sdot4(w1.z, a1.z, d, false);
+    d = __builtin_amdgcn_sdot4(w1.w, a1.w, d, false);
+    return d;
+}
+
+// Sums U per-lane values (one per row) across the 64 lanes with U - 1 + 6 -
+// log2(U) shuffles instead of 6 U: each halving step keeps half of the rows
+// and adds the partner lane's share of them.  Returns the total of row
+// row_of_lane(lane) (every lane holds one; lanes whose low bits are zero are
+// the ones that store).
+template <int U>
+__device__ inline double reduce_rows(double (&v)[U], int lane)
+{
+    int n = U;
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) {
+        if (n > 1) {
+            const bool upper = (lane & mask) != 0;
+#pragma unroll
+            for (int i = 0; i < n / 2; ++i) {
+                const double keep = upper ? v[i + n / 2] : v[i];
+                const double send = upper ? v[i] : v[i + n / 2];
+                v[i] = keep + __shfl_xor(send, mask);
+            }
+            n /= 2;
+        } else {
+            v[0] += __shfl_xor(v[0], mask);
+        }
+    }
+    return v[0];
+}
+
+// The row whose total reduce_rows<U> leaves in `lane`: the halving steps
+// consume lane bits 5, 4, ... in turn, the upper half of the rows going to
+// the lanes with the bit set.
+template <int U>
+__device__ inline int row_of_lane(int lane)
+{
+    int row = 0, n = U, bit = 32;
+    while (n > 1) {
+        n /= 2;
+        if (lane & bit)
+            row += n;
+        bit >>= 1;
+    }
+    return row;
+}
+
+// Whether `lane` is the one that stores its row's total (the lowest lane
+// holding it).
+template <int U>
+__device__ inline bool stores_row(int lane)
+{
+    int bits = 0, n = U, bit = 32;
+    while (n > 1) {
+        n /= 2;
+        bits |= bit;
+        bit >>= 1;
+    }
+    return (lane & ~bits) == 0;
+}
+
+// The lowest lane holding row r's total after reduce_rows<U>.
+template <int U>
+__device__ inline int lane_of_row(int r)
+{
+    int lane = 0, n = U, bit = 32;
+    while (n > 1) {
+        n /= 2;
+        if (r >= n) {
+            lane |= bit;
+            r -= n;
+        }
+        bit >>= 1;
+    }
+    return lane;
+}
+
+// The Q8 form of one normalised row, shared by a workgroup.
+struct RowQ8 {
+    int8_t q[kFusedMaxWidth];
+    double scale[kFusedMaxWidth / kBlock];
+};
+
+// RMSNorm (RMSNorm.h:44-56) of one row and its Int8Blocks quantization into
+// LDS.  Thread t owns elements [8t, 8t + 8), so four consecutive lanes hold
+// one 32-element block.  The row is either x or, with `table`, the embedding
+// row of `*token` (Embed.h:45-82), which workgroup 0 also stores to
+// hidden_out for the residual stream.  Workgroup 0 optionally writes the
+// normalised row (fp32) and its Q8 bytes for the debug view.
+__device__ void norm_q8_prologue(const float *x, const uint32_t *token, const uint8_t *table,
+                                 int64_t vocab, float embed_scale, float *hidden_out,
+                                 const float *weight, int width, float epsilon, RowQ8 &row,
+                                 double *sPartial, float *normalised_out, uint8_t *q8_out)
+{
+    // only the first 256 threads of a larger workgroup hold elements
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int waves = blockDim.x / 64;
+    const int i0 = t * 8;
+    const bool active = t < kThreads && i0 < width;
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        v[k] = 0.f;
+    if (active) {
+        if (table) {
+            uint32_t id = *token; // the sequence slot at the position
+            if (id >= (uint32_t) vocab) // ids are validated on the host; a guard, not a rule
+                id = 0;
+            const int64_t e0 = (int64_t) id * width + i0;
+            const uint16_t bits = reinterpret_cast<const uint16_t *>(table + vocab * width)[e0 / kBlock];
+            const float s = half_value(bits);
+            const int2 packed = *reinterpret_cast<const int2 *>(table + e0);
+            const int8_t *b = reinterpret_cast<const int8_t *>(&packed);
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                v[k] = (float) ((double) embed_scale * (double) (s * (float) b[k]));
+            if (hidden_out && blockIdx.x == 0) {
+                reinterpret_cast<float4 *>(hidden_out + i0)[0] = make_float4(v[0], v[1], v[2], v[3]);
+                reinterpret_cast<float4 *>(hidden_out + i0)[1] = make_float4(v[4], v[5], v[6], v[7]);
+            }
+        } else {
+            const float4 p = reinterpret_cast<const float4 *>(x + i0)[0];
+            const float4 r = reinterpret_cast<const float4 *>(x + i0)[1];
+            v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w;
+            v[4] = r.x; v[5] = r.y; v[6] = r.z; v[7] = r.w;
+        }
+    }
+    double squares = 0.0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        squares += (double) v[k] * (double) v[k];
+    squares = wave_sum_d(squares);
+    if (lane == 0)
+        sPartial[wave] = squares;
+    __syncthreads();
+    double total = 0.0;
+    for (int w = 0; w < waves; ++w)
+        total += sPartial[w];
+    const double scale = norm_scale(total, width, epsilon);
+
+    float n[8];
+    float amax = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        n[k] = active ? norm_value(v[k], scale, weight[i0 + k]) : 0.f;
+        amax = fmaxf(amax, fabsf(n[k]));
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    const uint16_t bits = scale_bits_from_amax(amax);
+    const float s = half_value(bits);
+    const float inverse = bits ? 1.0f / s : 0.f;
+    int packed[2] = {0, 0};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int q = bits ? quantize_value(n[k], s, inverse) : 0;
+        packed[k / 4] |= (q & 0xFF) << (8 * (k % 4));
+    }
+    if (active) {
+        *reinterpret_cast<int2 *>(row.q + i0) = make_int2(packed[0], packed[1]);
+        if ((t & 3) == 0)
+            row.scale[i0 / kBlock] = (double) s;
+        if (blockIdx.x == 0) {
+            if (normalised_out)
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    normalised_out[i0 + k] = n[k];
+            if (q8_out) {
+                *reinterpret_cast<int2 *>(q8_out + i0) = make_int2(packed[0], packed[1]);
+                if ((t & 3) == 0)
+                    reinterpret_cast<uint16_t *>(q8_out + width)[i0 / kBlock] = bits;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// The 32-byte weight block and fp16 scale of (row, block) in an Int8Blocks
+// tensor of `rows` x `inner`.
+struct WeightBlock {
+    int4 w0, w1;
+    uint16_t scale;
+};
+
+__device__ inline WeightBlock load_block(const uint8_t *w8, int64_t rows, int inner, int64_t row,
+                                         int block, bool valid)
+{
+    WeightBlock b;
+    if (valid) {
+        const int4 *p = reinterpret_cast<const int4 *>(w8 + row * inner + (int64_t) block * kBlock);
+        b.w0 = p[0];
+        b.w1 = p[1];
+        b.scale = reinterpret_cast<const uint16_t *>(w8 + rows * inner)[row * (inner / kBlock) + block];
+    } else {
+        b.w0 = make_int4(0, 0, 0, 0);
+        b.w1 = make_int4(0, 0, 0, 0);
+        b.scale = 0;
+    }
+    return b;
+}
+
+__device__ inline double block_term(const WeightBlock &b, const int4 &a0, const int4 &a1, double sa)
+{
+    return (double) dot32(b.w0, b.w1, a0, a1) * ((double) half_value(b.scale) * sa);
+}
+
+// ---- q|k|v + RoPE + fp16 KV ---------------------------------------------------
+// A pair task is the two rows (i, i + half) of one head of q, k or v; a wave
+// owns kPairsPerWave of them.  Lane l owns block l of every row (width <= 2048).
+constexpr int kPairsPerWave = 2;
+
+__global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a)
+{
+    __shared__ RowQ8 row;
+    __shared__ double sPartial[kWaves];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int half = a.head_dim / 2;
+    const int qWidth = a.heads * a.head_dim, kvWidth = a.kv_heads * a.head_dim;
+    const int outputs = qWidth + 2 * kvWidth;
+    const int pairs = (a.heads + 2 * a.kv_heads) * half;
+    const int nb = a.width / kBlock;
+    const int firstPair = (blockIdx.x * kWaves + wave) * kPairsPerWave;
+
+    WeightBlock lo[kPairsPerWave], hi[kPairsPerWave];
+    int rowLo[kPairsPerWave];
+#pragma unroll
+    for (int p = 0; p < kPairsPerWave; ++p) {
+        const int pair = firstPair + p;
+        const int head = pair / half, i = pair % half;
+        rowLo[p] = head * a.head_dim + i; // q heads, then k heads, then v heads
+        const bool valid = pair < pairs && lane < nb;
+        lo[p] = load_block(a.weights, outputs, a.width, rowLo[p], lane, valid);
+        hi[p] = load_block(a.weights, outputs, a.width, rowLo[p] + half, lane, valid);
+    }
+
+    const uint32_t *token = a.embedding ? a.sequence + *a.position : nullptr;
+    norm_q8_prologue(a.hidden, token, a.embedding, a.vocab, a.embed_scale, a.hidden_out,
+                     a.norm_weight, a.width, a.epsilon, row, sPartial, a.debug_normalised,
+                     a.debug_q8);
+
+    int4 a0 = make_int4(0, 0, 0, 0), a1 = a0;
+    double sa = 0.0;
+    if (lane < nb) {
+        a0 = reinterpret_cast<const int4 *>(row.q + lane * kBlock)[0];
+        a1 = reinterpret_cast<const int4 *>(row.q + lane * kBlock)[1];
+        sa = row.scale[lane];
+    }
+    const int position = *a.position;
+    constexpr int kRows = 2 * kPairsPerWave;
+    double y[kRows];
+#pragma unroll
+    for (int p = 0; p < kPairsPerWave; ++p) {
+        y[2 * p] = block_term(lo[p], a0, a1, sa);
+        y[2 * p + 1] = block_term(hi[p], a0, a1, sa);
+    }
+    const double total = reduce_rows<kRows>(y, lane);
+    double rowTotal[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r)
+        rowTotal[r] = __shfl(total, lane_of_row<kRows>(r));
+#pragma unroll
+    for (int p = 0; p < kPairsPerWave; ++p) {
+        const double yLo = rowTotal[2 * p], yHi = rowTotal[2 * p + 1];
+        const int pair = firstPair + p;
+        if (lane != 0 || pair >= pairs)
+            continue;
+        const int r = rowLo[p], i = pair % half;
+        const float fLo = (float) yLo, fHi = (float) yHi; // the product's fp32 outputs
+        const int64_t angle = (int64_t) position * half + i;
+        if (r < qWidth) {
+            float outLo, outHi;
+            rotate_pair(fLo, fHi, a.cosines[angle], a.sines[angle], &outLo, &outHi);
+            a.query[r] = outLo;
+            a.query[r + half] = outHi;
+        } else if (r < qWidth + kvWidth) {
+            float outLo, outHi;
+            rotate_pair(fLo, fHi, a.cosines[angle], a.sines[angle], &outLo, &outHi);
+            uint16_t *keys = a.key_cache + (int64_t) position * kvWidth + (r - qWidth);
+            keys[0] = half_bits(outLo);
+            keys[half] = half_bits(outHi);
+        } else {
+            uint16_t *values = a.value_cache + (int64_t) position * kvWidth + (r - qWidth - kvWidth);
+            values[0] = half_bits(fLo);
+            values[half] = half_bits(fHi);
+        }
+    }
+}
+
+// ---- split-key attention with the merge in the last workgroup -------------------
+// A workgroup of 1024 threads owns a contiguous key range (whole 32-key
+// tiles, at most kDecodeSplits ranges) and every head.  Each tile's keys and
+// values are fetched with all of the tile's loads in flight at once, scored
+// in double by four threads a (head, key) pair, folded into a running (max,
+// sum, value sums) per head.  The last workgroup to finish merges the ranges,
+// with each batch of partial loads issued before any is used.
+constexpr int kAttnThreads = 1024;
+constexpr int kAttnWaves = kAttnThreads / 64;
+constexpr int kKeyTile = 32;
+constexpr int kMaxQueryWidth = 2048;
+constexpr int kMaxKvWidth = 256;
+constexpr int kOutPerThread = kMaxQueryWidth / kAttnThreads;          // 2: heads h and h + 4
+constexpr int kTileBytes = kKeyTile * kMaxKvWidth * 2;                // 16 KiB
+constexpr int kTileVectors = kTileBytes / 16 / kAttnThreads;          // 1
+constexpr int kMergeBatch = 16;
+
+__device__ inline int split_keys(int keyCount)
+{
+    const int tiles = (keyCount + kKeyTile - 1) / kKeyTile;
+    return ((tiles + kDecodeSplits - 1) / kDecodeSplits) * kKeyTile;
+}
+
+struct TileLoads {
+    int4 k[kTileVectors], v[kTileVectors];
+};
+
+__device__ inline void load_tile(TileLoads &t, const uint16_t *keys, const uint16_t *values,
+                                 int first, int count, int kvWidth)
+{
+    const int vectors = count * kvWidth / 8; // 8 halves a vector
+    const int4 *k = reinterpret_cast<const int4 *>(keys + (int64_t) first * kvWidth);
+    const int4 *v = reinterpret_cast<const int4 *>(values + (int64_t) first * kvWidth);
+#pragma unroll
+    for (int i = 0; i < kTileVectors; ++i) {
+        const int at = threadIdx.x + i * kAttnThreads;
+        if (at < vectors) {
+            t.k[i] = k[at];
+            t.v[i] = v[at];
+        } else {
+            t.k[i] = make_int4(0, 0, 0, 0);
+            t.v[i] = make_int4(0, 0, 0, 0);
+        }
+    }
+}
+
+__global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a)
+{
+    __shared__ double sQuery[kMaxQueryWidth + 2 * kMaxHeads]; // head rows padded by 2
+    __shared__ double sPart[kAttnThreads];
+    __shared__ uint32_t sKeys[kKeyTile * (kMaxKvWidth / 2 + 1)];
+    __shared__ int4 sValues[kTileBytes / 16];
+    __shared__ double sWeights[kMaxHeads * kKeyTile];
+    __shared__ double sMax[kMaxHeads], sSum[kMaxHeads], sFactor[kMaxHeads];
+    __shared__ double sMergeMax[kMaxHeads * kDecodeSplits], sMergeSum[kMaxHeads * kDecodeSplits];
+    __shared__ int sLast;
+
+    const int split = blockIdx.x;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int keyCount = *a.position + 1;
+    const int perSplit = split_keys(keyCount);
+    const int splits = (keyCount + perSplit - 1) / perSplit;
+    const int k0 = split * perSplit;
+    if (k0 >= keyCount)
+        return;
+    const int k1 = min(k0 + perSplit, keyCount);
+    const int heads = a.heads, hd = a.head_dim;
+    const int qWidth = heads * hd, kvWidth = a.kv_heads * hd;
+    const int perKv = heads / a.kv_heads;
+    const int keyWords = kvWidth / 2, keyStride = kMaxKvWidth / 2 + 1;
+    const int dots = heads * kKeyTile;
+    // threads a dot product: a power of two, each part at least four channels
+    int perDot = dots >= kAttnThreads ? 1 : kAttnThreads / dots;
+    while (perDot > 1 && hd / perDot < 4)
+        perDot >>= 1;
+
+    // the query (fp32 -> double) and the first tile, all loads in flight
+    float2 q2 = make_float2(0.f, 0.f);
+    if (2 * t < qWidth)
+        q2 = reinterpret_cast<const float2 *>(a.query)[t];
+    TileLoads tile;
+    load_tile(tile, a.key_cache, a.value_cache, k0, min(kKeyTile, k1 - k0), kvWidth);
+    if (2 * t < qWidth) {
+        const int h = (2 * t) / hd; // both halves of the pair are in one head (hd even)
+        sQuery[2 * t + 2 * h] = q2.x;
+        sQuery[2 * t + 1 + 2 * h] = q2.y;
+    }
+    if (t < heads) {
+        sMax[t] = -INFINITY;
+        sSum[t] = 0.0;
+    }
+    double acc[kOutPerThread];
+    int outHead[kOutPerThread], outColumn[kOutPerThread]; // division-free inner loops
+#pragma unroll
+    for (int i = 0; i < kOutPerThread; ++i) {
+        const int idx = t + i * kAttnThreads; // head idx / hd, channel idx % hd
+        acc[i] = 0.0;
+        outHead[i] = idx < qWidth ? idx / hd : 0;
+        outColumn[i] = idx < qWidth ? (outHead[i] / perKv) * hd + idx % hd : 0;
+    }
+    // the (head, key, part) of this thread's share of the scores: the parts
+    // of one dot product sit in different waves, so a wave reads one or two
+    // query rows (broadcast) and 32 different key rows (different banks)
+    const int dotsPerPass = kAttnThreads / perDot;
+    const int myDot = t % dotsPerPass, part = t / dotsPerPass;
+    const int myHead = myDot / kKeyTile, myKey = myDot % kKeyTile;
+    const int span = hd / perDot;
+    const int qBase = myHead * (hd + 2) + part * span;
+    const int kBase = ((myHead / perKv) * hd + part * span) / 2;
+
+    for (int t0 = k0; t0 < k1; t0 += kKeyTile) {
+        const int nk = min(kKeyTile, k1 - t0);
+        {
+            const int vectors = nk * kvWidth / 8;
+#pragma unroll
+            for (int i = 0; i < kTileVectors; ++i) {
+                const int at = t + i * kAttnThreads;
+                if (at < vectors) {
+                    const int j = at / (keyWords / 4), w = (at % (keyWords / 4)) * 4;
+                    uint32_t *dst = sKeys + j * keyStride + w;
+                    dst[0] = (uint32_t) tile.k[i].x;
+                    dst[1] = (uint32_t) tile.k[i].y;
+                    dst[2] = (uint32_t) tile.k[i].z;
+                    dst[3] = (uint32_t) tile.k[i].w;
+                    sValues[at] = tile.v[i];
+                }
+            }
+        }
+        __syncthreads();
+        if (t0 + kKeyTile < k1)
+            load_tile(tile, a.key_cache, a.value_cache, t0 + kKeyTile,
+                      min(kKeyTile, k1 - t0 - kKeyTile), kvWidth);
+
+        {
+            double partial = 0.0;
+            if (myDot < dots && myKey < nk) {
+                const double *q = sQuery + qBase; // padded head row
+                const uint32_t *k = sKeys + myKey * keyStride + kBase;
+                double p0 = 0.0, p1 = 0.0, p2 = 0.0, p3 = 0.0;
+                int c = 0;
+                for (; c + 4 <= span; c += 4) {
+                    const uint32_t x = k[c / 2], y = k[c / 2 + 1];
+                    p0 += q[c] * (double) half_value((uint16_t) (x & 0xFFFFu));
+                    p1 += q[c + 1] * (double) half_value((uint16_t) (x >> 16));
+                    p2 += q[c + 2] * (double) half_value((uint16_t) (y & 0xFFFFu));
+                    p3 += q[c + 3] * (double) half_value((uint16_t) (y >> 16));
+                }
+                for (; c < span; c += 2) {
+                    const uint32_t x = k[c / 2];
+                    p0 += q[c] * (double) half_value((uint16_t) (x & 0xFFFFu));
+                    p1 += q[c + 1] * (double) half_value((uint16_t) (x >> 16));
+                }
+                partial = (p0 + p1) + (p2 + p3);
+            }
+            sPart[t] = partial;
+        }
+        __syncthreads();
+        if (t < dots) {
+            double total = 0.0;
+            for (int p = 0; p < perDot; ++p)
+                total += sPart[p * dotsPerPass + t];
+            sWeights[t] = (t % kKeyTile) < nk ? (double) a.scale * total : -INFINITY;
+        }
+        __syncthreads();
+
+        for (int head = wave; head < heads; head += kAttnWaves) {
+            const double s = lane < kKeyTile ? sWeights[head * kKeyTile + lane] : -INFINITY;
+            const double previous = sMax[head];
+            const double largest = fmax(previous, wave_max_d(s));
+            const double w = lane < nk ? exp(s - largest) : 0.0;
+            const double total = wave_sum_d(w);
+            if (lane < kKeyTile)
+                sWeights[head * kKeyTile + lane] = w;
+            if (lane == 0) {
+                const double factor = previous == -INFINITY ? 0.0 : exp(previous - largest);
+                sFactor[head] = factor;
+                sSum[head] = sSum[head] * factor + total;
+                sMax[head] = largest;
+            }
+        }
+        __syncthreads();
+
+        const uint16_t *vTile = reinterpret_cast<const uint16_t *>(sValues);
+#pragma unroll
+        for (int i = 0; i < kOutPerThread; ++i)
+            acc[i] *= sFactor[outHead[i]];
+        for (int j = 0; j < nk; ++j) {
+            const uint16_t *vRow = vTile + j * kvWidth;
+            const double *w = sWeights + j;
+#pragma unroll
+            for (int i = 0; i < kOutPerThread; ++i)
+                acc[i] += w[outHead[i] * kKeyTile] * (double) half_value(vRow[outColumn[i]]);
+        }
+        __syncthreads(); // the next tile overwrites the LDS tiles
+    }
+
+    double *o = a.ws_o + (int64_t) split * qWidth;
+#pragma unroll
+    for (int i = 0; i < kOutPerThread; ++i) {
+        const int idx = t + i * kAttnThreads;
+        if (idx < qWidth)
+            o[idx] = acc[i];
+    }
+    if (t < heads) {
+        a.ws_ml[(split * heads + t) * 2] = sMax[t];
+        a.ws_ml[(split * heads + t) * 2 + 1] = sSum[t];
+    }
+    // one thread publishes the workgroup's writes (release) and takes the
+    // ticket; the last one's acquire makes every partial visible to it
+    __syncthreads();
+    if (t == 0) {
+        __threadfence();
+        sLast = atomicAdd(a.counter, 1) == splits - 1;
+        if (sLast)
+            __threadfence();
+    }
+    __syncthreads();
+    if (!sLast)
+        return;
+
+    // the merge (MultiQueryAttention.h:43-49): every split rescaled to the
+    // row's maximum, the sums divided by the total, rounded and quantized
+    for (int idx = t; idx < heads * splits; idx += kAttnThreads) {
+        const int s = idx / heads, head = idx % heads;
+        sMergeMax[head * kDecodeSplits + s] = a.ws_ml[idx * 2];
+        sMergeSum[head * kDecodeSplits + s] = a.ws_ml[idx * 2 + 1];
+    }
+    __syncthreads();
+    if (t < heads) {
+        double largest = -INFINITY;
+        for (int s = 0; s < splits; ++s)
+            largest = fmax(largest, sMergeMax[t * kDecodeSplits + s]);
+        sMax[t] = largest;
+    }
+    __syncthreads();
+    for (int idx = t; idx < heads * splits; idx += kAttnThreads) {
+        const int head = idx / splits, s = idx % splits;
+        sMergeMax[head * kDecodeSplits + s] = exp(sMergeMax[head * kDecodeSplits + s] - sMax[head]);
+    }
+    __syncthreads();
+    if (t < heads) {
+        double total = 0.0;
+        for (int s = 0; s < splits; ++s)
+            total += sMergeSum[t * kDecodeSplits + s] * sMergeMax[t * kDecodeSplits + s];
+        sSum[t] = total;
+    }
+    __syncthreads();
+
+    double weighted[kOutPerThread];
+#pragma unroll
+    for (int i = 0; i < kOutPerThread; ++i)
+        weighted[i] = 0.0;
+    for (int s0 = 0; s0 < splits; s0 += kMergeBatch) {
+        double partOf[kMergeBatch][kOutPerThread];
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u)
+#pragma unroll
+            for (int i = 0; i < kOutPerThread; ++i) {
+                const int idx = t + i * kAttnThreads;
+                partOf[u][i] = (s0 + u < splits && idx < qWidth)
+                                   ? a.ws_o[(int64_t) (s0 + u) * qWidth + idx] : 0.0;
+            }
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u)
+#pragma unroll
+            for (int i = 0; i < kOutPerThread; ++i)
+                if (s0 + u < splits)
+                    weighted[i] += partOf[u][i] * sMergeMax[outHead[i] * kDecodeSplits + s0 + u];
+    }
+#pragma unroll
+    for (int i = 0; i < kOutPerThread; ++i) {
+        const int idx = t + i * kAttnThreads;
+        if (idx >= qWidth) // whole 32-blocks leave together
+            break;
+        const float v = (float) (weighted[i] / sSum[outHead[i]]);
+        if (a.out)
+            a.out[idx] = v;
+        float amax = fabsf(v);
+        for (int mask = 16; mask >= 1; mask >>= 1)
+            amax = fmaxf(amax, __shfl_xor(amax, mask));
+        const uint16_t bits = scale_bits_from_amax(amax);
+        const float sc = half_value(bits);
+        a.q8[idx] = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);
+        if ((t & 31) == 0)
+            reinterpret_cast<uint16_t *>(a.q8 + qWidth)[idx / kBlock] = bits;
+    }
+    if (t == 0)
+        atomicExch(a.counter, 0); // ready for the next launch
+}
+
+// ---- gate|up + GeGLU + Q8 -----------------------------------------------------------
+// A workgroup of eight waves owns one 32-element block of the GeGLU output:
+// gate rows [32 b, 32 b + 32) and the matching up rows; a wave owns four of
+// them (eight rows, reduced together).
+constexpr int kGluThreads = 512;
+constexpr int kGluWaves = kGluThreads / 64;
+constexpr int kGluPerWave = kBlock / kGluWaves; // 4
+
+__global__ __launch_bounds__(kGluThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void gateup_geglu_kernel(GateUpArgs a)
+{
+    __shared__ RowQ8 row;
+    __shared__ double sPartial[kGluWaves];
+    __shared__ float sGate[kBlock], sUp[kBlock];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nb = a.width / kBlock;
+    const int F = a.intermediate;
+    const int o0 = blockIdx.x * kBlock + wave * kGluPerWave;
+    const bool valid = lane < nb;
+
+    // rows 0..3 gate, 4..7 up
+    WeightBlock w[2 * kGluPerWave];
+#pragma unroll
+    for (int k = 0; k < kGluPerWave; ++k) {
+        w[k] = load_block(a.weights, 2 * (int64_t) F, a.width, o0 + k, lane, valid);
+        w[kGluPerWave + k] =
+            load_block(a.weights, 2 * (int64_t) F, a.width, (int64_t) F + o0 + k, lane, valid);
+    }
+    norm_q8_prologue(a.hidden, nullptr, nullptr, 0, 0.f, nullptr, a.norm_weight, a.width,
+                     a.epsilon, row, sPartial, nullptr, nullptr);
+    int4 a0 = make_int4(0, 0, 0, 0), a1 = a0;
+    double sa = 0.0;
+    if (valid) {
+        a0 = reinterpret_cast<const int4 *>(row.q + lane * kBlock)[0];
+        a1 = reinterpret_cast<const int4 *>(row.q + lane * kBlock)[1];
+        sa = row.scale[lane];
+    }
+    double y[2 * kGluPerWave];
+#pragma unroll
+    for (int k = 0; k < 2 * kGluPerWave; ++k)
+        y[k] = block_term(w[k], a0, a1, sa);
+    const double total = reduce_rows<2 * kGluPerWave>(y, lane);
+    if (stores_row<2 * kGluPerWave>(lane)) {
+        const int r = row_of_lane<2 * kGluPerWave>(lane);
+        const int o = wave * kGluPerWave + (r % kGluPerWave);
+        if (r < kGluPerWave)
+            sGate[o] = (float) total;
+        else
+            sUp[o] = (float) total;
+    }
+    __syncthreads();
+    if (threadIdx.x < kBlock) {
+        const int o = blockIdx.x * kBlock + threadIdx.x;
+        const float v = geglu(sGate[threadIdx.x], sUp[threadIdx.x]);
+        if (a.debug_activated)
+            a.debug_activated[o] = v;
+        float amax = fabsf(v);
+        for (int mask = 16; mask >= 1; mask >>= 1)
+            amax = fmaxf(amax, __shfl_xor(amax, mask));
+        const uint16_t bits = scale_bits_from_amax(amax);
+        const float sc = half_value(bits);
+        a.q8[o] = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);
+        if (threadIdx.x == 0)
+            reinterpret_cast<uint16_t *>(a.q8 + F)[blockIdx.x] = bits;
+    }
+}
+
+// ---- final norm + tied lm_head + argmax ----------------------------------------------
+// The final norm and its Q8 row come from a one-workgroup kernel; the lm_head
+// is then a one-shot product (every wave loads its eight rows' blocks once,
+// the activation block of its lane straight from the Q8 row) whose rows are
+// reduced together.  Each workgroup folds its rows into one 64-bit candidate
+// (an order-preserving key of the logit above the complemented row index) and
+// merges it into a single device word with one atomicMax, so the largest logit
+// wins and, among equal logits, the lowest index -- the first maximum.  No
+// workgroup waits for another; a one-thread kernel then turns the word into
+// the token id, stores it in the sequence slot after the position, advances
+// the position and clears the word.
+constexpr int kHeadRows = 8;
+
+// Larger floats give larger keys; NaN gives 0, below every ordered value, so
+// it is never chosen (a NaN logit never compares greater in the scan either).
+__device__ inline unsigned long long candidate_key(float value, uint32_t index)
+{
+    const uint32_t bits = __float_as_uint(value);
+    uint32_t key = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+    if (value != value)
+        key = 0;
+    return ((unsigned long long) key << 32) | (unsigned long long) (0xFFFFFFFFu - index);
+}
+
+__device__ inline unsigned long long fold_wave_max(unsigned long long c)
+{
+    for (int mask = 32; mask >= 1; mask >>= 1) {
+        const unsigned long long other = __shfl_xor(c, mask);
+        c = other > c ? other : c;
+    }
+    return c;
+}
+
+__global__ __launch_bounds__(kThreads) void final_norm_kernel(HeadArgs a)
+{
+    __shared__ RowQ8 row;
+    __shared__ double sPartial[kWaves];
+    norm_q8_prologue(a.hidden, nullptr, nullptr, 0, 0.f, nullptr, a.norm_weight, a.width,
+                     a.epsilon, row, sPartial, a.normalised_out, a.q8);
+}
+
+__global__ __launch_bounds__(kThreads) void lmhead_argmax_kernel(HeadArgs a)
+{
+    __shared__ unsigned long long sBest[kWaves];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nb = a.width / kBlock;
+    const bool valid = lane < nb;
+    const int64_t V = a.vocab;
+    const int64_t r0 = ((int64_t) blockIdx.x * kWaves + wave) * kHeadRows;
+
+    WeightBlock w[kHeadRows];
+#pragma unroll
+    for (int k = 0; k < kHeadRows; ++k)
+        w[k] = load_block(a.weights, V, a.width, r0 + k, lane, valid && r0 + k < V);
+    int4 a0 = make_int4(0, 0, 0, 0), a1 = a0;
+    double sa = 0.0;
+    if (valid) {
+        a0 = reinterpret_cast<const int4 *>(a.q8 + lane * kBlock)[0];
+        a1 = reinterpret_cast<const int4 *>(a.q8 + lane * kBlock)[1];
+        sa = (double) half_value(reinterpret_cast<const uint16_t *>(a.q8 + a.width)[lane]);
+    }
+    double y[kHeadRows];
+#pragma unroll
+    for (int k = 0; k < kHeadRows; ++k)
+        y[k] = block_term(w[k], a0, a1, sa);
+    const double total = reduce_rows<kHeadRows>(y, lane);
+    const int64_t row = r0 + row_of_lane<kHeadRows>(lane);
+    unsigned long long best = 0;
+    if (stores_row<kHeadRows>(lane) && row < V) {
+        const float logit = (float) total;
+        a.logits[row] = logit;
+        best = candidate_key(logit, (uint32_t) row);
+    }
+    best = fold_wave_max(best);
+    if (lane == 0)
+        sBest[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long c = sBest[0];
+        for (int k = 1; k < kWaves; ++k)
+            c = sBest[k] > c ? sBest[k] : c;
+        if (c != 0)
+            atomicMax(a.best, c);
+    }
+}
+
+__global__ void head_finalize_kernel(HeadArgs a)
+{
+    const unsigned long long c = *a.best;
+    const uint32_t token = c == 0 ? 0u : 0xFFFFFFFFu - (uint32_t) (c & 0xFFFFFFFFull);
+    const int position = *a.position;
+    if (a.sequence)
+        a.sequence[position + 1] = token;
+    if (a.advance)
+        *a.position = position + 1;
+    *a.best = 0;
+}
+
+} // namespace
+
+// ============================================================================
+// Launchers
+// ============================================================================
+bool fused_decode_supported(int width, int heads, int kv_heads, int head_dim, int intermediate)
+{
+    const int qWidth = heads * head_dim, kvWidth = kv_heads * head_dim;
+    const int dots = heads * kKeyTile;
+    return kvWidth % 8 == 0 && width % kBlock == 0 && width <= kFusedMaxWidth && head_dim % 4 == 0
+           && qWidth <= kMaxQueryWidth && qWidth % kBlock == 0 && kvWidth <= kMaxKvWidth
+           && heads <= kMaxHeads && heads % kv_heads == 0 && (dots & (dots - 1)) == 0
+           && intermediate % kBlock == 0 && intermediate <= 16384 && (head_dim / 2) > 0;
+}
+
+size_t decode_workspace_bytes(int heads, int head_dim)
+{
+    return (size_t) kDecodeSplits * ((size_t) heads * head_dim + 2 * heads) * sizeof(double);
+}
+
+static int head_groups(int vocab)
+{
+    return (vocab + kWaves * kHeadRows - 1) / (kWaves * kHeadRows);
+}
+
+hipError_t launch_qkv_rope(const QkvArgs &a, hipStream_t stream)
+{
+    const int pairs = (a.heads + 2 * a.kv_heads) * (a.head_dim / 2);
+    const int perGroup = kWaves * kPairsPerWave;
+    hipLaunchKernelGGL(qkv_rope_kernel, dim3((pairs + perGroup - 1) / perGroup), dim3(kThreads), 0,
+                       stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention(const AttentionArgs &a, hipStream_t stream)
+{
+    hipLaunchKernelGGL(attention_kernel, dim3(kDecodeSplits), dim3(kAttnThreads), 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_gateup_geglu(const GateUpArgs &a, hipStream_t stream)
+{
+    hipLaunchKernelGGL(gateup_geglu_kernel, dim3(a.intermediate / kBlock), dim3(kGluThreads), 0,
+                       stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_final_norm(const HeadArgs &a, hipStream_t stream)
+{
+    hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(kThreads), 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_lmhead_argmax(const HeadArgs &a, hipStream_t stream)
+{
+    hipLaunchKernelGGL(lmhead_argmax_kernel, dim3(head_groups(a.vocab)), dim3(kThreads), 0, stream,
+                       a);
+    return hipGetLastError();
+}
+
+hipError_t launch_head_finalize(const HeadArgs &a, hipStream_t stream)
+{
+    hipLaunchKernelGGL(head_finalize_kernel, dim3(1), dim3(1), 0, stream, a);
+    return hipGetLastError();
+}
+
+} // namespace gq8

@@ -4,6 +4,7 @@
 // Gemma.cpp).  Host C++ over the HIP runtime; every device buffer is owned
 // here and every refusal is checked before anything is launched.
 #include "gemma_q8.h"
+#include "gq8_decode.hpp"
 #include "gq8_kernels.hpp"
 #include "gq8_numerics.hpp"
 
@@ -417,6 +418,12 @@ struct gq8_decoder {
     uint8_t *debugQ8 = nullptr;   // (layers + 1) x 4 x q8_bytes(1, maxInner)
     float *debugAttended = nullptr, *debugActivated = nullptr, *debugNormalised = nullptr;
 
+    // the fused one-token path
+    bool useFused = true;
+    bool fusedSupported = false;
+    double *decodeO = nullptr, *decodeMl = nullptr;
+    int *counters = nullptr; // [0] attention; [2..3] the lm_head's packed 64-bit maximum
+
     hipGraphExec_t graph = nullptr;
     bool capturing = false;
 
@@ -671,11 +678,20 @@ extern "C" int gq8_decoder_create(const gq8_shape *shape, gq8_decoder **out)
     GQ8_ALLOC(d->debugNormalised, R * W * sizeof(float));
     GQ8_ALLOC(d->debugAttended, R * d->qWidth * sizeof(float));
     GQ8_ALLOC(d->debugActivated, R * (int64_t) s.intermediate * sizeof(float));
+    d->fusedSupported = gq8::fused_decode_supported(s.width, s.heads, s.kv_heads, s.head_dim,
+                                                    s.intermediate);
+    {
+        const size_t wsBytes = gq8::decode_workspace_bytes(s.heads, s.head_dim);
+        GQ8_ALLOC(d->decodeO, wsBytes);
+        d->decodeMl = d->decodeO + (size_t) gq8::kDecodeSplits * s.heads * s.head_dim;
+        GQ8_ALLOC(d->counters, 4 * sizeof(int));
+    }
 #undef GQ8_ALLOC
     if (hipHostMalloc((void **) &d->pinnedToken, sizeof(uint32_t) * 4) != hipSuccess)
         return cleanup(fail(GQ8_ERR_MEMORY, "pinned allocation failed"));
     if (hipMemset(d->sequence, 0, ((size_t) s.max_positions + 1) * sizeof(uint32_t)) != hipSuccess
         || hipMemset(d->position, 0, sizeof(int)) != hipSuccess
+        || hipMemset(d->counters, 0, 4 * sizeof(int)) != hipSuccess
         || hipMemset(d->keyCache, 0, cacheElements * sizeof(uint16_t)) != hipSuccess
         || hipMemset(d->valueCache, 0, cacheElements * sizeof(uint16_t)) != hipSuccess
         || hipDeviceSynchronize() != hipSuccess)
@@ -893,6 +909,18 @@ extern "C" int gq8_decoder_position(const gq8_decoder *d)
     return d ? d->hostPosition : -1;
 }
 
+extern "C" int gq8_decoder_set_fused(gq8_decoder *d, int enabled)
+{
+    if (!d)
+        return fail(GQ8_ERR_ARGUMENT, "null decoder");
+    d->useFused = enabled != 0;
+    if (d->graph) { // a captured step follows the path it was captured with
+        (void) hipGraphExecDestroy(d->graph);
+        d->graph = nullptr;
+    }
+    return GQ8_OK;
+}
+
 extern "C" int gq8_decoder_set_debug(gq8_decoder *d, int enabled)
 {
     if (!d)
@@ -979,6 +1007,116 @@ struct StageTimer {
         GQ8_LAUNCH(expr);                         \
     } while (0)
 
+// The one-token step through the fused kernels (gq8_decode.hip): five
+// launches a layer and one for the head, which also chooses the next id and
+// advances the device position.
+int encode_fused_token(gq8_decoder *d, float *logits, bool sample)
+{
+    const gq8_shape &s = d->shape;
+    const int W = s.width, F = s.intermediate;
+    hipStream_t st = d->stream;
+    const bool dbg = d->debug && !d->capturing;
+    auto debugValues = [&](int which, int layer) {
+        return dbg ? d->debugValues + ((int64_t) layer * 4 + which) * d->maxInner : nullptr;
+    };
+    auto debugQ8 = [&](int which, int layer) {
+        return dbg ? d->debugQ8 + ((int64_t) layer * 4 + which) * gq8::q8_bytes(1, d->maxInner)
+                   : nullptr;
+    };
+
+    for (int l = 0; l < s.layers; ++l) {
+        const size_t layerCache = (size_t) l * s.max_positions * d->kvWidth;
+        gq8::QkvArgs q{};
+        q.hidden = d->hidden;
+        q.sequence = d->sequence;
+        q.embedding = l == 0 ? d->embedding : nullptr;
+        q.vocab = s.vocab;
+        q.embed_scale = s.embedding_scale;
+        q.hidden_out = l == 0 ? d->hidden : nullptr;
+        q.norm_weight = d->inputNorm[l];
+        q.width = W;
+        q.epsilon = s.rms_epsilon;
+        q.weights = d->qkv[l];
+        q.heads = s.heads;
+        q.kv_heads = s.kv_heads;
+        q.head_dim = s.head_dim;
+        q.position = d->position;
+        q.cosines = d->cosines;
+        q.sines = d->sines;
+        q.query = d->qkvRows;
+        q.key_cache = d->keyCache + layerCache;
+        q.value_cache = d->valueCache + layerCache;
+        q.debug_normalised = debugValues(0, l);
+        q.debug_q8 = debugQ8(0, l);
+        GQ8_STAGE(kStageQkv, gq8::launch_qkv_rope(q, st));
+
+        gq8::AttentionArgs at{};
+        at.query = d->qkvRows;
+        at.key_cache = q.key_cache;
+        at.value_cache = q.value_cache;
+        at.heads = s.heads;
+        at.kv_heads = s.kv_heads;
+        at.head_dim = s.head_dim;
+        at.position = d->position;
+        at.scale = 1.f / std::sqrt((float) s.head_dim);
+        at.ws_o = d->decodeO;
+        at.ws_ml = d->decodeMl;
+        at.counter = d->counters;
+        at.out = debugValues(1, l);
+        at.q8 = d->x8;
+        GQ8_STAGE(kStageAttention, gq8::launch_attention(at, st));
+        if (dbg && copy_last_q8_row(d, d->x8, 1, d->qWidth, debugQ8(1, l)))
+            return GQ8_ERR_DEVICE;
+
+        GQ8_STAGE(kStageO, gq8::launch_q8_product(d->x8, 1, 0, 1, d->out[l], d->qWidth, W,
+                                                  d->hidden, W, 1, st));
+
+        gq8::GateUpArgs g{};
+        g.hidden = d->hidden;
+        g.norm_weight = d->postNorm[l];
+        g.width = W;
+        g.epsilon = s.rms_epsilon;
+        g.weights = d->gateUp[l];
+        g.intermediate = F;
+        g.q8 = d->x8;
+        g.debug_activated = debugValues(2, l);
+        GQ8_STAGE(kStageGateUp, gq8::launch_gateup_geglu(g, st));
+        if (dbg && copy_last_q8_row(d, d->x8, 1, F, debugQ8(2, l)))
+            return GQ8_ERR_DEVICE;
+
+        GQ8_STAGE(kStageDown, gq8::launch_q8_product(d->x8, 1, 0, 1, d->down[l], F, W, d->hidden,
+                                                     W, 1, st));
+        if (dbg && capture_debug(d, 3, l, d->hidden, 1, W, nullptr))
+            return GQ8_ERR_DEVICE;
+    }
+
+    gq8::HeadArgs h{};
+    h.hidden = d->hidden;
+    h.norm_weight = d->finalNorm;
+    h.width = W;
+    h.epsilon = s.rms_epsilon;
+    h.weights = d->embedding;
+    h.vocab = s.vocab;
+    h.logits = logits;
+    h.normalised_out = d->normalisedRows;
+    h.q8 = d->x8;
+    h.best = reinterpret_cast<unsigned long long *>(d->counters + 2);
+    h.sequence = sample ? d->sequence : nullptr;
+    h.position = d->position;
+    h.advance = 1;
+    GQ8_STAGE(kStageNorm, gq8::launch_final_norm(h, st));
+    GQ8_STAGE(kStageLogits, gq8::launch_lmhead_argmax(h, st));
+    GQ8_STAGE(kStageArgmax, gq8::launch_head_finalize(h, st));
+    if (dbg && copy_last_q8_row(d, d->x8, 1, W, debugQ8(0, s.layers)))
+        return GQ8_ERR_DEVICE;
+    if (dbg) {
+        float *slot = d->debugValues + (int64_t) s.layers * 4 * d->maxInner;
+        GQ8_HIP(hipMemcpyAsync(slot, d->normalisedRows, W * sizeof(float), hipMemcpyDeviceToDevice,
+                               st));
+    }
+    return GQ8_OK;
+}
+
 // Decoder::step's recording (Decoder.cpp:579-706) for `rows` tokens read
 // from the sequence slots at the device position; logits of the last
 // logitsRows rows; with sample, the argmax of the last row is written to the
@@ -990,6 +1128,8 @@ int encode_step(gq8_decoder *d, int rows, float *logits, int logitsRows, bool sa
     hipStream_t st = d->stream;
     const float attentionScale = 1.f / std::sqrt((float) s.head_dim);
     const bool dbg = d->debug;
+    if (rows == 1 && logits && logitsRows == 1 && d->useFused && d->fusedSupported)
+        return encode_fused_token(d, logits, sample);
 
     GQ8_STAGE(kStageEmbed, gq8::launch_embed(d->sequence, d->position, rows, d->embedding, s.vocab, W,
                                  s.embedding_scale, d->hidden, st));

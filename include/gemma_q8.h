@@ -203,6 +203,10 @@ int gq8_decoder_position(const gq8_decoder *decoder);
  * or nothing when logits == NULL.  Synchronous on the decoder's stream. */
 int gq8_decoder_step(gq8_decoder *decoder, const uint32_t *tokens, int n, float *logits,
                      int logits_rows);
+/* One-token steps run through the fused kernels (five launches a layer)
+ * when the shape allows; 0 selects the unfused kernels (both compute the same
+ * arithmetic).  On by default. */
+int gq8_decoder_set_fused(gq8_decoder *decoder, int enabled);
 /* Decoder::hiddenStates (Decoder.h:119-121): the last step's rows after the
  * final norm, [rows, width] fp32, copied to the host. */
 int gq8_decoder_hidden(gq8_decoder *decoder, float *host_out, int rows);

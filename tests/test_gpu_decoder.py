@@ -112,25 +112,35 @@ def test_small_model_one_token_at_a_time_and_two_blocks(torch_cuda):
     assert worst_error(last[0], ref[-1]) <= 1e-5
 
 
-def test_small_model_intermediates_bisect(torch_cuda):
-    """The Q8 bytes of each layer's product inputs equal the oracle's."""
+@pytest.mark.parametrize("fused", [True, False])
+def test_small_model_intermediates_bisect(torch_cuda, fused):
+    """The Q8 bytes of each layer's product inputs equal the oracle's, for the
+    last token of the prompt fed as a one-token step (the fused kernels, or
+    the unfused ones)."""
     torch = torch_cuda
     shape = small_shape()
     decoder, model = build_pair(shape, small_weights(shape))
+    decoder.set_fused(fused)
+    gpu_step(torch, decoder, PROMPT[:-1])
     decoder.set_debug(True)
-    gpu_step(torch, decoder, PROMPT)
-    model.step(np.array(PROMPT))
+    got = gpu_step(torch, decoder, PROMPT[-1:])
+    _, ref, _ = model.step(np.array(PROMPT))
+    assert worst_error(got[0], ref[-1]) <= 1e-5
     inner = {0: shape.width, 1: shape.query_width, 2: shape.intermediate}
     mismatched = 0
     for layer in range(shape.layers):
         for which in (0, 1, 2):
             values, q8 = decoder.debug(which, layer)
-            ref = model.debug(which, layer)
-            assert worst_error(values, ref) <= 1e-5
+            ref_values = model.debug(which, layer)
+            assert worst_error(values, ref_values) <= 1e-5, (layer, which)
             rq, rs = model.debug_q(which, layer)
             n = inner[which]
             mismatched += int(np.sum(q8[:n].view(np.int8) != rq))
             mismatched += int(np.sum(q8[n:].view(np.uint16) != rs))
+        hidden, _ = decoder.debug(3, layer)
+        assert worst_error(hidden, model.debug(3, layer)) <= 1e-5
+    final, q8 = decoder.debug(0, shape.layers)
+    assert worst_error(final, model.debug(0, shape.layers)) <= 1e-5
     print(f"Q8 activation bytes differing from the oracle: {mismatched}")
     assert mismatched == 0
 
@@ -234,6 +244,27 @@ def test_two_layer_gemma_workload(torch_cuda):
     err = worst_error(got, ref_logits[-1])
     print(f"2-layer last-row logits: worst {err:.3g}, exact {exact_fraction(got, ref_logits[-1]):.4f}")
     assert err <= LOGIT_TOLERANCE
+
+
+def test_fused_and_unfused_steps_agree(torch_cuda):
+    """The fused one-token kernels and the unfused ones compute the same
+    arithmetic: identical greedy ids and (almost always) identical logits."""
+    torch = torch_cuda
+    shape = G.DecoderShape.gemma_2b(layers=2, max_positions=64, max_step_rows=16)
+    decoder = G.Decoder(shape)
+    decoder.fill_synthetic(16)
+    prompt = O.prompt_ids(0xC0FFEE + 3, shape.vocab, 9)
+    runs = {}
+    for fused in (True, False):
+        decoder.set_fused(fused)
+        tokens, _ = decoder.generate(prompt, 12, eos=-1, use_graph=fused)
+        decoder.begin_sequence()
+        gpu_step(torch, decoder, prompt[:-1])
+        logits = gpu_step(torch, decoder, prompt[-1:])[0]
+        runs[fused] = (list(tokens), logits)
+    assert runs[True][0] == runs[False][0]
+    assert worst_error(runs[True][1], runs[False][1]) <= 1e-6
+    assert exact_fraction(runs[True][1], runs[False][1]) >= 0.999
 
 
 @pytest.mark.slow
