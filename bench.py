@@ -95,6 +95,9 @@ def main() -> int:
     ap.add_argument("--cpu-steps", type=int, default=8, help="decode steps of the CPU sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-graph", action="store_true", help="launch steps without hipGraph replay")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="first copy MIB MiB device-to-device three times (a kernel of known "
+                         "bytes to scale the FETCH_SIZE / WRITE_SIZE counters by)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -109,6 +112,14 @@ def main() -> int:
         log("no GPU visible")
         return 1
     threads = args.threads if args.threads > 0 else (os.cpu_count() or 1)
+    if args.copy_probe > 0:
+        src = torch.ones(args.copy_probe << 18, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: 3 x {args.copy_probe} MiB device-to-device")
+        del src, dst
     max_positions = 8192
     shape = G.DecoderShape.gemma_2b(layers=args.layers, max_positions=max_positions,
                                     max_step_rows=512)
@@ -139,7 +150,9 @@ def main() -> int:
     log(f"decode: {tok_s:.1f} tok/s, {seconds / args.steps * 1e3:.3f} ms/step, "
         f"{step_gbs:.0f} GB/s of {step_bytes / 1e9:.4f} GB/token; first ids {list(tokens[:6])}")
 
-    # stage timing with HIP events on the decoder's stream over the same K steps
+    # the stage breakdown: every launch group of K more steps bracketed by HIP
+    # events on the decoder's stream (the event packets add about a
+    # microsecond to each bracket)
     decoder.generate(prompt, 1, eos=-1, use_graph=False)
     decoder.set_timing(True)
     decoder.decode(args.steps, use_graph=False)
@@ -150,8 +163,11 @@ def main() -> int:
         if n:
             log(f"  {name:10s} {ms / args.steps * 1e3:8.1f} us/step  {n // args.steps:3d} launches/step"
                 f"  {100 * ms / total_ms:5.1f} %")
+    # the dominant product kernel's own duration: launched alone, back to back
+    # over every layer's weights (so from HBM, as in a step), between two HIP
+    # events on the decoder's stream
     dominant = max(("gate_up", "lm_head", "down"), key=lambda k: timing[k][0])
-    ms, launches = timing[dominant]
+    ms, launches = decoder.time_kernel(dominant, max(1, args.steps // 8))
     per_launch_s = ms / launches / 1e3
     launch_bytes = stage_bytes(shape, dominant)
     achieved = launch_bytes / per_launch_s / 1e9

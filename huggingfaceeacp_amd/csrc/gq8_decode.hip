@@ -144,52 +144,92 @@ struct RowQ8 {
 };
 
 // RMSNorm (RMSNorm.h:44-56) of one row and its Int8Blocks quantization into
-// LDS.  Thread t owns elements [8t, 8t + 8), so four consecutive lanes hold
-// one 32-element block.  The row is either x or, with `table`, the embedding
-// row of `*token` (Embed.h:45-82), which workgroup 0 also stores to
-// hidden_out for the residual stream.  Workgroup 0 optionally writes the
-// normalised row (fp32) and its Q8 bytes for the debug view.
-__device__ void norm_q8_prologue(const float *x, const uint32_t *token, const uint8_t *table,
-                                 int64_t vocab, float embed_scale, float *hidden_out,
-                                 const float *weight, int width, float epsilon, RowQ8 &row,
-                                 double *sPartial, float *normalised_out, uint8_t *q8_out)
+// LDS, in two parts so that a kernel can issue the row's loads before its
+// weight loads (the loads of one wave complete in order, so the norm then
+// runs while the weights stream in).  Thread t owns elements [E t, E t + E)
+// (E = 8 for 256-thread workgroups, 4 for 512), so 32 / E consecutive lanes
+// hold one 32-element block.  The row is either x or, with `table`, the
+// embedding row of `*token` (Embed.h:45-82), which workgroup 0 also stores to
+// hidden_out for the residual stream.
+template <int E>
+struct RowSlice {
+    float v[E];
+    float w[E];
+    bool active;
+};
+
+template <int E>
+__device__ inline void load4(const float *p, float *out)
 {
-    // only the first 256 threads of a larger workgroup hold elements
+#pragma unroll
+    for (int k = 0; k < E; k += 4) {
+        const float4 f = reinterpret_cast<const float4 *>(p)[k / 4];
+        out[k] = f.x;
+        out[k + 1] = f.y;
+        out[k + 2] = f.z;
+        out[k + 3] = f.w;
+    }
+}
+
+template <int E>
+__device__ inline RowSlice<E> load_row_slice(const float *x, const uint32_t *token,
+                                             const uint8_t *table, int64_t vocab,
+                                             float embed_scale, float *hidden_out,
+                                             const float *weight, int width)
+{
+    static_assert(E == 4 || E == 8, "four or eight elements a thread");
+    // branch-free: an inactive thread reads elements [0, E) and is zeroed at use
+    RowSlice<E> r;
+    const int t = threadIdx.x;
+    r.active = t * E < width;
+    const int i0 = r.active ? t * E : 0;
+    load4<E>(weight + i0, r.w);
+    if (table) {
+        uint32_t id = *token; // the sequence slot at the position
+        if (id >= (uint32_t) vocab) // ids are validated on the host; a guard, not a rule
+            id = 0;
+        const int64_t e0 = (int64_t) id * width + i0;
+        const uint16_t bits = reinterpret_cast<const uint16_t *>(table + vocab * width)[e0 / kBlock];
+        const float s = half_value(bits);
+        int8_t b[E];
+        if (E == 8) {
+            const int2 packed = *reinterpret_cast<const int2 *>(table + e0);
+            __builtin_memcpy(b, &packed, E);
+        } else {
+            const int packed = *reinterpret_cast<const int *>(table + e0);
+            __builtin_memcpy(b, &packed, E);
+        }
+#pragma unroll
+        for (int k = 0; k < E; ++k)
+            r.v[k] = (float) ((double) embed_scale * (double) (s * (float) b[k]));
+        if (hidden_out && blockIdx.x == 0 && r.active)
+#pragma unroll
+            for (int k = 0; k < E; k += 4)
+                reinterpret_cast<float4 *>(hidden_out + i0)[k / 4] =
+                    make_float4(r.v[k], r.v[k + 1], r.v[k + 2], r.v[k + 3]);
+    } else {
+        load4<E>(x + i0, r.v);
+    }
+    return r;
+}
+
+// The norm of the loaded slices and the Q8 row in LDS.  Workgroup 0
+// optionally writes the normalised row (fp32) and its Q8 bytes (the debug
+// view and the final-norm outputs).
+template <int E>
+__device__ void norm_q8_finish(const RowSlice<E> &r, int width, float epsilon, RowQ8 &row,
+                               double *sPartial, float *normalised_out, uint8_t *q8_out)
+{
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int waves = blockDim.x / 64;
-    const int i0 = t * 8;
-    const bool active = t < kThreads && i0 < width;
-    float v[8];
+    const int i0 = t * E;
+    float v[E];
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
-        v[k] = 0.f;
-    if (active) {
-        if (table) {
-            uint32_t id = *token; // the sequence slot at the position
-            if (id >= (uint32_t) vocab) // ids are validated on the host; a guard, not a rule
-                id = 0;
-            const int64_t e0 = (int64_t) id * width + i0;
-            const uint16_t bits = reinterpret_cast<const uint16_t *>(table + vocab * width)[e0 / kBlock];
-            const float s = half_value(bits);
-            const int2 packed = *reinterpret_cast<const int2 *>(table + e0);
-            const int8_t *b = reinterpret_cast<const int8_t *>(&packed);
-#pragma unroll
-            for (int k = 0; k < 8; ++k)
-                v[k] = (float) ((double) embed_scale * (double) (s * (float) b[k]));
-            if (hidden_out && blockIdx.x == 0) {
-                reinterpret_cast<float4 *>(hidden_out + i0)[0] = make_float4(v[0], v[1], v[2], v[3]);
-                reinterpret_cast<float4 *>(hidden_out + i0)[1] = make_float4(v[4], v[5], v[6], v[7]);
-            }
-        } else {
-            const float4 p = reinterpret_cast<const float4 *>(x + i0)[0];
-            const float4 r = reinterpret_cast<const float4 *>(x + i0)[1];
-            v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w;
-            v[4] = r.x; v[5] = r.y; v[6] = r.z; v[7] = r.w;
-        }
-    }
+    for (int k = 0; k < E; ++k)
+        v[k] = r.active ? r.v[k] : 0.f;
     double squares = 0.0;
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
+    for (int k = 0; k < E; ++k)
         squares += (double) v[k] * (double) v[k];
     squares = wave_sum_d(squares);
     if (lane == 0)
@@ -200,36 +240,37 @@ __device__ void norm_q8_prologue(const float *x, const uint32_t *token, const ui
         total += sPartial[w];
     const double scale = norm_scale(total, width, epsilon);
 
-    float n[8];
+    float n[E];
     float amax = 0.f;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        n[k] = active ? norm_value(v[k], scale, weight[i0 + k]) : 0.f;
+    for (int k = 0; k < E; ++k) {
+        n[k] = r.active ? norm_value(v[k], scale, r.w[k]) : 0.f;
         amax = fmaxf(amax, fabsf(n[k]));
     }
-    amax = fmaxf(amax, __shfl_xor(amax, 1));
-    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    for (int mask = 1; mask < kBlock / E; mask <<= 1)
+        amax = fmaxf(amax, __shfl_xor(amax, mask));
     const uint16_t bits = scale_bits_from_amax(amax);
     const float s = half_value(bits);
     const float inverse = bits ? 1.0f / s : 0.f;
-    int packed[2] = {0, 0};
+    int packed[E / 4] = {};
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < E; ++k) {
         const int q = bits ? quantize_value(n[k], s, inverse) : 0;
         packed[k / 4] |= (q & 0xFF) << (8 * (k % 4));
     }
-    if (active) {
-        *reinterpret_cast<int2 *>(row.q + i0) = make_int2(packed[0], packed[1]);
-        if ((t & 3) == 0)
+    const bool first = (t % (kBlock / E)) == 0; // the block's first thread
+    if (r.active) {
+        __builtin_memcpy(row.q + i0, packed, E);
+        if (first)
             row.scale[i0 / kBlock] = (double) s;
         if (blockIdx.x == 0) {
             if (normalised_out)
 #pragma unroll
-                for (int k = 0; k < 8; ++k)
+                for (int k = 0; k < E; ++k)
                     normalised_out[i0 + k] = n[k];
             if (q8_out) {
-                *reinterpret_cast<int2 *>(q8_out + i0) = make_int2(packed[0], packed[1]);
-                if ((t & 3) == 0)
+                __builtin_memcpy(q8_out + i0, packed, E);
+                if (first)
                     reinterpret_cast<uint16_t *>(q8_out + width)[i0 / kBlock] = bits;
             }
         }
@@ -238,32 +279,39 @@ __device__ void norm_q8_prologue(const float *x, const uint32_t *token, const ui
 }
 
 // The 32-byte weight block and fp16 scale of (row, block) in an Int8Blocks
-// tensor of `rows` x `inner`.
+// tensor of `rows` x `inner`.  The loads are unconditional (an invalid pair
+// reads block 0 of row 0 with its scale masked to zero) and the scale comes in the
+// aligned 32-bit word holding it, so the compiler neither branches around the
+// loads nor packs 16-bit results: every load of a wave is in flight before
+// the first wait.
 struct WeightBlock {
     int4 w0, w1;
-    uint16_t scale;
+    uint32_t scalePair; // the fp16 scale is the high half when `high`
+    bool high;
 };
 
 __device__ inline WeightBlock load_block(const uint8_t *w8, int64_t rows, int inner, int64_t row,
                                          int block, bool valid)
 {
     WeightBlock b;
-    if (valid) {
-        const int4 *p = reinterpret_cast<const int4 *>(w8 + row * inner + (int64_t) block * kBlock);
-        b.w0 = p[0];
-        b.w1 = p[1];
-        b.scale = reinterpret_cast<const uint16_t *>(w8 + rows * inner)[row * (inner / kBlock) + block];
-    } else {
-        b.w0 = make_int4(0, 0, 0, 0);
-        b.w1 = make_int4(0, 0, 0, 0);
-        b.scale = 0;
-    }
+    const int64_t r = valid ? row : 0;
+    const int c = valid ? block : 0;
+    const int4 *p = reinterpret_cast<const int4 *>(w8 + r * inner + (int64_t) c * kBlock);
+    b.w0 = p[0];
+    b.w1 = p[1];
+    const int64_t index = r * (inner / kBlock) + c;
+    // masking (not selecting) the word keeps the load unconditional; a zero
+    // scale zeroes the term
+    b.scalePair = reinterpret_cast<const uint32_t *>(w8 + rows * inner)[index >> 1]
+                  & (valid ? 0xFFFFFFFFu : 0u);
+    b.high = (index & 1) != 0;
     return b;
 }
 
 __device__ inline double block_term(const WeightBlock &b, const int4 &a0, const int4 &a1, double sa)
 {
-    return (double) dot32(b.w0, b.w1, a0, a1) * ((double) half_value(b.scale) * sa);
+    const uint16_t bits = (uint16_t) (b.high ? b.scalePair >> 16 : b.scalePair & 0xFFFFu);
+    return (double) dot32(b.w0, b.w1, a0, a1) * ((double) half_value(bits) * sa);
 }
 
 // ---- q|k|v + RoPE + fp16 KV ---------------------------------------------------
@@ -283,6 +331,10 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a)
     const int nb = a.width / kBlock;
     const int firstPair = (blockIdx.x * kWaves + wave) * kPairsPerWave;
 
+    const uint32_t *token = a.embedding ? a.sequence + *a.position : nullptr;
+    const RowSlice<8> slice = load_row_slice<8>(a.hidden, token, a.embedding, a.vocab,
+                                                a.embed_scale, a.hidden_out, a.norm_weight,
+                                                a.width);
     WeightBlock lo[kPairsPerWave], hi[kPairsPerWave];
     int rowLo[kPairsPerWave];
 #pragma unroll
@@ -294,11 +346,9 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a)
         lo[p] = load_block(a.weights, outputs, a.width, rowLo[p], lane, valid);
         hi[p] = load_block(a.weights, outputs, a.width, rowLo[p] + half, lane, valid);
     }
+    __builtin_amdgcn_sched_barrier(0); // every load issued before the norm's first wait
 
-    const uint32_t *token = a.embedding ? a.sequence + *a.position : nullptr;
-    norm_q8_prologue(a.hidden, token, a.embedding, a.vocab, a.embed_scale, a.hidden_out,
-                     a.norm_weight, a.width, a.epsilon, row, sPartial, a.debug_normalised,
-                     a.debug_q8);
+    norm_q8_finish(slice, a.width, a.epsilon, row, sPartial, a.debug_normalised, a.debug_q8);
 
     int4 a0 = make_int4(0, 0, 0, 0), a1 = a0;
     double sa = 0.0;
@@ -658,6 +708,8 @@ void gateup_geglu_kernel(GateUpArgs a)
     const int o0 = blockIdx.x * kBlock + wave * kGluPerWave;
     const bool valid = lane < nb;
 
+    const RowSlice<4> slice = load_row_slice<4>(a.hidden, nullptr, nullptr, 0, 0.f, nullptr,
+                                                a.norm_weight, a.width);
     // rows 0..3 gate, 4..7 up
     WeightBlock w[2 * kGluPerWave];
 #pragma unroll
@@ -666,8 +718,8 @@ void gateup_geglu_kernel(GateUpArgs a)
         w[kGluPerWave + k] =
             load_block(a.weights, 2 * (int64_t) F, a.width, (int64_t) F + o0 + k, lane, valid);
     }
-    norm_q8_prologue(a.hidden, nullptr, nullptr, 0, 0.f, nullptr, a.norm_weight, a.width,
-                     a.epsilon, row, sPartial, nullptr, nullptr);
+    __builtin_amdgcn_sched_barrier(0); // every load issued before the norm's first wait
+    norm_q8_finish(slice, a.width, a.epsilon, row, sPartial, nullptr, nullptr);
     int4 a0 = make_int4(0, 0, 0, 0), a1 = a0;
     double sa = 0.0;
     if (valid) {
@@ -711,11 +763,12 @@ void gateup_geglu_kernel(GateUpArgs a)
 // the activation block of its lane straight from the Q8 row) whose rows are
 // reduced together.  Each workgroup folds its rows into one 64-bit candidate
 // (an order-preserving key of the logit above the complemented row index) and
-// merges it into a single device word with one atomicMax, so the largest logit
-// wins and, among equal logits, the lowest index -- the first maximum.  No
-// workgroup waits for another; a one-thread kernel then turns the word into
-// the token id, stores it in the sequence slot after the position, advances
-// the position and clears the word.
+// merges it into one of kHeadSlots device words (spread over cache lines, so
+// that the atomics do not queue on one address) with one atomicMax, so the
+// largest logit wins and, among equal logits, the lowest index -- the first
+// maximum.  No workgroup waits for another; a one-wave kernel then folds the
+// slots, turns the winner into the token id, stores it in the sequence slot
+// after the position, advances the position and clears the slots.
 constexpr int kHeadRows = 8;
 
 // Larger floats give larger keys; NaN gives 0, below every ordered value, so
@@ -742,8 +795,9 @@ __global__ __launch_bounds__(kThreads) void final_norm_kernel(HeadArgs a)
 {
     __shared__ RowQ8 row;
     __shared__ double sPartial[kWaves];
-    norm_q8_prologue(a.hidden, nullptr, nullptr, 0, 0.f, nullptr, a.norm_weight, a.width,
-                     a.epsilon, row, sPartial, a.normalised_out, a.q8);
+    const RowSlice<8> slice = load_row_slice<8>(a.hidden, nullptr, nullptr, 0, 0.f, nullptr,
+                                                a.norm_weight, a.width);
+    norm_q8_finish(slice, a.width, a.epsilon, row, sPartial, a.normalised_out, a.q8);
 }
 
 __global__ __launch_bounds__(kThreads) void lmhead_argmax_kernel(HeadArgs a)
@@ -759,13 +813,11 @@ __global__ __launch_bounds__(kThreads) void lmhead_argmax_kernel(HeadArgs a)
 #pragma unroll
     for (int k = 0; k < kHeadRows; ++k)
         w[k] = load_block(a.weights, V, a.width, r0 + k, lane, valid && r0 + k < V);
-    int4 a0 = make_int4(0, 0, 0, 0), a1 = a0;
-    double sa = 0.0;
-    if (valid) {
-        a0 = reinterpret_cast<const int4 *>(a.q8 + lane * kBlock)[0];
-        a1 = reinterpret_cast<const int4 *>(a.q8 + lane * kBlock)[1];
-        sa = (double) half_value(reinterpret_cast<const uint16_t *>(a.q8 + a.width)[lane]);
-    }
+    const int ab = valid ? lane : 0; // an invalid lane's terms are zeroed by block_term
+    const int4 a0 = reinterpret_cast<const int4 *>(a.q8 + ab * kBlock)[0];
+    const int4 a1 = reinterpret_cast<const int4 *>(a.q8 + ab * kBlock)[1];
+    const double sa = (double) half_value(reinterpret_cast<const uint16_t *>(a.q8 + a.width)[ab]);
+    __builtin_amdgcn_sched_barrier(0); // every load issued before the first wait
     double y[kHeadRows];
 #pragma unroll
     for (int k = 0; k < kHeadRows; ++k)
@@ -787,20 +839,26 @@ __global__ __launch_bounds__(kThreads) void lmhead_argmax_kernel(HeadArgs a)
         for (int k = 1; k < kWaves; ++k)
             c = sBest[k] > c ? sBest[k] : c;
         if (c != 0)
-            atomicMax(a.best, c);
+            atomicMax(a.best + (blockIdx.x % kHeadSlots) * kHeadSlotStride, c);
     }
 }
 
-__global__ void head_finalize_kernel(HeadArgs a)
+// One wave folds the slots, stores the id and clears the slots.
+__global__ __launch_bounds__(64) void head_finalize_kernel(HeadArgs a)
 {
-    const unsigned long long c = *a.best;
-    const uint32_t token = c == 0 ? 0u : 0xFFFFFFFFu - (uint32_t) (c & 0xFFFFFFFFull);
-    const int position = *a.position;
-    if (a.sequence)
-        a.sequence[position + 1] = token;
-    if (a.advance)
-        *a.position = position + 1;
-    *a.best = 0;
+    const int lane = threadIdx.x;
+    unsigned long long *slot = a.best + lane * kHeadSlotStride;
+    const unsigned long long c = fold_wave_max(lane < kHeadSlots ? *slot : 0ull);
+    if (lane < kHeadSlots)
+        *slot = 0;
+    if (lane == 0) {
+        const uint32_t token = c == 0 ? 0u : 0xFFFFFFFFu - (uint32_t) (c & 0xFFFFFFFFull);
+        const int position = *a.position;
+        if (a.sequence)
+            a.sequence[position + 1] = token;
+        if (a.advance)
+            *a.position = position + 1;
+    }
 }
 
 } // namespace
@@ -865,7 +923,7 @@ hipError_t launch_lmhead_argmax(const HeadArgs &a, hipStream_t stream)
 
 hipError_t launch_head_finalize(const HeadArgs &a, hipStream_t stream)
 {
-    hipLaunchKernelGGL(head_finalize_kernel, dim3(1), dim3(1), 0, stream, a);
+    hipLaunchKernelGGL(head_finalize_kernel, dim3(1), dim3(64), 0, stream, a);
     return hipGetLastError();
 }
 

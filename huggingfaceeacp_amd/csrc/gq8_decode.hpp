@@ -12,6 +12,8 @@ namespace gq8 {
 
 constexpr int kFusedMaxWidth = 2048; // a normalised row held in LDS as Q8
 constexpr int kDecodeSplits = 64;    // attention workgroups over one row's keys
+constexpr int kHeadSlots = 64;       // lm_head argmax words (one wave folds them)
+constexpr int kHeadSlotStride = 16;  // 128 bytes between words
 
 struct QkvArgs {
     const float *hidden;      // the residual stream row (unused when embedding)
@@ -66,7 +68,8 @@ struct HeadArgs {
     uint8_t *q8;              // the final-norm row's Q8 (written, then read by the lm_head)
     float *logits;            // fp32 [vocab]
     float *normalised_out;    // the final-norm row (hiddenStates)
-    unsigned long long *best; // packed (logit key, complemented row) maximum, zero between launches
+    unsigned long long *best; // kHeadSlots packed (logit key, complemented row) maxima,
+                              // kHeadSlotStride apart, zero between launches
     uint32_t *sequence;       // the argmax goes to sequence[*position + 1] (optional)
     int *position;
     int advance;              // nonzero: *position += 1 after the argmax

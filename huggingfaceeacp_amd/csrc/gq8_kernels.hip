@@ -329,43 +329,55 @@ __global__ __launch_bounds__(kThreads) void q8_matvec_kernel(
     const int64_t wElements = (int64_t) outputs * inner;
     const uint16_t *wScales = reinterpret_cast<const uint16_t *>(w8 + wElements);
 
+    // Branch-free loads: an invalid (row, block) reads block 0 of row 0 and
+    // its scale is zeroed at use; the scales come in their aligned 32-bit
+    // words.  Every load of the wave is then in flight before the first wait.
     int4 wa[U][S], wb[U][S];
-    uint16_t wsBits[U][S];
+    uint32_t wsPair[U][S];
+    bool wsHigh[U][S];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int o = row0 + u;
 #pragma unroll
         for (int j = 0; j < S; ++j) {
             const int b = lane + 64 * (part + WPR * j);
-            if (o < outputs && b < nb) {
-                const int4 *p = reinterpret_cast<const int4 *>(w8 + (int64_t) o * inner + (int64_t) b * kBlock);
-                wa[u][j] = p[0];
-                wb[u][j] = p[1];
-                wsBits[u][j] = wScales[(int64_t) o * nb + b];
-            } else {
-                wa[u][j] = make_int4(0, 0, 0, 0);
-                wb[u][j] = make_int4(0, 0, 0, 0);
-                wsBits[u][j] = 0;
-            }
+            const bool valid = o < outputs && b < nb;
+            const int64_t r = valid ? o : 0;
+            const int c = valid ? b : 0;
+            const int4 *p = reinterpret_cast<const int4 *>(w8 + r * inner + (int64_t) c * kBlock);
+            wa[u][j] = p[0];
+            wb[u][j] = p[1];
+            const int64_t index = r * nb + c;
+            // masking (not selecting) the word keeps the load unconditional
+            wsPair[u][j] = reinterpret_cast<const uint32_t *>(wScales)[index >> 1]
+                           & (valid ? 0xFFFFFFFFu : 0u);
+            wsHigh[u][j] = (index & 1) != 0;
         }
     }
     int4 a0[S], a1[S];
-    double sa[S];
+    uint16_t saBits[S];
     const uint16_t *xScales = reinterpret_cast<const uint16_t *>(x8 + x_elements);
 #pragma unroll
     for (int j = 0; j < S; ++j) {
         const int b = lane + 64 * (part + WPR * j);
-        if (b < nb) {
-            const int4 *p = reinterpret_cast<const int4 *>(x8 + (int64_t) x_row * inner + (int64_t) b * kBlock);
-            a0[j] = p[0];
-            a1[j] = p[1];
-            sa[j] = (double) half_value(xScales[(int64_t) x_row * nb + b]);
-        } else {
-            a0[j] = make_int4(0, 0, 0, 0);
-            a1[j] = make_int4(0, 0, 0, 0);
-            sa[j] = 0.0;
-        }
+        const bool valid = b < nb;
+        const int c = valid ? b : 0;
+        const int4 *p = reinterpret_cast<const int4 *>(x8 + (int64_t) x_row * inner + (int64_t) c * kBlock);
+        a0[j] = p[0];
+        a1[j] = p[1];
+        saBits[j] = xScales[(int64_t) x_row * nb + c] & (valid ? 0xFFFFu : 0u);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    double sa[S];
+#pragma unroll
+    for (int j = 0; j < S; ++j)
+        sa[j] = (double) half_value(saBits[j]);
+    uint16_t wsBits[U][S];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int j = 0; j < S; ++j)
+            wsBits[u][j] = (uint16_t) (wsHigh[u][j] ? wsPair[u][j] >> 16 : wsPair[u][j] & 0xFFFFu);
 
     double acc[U];
 #pragma unroll

@@ -422,12 +422,13 @@ struct gq8_decoder {
     bool useFused = true;
     bool fusedSupported = false;
     double *decodeO = nullptr, *decodeMl = nullptr;
-    int *counters = nullptr; // [0] attention; [2..3] the lm_head's packed 64-bit maximum
+    int *counters = nullptr; // [0] attention
+    unsigned long long *headBest = nullptr; // the lm_head argmax slots
 
     hipGraphExec_t graph = nullptr;
     bool capturing = false;
 
-    bool timing = false;
+    unsigned timing = 0; // bit s: bracket stage s with events
     struct Mark {
         int stage;
         hipEvent_t start, stop;
@@ -685,6 +686,7 @@ extern "C" int gq8_decoder_create(const gq8_shape *shape, gq8_decoder **out)
         GQ8_ALLOC(d->decodeO, wsBytes);
         d->decodeMl = d->decodeO + (size_t) gq8::kDecodeSplits * s.heads * s.head_dim;
         GQ8_ALLOC(d->counters, 4 * sizeof(int));
+        GQ8_ALLOC(d->headBest, gq8::kHeadSlots * gq8::kHeadSlotStride * sizeof(unsigned long long));
     }
 #undef GQ8_ALLOC
     if (hipHostMalloc((void **) &d->pinnedToken, sizeof(uint32_t) * 4) != hipSuccess)
@@ -692,6 +694,8 @@ extern "C" int gq8_decoder_create(const gq8_shape *shape, gq8_decoder **out)
     if (hipMemset(d->sequence, 0, ((size_t) s.max_positions + 1) * sizeof(uint32_t)) != hipSuccess
         || hipMemset(d->position, 0, sizeof(int)) != hipSuccess
         || hipMemset(d->counters, 0, 4 * sizeof(int)) != hipSuccess
+        || hipMemset(d->headBest, 0, gq8::kHeadSlots * gq8::kHeadSlotStride * sizeof(unsigned long long))
+               != hipSuccess
         || hipMemset(d->keyCache, 0, cacheElements * sizeof(uint16_t)) != hipSuccess
         || hipMemset(d->valueCache, 0, cacheElements * sizeof(uint16_t)) != hipSuccess
         || hipDeviceSynchronize() != hipSuccess)
@@ -981,7 +985,7 @@ struct StageTimer {
     hipEvent_t start = nullptr;
     StageTimer(gq8_decoder *decoder, int s) : d(decoder), stage(s)
     {
-        if (d->timing && !d->capturing) {
+        if (s >= 0 && s < GQ8_STAGE_COUNT && ((d->timing >> s) & 1u) && !d->capturing) {
             start = take_event(d);
             if (start)
                 (void) hipEventRecord(start, d->stream);
@@ -1100,7 +1104,7 @@ int encode_fused_token(gq8_decoder *d, float *logits, bool sample)
     h.logits = logits;
     h.normalised_out = d->normalisedRows;
     h.q8 = d->x8;
-    h.best = reinterpret_cast<unsigned long long *>(d->counters + 2);
+    h.best = d->headBest;
     h.sequence = sample ? d->sequence : nullptr;
     h.position = d->position;
     h.advance = 1;
@@ -1466,11 +1470,85 @@ extern "C" int gq8_decoder_tokens(gq8_decoder *d, int first, int count, int32_t 
     return GQ8_OK;
 }
 
-extern "C" int gq8_decoder_set_timing(gq8_decoder *d, int enabled)
+extern "C" int gq8_decoder_set_timing(gq8_decoder *d, int stage_mask)
 {
     if (!d)
         return fail(GQ8_ERR_ARGUMENT, "null decoder");
-    d->timing = enabled != 0;
+    d->timing = (unsigned) stage_mask & ((1u << GQ8_STAGE_COUNT) - 1u);
+    return GQ8_OK;
+}
+
+// Times one fused one-token kernel alone: `repeats` rounds over every layer's
+// weights (gate|up, down) or of the lm_head, back to back on the decoder's
+// stream between two HIP events.  The layers' weights rotate as in a step,
+// so the kernel streams them from HBM as it does there.  Only scratch is
+// written (the Q8 row, a scratch residual row, the logits row); the lm_head
+// rounds are followed, outside the events, by a finalize that clears the
+// argmax slots without touching the sequence or the position.
+extern "C" int gq8_decoder_time_kernel(gq8_decoder *d, int stage, int repeats, double *milliseconds,
+                                       int *launches)
+{
+    if (!d || !milliseconds || !launches || repeats <= 0)
+        return fail(GQ8_ERR_ARGUMENT, "decoder_time_kernel: bad arguments");
+    if (!d->fusedSupported)
+        return fail(GQ8_ERR_SHAPE, "decoder_time_kernel: the shape has no fused kernels");
+    if (stage != kStageGateUp && stage != kStageDown && stage != kStageLogits)
+        return fail(GQ8_ERR_ARGUMENT, "decoder_time_kernel: stage must be gate|up, down or lm_head");
+    const gq8_shape &s = d->shape;
+    const int W = s.width, F = s.intermediate;
+    hipStream_t st = d->stream;
+    hipEvent_t start = take_event(d), stop = take_event(d);
+    if (!start || !stop)
+        return fail(GQ8_ERR_DEVICE, "decoder_time_kernel: no events");
+    gq8::HeadArgs h{};
+    h.hidden = d->hidden;
+    h.norm_weight = d->finalNorm;
+    h.width = W;
+    h.epsilon = s.rms_epsilon;
+    h.weights = d->embedding;
+    h.vocab = s.vocab;
+    h.logits = d->logits;
+    h.normalised_out = nullptr;
+    h.q8 = d->x8;
+    h.best = d->headBest;
+    h.sequence = nullptr;
+    h.position = d->position;
+    h.advance = 0;
+    int count = 0;
+    GQ8_HIP(hipEventRecord(start, st));
+    for (int r = 0; r < repeats; ++r) {
+        if (stage == kStageLogits) {
+            GQ8_LAUNCH(gq8::launch_lmhead_argmax(h, st));
+            ++count;
+            continue;
+        }
+        for (int l = 0; l < s.layers; ++l, ++count) {
+            if (stage == kStageGateUp) {
+                gq8::GateUpArgs g{};
+                g.hidden = d->hidden;
+                g.norm_weight = d->postNorm[l];
+                g.width = W;
+                g.epsilon = s.rms_epsilon;
+                g.weights = d->gateUp[l];
+                g.intermediate = F;
+                g.q8 = d->x8;
+                GQ8_LAUNCH(gq8::launch_gateup_geglu(g, st));
+            } else {
+                GQ8_LAUNCH(gq8::launch_q8_product(d->x8, 1, 0, 1, d->down[l], F, W,
+                                                  d->normalisedRows, W, 1, st));
+            }
+        }
+    }
+    GQ8_HIP(hipEventRecord(stop, st));
+    if (stage == kStageLogits)
+        GQ8_LAUNCH(gq8::launch_head_finalize(h, st));
+    GQ8_HIP(hipStreamSynchronize(st));
+    float ms = 0.f;
+    GQ8_HIP(hipEventElapsedTime(&ms, start, stop));
+    d->spareEvents.push_back(start);
+    d->spareEvents.push_back(stop);
+    *milliseconds = ms;
+    *launches = count;
     return GQ8_OK;
 }
 

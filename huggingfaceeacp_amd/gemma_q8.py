@@ -120,6 +120,7 @@ def library() -> ctypes.CDLL:
         "gq8_decoder_tokens": (i32, [P, i32, i32, P]),
         "gq8_decoder_set_timing": (i32, [P, i32]),
         "gq8_decoder_timing": (i32, [P, P, P]),
+        "gq8_decoder_time_kernel": (i32, [P, i32, i32, ctypes.POINTER(f64), ctypes.POINTER(i32)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -380,8 +381,23 @@ class Decoder:
         check(library().gq8_decoder_tokens(self.handle, first, count, _host(out)))
         return out
 
-    def set_timing(self, enabled: bool) -> None:
-        check(library().gq8_decoder_set_timing(self.handle, int(enabled)))
+    def set_timing(self, enabled, stages=None) -> None:
+        """Bracket the launches of `stages` (names from STAGES; default all)
+        with HIP events while enabled."""
+        mask = 0
+        if enabled:
+            for name in (STAGES if stages is None else stages):
+                mask |= 1 << STAGES.index(name)
+        check(library().gq8_decoder_set_timing(self.handle, mask))
+
+    def time_kernel(self, stage: str, repeats: int):
+        """(milliseconds, launches) of one fused kernel ("gate_up", "down" or
+        "lm_head") launched alone over every layer's weights, `repeats` rounds."""
+        ms = ctypes.c_double(0.0)
+        launches = ctypes.c_int(0)
+        check(library().gq8_decoder_time_kernel(self.handle, STAGES.index(stage), int(repeats),
+                                                ctypes.byref(ms), ctypes.byref(launches)))
+        return ms.value, launches.value
 
     def timing(self) -> dict:
         """{stage: (total milliseconds, launches)} since the last call."""

@@ -246,15 +246,25 @@ int gq8_generate(gq8_decoder *decoder, const int32_t *prompt, int prompt_length,
 int gq8_decoder_decode(gq8_decoder *decoder, int steps, int use_graph);
 int gq8_decoder_tokens(gq8_decoder *decoder, int first, int count, int32_t *host_out);
 
-/* Stage timing: while enabled, every launch group of a step recorded outside
- * a graph is bracketed by HIP events on the decoder's stream.  Stages: 0 embed,
- * 1 norm, 2 qkv product, 3 rope+kv, 4 attention, 5 o product, 6 gate|up
- * product, 7 geglu, 8 down product, 9 lm_head product, 10 argmax.
+/* Stage timing: every launch of a stage whose bit is set in stage_mask (0
+ * turns timing off) that a step records outside a graph is bracketed by HIP
+ * events on the decoder's stream.  Stages: 0 embed, 1 norm, 2 qkv product,
+ * 3 rope+kv, 4 attention, 5 o product, 6 gate|up product, 7 geglu, 8 down
+ * product, 9 lm_head product, 10 argmax.  Bracketing only the stages of
+ * interest keeps the other launches free of event packets.
  * gq8_decoder_timing fills per-stage totals (milliseconds) and launch counts
- * since the last reset, and resets. */
+ * since the last reset, and resets.  No reference counterpart: measurement. */
 enum { GQ8_STAGE_COUNT = 11 };
-int gq8_decoder_set_timing(gq8_decoder *decoder, int enabled);
+int gq8_decoder_set_timing(gq8_decoder *decoder, int stage_mask);
 int gq8_decoder_timing(gq8_decoder *decoder, double *milliseconds, int *launches);
+/* Times one fused one-token kernel alone (stage 6 gate|up, 8 down or 9
+ * lm_head): `repeats` rounds over every layer's weights (the lm_head: one
+ * launch a round) back to back between two HIP events on the decoder's
+ * stream; fills the milliseconds and the launch count.  Writes scratch only
+ * (the sequence, the position and the KV cache are untouched).  No reference
+ * counterpart: measurement. */
+int gq8_decoder_time_kernel(gq8_decoder *decoder, int stage, int repeats, double *milliseconds,
+                            int *launches);
 
 #ifdef __cplusplus
 }
