@@ -398,294 +398,287 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a)
     }
 }
 
-// ---- split-key attention with the merge in the last workgroup -------------------
-// A workgroup of 1024 threads owns a contiguous key range (whole 32-key
-// tiles, at most kDecodeSplits ranges) and every head.  Each tile's keys and
-// values are fetched with all of the tile's loads in flight at once, scored
-// in double by four threads a (head, key) pair, folded into a running (max,
-// sum, value sums) per head.  The last workgroup to finish merges the ranges,
-// with each batch of partial loads issued before any is used.
-constexpr int kAttnThreads = 1024;
+// ---- split-key attention, merged per head group by its last workgroup ---------
+// The grid is (key split, head group).  A workgroup of eight waves owns the
+// keys [k0, k0 + n) of one split and the G heads of one group (G = 1 when a
+// head is at least a 32-element block wide, else the heads of one block).
+// Lane l owns channels [C l, C l + C) of a head, so the query lives in
+// registers and no LDS staging is needed.  Keys go in rounds of 64, wave w
+// taking keys w, w + 8, ..., w + 56 of a round:
+//   scores   the round's keys and values are loaded at once; the eight keys'
+//            per-lane partial dots (C channels, every head of the group) are
+//            summed across the wave together (reduce_rows);
+//   softmax  wave g takes head g: the split's maximum, exp(s - max) and sum;
+//   values   the same keys (the first round's values still in registers);
+//            the eight waves' sums are added in LDS, in wave order.
+// The split's partial (double) is stored with agent-scope stores, which are
+// coherent across the chip's L2s, and the workgroup waits for them to
+// complete before taking its group's ticket; the last workgroup of a group
+// reads the partials with agent-scope loads.  No L2 write-back fence is
+// needed, which with hundreds of workgroups would cost more than the work.
+// The last workgroup merges the splits (MultiQueryAttention.h:43-49: every
+// split rescaled to the row maximum, the sums divided by the total), rounds
+// to fp32 and quantizes the group's 32-element blocks.  Scores, weights and
+// sums are double throughout.
+constexpr int kAttnThreads = 512;
 constexpr int kAttnWaves = kAttnThreads / 64;
-constexpr int kKeyTile = 32;
-constexpr int kMaxQueryWidth = 2048;
-constexpr int kMaxKvWidth = 256;
-constexpr int kOutPerThread = kMaxQueryWidth / kAttnThreads;          // 2: heads h and h + 4
-constexpr int kTileBytes = kKeyTile * kMaxKvWidth * 2;                // 16 KiB
-constexpr int kTileVectors = kTileBytes / 16 / kAttnThreads;          // 1
-constexpr int kMergeBatch = 16;
+constexpr int kScoreBatch = 8;                          // keys a wave takes a round
+constexpr int kRoundKeys = kAttnWaves * kScoreBatch;    // 64
+constexpr int kMaxSplitKeys = 256;                      // so the window is at most 16384
+constexpr int kMaxGroupWidth = 256;                     // G * head_dim
+constexpr int kMergeBatch = 32;
 
-__device__ inline int split_keys(int keyCount)
-{
-    const int tiles = (keyCount + kKeyTile - 1) / kKeyTile;
-    return ((tiles + kDecodeSplits - 1) / kDecodeSplits) * kKeyTile;
-}
-
-struct TileLoads {
-    int4 k[kTileVectors], v[kTileVectors];
+struct SplitPlan {
+    int splits, perSplit;
 };
 
-__device__ inline void load_tile(TileLoads &t, const uint16_t *keys, const uint16_t *values,
-                                 int first, int count, int kvWidth)
+// Whole rounds a split, as few as kDecodeSplits splits allow.
+__device__ inline SplitPlan plan_splits(int keyCount)
 {
-    const int vectors = count * kvWidth / 8; // 8 halves a vector
-    const int4 *k = reinterpret_cast<const int4 *>(keys + (int64_t) first * kvWidth);
-    const int4 *v = reinterpret_cast<const int4 *>(values + (int64_t) first * kvWidth);
-#pragma unroll
-    for (int i = 0; i < kTileVectors; ++i) {
-        const int at = threadIdx.x + i * kAttnThreads;
-        if (at < vectors) {
-            t.k[i] = k[at];
-            t.v[i] = v[at];
-        } else {
-            t.k[i] = make_int4(0, 0, 0, 0);
-            t.v[i] = make_int4(0, 0, 0, 0);
-        }
+    const int roundsPerSplit =
+        (keyCount + kRoundKeys * kDecodeSplits - 1) / (kRoundKeys * kDecodeSplits);
+    const int perSplit = roundsPerSplit * kRoundKeys;
+    return {(keyCount + perSplit - 1) / perSplit, perSplit};
+}
+
+// C consecutive halves of an fp16 row.
+template <int C>
+__device__ inline void load_halves(const uint16_t *p, uint16_t (&h)[C])
+{
+    if constexpr (C == 4) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(p);
+        h[0] = (uint16_t) (v.x & 0xFFFFu); h[1] = (uint16_t) (v.x >> 16);
+        h[2] = (uint16_t) (v.y & 0xFFFFu); h[3] = (uint16_t) (v.y >> 16);
+    } else if constexpr (C == 2) {
+        const uint32_t v = *reinterpret_cast<const uint32_t *>(p);
+        h[0] = (uint16_t) (v & 0xFFFFu); h[1] = (uint16_t) (v >> 16);
+    } else {
+        h[0] = *p;
     }
 }
 
+__device__ inline void store_agent(double *p, double v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ inline double load_agent(const double *p)
+{
+    return __hip_atomic_load(const_cast<double *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int C, int G>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a)
 {
-    __shared__ double sQuery[kMaxQueryWidth + 2 * kMaxHeads]; // head rows padded by 2
-    __shared__ double sPart[kAttnThreads];
-    __shared__ uint32_t sKeys[kKeyTile * (kMaxKvWidth / 2 + 1)];
-    __shared__ int4 sValues[kTileBytes / 16];
-    __shared__ double sWeights[kMaxHeads * kKeyTile];
-    __shared__ double sMax[kMaxHeads], sSum[kMaxHeads], sFactor[kMaxHeads];
-    __shared__ double sMergeMax[kMaxHeads * kDecodeSplits], sMergeSum[kMaxHeads * kDecodeSplits];
+    constexpr int kRows = kScoreBatch * G; // reduce_rows width: (key, head) pairs
+    __shared__ double sScore[G][kMaxSplitKeys];
+    __shared__ double sAcc[kAttnWaves][kMaxGroupWidth];
+    __shared__ double sMax[G], sSum[G];
+    __shared__ double sSplitMax[G][kDecodeSplits], sSplitSum[G][kDecodeSplits];
     __shared__ int sLast;
 
-    const int split = blockIdx.x;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int keyCount = *a.position + 1;
-    const int perSplit = split_keys(keyCount);
-    const int splits = (keyCount + perSplit - 1) / perSplit;
-    const int k0 = split * perSplit;
-    if (k0 >= keyCount)
-        return;
-    const int k1 = min(k0 + perSplit, keyCount);
-    const int heads = a.heads, hd = a.head_dim;
-    const int qWidth = heads * hd, kvWidth = a.kv_heads * hd;
+    const int hd = a.head_dim, kvWidth = a.kv_heads * hd;
+    const int heads = a.heads, qWidth = heads * hd;
     const int perKv = heads / a.kv_heads;
-    const int keyWords = kvWidth / 2, keyStride = kMaxKvWidth / 2 + 1;
-    const int dots = heads * kKeyTile;
-    // threads a dot product: a power of two, each part at least four channels
-    int perDot = dots >= kAttnThreads ? 1 : kAttnThreads / dots;
-    while (perDot > 1 && hd / perDot < 4)
-        perDot >>= 1;
+    const int group = blockIdx.y, h0 = group * G;
+    const int groupWidth = G * hd;
+    const int split = blockIdx.x;
 
-    // the query (fp32 -> double) and the first tile, all loads in flight
-    float2 q2 = make_float2(0.f, 0.f);
-    if (2 * t < qWidth)
-        q2 = reinterpret_cast<const float2 *>(a.query)[t];
-    TileLoads tile;
-    load_tile(tile, a.key_cache, a.value_cache, k0, min(kKeyTile, k1 - k0), kvWidth);
-    if (2 * t < qWidth) {
-        const int h = (2 * t) / hd; // both halves of the pair are in one head (hd even)
-        sQuery[2 * t + 2 * h] = q2.x;
-        sQuery[2 * t + 1 + 2 * h] = q2.y;
-    }
-    if (t < heads) {
-        sMax[t] = -INFINITY;
-        sSum[t] = 0.0;
-    }
-    double acc[kOutPerThread];
-    int outHead[kOutPerThread], outColumn[kOutPerThread]; // division-free inner loops
+    // the query channels of this lane, before the position is known
+    // (unconditional loads, masked: a selected load would be sunk into a
+    // branch and waited for on its own)
+    const bool active = lane * C < hd;
+    const int c0 = active ? lane * C : 0;
+    const uint32_t keep = active ? 0xFFFFFFFFu : 0u;
+    double q[G][C];
 #pragma unroll
-    for (int i = 0; i < kOutPerThread; ++i) {
-        const int idx = t + i * kAttnThreads; // head idx / hd, channel idx % hd
-        acc[i] = 0.0;
-        outHead[i] = idx < qWidth ? idx / hd : 0;
-        outColumn[i] = idx < qWidth ? (outHead[i] / perKv) * hd + idx % hd : 0;
-    }
-    // the (head, key, part) of this thread's share of the scores: the parts
-    // of one dot product sit in different waves, so a wave reads one or two
-    // query rows (broadcast) and 32 different key rows (different banks)
-    const int dotsPerPass = kAttnThreads / perDot;
-    const int myDot = t % dotsPerPass, part = t / dotsPerPass;
-    const int myHead = myDot / kKeyTile, myKey = myDot % kKeyTile;
-    const int span = hd / perDot;
-    const int qBase = myHead * (hd + 2) + part * span;
-    const int kBase = ((myHead / perKv) * hd + part * span) / 2;
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int i = 0; i < C; ++i)
+            q[g][i] = (double) __uint_as_float(__float_as_uint(a.query[(h0 + g) * hd + c0 + i]) & keep);
 
-    for (int t0 = k0; t0 < k1; t0 += kKeyTile) {
-        const int nk = min(kKeyTile, k1 - t0);
-        {
-            const int vectors = nk * kvWidth / 8;
+    const int keyCount = *a.position + 1;
+    const SplitPlan plan = plan_splits(keyCount);
+    if (split >= plan.splits)
+        return;
+    const int k0 = split * plan.perSplit;
+    const int n = min(plan.perSplit, keyCount - k0);
+    const uint16_t *keys = a.key_cache + (int64_t) k0 * kvWidth;
+    const uint16_t *values = a.value_cache + (int64_t) k0 * kvWidth;
+    int kvOffset[G];
 #pragma unroll
-            for (int i = 0; i < kTileVectors; ++i) {
-                const int at = t + i * kAttnThreads;
-                if (at < vectors) {
-                    const int j = at / (keyWords / 4), w = (at % (keyWords / 4)) * 4;
-                    uint32_t *dst = sKeys + j * keyStride + w;
-                    dst[0] = (uint32_t) tile.k[i].x;
-                    dst[1] = (uint32_t) tile.k[i].y;
-                    dst[2] = (uint32_t) tile.k[i].z;
-                    dst[3] = (uint32_t) tile.k[i].w;
-                    sValues[at] = tile.v[i];
-                }
+    for (int g = 0; g < G; ++g)
+        kvOffset[g] = ((h0 + g) / perKv) * hd + c0;
+
+    // a round's rows for this wave: keys r0 + wave + 8 b, clamped into range
+    // (the clamped duplicates are masked where they are used)
+    uint16_t kh[kScoreBatch][G][C], vh[kScoreBatch][G][C];
+    auto load_round = [&](const uint16_t *base, int r0, uint16_t (&dst)[kScoreBatch][G][C]) {
+#pragma unroll
+        for (int b = 0; b < kScoreBatch; ++b) {
+            const int j = min(r0 + wave + b * kAttnWaves, n - 1);
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+                load_halves<C>(base + (int64_t) j * kvWidth + kvOffset[g], dst[b][g]);
+        }
+    };
+    load_round(keys, 0, kh);
+    load_round(values, 0, vh);
+
+    for (int r0 = 0; r0 < n; r0 += kRoundKeys) {
+        if (r0 > 0)
+            load_round(keys, r0, kh);
+        double y[kRows];
+#pragma unroll
+        for (int b = 0; b < kScoreBatch; ++b)
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                double p = 0.0;
+#pragma unroll
+                for (int i = 0; i < C; ++i)
+                    p += q[g][i] * (double) half_value(kh[b][g][i]);
+                y[b * G + g] = p;
             }
+        const double total = reduce_rows<kRows>(y, lane);
+        if (stores_row<kRows>(lane)) {
+            const int r = row_of_lane<kRows>(lane);
+            const int j = r0 + wave + (r / G) * kAttnWaves;
+            if (j < n)
+                sScore[r % G][j] = (double) a.scale * total;
         }
-        __syncthreads();
-        if (t0 + kKeyTile < k1)
-            load_tile(tile, a.key_cache, a.value_cache, t0 + kKeyTile,
-                      min(kKeyTile, k1 - t0 - kKeyTile), kvWidth);
-
-        {
-            double partial = 0.0;
-            if (myDot < dots && myKey < nk) {
-                const double *q = sQuery + qBase; // padded head row
-                const uint32_t *k = sKeys + myKey * keyStride + kBase;
-                double p0 = 0.0, p1 = 0.0, p2 = 0.0, p3 = 0.0;
-                int c = 0;
-                for (; c + 4 <= span; c += 4) {
-                    const uint32_t x = k[c / 2], y = k[c / 2 + 1];
-                    p0 += q[c] * (double) half_value((uint16_t) (x & 0xFFFFu));
-                    p1 += q[c + 1] * (double) half_value((uint16_t) (x >> 16));
-                    p2 += q[c + 2] * (double) half_value((uint16_t) (y & 0xFFFFu));
-                    p3 += q[c + 3] * (double) half_value((uint16_t) (y >> 16));
-                }
-                for (; c < span; c += 2) {
-                    const uint32_t x = k[c / 2];
-                    p0 += q[c] * (double) half_value((uint16_t) (x & 0xFFFFu));
-                    p1 += q[c + 1] * (double) half_value((uint16_t) (x >> 16));
-                }
-                partial = (p0 + p1) + (p2 + p3);
-            }
-            sPart[t] = partial;
-        }
-        __syncthreads();
-        if (t < dots) {
-            double total = 0.0;
-            for (int p = 0; p < perDot; ++p)
-                total += sPart[p * dotsPerPass + t];
-            sWeights[t] = (t % kKeyTile) < nk ? (double) a.scale * total : -INFINITY;
-        }
-        __syncthreads();
-
-        for (int head = wave; head < heads; head += kAttnWaves) {
-            const double s = lane < kKeyTile ? sWeights[head * kKeyTile + lane] : -INFINITY;
-            const double previous = sMax[head];
-            const double largest = fmax(previous, wave_max_d(s));
-            const double w = lane < nk ? exp(s - largest) : 0.0;
-            const double total = wave_sum_d(w);
-            if (lane < kKeyTile)
-                sWeights[head * kKeyTile + lane] = w;
-            if (lane == 0) {
-                const double factor = previous == -INFINITY ? 0.0 : exp(previous - largest);
-                sFactor[head] = factor;
-                sSum[head] = sSum[head] * factor + total;
-                sMax[head] = largest;
-            }
-        }
-        __syncthreads();
-
-        const uint16_t *vTile = reinterpret_cast<const uint16_t *>(sValues);
-#pragma unroll
-        for (int i = 0; i < kOutPerThread; ++i)
-            acc[i] *= sFactor[outHead[i]];
-        for (int j = 0; j < nk; ++j) {
-            const uint16_t *vRow = vTile + j * kvWidth;
-            const double *w = sWeights + j;
-#pragma unroll
-            for (int i = 0; i < kOutPerThread; ++i)
-                acc[i] += w[outHead[i] * kKeyTile] * (double) half_value(vRow[outColumn[i]]);
-        }
-        __syncthreads(); // the next tile overwrites the LDS tiles
     }
-
-    double *o = a.ws_o + (int64_t) split * qWidth;
-#pragma unroll
-    for (int i = 0; i < kOutPerThread; ++i) {
-        const int idx = t + i * kAttnThreads;
-        if (idx < qWidth)
-            o[idx] = acc[i];
-    }
-    if (t < heads) {
-        a.ws_ml[(split * heads + t) * 2] = sMax[t];
-        a.ws_ml[(split * heads + t) * 2 + 1] = sSum[t];
-    }
-    // one thread publishes the workgroup's writes (release) and takes the
-    // ticket; the last one's acquire makes every partial visible to it
     __syncthreads();
-    if (t == 0) {
-        __threadfence();
-        sLast = atomicAdd(a.counter, 1) == splits - 1;
-        if (sLast)
-            __threadfence();
+
+    // softmax of the split, one wave a head; the weights replace the scores
+    if (wave < G) {
+        double largest = -INFINITY;
+        for (int j = lane; j < n; j += 64)
+            largest = fmax(largest, sScore[wave][j]);
+        largest = wave_max_d(largest);
+        double sum = 0.0;
+        for (int j = lane; j < n; j += 64) {
+            const double w = exp(sScore[wave][j] - largest);
+            sScore[wave][j] = w;
+            sum += w;
+        }
+        sum = wave_sum_d(sum);
+        if (lane == 0) {
+            sMax[wave] = largest;
+            sSum[wave] = sum;
+        }
     }
+    __syncthreads();
+
+    double acc[G][C];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int i = 0; i < C; ++i)
+            acc[g][i] = 0.0;
+    for (int r0 = 0; r0 < n; r0 += kRoundKeys) {
+        if (r0 > 0)
+            load_round(values, r0, vh);
+#pragma unroll
+        for (int b = 0; b < kScoreBatch; ++b) {
+            const int j = r0 + wave + b * kAttnWaves;
+            if (j >= n)
+                break;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const double w = sScore[g][j];
+#pragma unroll
+                for (int i = 0; i < C; ++i)
+                    acc[g][i] += w * (double) half_value(vh[b][g][i]);
+            }
+        }
+    }
+    if (active)
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int i = 0; i < C; ++i)
+                sAcc[wave][g * hd + c0 + i] = acc[g][i];
+    __syncthreads();
+
+    // the split's partial: the waves' sums in wave order, then (max, sum)
+    if (t < groupWidth) {
+        double o = 0.0;
+        for (int w = 0; w < kAttnWaves; ++w)
+            o += sAcc[w][t];
+        store_agent(a.ws_o + (int64_t) split * qWidth + h0 * hd + t, o);
+    }
+    if (t < G) {
+        store_agent(a.ws_ml + (split * heads + h0 + t) * 2, sMax[t]);
+        store_agent(a.ws_ml + (split * heads + h0 + t) * 2 + 1, sSum[t]);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // the stores have completed
+    __syncthreads();
+    if (t == 0)
+        sLast = __hip_atomic_fetch_add(a.counter + group, 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT) == plan.splits - 1;
     __syncthreads();
     if (!sLast)
         return;
 
-    // the merge (MultiQueryAttention.h:43-49): every split rescaled to the
-    // row's maximum, the sums divided by the total, rounded and quantized
-    for (int idx = t; idx < heads * splits; idx += kAttnThreads) {
-        const int s = idx / heads, head = idx % heads;
-        sMergeMax[head * kDecodeSplits + s] = a.ws_ml[idx * 2];
-        sMergeSum[head * kDecodeSplits + s] = a.ws_ml[idx * 2 + 1];
+    // the merge of the group's splits
+    const int splits = plan.splits;
+    if (t < G * splits) {
+        const int g = t / splits, sp = t % splits;
+        sSplitMax[g][sp] = load_agent(a.ws_ml + (sp * heads + h0 + g) * 2);
+        sSplitSum[g][sp] = load_agent(a.ws_ml + (sp * heads + h0 + g) * 2 + 1);
     }
     __syncthreads();
-    if (t < heads) {
+    if (t < G) {
         double largest = -INFINITY;
-        for (int s = 0; s < splits; ++s)
-            largest = fmax(largest, sMergeMax[t * kDecodeSplits + s]);
+        for (int sp = 0; sp < splits; ++sp)
+            largest = fmax(largest, sSplitMax[t][sp]);
         sMax[t] = largest;
     }
     __syncthreads();
-    for (int idx = t; idx < heads * splits; idx += kAttnThreads) {
-        const int head = idx / splits, s = idx % splits;
-        sMergeMax[head * kDecodeSplits + s] = exp(sMergeMax[head * kDecodeSplits + s] - sMax[head]);
+    if (t < G * splits) {
+        const int g = t / splits, sp = t % splits;
+        sSplitMax[g][sp] = exp(sSplitMax[g][sp] - sMax[g]); // now the split's factor
     }
     __syncthreads();
-    if (t < heads) {
+    if (t < G) {
         double total = 0.0;
-        for (int s = 0; s < splits; ++s)
-            total += sMergeSum[t * kDecodeSplits + s] * sMergeMax[t * kDecodeSplits + s];
+        for (int sp = 0; sp < splits; ++sp)
+            total += sSplitSum[t][sp] * sSplitMax[t][sp];
         sSum[t] = total;
     }
     __syncthreads();
-
-    double weighted[kOutPerThread];
-#pragma unroll
-    for (int i = 0; i < kOutPerThread; ++i)
-        weighted[i] = 0.0;
+    if (t >= ((groupWidth + 63) / 64) * 64)
+        return; // whole waves remain for the block reductions
+    const int g = min(t / hd, G - 1);
+    double weighted = 0.0;
     for (int s0 = 0; s0 < splits; s0 += kMergeBatch) {
-        double partOf[kMergeBatch][kOutPerThread];
+        double part[kMergeBatch];
 #pragma unroll
         for (int u = 0; u < kMergeBatch; ++u)
-#pragma unroll
-            for (int i = 0; i < kOutPerThread; ++i) {
-                const int idx = t + i * kAttnThreads;
-                partOf[u][i] = (s0 + u < splits && idx < qWidth)
-                                   ? a.ws_o[(int64_t) (s0 + u) * qWidth + idx] : 0.0;
-            }
+            part[u] = (s0 + u < splits && t < groupWidth)
+                          ? load_agent(a.ws_o + (int64_t) (s0 + u) * qWidth + h0 * hd + t) : 0.0;
 #pragma unroll
         for (int u = 0; u < kMergeBatch; ++u)
-#pragma unroll
-            for (int i = 0; i < kOutPerThread; ++i)
-                if (s0 + u < splits)
-                    weighted[i] += partOf[u][i] * sMergeMax[outHead[i] * kDecodeSplits + s0 + u];
+            if (s0 + u < splits)
+                weighted += part[u] * sSplitMax[g][s0 + u];
     }
-#pragma unroll
-    for (int i = 0; i < kOutPerThread; ++i) {
-        const int idx = t + i * kAttnThreads;
-        if (idx >= qWidth) // whole 32-blocks leave together
-            break;
-        const float v = (float) (weighted[i] / sSum[outHead[i]]);
-        if (a.out)
-            a.out[idx] = v;
-        float amax = fabsf(v);
-        for (int mask = 16; mask >= 1; mask >>= 1)
-            amax = fmaxf(amax, __shfl_xor(amax, mask));
+    const int idx = h0 * hd + t;
+    const float v = t < groupWidth ? (float) (weighted / sSum[g]) : 0.f;
+    if (a.out && t < groupWidth)
+        a.out[idx] = v;
+    float amax = fabsf(v);
+    for (int mask = 16; mask >= 1; mask >>= 1)
+        amax = fmaxf(amax, __shfl_xor(amax, mask));
+    if (t < groupWidth) { // whole 32-blocks: groupWidth is a multiple of 32
         const uint16_t bits = scale_bits_from_amax(amax);
         const float sc = half_value(bits);
         a.q8[idx] = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);
         if ((t & 31) == 0)
             reinterpret_cast<uint16_t *>(a.q8 + qWidth)[idx / kBlock] = bits;
     }
-    if (t == 0)
-        atomicExch(a.counter, 0); // ready for the next launch
+    if (t == 0) // ready for the next launch
+        __hip_atomic_store(a.counter + group, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- gate|up + GeGLU + Q8 -----------------------------------------------------------
@@ -866,14 +859,33 @@ __global__ __launch_bounds__(64) void head_finalize_kernel(HeadArgs a)
 // ============================================================================
 // Launchers
 // ============================================================================
-bool fused_decode_supported(int width, int heads, int kv_heads, int head_dim, int intermediate)
+// Channels a lane owns and heads a workgroup merges, by head width.
+static bool attention_layout(int head_dim, int *channels, int *group)
+{
+    if (head_dim == 256 || head_dim == 128 || head_dim == 64) {
+        *channels = head_dim / 64;
+        *group = 1;
+        return true;
+    }
+    if (head_dim == 32 || head_dim == 16) {
+        *channels = 1;
+        *group = 32 / head_dim;
+        return true;
+    }
+    return false;
+}
+
+bool fused_decode_supported(int width, int heads, int kv_heads, int head_dim, int intermediate,
+                            int max_positions)
 {
     const int qWidth = heads * head_dim, kvWidth = kv_heads * head_dim;
-    const int dots = heads * kKeyTile;
-    return kvWidth % 8 == 0 && width % kBlock == 0 && width <= kFusedMaxWidth && head_dim % 4 == 0
-           && qWidth <= kMaxQueryWidth && qWidth % kBlock == 0 && kvWidth <= kMaxKvWidth
-           && heads <= kMaxHeads && heads % kv_heads == 0 && (dots & (dots - 1)) == 0
-           && intermediate % kBlock == 0 && intermediate <= 16384 && (head_dim / 2) > 0;
+    int channels = 0, group = 0;
+    return attention_layout(head_dim, &channels, &group) && heads % group == 0
+           && group <= kAttnWaves && group * head_dim <= kMaxGroupWidth
+           && width % kBlock == 0 && width <= kFusedMaxWidth && qWidth % kBlock == 0
+           && heads % kv_heads == 0 && kvWidth % 8 == 0
+           && max_positions <= kDecodeSplits * kMaxSplitKeys && intermediate % kBlock == 0
+           && intermediate <= 16384;
 }
 
 size_t decode_workspace_bytes(int heads, int head_dim)
@@ -897,7 +909,18 @@ hipError_t launch_qkv_rope(const QkvArgs &a, hipStream_t stream)
 
 hipError_t launch_attention(const AttentionArgs &a, hipStream_t stream)
 {
-    hipLaunchKernelGGL(attention_kernel, dim3(kDecodeSplits), dim3(kAttnThreads), 0, stream, a);
+    int channels = 0, group = 0;
+    if (!attention_layout(a.head_dim, &channels, &group) || a.heads % group != 0)
+        return hipErrorInvalidValue;
+    const dim3 grid(kDecodeSplits, a.heads / group);
+    if (channels == 4)
+        hipLaunchKernelGGL((attention_kernel<4, 1>), grid, dim3(kAttnThreads), 0, stream, a);
+    else if (channels == 2)
+        hipLaunchKernelGGL((attention_kernel<2, 1>), grid, dim3(kAttnThreads), 0, stream, a);
+    else if (group == 1)
+        hipLaunchKernelGGL((attention_kernel<1, 1>), grid, dim3(kAttnThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL((attention_kernel<1, 2>), grid, dim3(kAttnThreads), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -12,6 +12,7 @@ namespace gq8 {
 
 constexpr int kFusedMaxWidth = 2048; // a normalised row held in LDS as Q8
 constexpr int kDecodeSplits = 64;    // attention workgroups over one row's keys
+constexpr int kDecodeCounters = 64; // attention head-group tickets
 constexpr int kHeadSlots = 64;       // lm_head argmax words (one wave folds them)
 constexpr int kHeadSlotStride = 16;  // 128 bytes between words
 
@@ -42,7 +43,7 @@ struct AttentionArgs {
     const int *position;      // keys [0, *position] are attended
     float scale;
     double *ws_o, *ws_ml;     // kDecodeSplits partials
-    int *counter;             // zero between launches
+    int *counter;             // one a head group (kDecodeCounters), zero between launches
     float *out;               // optional fp32 row
     uint8_t *q8;              // Q8 row for o_proj
 };
@@ -75,7 +76,8 @@ struct HeadArgs {
     int advance;              // nonzero: *position += 1 after the argmax
 };
 
-bool fused_decode_supported(int width, int heads, int kv_heads, int head_dim, int intermediate);
+bool fused_decode_supported(int width, int heads, int kv_heads, int head_dim, int intermediate,
+                            int max_positions);
 size_t decode_workspace_bytes(int heads, int head_dim);
 
 hipError_t launch_qkv_rope(const QkvArgs &a, hipStream_t stream);

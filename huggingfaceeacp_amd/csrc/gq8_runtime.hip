@@ -422,7 +422,7 @@ struct gq8_decoder {
     bool useFused = true;
     bool fusedSupported = false;
     double *decodeO = nullptr, *decodeMl = nullptr;
-    int *counters = nullptr; // [0] attention
+    int *counters = nullptr; // attention head-group tickets
     unsigned long long *headBest = nullptr; // the lm_head argmax slots
 
     hipGraphExec_t graph = nullptr;
@@ -680,12 +680,12 @@ extern "C" int gq8_decoder_create(const gq8_shape *shape, gq8_decoder **out)
     GQ8_ALLOC(d->debugAttended, R * d->qWidth * sizeof(float));
     GQ8_ALLOC(d->debugActivated, R * (int64_t) s.intermediate * sizeof(float));
     d->fusedSupported = gq8::fused_decode_supported(s.width, s.heads, s.kv_heads, s.head_dim,
-                                                    s.intermediate);
+                                                    s.intermediate, s.max_positions);
     {
         const size_t wsBytes = gq8::decode_workspace_bytes(s.heads, s.head_dim);
         GQ8_ALLOC(d->decodeO, wsBytes);
         d->decodeMl = d->decodeO + (size_t) gq8::kDecodeSplits * s.heads * s.head_dim;
-        GQ8_ALLOC(d->counters, 4 * sizeof(int));
+        GQ8_ALLOC(d->counters, gq8::kDecodeCounters * sizeof(int));
         GQ8_ALLOC(d->headBest, gq8::kHeadSlots * gq8::kHeadSlotStride * sizeof(unsigned long long));
     }
 #undef GQ8_ALLOC
@@ -693,7 +693,7 @@ extern "C" int gq8_decoder_create(const gq8_shape *shape, gq8_decoder **out)
         return cleanup(fail(GQ8_ERR_MEMORY, "pinned allocation failed"));
     if (hipMemset(d->sequence, 0, ((size_t) s.max_positions + 1) * sizeof(uint32_t)) != hipSuccess
         || hipMemset(d->position, 0, sizeof(int)) != hipSuccess
-        || hipMemset(d->counters, 0, 4 * sizeof(int)) != hipSuccess
+        || hipMemset(d->counters, 0, gq8::kDecodeCounters * sizeof(int)) != hipSuccess
         || hipMemset(d->headBest, 0, gq8::kHeadSlots * gq8::kHeadSlotStride * sizeof(unsigned long long))
                != hipSuccess
         || hipMemset(d->keyCache, 0, cacheElements * sizeof(uint16_t)) != hipSuccess
