@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 MODE_Q8 = 0
 MODE_REFERENCE = 1
+MODE_Q8_PATH_F32 = 2  # the Q8 path with fp32 product inputs and an fp32 KV cache
 
 T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN, T_INPUT_NORM, T_POST_NORM = range(9)
 PER_LAYER = 9
