@@ -28,6 +28,12 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes a launch moves, from two rocprofv3 counter passes over the decode
+# kernels: FETCH_SIZE scaled by what it reads for a 256 MiB copy (x 1.99977),
+# plus WRITE_SIZE (the passes and their commands are in
+# profiles/decode_kernels_gemma2b_hbm_traffic.md).  A kernel change
+# re-measures these.
+MEASURED_TRAFFIC = {"gate_up": 71572184, "lm_head": 558419832, "down": 35954732}
 METRIC = "Gemma-2B Q8_0 decode tok/s (b=1, ctx 512) + % of HBM roofline"
 STAGE_LABELS = {
     "gate_up": "gateup_geglu_kernel (post-attention norm + gate|up 2048 -> 2x16384 + GeGLU + Q8)",
@@ -55,32 +61,39 @@ def stage_bytes(shape, stage: str) -> int:
     raise ValueError(stage)
 
 
-def cpu_baseline(layers: int, sample_steps: int, threads: int) -> dict:
-    """The oracle's Q8 decoder (C, OpenMP) on the host cores, bounded sample."""
+def cpu_baseline(layers: int, seconds_target: float, threads: int) -> dict:
+    """The oracle's Q8 decoder (C, OpenMP over the host cores): a bounded
+    sample of the same decode loop, after a short untimed prefill."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     O.lib()
-    shape = O.gemma_2b_shape(layers=layers, max_positions=64)
+    prompt_tokens, max_positions = 32, 1024
+    shape = O.gemma_2b_shape(layers=layers, max_positions=max_positions)
     model = O.Model(shape, O.MODE_Q8)
     t0 = time.perf_counter()
     assert model.fill_synthetic() == 0
     load = time.perf_counter() - t0
-    prompt = O.prompt_ids(0xC0FFEE + 2, shape.vocab, 4)
+    prompt = O.prompt_ids(0xC0FFEE + 2, shape.vocab, prompt_tokens)
     status, logits, _ = model.step(prompt)
     assert status == 0
     token = O.argmax(logits[-1])
+    steps = 0
     t0 = time.perf_counter()
-    for _ in range(sample_steps):
+    while steps < 8 or (time.perf_counter() - t0 < seconds_target
+                        and prompt_tokens + steps < max_positions - 1):
         status, logits, _ = model.step(np.array([token], dtype=np.int32))
+        assert status == 0
         token = O.argmax(logits[0])
+        steps += 1
     seconds = time.perf_counter() - t0
     model.close()
-    log(f"cpu baseline: weights {load:.1f} s, {sample_steps} steps in {seconds:.2f} s")
-    return {"value": round(sample_steps / seconds, 3), "unit": "tok/s", "cores": threads,
+    log(f"cpu baseline: weights {load:.1f} s, {steps} steps in {seconds:.2f} s")
+    return {"value": round(steps / seconds, 3), "unit": "tok/s", "cores": threads,
             "kind": "port",
-            "sample": f"oracle C Q8 decoder (OpenMP, {threads} threads), {layers} layers at full "
-                      f"Gemma-2B shape, 4-token seeded prompt, {sample_steps} greedy decode steps "
-                      f"timed (positions 4..{4 + sample_steps - 1}); host "
+            "sample": f"oracle C Q8 decoder (OpenMP, {threads} threads) at the full Gemma-2B "
+                      f"shape ({layers} layers), {prompt_tokens}-token seeded prompt prefilled "
+                      f"untimed, then {steps} greedy decode steps timed (positions "
+                      f"{prompt_tokens}..{prompt_tokens + steps - 1}, about {seconds:.0f} s); host "
                       f"'{platform.processor() or platform.machine()}'"}
 
 
@@ -92,7 +105,8 @@ def main() -> int:
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--layers", type=int, default=18)
     ap.add_argument("--threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "0") or 0))
-    ap.add_argument("--cpu-steps", type=int, default=8, help="decode steps of the CPU sample")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="timed seconds of the CPU baseline's decode sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-graph", action="store_true", help="launch steps without hipGraph replay")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -173,7 +187,7 @@ def main() -> int:
     achieved = launch_bytes / per_launch_s / 1e9
     roofline = {"bound": "hbm", "kernel": STAGE_LABELS[dominant], "achieved": round(achieved, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": None, "bytes_per_launch": launch_bytes,
+                "traffic": MEASURED_TRAFFIC.get(dominant), "bytes_per_launch": launch_bytes,
                 "avg_launch_us": round(per_launch_s * 1e6, 2)}
 
     result = {
@@ -201,7 +215,7 @@ def main() -> int:
         "cpu_baseline": None,
     }
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(args.layers, args.cpu_steps, threads)
+        result["cpu_baseline"] = cpu_baseline(args.layers, args.cpu_seconds, threads)
     print(json.dumps(result), flush=True)
     return 0
 
