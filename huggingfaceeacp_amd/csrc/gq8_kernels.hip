@@ -874,6 +874,9 @@ hipError_t launch_q8_product(const uint8_t *x8, int x_rows_total, int x_row0, in
     const int64_t xElements = (int64_t) x_rows_total * inner;
     if (rows == 1)
         return launch_matvec(x8, xElements, x_row0, w8, inner, outputs, y, residual, stream);
+    if (rows >= kGemmMinRows)
+        return launch_q8_gemm(x8, xElements, x_row0, rows, w8, inner, outputs, y, y_stride,
+                              residual, stream);
     int b = 8;
     while (b > 1 && (b > rows || product_lds(b, inner) > kProductLdsLimit))
         b >>= 1;

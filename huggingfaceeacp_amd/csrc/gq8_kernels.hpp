@@ -47,6 +47,11 @@ hipError_t launch_kv_store(const float *k, const float *v, int src_stride, int r
                            const int *pos_ptr, int pos_value, hipStream_t stream);
 
 // x8: Q8 row buffer of x_rows_total rows; rows [x_row0, x_row0 + rows) are used.
+// Steps of kGemmMinRows rows or more run on the int8 MFMA GEMM (gq8_gemm.hip).
+constexpr int kGemmMinRows = 32;
+hipError_t launch_q8_gemm(const uint8_t *x8, int64_t x_elements, int x_row0, int rows,
+                          const uint8_t *w8, int inner, int outputs, float *y, int y_stride,
+                          int residual, hipStream_t stream);
 hipError_t launch_q8_product(const uint8_t *x8, int x_rows_total, int x_row0, int rows,
                              const uint8_t *w8, int inner, int outputs, float *y, int y_stride,
                              int residual, hipStream_t stream);

@@ -205,6 +205,48 @@ def test_q8_product_rows_and_residual(torch_cuda, rows):
         assert worst_error(got[r], ref) <= 1e-6
 
 
+@pytest.mark.parametrize("rows,inner,outputs", [(32, 2048, 2560), (64, 2048, 2048),
+                                                 (100, 16384, 2048), (130, 64, 96),
+                                                 (33, 2048, 32768)])
+def test_q8_gemm_rows_are_the_one_row_products(torch_cuda, rows, inner, outputs):
+    """Steps of 32 rows or more run on the int8 MFMA GEMM; each row is the
+    exact block dot scaled and summed in double in block order, as the oracle
+    does, so the rows are bit-identical to the one-row products.  Shapes cover
+    whole and partial 64 x 64 tiles and K chunks."""
+    torch = torch_cuda
+    w = O.quantize_int8_blocks(spread(inner * outputs, 81, 0.02))
+    x = spread(rows * inner, 82, 1.0)
+    q_all, s_all = O.quantize_row(x)
+    x8 = np.concatenate([q_all.view(np.uint8), s_all.view(np.uint8)])
+    y = empty(torch, rows * outputs, torch.float32)
+    G.q8_product(dev(x8), dev(w), rows, inner, outputs, y.data_ptr(), outputs)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy().reshape(rows, outputs)
+    nb = inner // 32
+    for r in range(rows):
+        ref = O.q8_matvec(q_all[r * inner:(r + 1) * inner], s_all[r * nb:(r + 1) * nb], w,
+                          outputs, inner)
+        assert np.array_equal(got[r], ref), f"row {r}"
+
+
+def test_q8_gemm_residual(torch_cuda):
+    torch = torch_cuda
+    rows, inner, outputs = 48, 2048, 2048
+    w = O.quantize_int8_blocks(spread(inner * outputs, 83, 0.02))
+    x = spread(rows * inner, 84, 1.0)
+    q_all, s_all = O.quantize_row(x)
+    x8 = np.concatenate([q_all.view(np.uint8), s_all.view(np.uint8)])
+    base = spread(rows * outputs, 85, 1.0)
+    y = to_device(torch, base)
+    G.q8_product(dev(x8), dev(w), rows, inner, outputs, y.data_ptr(), outputs, residual=True)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy().reshape(rows, outputs)
+    for r in range(rows):
+        ref = O.q8_matvec(q_all[r * inner:(r + 1) * inner], s_all[r * 64:(r + 1) * 64], w,
+                          outputs, inner).astype(np.float64) + base[r * outputs:(r + 1) * outputs]
+        assert worst_error(got[r], ref) <= 1e-6
+
+
 def test_kv_store_f16(torch_cuda):
     torch = torch_cuda
     rows, kv, pos, maxpos = 3, 256, 5, 16
