@@ -97,6 +97,62 @@ def cpu_baseline(layers: int, seconds_target: float, threads: int) -> dict:
                       f"'{platform.processor() or platform.machine()}'"}
 
 
+PREFILL_METRIC = "Gemma-2B Q8_0 prefill tok/s (b=1, 2048-token prompt) + int8 MFMA utilisation"
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+
+
+def prefill_bench(args, G, torch) -> dict:
+    """The prefill workload: a 2048-token seeded prompt through all 18 layers
+    as one step (every linear an int8 MFMA GEMM of M = 2048), logits of the
+    last row only; W untimed prefills, then K timed."""
+    rows = args.prompt
+    shape = G.DecoderShape.gemma_2b(layers=args.layers, max_positions=max(rows + 1, 2048),
+                                    max_step_rows=rows)
+    decoder = G.Decoder(shape)
+    threads = args.threads if args.threads > 0 else (os.cpu_count() or 1)
+    decoder.fill_synthetic(threads)
+    prompt = G.prompt_ids(0xC0FFEE + 3, shape.vocab, rows).astype(np.uint32)
+    ids = torch.from_numpy(prompt.copy()).to("cuda")
+    logits = torch.empty(shape.vocab, dtype=torch.float32, device="cuda")
+
+    def once():
+        decoder.begin_sequence()
+        decoder.step(ids.data_ptr(), rows, logits.data_ptr(), 1)
+
+    for _ in range(args.warmup):
+        once()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        once()
+    torch.cuda.synchronize()
+    seconds = (time.perf_counter() - t0) / args.steps
+    linear = args.layers * (shape.width * (shape.query_width + 2 * shape.kv_width)
+                            + shape.query_width * shape.width
+                            + 2 * shape.width * shape.intermediate
+                            + shape.intermediate * shape.width)
+    int_ops = 2 * rows * linear + 2 * shape.width * shape.vocab  # lm_head: the last row
+    tops = int_ops / seconds / 1e12
+    log(f"prefill of {rows} tokens: {seconds * 1e3:.2f} ms, {int_ops / 1e12:.3f} T int8 ops, "
+        f"{tops:.1f} TOP/s")
+    return {
+        "metric": PREFILL_METRIC, "value": round(rows / seconds, 1), "unit": "tok/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(seconds * 1e3, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic: seeded N(0,0.02) weights / N(0,0.1) norms quantized to Int8Blocks, "
+                "seeded uniform prompt ids",
+        "config": {"workload": f"Gemma-2B Int8Blocks prefill, {args.layers} layers, "
+                               f"{rows}-token prompt as one step, last-row logits",
+                   "layers": args.layers, "prompt_tokens": rows},
+        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS,
+                     "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None,
+                     "counted": "2 M K N int8 ops over every linear plus the last row's lm_head; "
+                                "attention's fp64 work not counted"},
+        "cpu_baseline": None,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -109,6 +165,9 @@ def main() -> int:
                     help="timed seconds of the CPU baseline's decode sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-graph", action="store_true", help="launch steps without hipGraph replay")
+    ap.add_argument("--mode", choices=("decode", "prefill"), default="decode",
+                    help="decode: the headline decode loop; prefill: the 2048-token prefill "
+                         "(use with --prompt 2048)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first copy MIB MiB device-to-device three times (a kernel of known "
                          "bytes to scale the FETCH_SIZE / WRITE_SIZE counters by)")
@@ -125,6 +184,9 @@ def main() -> int:
     if not torch.cuda.is_available():
         log("no GPU visible")
         return 1
+    if args.mode == "prefill":
+        print(json.dumps(prefill_bench(args, G, torch)), flush=True)
+        return 0
     threads = args.threads if args.threads > 0 else (os.cpu_count() or 1)
     if args.copy_probe > 0:
         src = torch.ones(args.copy_probe << 18, dtype=torch.float32, device="cuda")

@@ -11,13 +11,13 @@
 // block by block in order, exactly as the one-row kernels and the oracle do
 // -- so a prompt row computed here equals the same row computed alone.
 //
-// Tiling: a workgroup of four waves owns a 64 x 64 tile of y, a wave 32 x 32
-// (2 x 2 MFMA tiles).  K goes in chunks of eight blocks: each lane loads its
-// eight-byte fragments of the chunk straight from global memory (they are
-// contiguous 8-byte pieces of 32-byte blocks; a row of A and B is shared by
-// two waves, which L1 serves), and the chunk's fp16 scales are staged in LDS
-// as doubles.  The double epilogue (three fp64 operations an element and
-// block) bounds the kernel, not the MFMA.
+// Tiling: a workgroup of eight waves owns a 128 x 64 tile of y (rows x
+// outputs), a wave 32 x 32 (2 x 2 MFMA tiles).  K goes in chunks of eight
+// blocks (256 bytes).  A chunk of both operands and its fp16 scales (as
+// doubles) is staged in LDS with 16-byte loads (66 KB), so two workgroups
+// share a CU and one's loads overlap the other's arithmetic.  The double
+// epilogue (a conversion, a scale product and a fused multiply-add per element
+// and block) bounds the kernel, not the MFMA.
 //
 // MFMA operand layout (checked on gfx950): for A 16 x 32 and B given as
 // B[j][k] 16 x 32, lane l supplies A[l % 16][8 (l / 16) .. + 8) and
@@ -31,38 +31,59 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kGemmTile = 64;
-constexpr int kGemmThreads = 256;
-constexpr int kGemmChunk = 8; // blocks a chunk
+constexpr int kTileM = 128, kTileN = 64;
+constexpr int kGemmThreads = 512;
+constexpr int kChunk = 8;                       // blocks a chunk
+constexpr int kChunkBytes = kChunk * kBlock;    // 256
+constexpr int kRowBytes = kChunkBytes + 16;     // padded LDS row: conflict-free fragment reads
+constexpr int kStageRows = kTileM + kTileN;     // 192 operand rows a chunk
+constexpr int kStageVectors = kStageRows * kChunkBytes / 16 / kGemmThreads; // 6 a thread
+constexpr int kStageScales = kStageRows * kChunk;                           // 1536
 
-__global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(
+constexpr int kScalePieces = (kStageScales + kGemmThreads - 1) / kGemmThreads; // 3 a thread
+
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void q8_gemm_kernel(
     const uint8_t *__restrict__ x8, int64_t xElements, int xRow0, int rows,
     const uint8_t *__restrict__ w8, int inner, int outputs, float *__restrict__ y, int yStride,
     int residual)
 {
-    __shared__ double sScaleX[kGemmTile][kGemmChunk + 1];
-    __shared__ double sScaleW[kGemmTile][kGemmChunk + 1];
+    // rows [0, 128) of a buffer are A (activation rows), [128, 192) B (weight rows)
+    __shared__ __attribute__((aligned(16))) uint8_t sOps[1][kStageRows * kRowBytes];
+    __shared__ double sScales[1][kStageRows][kChunk + 1];
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int m0 = blockIdx.y * kGemmTile, n0 = blockIdx.x * kGemmTile;
+    const int m0 = blockIdx.y * kTileM, n0 = blockIdx.x * kTileN;
     const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
     const int nb = inner / kBlock;
     const uint16_t *xScales = reinterpret_cast<const uint16_t *>(x8 + xElements);
     const uint16_t *wScales = reinterpret_cast<const uint16_t *>(w8 + (int64_t) outputs * inner);
 
-    // this lane's fragment rows (clamped into range: the rows past the end
-    // are computed and never stored)
-    const int kg = (lane >> 4) * 8;
-    const uint8_t *aRow[2], *bRow[2];
+    // the global source of the staged pieces this thread moves: row r of the
+    // stage (clamped into range; rows past the end are computed, never stored)
+    // 32-bit byte offsets from the two operand bases: the first kStageVectors
+    // / 3 pieces of every thread are A rows (128 rows x 16 pieces = 2048 =
+    // 4 x 512), the rest B rows
+    const uint8_t *aBase = x8 + (int64_t) xRow0 * inner;
+    const uint16_t *aScales = xScales + (int64_t) xRow0 * nb;
+    uint32_t srcOff[kStageVectors];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int m = min(m0 + wm + i * 16 + (lane & 15), rows - 1);
-        const int n = min(n0 + wn + i * 16 + (lane & 15), outputs - 1);
-        aRow[i] = x8 + (int64_t) (xRow0 + m) * inner + kg;
-        bRow[i] = w8 + (int64_t) n * inner + kg;
+    for (int i = 0; i < kStageVectors; ++i) {
+        const int piece = t + i * kGemmThreads;     // 16-byte pieces, 16 a row
+        const int r = piece >> 4, col = (piece & 15) * 16;
+        srcOff[i] = r < kTileM ? (uint32_t) min(m0 + r, rows - 1) * (uint32_t) inner + col
+                               : (uint32_t) min(n0 + r - kTileM, outputs - 1) * (uint32_t) inner + col;
     }
-    // the scale rows this thread stages
-    const int stageRow = t / kGemmChunk, stageBlock = t % kGemmChunk; // 32 rows a pass
+    uint32_t scaleOff[kScalePieces];
+#pragma unroll
+    for (int i = 0; i < kScalePieces; ++i) {
+        const int e = t + i * kGemmThreads;
+        const int r = e / kChunk, b = e % kChunk;
+        scaleOff[i] = (r < kTileM ? (uint32_t) min(m0 + r, rows - 1)
+                                  : (uint32_t) min(n0 + r - kTileM, outputs - 1)) * (uint32_t) nb + b;
+    }
+    static_assert(kTileM * 16 == 4 * kGemmThreads && kStageVectors == 6, "piece split");
+    static_assert(kTileM * kChunk == 2 * kGemmThreads && kScalePieces == 3, "scale split");
     double acc[2][2][4];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -72,55 +93,68 @@ __global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(
             for (int r = 0; r < 4; ++r)
                 acc[i][j][r] = 0.0;
 
-    for (int c0 = 0; c0 < nb; c0 += kGemmChunk) {
-        const int nc = min(kGemmChunk, nb - c0);
-        // the chunk's fragments, all loads in flight (a block past the end
-        // re-reads the last one and is not used)
-        long af[kGemmChunk][2], bf[kGemmChunk][2];
+    // this lane's fragment offsets in a stage
+    const int kg = (lane >> 4) * 8;
+    int aOff[2], bOff[2];
 #pragma unroll
-        for (int kb = 0; kb < kGemmChunk; ++kb) {
-            const int64_t at = (int64_t) (c0 + min(kb, nc - 1)) * kBlock;
+    for (int i = 0; i < 2; ++i) {
+        aOff[i] = (wm + i * 16 + (lane & 15)) * kRowBytes + kg;
+        bOff[i] = (kTileM + wn + i * 16 + (lane & 15)) * kRowBytes + kg;
+    }
+
+    const int chunks = nb / kChunk;
+    for (int c = 0; c < chunks; ++c) {
+        __syncthreads(); // the previous chunk has been read
+        {
+            const int64_t c0 = (int64_t) c * kChunk;
+            int4 v[kStageVectors];
+            uint16_t sc[kScalePieces];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                af[kb][i] = *reinterpret_cast<const long *>(aRow[i] + at);
-                bf[kb][i] = *reinterpret_cast<const long *>(bRow[i] + at);
+            for (int i = 0; i < kStageVectors; ++i)
+                v[i] = *reinterpret_cast<const int4 *>((i < 4 ? aBase : w8) + srcOff[i] + c0 * kBlock);
+#pragma unroll
+            for (int i = 0; i < kScalePieces; ++i)
+                sc[i] = (i < 2 ? aScales : wScales)[scaleOff[i] + c0];
+#pragma unroll
+            for (int i = 0; i < kStageVectors; ++i) {
+                const int piece = t + i * kGemmThreads;
+                *reinterpret_cast<int4 *>(&sOps[0][(piece >> 4) * kRowBytes + (piece & 15) * 16]) = v[i];
+            }
+#pragma unroll
+            for (int i = 0; i < kScalePieces; ++i) {
+                const int e = t + i * kGemmThreads;
+                sScales[0][e / kChunk][e % kChunk] = (double) half_value(sc[i]);
             }
         }
-        // the chunk's scales as doubles
-        __syncthreads(); // the previous chunk's scales are read
-#pragma unroll
-        for (int pass = 0; pass < kGemmTile / (kGemmThreads / kGemmChunk); ++pass) {
-            const int r = stageRow + pass * (kGemmThreads / kGemmChunk);
-            const int b = c0 + min(stageBlock, nc - 1);
-            const int m = min(m0 + r, rows - 1), n = min(n0 + r, outputs - 1);
-            sScaleX[r][stageBlock] = (double) half_value(xScales[(int64_t) (xRow0 + m) * nb + b]);
-            sScaleW[r][stageBlock] = (double) half_value(wScales[(int64_t) n * nb + b]);
-        }
         __syncthreads();
+        const uint8_t *ops = sOps[0];
+#pragma unroll 1
+        for (int kb = 0; kb < kChunk; ++kb) {
+            long af[2], bf[2];
 #pragma unroll
-        for (int kb = 0; kb < kGemmChunk; ++kb) {
-            if (kb >= nc)
-                break;
-            double sw[2], sx[2][4];
+            for (int i = 0; i < 2; ++i) {
+                af[i] = *reinterpret_cast<const long *>(ops + aOff[i] + kb * kBlock);
+                bf[i] = *reinterpret_cast<const long *>(ops + bOff[i] + kb * kBlock);
+            }
+            double sw[2];
 #pragma unroll
             for (int j = 0; j < 2; ++j)
-                sw[j] = sScaleW[wn + j * 16 + (lane & 15)][kb];
+                sw[j] = sScales[0][kTileM + wn + j * 16 + (lane & 15)][kb];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < 2; ++i) {
+                double sx[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    sx[i][r] = sScaleX[wm + i * 16 + (lane >> 4) * 4 + r][kb];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
+                    sx[r] = sScales[0][wm + i * 16 + (lane >> 4) * 4 + r][kb];
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const v4i zero = {0, 0, 0, 0};
-                    const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[kb][i], bf[kb][j], zero,
-                                                                      0, 0, 0);
+                    const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[i], bf[j], zero, 0, 0, 0);
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        acc[i][j][r] += (double) d[r] * (sw[j] * sx[i][r]);
+                        acc[i][j][r] += (double) d[r] * (sw[j] * sx[r]);
                 }
+            }
         }
     }
 
@@ -143,13 +177,18 @@ __global__ __launch_bounds__(kGemmThreads) void q8_gemm_kernel(
 
 } // namespace
 
+bool q8_gemm_supported(int rows, int inner, int outputs)
+{
+    return rows >= kGemmMinRows && inner % kChunkBytes == 0 && outputs > 0;
+}
+
 hipError_t launch_q8_gemm(const uint8_t *x8, int64_t x_elements, int x_row0, int rows,
                           const uint8_t *w8, int inner, int outputs, float *y, int y_stride,
                           int residual, hipStream_t stream)
 {
-    if (rows <= 0 || outputs <= 0 || inner <= 0 || inner % kBlock != 0 || y_stride < outputs)
+    if (rows <= 0 || outputs <= 0 || inner <= 0 || inner % kChunkBytes != 0 || y_stride < outputs)
         return hipErrorInvalidValue;
-    const dim3 grid((outputs + kGemmTile - 1) / kGemmTile, (rows + kGemmTile - 1) / kGemmTile);
+    const dim3 grid((outputs + kTileN - 1) / kTileN, (rows + kTileM - 1) / kTileM);
     hipLaunchKernelGGL(q8_gemm_kernel, grid, dim3(kGemmThreads), 0, stream, x8, x_elements, x_row0,
                        rows, w8, inner, outputs, y, y_stride, residual);
     return hipGetLastError();

@@ -874,7 +874,7 @@ hipError_t launch_q8_product(const uint8_t *x8, int x_rows_total, int x_row0, in
     const int64_t xElements = (int64_t) x_rows_total * inner;
     if (rows == 1)
         return launch_matvec(x8, xElements, x_row0, w8, inner, outputs, y, residual, stream);
-    if (rows >= kGemmMinRows)
+    if (q8_gemm_supported(rows, inner, outputs))
         return launch_q8_gemm(x8, xElements, x_row0, rows, w8, inner, outputs, y, y_stride,
                               residual, stream);
     int b = 8;
@@ -921,6 +921,9 @@ hipError_t launch_mqa(const float *queries, int q_stride, const uint16_t *key_ca
         return hipErrorInvalidValue;
     if (q8 && (heads * head_dim) % kBlock != 0)
         return hipErrorInvalidValue;
+    if (rows >= kPrefillAttentionMinRows && prefill_attention_supported(head_dim))
+        return launch_prefill_attention(queries, q_stride, key_cache, value_cache, heads, kv_heads,
+                                        head_dim, rows, pos_ptr, pos_value, scale, out, q8, stream);
     double *wsO = reinterpret_cast<double *>(workspace);
     double *wsMl = wsO + (int64_t) rows * kMaxSplits * heads * head_dim;
     hipLaunchKernelGGL(mqa_partial_kernel, dim3(kMaxSplits, rows), dim3(kThreads), 0, stream,

@@ -47,8 +47,10 @@ hipError_t launch_kv_store(const float *k, const float *v, int src_stride, int r
                            const int *pos_ptr, int pos_value, hipStream_t stream);
 
 // x8: Q8 row buffer of x_rows_total rows; rows [x_row0, x_row0 + rows) are used.
-// Steps of kGemmMinRows rows or more run on the int8 MFMA GEMM (gq8_gemm.hip).
+// Steps of kGemmMinRows rows or more whose inner size is a whole number of
+// 256-byte chunks run on the int8 MFMA GEMM (gq8_gemm.hip).
 constexpr int kGemmMinRows = 32;
+bool q8_gemm_supported(int rows, int inner, int outputs);
 hipError_t launch_q8_gemm(const uint8_t *x8, int64_t x_elements, int x_row0, int rows,
                           const uint8_t *w8, int inner, int outputs, float *y, int y_stride,
                           int residual, hipStream_t stream);
@@ -61,6 +63,16 @@ constexpr int kMaxHeads = 16;
 constexpr int kMaxHeadDim = 256;
 
 size_t mqa_workspace_bytes(int rows, int heads, int head_dim, int max_keys);
+
+// Blocks of kPrefillAttentionMinRows rows or more with a head width of 64, 128
+// or 256 take the fp64-MFMA prefill kernel (gq8_prefill_attention.hip); no
+// workspace.
+constexpr int kPrefillAttentionMinRows = 16;
+bool prefill_attention_supported(int head_dim);
+hipError_t launch_prefill_attention(const float *queries, int q_stride, const uint16_t *key_cache,
+                                    const uint16_t *value_cache, int heads, int kv_heads,
+                                    int head_dim, int rows, const int *pos_ptr, int pos_value,
+                                    float scale, float *out, uint8_t *q8, hipStream_t stream);
 
 // Rows of queries (row stride q_stride) at positions base + r where
 // base = (*pos_ptr if pos_ptr) + pos_value; row r attends keys [0, base + r].

@@ -207,12 +207,13 @@ def test_q8_product_rows_and_residual(torch_cuda, rows):
 
 @pytest.mark.parametrize("rows,inner,outputs", [(32, 2048, 2560), (64, 2048, 2048),
                                                  (100, 16384, 2048), (130, 64, 96),
-                                                 (33, 2048, 32768)])
+                                                 (33, 2048, 32768), (300, 512, 200)])
 def test_q8_gemm_rows_are_the_one_row_products(torch_cuda, rows, inner, outputs):
-    """Steps of 32 rows or more run on the int8 MFMA GEMM; each row is the
-    exact block dot scaled and summed in double in block order, as the oracle
-    does, so the rows are bit-identical to the one-row products.  Shapes cover
-    whole and partial 64 x 64 tiles and K chunks."""
+    """Steps of 32 rows or more run on the int8 MFMA GEMM (an inner size of
+    64 takes the row kernel); each row is the exact block dot scaled and
+    summed in double in block order, as the oracle does, so the rows are
+    bit-identical to the one-row products.  Shapes cover whole and partial
+    128 x 64 tiles and one to 64 K chunks."""
     torch = torch_cuda
     w = O.quantize_int8_blocks(spread(inner * outputs, 81, 0.02))
     x = spread(rows * inner, 82, 1.0)
@@ -308,6 +309,37 @@ def test_mqa_prefill_equals_rows_of_decodes(torch_cuda):
         ref = O.mqa_row_f16(q[r * heads * hd:(r + 1) * heads * hd], kc, vc, heads, kvh, hd,
                             offset + r + 1, 0.0625)
         assert worst_error(got[r], ref) <= 2e-6
+
+
+@pytest.mark.parametrize("rows,offset,hd", [(32, 0, 256), (45, 100, 256), (16, 7, 128),
+                                            (20, 0, 64)])
+def test_prefill_attention_blocks(torch_cuda, rows, offset, hd):
+    """Blocks of 16+ rows take the fp64-MFMA prefill kernel: every row equals
+    a decode over its own keys (MultiQueryAttentionTests.cpp:217-256), and keys
+    past the block's last position (poisoned here) are never read."""
+    torch = torch_cuda
+    heads, kvh = 8, 2 if hd == 64 else 1
+    total = offset + rows
+    q = spread(rows * heads * hd, 61 + rows, 1.0)
+    kc, vc = _cache(total + 8, kvh * hd, 62), _cache(total + 8, kvh * hd, 63)
+    kw = kvh * hd
+    kp, vp = kc.copy().reshape(total + 8, kw), vc.copy().reshape(total + 8, kw)
+    kp[total:] = np.float16(3e4).view(np.uint16)
+    vp[total:] = np.float16(-3e4).view(np.uint16)
+    ws_bytes = G.mqa_workspace_bytes(rows, heads, hd, total)
+    ws = empty(torch, ws_bytes, torch.uint8)
+    out = empty(torch, rows * heads * hd, torch.float32)
+    G.mqa_prefill(dev(q), dev(kp), dev(vp), heads, kvh, hd, rows, offset, 1.0 / math.sqrt(hd),
+                  out.data_ptr(), ws.data_ptr(), ws_bytes)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(rows, heads * hd)
+    exact = []
+    for r in range(rows):
+        ref = O.mqa_row_f16(q[r * heads * hd:(r + 1) * heads * hd], kc, vc, heads, kvh, hd,
+                            offset + r + 1, 1.0 / math.sqrt(hd))
+        assert worst_error(got[r], ref) <= 2e-6, f"row {r}"
+        exact.append(exact_fraction(got[r], ref))
+    print(f"prefill attention rows={rows} hd={hd}: bit-identical {np.mean(exact):.4f}")
 
 
 def test_mqa_causal_never_reads_later_keys(torch_cuda):
