@@ -854,6 +854,730 @@ __global__ __launch_bounds__(64) void head_finalize_kernel(HeadArgs a)
     }
 }
 
+// ============================================================================
+// The dataflow decode step (one launch a token)
+// ============================================================================
+// Item order = dependency order: per layer the q|k|v items, the attention
+// (split, head group) items, the o, gate|up and down items; then the final
+// norm, the lm_head items and the finalize item.  Workgroups start in id order
+// on each XCD, so an item only ever waits on items that started before it:
+// the earliest unfinished item has nothing left to wait for, and every wait
+// ends.  A wait is a bounded spin; giving up sets the error word, which every
+// other wait checks, so a failure ends the launch instead of hanging it.
+//
+// Data that crosses items (hidden, q, the fp16 K/V row of the step, the Q8
+// rows, attention partials) is written and read with agent-scope accesses,
+// which the eight XCD L2s keep coherent; a workgroup waits for its stores to
+// complete before it counts itself done.  Weights are read-only and cached.
+constexpr int kFlowWaves = kFlowThreads / 64;
+constexpr int kFlowSpinLimit = 1 << 20;
+constexpr int kFlowQkvPairs = kFlowWaves * kPairsPerWave;   // 16 pairs (32 rows) an item
+constexpr int kFlowORows = kFlowWaves * 2;                  // 16 rows an item
+constexpr int kFlowDownRows = kFlowWaves;                   // 8 rows an item
+constexpr int kFlowDownBlocks = 8;                          // blocks a lane (inner <= 16384)
+constexpr int kFlowHeadRows = kFlowWaves * kHeadRows;       // 64 rows an item
+
+enum { kPhaseQkv = 0, kPhaseAttention, kPhaseO, kPhaseGateUp, kPhaseDown };
+
+__device__ inline float ld_agent_f(const float *p)
+{
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint32_t ld_agent_u(const uint32_t *p)
+{
+    return __hip_atomic_load(const_cast<uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint64_t ld_agent_u64(const uint64_t *p)
+{
+    return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline int ld_agent_i(const int *p)
+{
+    return __hip_atomic_load(const_cast<int *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void st_agent_f(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void st_agent_u(uint32_t *p, uint32_t v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void st_agent_i(int *p, int v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ inline int *flow_counter(const FlowArgs &a, int index)
+{
+    return a.counters + index * kFlowCounterStride;
+}
+
+// Waits until counter `index` reaches `target`; false after giving up.
+__device__ __forceinline__ bool flow_wait(const FlowArgs &a, int index, int target)
+{
+    __shared__ int sOk;
+    if (threadIdx.x == 0) {
+        int ok = 1, spins = 0;
+        const int *counter = flow_counter(a, index);
+        while (ld_agent_i(counter) < target) {
+            if (ld_agent_i(a.error) != 0 || ++spins > kFlowSpinLimit) {
+                __hip_atomic_fetch_or(a.error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ok = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        sOk = ok;
+    }
+    __syncthreads();
+    return sOk != 0;
+}
+
+// Every thread's stores have completed; then the workgroup counts itself.
+__device__ __forceinline__ void flow_signal(const FlowArgs &a, int index)
+{
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(flow_counter(a, index), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Four consecutive elements of the residual row (agent loads) or, on the
+// first layer, of the embedding row of sequence[position] (thread 0's item
+// 0 also publishes it as the residual row), with their norm weights.
+__device__ __forceinline__ RowSlice<4> flow_row_slice(const FlowArgs &a, const float *weight, bool embedding,
+                                      bool publish, int position)
+{
+    RowSlice<4> r;
+    const int t = threadIdx.x;
+    r.active = t * 4 < a.width;
+    const int i0 = r.active ? t * 4 : 0;
+    load4<4>(weight + i0, r.w);
+    if (embedding) {
+        uint32_t id = a.sequence[position];
+        if (id >= (uint32_t) a.vocab) // ids are validated on the host; a guard, not a rule
+            id = 0;
+        const int64_t e0 = (int64_t) id * a.width + i0;
+        const int64_t V = a.vocab;
+        const uint16_t bits = reinterpret_cast<const uint16_t *>(a.embedding + V * a.width)[e0 / kBlock];
+        const float sc = half_value(bits);
+        const int packed = *reinterpret_cast<const int *>(a.embedding + e0);
+        int8_t b[4];
+        __builtin_memcpy(b, &packed, 4);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            r.v[k] = (float) ((double) a.embed_scale * (double) (sc * (float) b[k]));
+        if (publish && r.active)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                st_agent_f(a.hidden + i0 + k, r.v[k]);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            r.v[k] = ld_agent_f(a.hidden + i0 + k);
+    }
+    return r;
+}
+
+// The activation block `block` of a Q8 row in the word layout (bytes, then
+// one scale word a block), read with agent loads.
+__device__ inline void flow_act_block(const uint32_t *q8, int inner, int block, int4 &a0, int4 &a1,
+                                      double &sa)
+{
+    const uint32_t *w = q8 + block * (kBlock / 4);
+    a0 = make_int4((int) ld_agent_u(w), (int) ld_agent_u(w + 1), (int) ld_agent_u(w + 2),
+                   (int) ld_agent_u(w + 3));
+    a1 = make_int4((int) ld_agent_u(w + 4), (int) ld_agent_u(w + 5), (int) ld_agent_u(w + 6),
+                   (int) ld_agent_u(w + 7));
+    sa = (double) half_value((uint16_t) ld_agent_u(q8 + inner / 4 + block));
+}
+
+// Packs the byte of each of four consecutive lanes into the first lane's
+// word and stores it (agent); lanes 32 k store the block's scale word.
+__device__ inline void flow_store_q8(uint32_t *q8, int inner, int idx, uint8_t byte, uint16_t bits,
+                                     bool live)
+{
+    const uint32_t b = byte;
+    const uint32_t w = b | ((uint32_t) __shfl_down((int) b, 1) << 8)
+                       | ((uint32_t) __shfl_down((int) b, 2) << 16)
+                       | ((uint32_t) __shfl_down((int) b, 3) << 24);
+    if (live && (idx & 3) == 0)
+        st_agent_u(q8 + idx / 4, w);
+    if (live && (idx & 31) == 0)
+        st_agent_u(q8 + inner / 4 + idx / kBlock, bits);
+}
+
+__device__ __forceinline__ void flow_qkv(const FlowArgs &a, int l, int item)
+{
+    __shared__ RowQ8 row;
+    __shared__ double sPartial[kFlowWaves];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int hd = a.head_dim, half = hd / 2;
+    const int qWidth = a.heads * hd, kvWidth = a.kv_heads * hd;
+    const int outputs = qWidth + 2 * kvWidth;
+    const int pairs = (a.heads + 2 * a.kv_heads) * half;
+    const int nb = a.width / kBlock;
+    const int firstPair = (item * kFlowWaves + wave) * kPairsPerWave;
+    const uint8_t *weights = a.qkv + a.qkv_stride * l;
+
+    WeightBlock lo[kPairsPerWave], hi[kPairsPerWave];
+#pragma unroll
+    for (int p = 0; p < kPairsPerWave; ++p) {
+        const int pair = firstPair + p;
+        const int rowLo = (pair / half) * hd + pair % half;
+        const bool valid = pair < pairs && lane < nb;
+        lo[p] = load_block(weights, outputs, a.width, rowLo, lane, valid);
+        hi[p] = load_block(weights, outputs, a.width, rowLo + half, lane, valid);
+    }
+    const int position = *a.position;
+    __builtin_amdgcn_sched_barrier(0);
+    if (l > 0 && !flow_wait(a, (l - 1) * kFlowPhases + kPhaseDown, a.down_items))
+        return;
+    const RowSlice<4> slice = flow_row_slice(a, a.input_norm + a.norm_stride * l, l == 0,
+                                             l == 0 && item == 0,
+                                             position);
+    norm_q8_finish<4>(slice, a.width, a.epsilon, row, sPartial, nullptr, nullptr);
+
+    int4 a0 = make_int4(0, 0, 0, 0), a1 = a0;
+    double sa = 0.0;
+    if (lane < nb) {
+        a0 = reinterpret_cast<const int4 *>(row.q + lane * kBlock)[0];
+        a1 = reinterpret_cast<const int4 *>(row.q + lane * kBlock)[1];
+        sa = row.scale[lane];
+    }
+    constexpr int kRows = 2 * kPairsPerWave;
+    double y[kRows];
+#pragma unroll
+    for (int p = 0; p < kPairsPerWave; ++p) {
+        y[2 * p] = block_term(lo[p], a0, a1, sa);
+        y[2 * p + 1] = block_term(hi[p], a0, a1, sa);
+    }
+    const double total = reduce_rows<kRows>(y, lane);
+    double rowTotal[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r)
+        rowTotal[r] = __shfl(total, lane_of_row<kRows>(r));
+    // lane 0: the wave's two pairs are the consecutive elements (i, i + 1) and
+    // (i + half, i + half + 1) of one head: two-element stores
+    if (lane == 0 && firstPair < pairs) {
+        const int head = firstPair / half, i = firstPair % half;
+        const int rLo = head * hd + i;
+        const bool second = firstPair + 1 < pairs;
+        float fLo[2] = {(float) rowTotal[0], (float) rowTotal[2]};
+        float fHi[2] = {(float) rowTotal[1], (float) rowTotal[3]};
+        if (rLo < qWidth + kvWidth) { // q and k heads rotate
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const int64_t angle = (int64_t) position * half + i + p;
+                float outLo, outHi;
+                rotate_pair(fLo[p], fHi[p], a.cosines[angle], a.sines[angle], &outLo, &outHi);
+                fLo[p] = outLo;
+                fHi[p] = outHi;
+            }
+        }
+        if (rLo < qWidth) {
+            st_agent_f(a.query + rLo, fLo[0]);
+            st_agent_f(a.query + rLo + half, fHi[0]);
+            if (second) {
+                st_agent_f(a.query + rLo + 1, fLo[1]);
+                st_agent_f(a.query + rLo + half + 1, fHi[1]);
+            }
+        } else {
+            const bool isKey = rLo < qWidth + kvWidth;
+            uint16_t *cache = (isKey ? a.key_cache : a.value_cache)
+                              + ((int64_t) l * a.max_positions + position) * kvWidth;
+            const int c = rLo - qWidth - (isKey ? 0 : kvWidth);
+            const uint32_t wordLo = (uint32_t) half_bits(fLo[0]) | ((uint32_t) half_bits(fLo[1]) << 16);
+            const uint32_t wordHi = (uint32_t) half_bits(fHi[0]) | ((uint32_t) half_bits(fHi[1]) << 16);
+            st_agent_u(reinterpret_cast<uint32_t *>(cache + c), wordLo);
+            st_agent_u(reinterpret_cast<uint32_t *>(cache + c + half), wordHi);
+        }
+    }
+    flow_signal(a, l * kFlowPhases + kPhaseQkv);
+}
+
+// Attention plan of the flow kernel: whole 64-key rounds a split, at most
+// `maxSplits` splits.
+__device__ inline SplitPlan flow_plan(int keyCount, int maxSplits)
+{
+    const int roundsPerSplit = (keyCount + kRoundKeys * maxSplits - 1) / (kRoundKeys * maxSplits);
+    const int perSplit = roundsPerSplit * kRoundKeys;
+    return {(keyCount + perSplit - 1) / perSplit, perSplit};
+}
+
+template <int C>
+__device__ inline void load_halves_agent(const uint16_t *p, uint16_t (&h)[C])
+{
+    if constexpr (C == 4) {
+        const uint64_t v = ld_agent_u64(reinterpret_cast<const uint64_t *>(p));
+        h[0] = (uint16_t) (v & 0xFFFFu); h[1] = (uint16_t) ((v >> 16) & 0xFFFFu);
+        h[2] = (uint16_t) ((v >> 32) & 0xFFFFu); h[3] = (uint16_t) (v >> 48);
+    } else if constexpr (C == 2) {
+        const uint32_t v = ld_agent_u(reinterpret_cast<const uint32_t *>(p));
+        h[0] = (uint16_t) (v & 0xFFFFu); h[1] = (uint16_t) (v >> 16);
+    } else {
+        // one half: the aligned word holding it
+        const uintptr_t at = reinterpret_cast<uintptr_t>(p);
+        const uint32_t v = ld_agent_u(reinterpret_cast<const uint32_t *>(at & ~(uintptr_t) 3));
+        h[0] = (uint16_t) ((at & 2) ? v >> 16 : v & 0xFFFFu);
+    }
+}
+
+template <int C, int G>
+__device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int item)
+{
+    constexpr int kRows = kScoreBatch * G;
+    __shared__ double sScore[G][kMaxSplitKeys];
+    __shared__ double sAcc[kAttnWaves][kMaxGroupWidth];
+    __shared__ double sMax[G], sSum[G];
+    __shared__ double sSplitMax[G][kDecodeSplits], sSplitSum[G][kDecodeSplits];
+    __shared__ int sLast;
+
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int hd = a.head_dim, kvWidth = a.kv_heads * hd;
+    const int heads = a.heads, qWidth = heads * hd;
+    const int perKv = heads / a.kv_heads;
+    const int group = item / a.attn_splits, split = item % a.attn_splits;
+    const int h0 = group * G;
+    const int groupWidth = G * hd;
+
+    const int keyCount = *a.position + 1;
+    const SplitPlan plan = flow_plan(keyCount, a.attn_splits);
+    if (split >= plan.splits) {
+        // no work at this length; counted so that the finalize item (which
+        // advances the position) knows every item has read the position
+        __syncthreads();
+        if (t == 0)
+            __hip_atomic_fetch_add(flow_counter(a, a.layers * kFlowPhases + 2), 1, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    if (!flow_wait(a, l * kFlowPhases + kPhaseQkv, a.qkv_items))
+        return;
+
+    const bool active = lane * C < hd;
+    const int c0 = active ? lane * C : 0;
+    const uint32_t keep = active ? 0xFFFFFFFFu : 0u;
+    double q[G][C];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int i = 0; i < C; ++i)
+            q[g][i] = (double) __uint_as_float(
+                __float_as_uint(ld_agent_f(a.query + (h0 + g) * hd + c0 + i)) & keep);
+
+    const int k0 = split * plan.perSplit;
+    const int n = min(plan.perSplit, keyCount - k0);
+    const int64_t layerBase = (int64_t) l * a.max_positions * kvWidth;
+    const uint16_t *keys = a.key_cache + layerBase + (int64_t) k0 * kvWidth;
+    const uint16_t *values = a.value_cache + layerBase + (int64_t) k0 * kvWidth;
+    int kvOffset[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+        kvOffset[g] = ((h0 + g) / perKv) * hd + c0;
+
+    uint16_t kh[kScoreBatch][G][C], vh[kScoreBatch][G][C];
+    auto load_round = [&](const uint16_t *base, int r0, uint16_t (&dst)[kScoreBatch][G][C]) {
+#pragma unroll
+        for (int b = 0; b < kScoreBatch; ++b) {
+            const int j = min(r0 + wave + b * kAttnWaves, n - 1);
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+                load_halves_agent<C>(base + (int64_t) j * kvWidth + kvOffset[g], dst[b][g]);
+        }
+    };
+    load_round(keys, 0, kh);
+    load_round(values, 0, vh);
+
+    for (int r0 = 0; r0 < n; r0 += kRoundKeys) {
+        if (r0 > 0)
+            load_round(keys, r0, kh);
+        double y[kRows];
+#pragma unroll
+        for (int b = 0; b < kScoreBatch; ++b)
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                double p = 0.0;
+#pragma unroll
+                for (int i = 0; i < C; ++i)
+                    p += q[g][i] * (double) half_value(kh[b][g][i]);
+                y[b * G + g] = p;
+            }
+        const double total = reduce_rows<kRows>(y, lane);
+        if (stores_row<kRows>(lane)) {
+            const int r = row_of_lane<kRows>(lane);
+            const int j = r0 + wave + (r / G) * kAttnWaves;
+            if (j < n)
+                sScore[r % G][j] = (double) a.attn_scale * total;
+        }
+    }
+    __syncthreads();
+    if (wave < G) {
+        double largest = -INFINITY;
+        for (int j = lane; j < n; j += 64)
+            largest = fmax(largest, sScore[wave][j]);
+        largest = wave_max_d(largest);
+        double sum = 0.0;
+        for (int j = lane; j < n; j += 64) {
+            const double w = exp(sScore[wave][j] - largest);
+            sScore[wave][j] = w;
+            sum += w;
+        }
+        sum = wave_sum_d(sum);
+        if (lane == 0) {
+            sMax[wave] = largest;
+            sSum[wave] = sum;
+        }
+    }
+    __syncthreads();
+    double acc[G][C];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int i = 0; i < C; ++i)
+            acc[g][i] = 0.0;
+    for (int r0 = 0; r0 < n; r0 += kRoundKeys) {
+        if (r0 > 0)
+            load_round(values, r0, vh);
+#pragma unroll
+        for (int b = 0; b < kScoreBatch; ++b) {
+            const int j = r0 + wave + b * kAttnWaves;
+            if (j >= n)
+                break;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const double w = sScore[g][j];
+#pragma unroll
+                for (int i = 0; i < C; ++i)
+                    acc[g][i] += w * (double) half_value(vh[b][g][i]);
+            }
+        }
+    }
+    if (active)
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int i = 0; i < C; ++i)
+                sAcc[wave][g * hd + c0 + i] = acc[g][i];
+    __syncthreads();
+    if (t < groupWidth) {
+        double o = 0.0;
+        for (int w = 0; w < kAttnWaves; ++w)
+            o += sAcc[w][t];
+        store_agent(a.ws_o + (int64_t) split * qWidth + h0 * hd + t, o);
+    }
+    if (t < G) {
+        store_agent(a.ws_ml + (split * heads + h0 + t) * 2, sMax[t]);
+        store_agent(a.ws_ml + (split * heads + h0 + t) * 2 + 1, sSum[t]);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t == 0)
+        sLast = __hip_atomic_fetch_add(a.tickets + group, 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT) == plan.splits - 1;
+    __syncthreads();
+    if (!sLast)
+        return;
+
+    const int splits = plan.splits;
+    if (t < G * splits) {
+        const int g = t / splits, sp = t % splits;
+        sSplitMax[g][sp] = load_agent(a.ws_ml + (sp * heads + h0 + g) * 2);
+        sSplitSum[g][sp] = load_agent(a.ws_ml + (sp * heads + h0 + g) * 2 + 1);
+    }
+    __syncthreads();
+    if (t < G) {
+        double largest = -INFINITY;
+        for (int sp = 0; sp < splits; ++sp)
+            largest = fmax(largest, sSplitMax[t][sp]);
+        sMax[t] = largest;
+    }
+    __syncthreads();
+    if (t < G * splits) {
+        const int g = t / splits, sp = t % splits;
+        sSplitMax[g][sp] = exp(sSplitMax[g][sp] - sMax[g]);
+    }
+    __syncthreads();
+    if (t < G) {
+        double total = 0.0;
+        for (int sp = 0; sp < splits; ++sp)
+            total += sSplitSum[t][sp] * sSplitMax[t][sp];
+        sSum[t] = total;
+    }
+    __syncthreads();
+    const bool live = t < groupWidth;
+    const int g = min(t / hd, G - 1);
+    double weighted = 0.0;
+    for (int s0 = 0; s0 < splits; s0 += kMergeBatch) {
+        double part[kMergeBatch];
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u)
+            part[u] = (s0 + u < splits && live)
+                          ? load_agent(a.ws_o + (int64_t) (s0 + u) * qWidth + h0 * hd + t) : 0.0;
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u)
+            if (s0 + u < splits)
+                weighted += part[u] * sSplitMax[g][s0 + u];
+    }
+    const int idx = h0 * hd + t;
+    const float v = live ? (float) (weighted / sSum[g]) : 0.f;
+    float amax = fabsf(v);
+    for (int mask = 16; mask >= 1; mask >>= 1)
+        amax = fmaxf(amax, __shfl_xor(amax, mask));
+    const uint16_t bits = scale_bits_from_amax(amax);
+    const float sc = half_value(bits);
+    const uint8_t byte = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);
+    flow_store_q8(a.attn_q8, qWidth, idx, byte, bits, live);
+    if (t == 0)
+        __hip_atomic_store(a.tickets + group, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    flow_signal(a, l * kFlowPhases + kPhaseAttention);
+}
+
+__device__ __forceinline__ void flow_o(const FlowArgs &a, int l, int item)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int W = a.width, qWidth = a.heads * a.head_dim, nb = qWidth / kBlock;
+    const int r0 = item * kFlowORows + wave * 2;
+    const bool valid = lane < nb;
+    WeightBlock w[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+        w[k] = load_block(a.out + a.out_stride * l, W, qWidth, r0 + k, lane, valid && r0 + k < W);
+    __builtin_amdgcn_sched_barrier(0);
+    if (!flow_wait(a, l * kFlowPhases + kPhaseAttention, a.heads / (a.head_dim >= 32 ? 1 : 32 / a.head_dim)))
+        return;
+    int4 a0, a1;
+    double sa;
+    flow_act_block(a.attn_q8, qWidth, valid ? lane : 0, a0, a1, sa);
+    double y[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+        y[k] = block_term(w[k], a0, a1, sa);
+    const double total = reduce_rows<2>(y, lane);
+    const int row = r0 + row_of_lane<2>(lane);
+    if (stores_row<2>(lane) && row < W) {
+        const double old = (double) ld_agent_f(a.hidden + row);
+        st_agent_f(a.hidden + row, (float) (total + old));
+    }
+    flow_signal(a, l * kFlowPhases + kPhaseO);
+}
+
+__device__ __forceinline__ void flow_gateup(const FlowArgs &a, int l, int item)
+{
+    __shared__ RowQ8 row;
+    __shared__ double sPartial[kFlowWaves];
+    __shared__ float sGate[kBlock], sUp[kBlock];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nb = a.width / kBlock;
+    const int F = a.intermediate;
+    const int o0 = item * kBlock + wave * kGluPerWave;
+    const bool valid = lane < nb;
+    const uint8_t *weights = a.gate_up + a.gate_up_stride * l;
+    WeightBlock w[2 * kGluPerWave];
+#pragma unroll
+    for (int k = 0; k < kGluPerWave; ++k) {
+        w[k] = load_block(weights, 2 * (int64_t) F, a.width, o0 + k, lane, valid);
+        w[kGluPerWave + k] = load_block(weights, 2 * (int64_t) F, a.width, (int64_t) F + o0 + k,
+                                        lane, valid);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (!flow_wait(a, l * kFlowPhases + kPhaseO, a.o_items))
+        return;
+    const RowSlice<4> slice = flow_row_slice(a, a.post_norm + a.norm_stride * l, false, false, 0);
+    norm_q8_finish<4>(slice, a.width, a.epsilon, row, sPartial, nullptr, nullptr);
+    int4 a0 = make_int4(0, 0, 0, 0), a1 = a0;
+    double sa = 0.0;
+    if (valid) {
+        a0 = reinterpret_cast<const int4 *>(row.q + lane * kBlock)[0];
+        a1 = reinterpret_cast<const int4 *>(row.q + lane * kBlock)[1];
+        sa = row.scale[lane];
+    }
+    double y[2 * kGluPerWave];
+#pragma unroll
+    for (int k = 0; k < 2 * kGluPerWave; ++k)
+        y[k] = block_term(w[k], a0, a1, sa);
+    const double total = reduce_rows<2 * kGluPerWave>(y, lane);
+    if (stores_row<2 * kGluPerWave>(lane)) {
+        const int r = row_of_lane<2 * kGluPerWave>(lane);
+        const int o = wave * kGluPerWave + (r % kGluPerWave);
+        if (r < kGluPerWave)
+            sGate[o] = (float) total;
+        else
+            sUp[o] = (float) total;
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) { // the first wave: lanes 0..31 hold the block's 32 outputs
+        const bool live = threadIdx.x < kBlock;
+        const int o = item * kBlock + (live ? threadIdx.x : 0);
+        const float v = live ? geglu(sGate[threadIdx.x & 31], sUp[threadIdx.x & 31]) : 0.f;
+        float amax = fabsf(v);
+        for (int mask = 16; mask >= 1; mask >>= 1)
+            amax = fmaxf(amax, __shfl_xor(amax, mask));
+        const uint16_t bits = scale_bits_from_amax(amax);
+        const float sc = half_value(bits);
+        const uint8_t byte = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);
+        flow_store_q8(a.act_q8, F, o, byte, bits, live);
+    }
+    flow_signal(a, l * kFlowPhases + kPhaseGateUp);
+}
+
+__device__ __forceinline__ void flow_down(const FlowArgs &a, int l, int item)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int W = a.width, F = a.intermediate, nb = F / kBlock;
+    const int row = item * kFlowDownRows + wave;
+    WeightBlock w[kFlowDownBlocks];
+#pragma unroll
+    for (int j = 0; j < kFlowDownBlocks; ++j) {
+        const int b = lane + 64 * j;
+        w[j] = load_block(a.down + a.down_stride * l, W, F, row, b, row < W && b < nb);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (!flow_wait(a, l * kFlowPhases + kPhaseGateUp, a.gate_up_items))
+        return;
+    double acc = 0.0;
+#pragma unroll
+    for (int j = 0; j < kFlowDownBlocks; ++j) {
+        const int b = lane + 64 * j;
+        int4 a0, a1;
+        double sa;
+        flow_act_block(a.act_q8, F, b < nb ? b : 0, a0, a1, sa);
+        acc += block_term(w[j], a0, a1, sa);
+    }
+    const double total = wave_sum_d(acc);
+    if (lane == 0 && row < W) {
+        const double old = (double) ld_agent_f(a.hidden + row);
+        st_agent_f(a.hidden + row, (float) (total + old));
+    }
+    flow_signal(a, l * kFlowPhases + kPhaseDown);
+}
+
+__device__ __forceinline__ void flow_final_norm(const FlowArgs &a)
+{
+    __shared__ RowQ8 row;
+    __shared__ double sPartial[kFlowWaves];
+    if (!flow_wait(a, (a.layers - 1) * kFlowPhases + kPhaseDown, a.down_items))
+        return;
+    const RowSlice<4> slice = flow_row_slice(a, a.final_norm, false, false, 0);
+    norm_q8_finish<4>(slice, a.width, a.epsilon, row, sPartial, a.normalised, nullptr);
+    const int t = threadIdx.x;
+    if (t * 4 < a.width) {
+        uint32_t word;
+        __builtin_memcpy(&word, row.q + t * 4, 4);
+        st_agent_u(a.head_q8 + t, word);
+    }
+    if (t < a.width / kBlock)
+        st_agent_u(a.head_q8 + a.width / 4 + t, half_bits((float) row.scale[t]));
+    flow_signal(a, a.layers * kFlowPhases);
+}
+
+__device__ __forceinline__ void flow_lmhead(const FlowArgs &a, int item)
+{
+    __shared__ unsigned long long sBest[kFlowWaves];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nb = a.width / kBlock;
+    const bool valid = lane < nb;
+    const int64_t V = a.vocab;
+    const int64_t r0 = ((int64_t) item * kFlowWaves + wave) * kHeadRows;
+    WeightBlock w[kHeadRows];
+#pragma unroll
+    for (int k = 0; k < kHeadRows; ++k)
+        w[k] = load_block(a.embedding, V, a.width, r0 + k, lane, valid && r0 + k < V);
+    __builtin_amdgcn_sched_barrier(0);
+    if (!flow_wait(a, a.layers * kFlowPhases, 1))
+        return;
+    int4 a0, a1;
+    double sa;
+    flow_act_block(a.head_q8, a.width, valid ? lane : 0, a0, a1, sa);
+    double y[kHeadRows];
+#pragma unroll
+    for (int k = 0; k < kHeadRows; ++k)
+        y[k] = block_term(w[k], a0, a1, sa);
+    const double total = reduce_rows<kHeadRows>(y, lane);
+    const int64_t rowIndex = r0 + row_of_lane<kHeadRows>(lane);
+    unsigned long long best = 0;
+    if (stores_row<kHeadRows>(lane) && rowIndex < V) {
+        const float logit = (float) total;
+        a.logits[rowIndex] = logit;
+        best = candidate_key(logit, (uint32_t) rowIndex);
+    }
+    best = fold_wave_max(best);
+    if (lane == 0)
+        sBest[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long c = sBest[0];
+        for (int k = 1; k < kFlowWaves; ++k)
+            c = sBest[k] > c ? sBest[k] : c;
+        if (c != 0)
+            atomicMax(a.best + (item % kHeadSlots) * kHeadSlotStride, c);
+    }
+    flow_signal(a, a.layers * kFlowPhases + 1);
+}
+
+__device__ __forceinline__ void flow_finalize(const FlowArgs &a)
+{
+    // every other item has read the position: the lm_head items (whose wait
+    // chains back through every working item) and the idle attention splits
+    const int position = *a.position;
+    const int groups = a.attn_items / a.attn_splits;
+    const int idle = a.layers * groups * (a.attn_splits - flow_plan(position + 1, a.attn_splits).splits);
+    if (!flow_wait(a, a.layers * kFlowPhases + 1, a.head_items)
+        || !flow_wait(a, a.layers * kFlowPhases + 2, idle))
+        return;
+    const int t = threadIdx.x;
+    if (t < 64) {
+        unsigned long long *slot = a.best + t * kHeadSlotStride;
+        const unsigned long long c =
+            fold_wave_max(t < kHeadSlots ? (unsigned long long) ld_agent_u64(reinterpret_cast<uint64_t *>(slot)) : 0ull);
+        if (t < kHeadSlots)
+            __hip_atomic_store(reinterpret_cast<uint64_t *>(slot), (uint64_t) 0, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        if (t == 0) {
+            const uint32_t token = c == 0 ? 0u : 0xFFFFFFFFu - (uint32_t) (c & 0xFFFFFFFFull);
+            if (a.sample)
+                a.sequence[position + 1] = token;
+            *a.position = position + 1;
+        }
+    }
+    // every item has passed its wait: the counters start the next step at zero
+    const int counters = a.layers * kFlowPhases + kFlowExtraCounters;
+    for (int i = t; i < counters; i += kFlowThreads)
+        st_agent_i(flow_counter(a, i), 0);
+}
+
+template <int C, int G>
+__global__ __launch_bounds__(kFlowThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void flow_step_kernel(FlowArgs a)
+{
+    const int perLayer = a.qkv_items + a.attn_items + a.o_items + a.gate_up_items + a.down_items;
+    int item = blockIdx.x;
+    if (item < a.layers * perLayer) {
+        const int l = item / perLayer;
+        item -= l * perLayer;
+        if (item < a.qkv_items)
+            return flow_qkv(a, l, item);
+        item -= a.qkv_items;
+        if (item < a.attn_items)
+            return flow_attention<C, G>(a, l, item);
+        item -= a.attn_items;
+        if (item < a.o_items)
+            return flow_o(a, l, item);
+        item -= a.o_items;
+        if (item < a.gate_up_items)
+            return flow_gateup(a, l, item);
+        item -= a.gate_up_items;
+        return flow_down(a, l, item);
+    }
+    item -= a.layers * perLayer;
+    if (item == 0)
+        return flow_final_norm(a);
+    if (item <= a.head_items)
+        return flow_lmhead(a, item - 1);
+    flow_finalize(a);
+}
+
 } // namespace
 
 // ============================================================================
@@ -875,13 +1599,66 @@ static bool attention_layout(int head_dim, int *channels, int *group)
     return false;
 }
 
+bool flow_decode_supported(int width, int heads, int kv_heads, int head_dim, int intermediate,
+                           int max_positions)
+{
+    const int qWidth = heads * head_dim;
+    int channels = 0, group = 0;
+    return fused_decode_supported(width, heads, kv_heads, head_dim, intermediate, max_positions)
+           && attention_layout(head_dim, &channels, &group) && width % 4 == 0
+           && width <= kFlowThreads * 4 && qWidth <= 64 * kBlock && width <= 64 * kBlock
+           && intermediate <= 64 * kBlock * kFlowDownBlocks && intermediate % kBlock == 0
+           && (head_dim / 2) % 2 == 0
+           && flow_attention_splits(max_positions) * kMaxSplitKeys >= max_positions;
+}
+
+int flow_attention_splits(int max_positions)
+{
+    // enough splits that a split never takes more than kMaxSplitKeys keys
+    const int needed = (max_positions + kMaxSplitKeys - 1) / kMaxSplitKeys;
+    return needed < 16 ? 16 : (needed > kDecodeSplits ? kDecodeSplits : needed);
+}
+
+int flow_items(FlowArgs &a)
+{
+    int channels = 0, group = 1;
+    attention_layout(a.head_dim, &channels, &group);
+    const int pairs = (a.heads + 2 * a.kv_heads) * (a.head_dim / 2);
+    a.qkv_items = (pairs + kFlowQkvPairs - 1) / kFlowQkvPairs;
+    a.attn_items = a.attn_splits * (a.heads / group);
+    a.o_items = (a.width + kFlowORows - 1) / kFlowORows;
+    a.gate_up_items = a.intermediate / kBlock;
+    a.down_items = (a.width + kFlowDownRows - 1) / kFlowDownRows;
+    a.head_items = (int) ((a.vocab + kFlowHeadRows - 1) / kFlowHeadRows);
+    const int perLayer = a.qkv_items + a.attn_items + a.o_items + a.gate_up_items + a.down_items;
+    return a.layers * perLayer + 1 + a.head_items + 1;
+}
+
+hipError_t launch_flow_step(const FlowArgs &a, hipStream_t stream)
+{
+    int channels = 0, group = 0;
+    if (!attention_layout(a.head_dim, &channels, &group))
+        return hipErrorInvalidValue;
+    FlowArgs b = a;
+    const int grid = flow_items(b);
+    if (channels == 4)
+        hipLaunchKernelGGL((flow_step_kernel<4, 1>), dim3(grid), dim3(kFlowThreads), 0, stream, b);
+    else if (channels == 2)
+        hipLaunchKernelGGL((flow_step_kernel<2, 1>), dim3(grid), dim3(kFlowThreads), 0, stream, b);
+    else if (group == 1)
+        hipLaunchKernelGGL((flow_step_kernel<1, 1>), dim3(grid), dim3(kFlowThreads), 0, stream, b);
+    else
+        hipLaunchKernelGGL((flow_step_kernel<1, 2>), dim3(grid), dim3(kFlowThreads), 0, stream, b);
+    return hipGetLastError();
+}
+
 bool fused_decode_supported(int width, int heads, int kv_heads, int head_dim, int intermediate,
                             int max_positions)
 {
     const int qWidth = heads * head_dim, kvWidth = kv_heads * head_dim;
     int channels = 0, group = 0;
     return attention_layout(head_dim, &channels, &group) && heads % group == 0
-           && group <= kAttnWaves && group * head_dim <= kMaxGroupWidth
+           && heads / group <= kDecodeCounters && group <= kAttnWaves && group * head_dim <= kMaxGroupWidth
            && width % kBlock == 0 && width <= kFusedMaxWidth && qWidth % kBlock == 0
            && heads % kv_heads == 0 && kvWidth % 8 == 0
            && max_positions <= kDecodeSplits * kMaxSplitKeys && intermediate % kBlock == 0

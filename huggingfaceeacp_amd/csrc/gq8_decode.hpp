@@ -76,6 +76,57 @@ struct HeadArgs {
     int advance;              // nonzero: *position += 1 after the argmax
 };
 
+// ---- the dataflow decode step: one launch a token --------------------------------
+// Every piece of work of a one-token step (the q|k|v rows, the attention
+// splits, the o, gate|up and down rows of every layer, the final norm, the
+// lm_head rows and the id) is one workgroup, in dependency order; a workgroup
+// issues its weight loads, then waits (a bounded spin) until the phase it
+// reads from has finished, computes and publishes its outputs with
+// agent-scope (cross-L2 coherent) stores before counting itself done.
+constexpr int kFlowThreads = 512;
+constexpr int kFlowPhases = 5;        // per layer: qkv, attention, o, gate|up, down
+constexpr int kFlowCounterStride = 32; // ints between counters (128 bytes)
+constexpr int kFlowExtraCounters = 3;  // after the layers: final norm, lm_head, idle attention splits
+
+struct FlowArgs {
+    int layers, width, heads, kv_heads, head_dim, intermediate, vocab, max_positions;
+    float epsilon, embed_scale, attn_scale;
+    const uint8_t *embedding;                 // Int8Blocks [vocab, width], also the lm_head
+    // layer l of a kind at base + l * stride (bytes for the Int8Blocks
+    // tensors, floats for the norms): addresses the compiler knows are global
+    const uint8_t *qkv, *out, *gate_up, *down; // fused q|k|v, o, fused gate|up, down
+    int64_t qkv_stride, out_stride, gate_up_stride, down_stride;
+    const float *input_norm, *post_norm;
+    int64_t norm_stride;
+    const float *final_norm;
+    uint16_t *key_cache, *value_cache;        // [layers][max_positions][kv_heads * head_dim]
+    const float *cosines, *sines;
+    uint32_t *sequence;
+    int *position;
+    float *hidden;                            // the residual row
+    float *query;                             // the rotated q row
+    uint32_t *attn_q8;                        // Q8 of the attention row: bytes, then one word a block
+    uint32_t *act_q8;                         // Q8 of the GeGLU row: the same layout
+    uint32_t *head_q8;                        // Q8 of the final-norm row: the same layout
+    float *normalised;                        // the final-norm row
+    float *logits;
+    double *ws_o, *ws_ml;                     // attention partials (kDecodeSplits splits)
+    int *tickets;                             // attention head-group tickets
+    unsigned long long *best;                 // argmax slots
+    int *counters;                            // kFlowPhases * layers + 2 counters, strided
+    int *error;                               // nonzero after a wait gave up
+    int attn_splits;                          // attention split items a head group
+    int sample;                               // nonzero: the id goes to sequence[position + 1]
+    int qkv_items, attn_items, o_items, gate_up_items, down_items, head_items;
+};
+
+bool flow_decode_supported(int width, int heads, int kv_heads, int head_dim, int intermediate,
+                           int max_positions);
+int flow_attention_splits(int max_positions);
+// Fills the item counts of a; returns the grid size.
+int flow_items(FlowArgs &a);
+hipError_t launch_flow_step(const FlowArgs &a, hipStream_t stream);
+
 bool fused_decode_supported(int width, int heads, int kv_heads, int head_dim, int intermediate,
                             int max_positions);
 size_t decode_workspace_bytes(int heads, int head_dim);

@@ -393,8 +393,10 @@ struct gq8_decoder {
     hipStream_t stream = nullptr;
 
     uint8_t *embedding = nullptr;
-    std::vector<uint8_t *> qkv, out, gateUp, down;
+    std::vector<uint8_t *> qkv, out, gateUp, down; // layer l at the kind's base + l * stride
     std::vector<float *> inputNorm, postNorm;
+    int64_t qkvStride = 0, outStride = 0, gateUpStride = 0, downStride = 0; // bytes
+    int64_t normStride = 0;                                                 // floats
     float *finalNorm = nullptr;
     std::vector<char> present;
 
@@ -421,6 +423,12 @@ struct gq8_decoder {
     // the fused one-token path
     bool useFused = true;
     bool fusedSupported = false;
+    // the dataflow step (one launch a token)
+    bool useFlow = false;
+    bool flowSupported = false;
+    uint32_t *flowAttnQ8 = nullptr, *flowActQ8 = nullptr, *flowHeadQ8 = nullptr;
+    int *flowCounters = nullptr;
+    int *flowError = nullptr;
     double *decodeO = nullptr, *decodeMl = nullptr;
     int *counters = nullptr; // attention head-group tickets
     unsigned long long *headBest = nullptr; // the lm_head argmax slots
@@ -633,13 +641,29 @@ extern "C" int gq8_decoder_create(const gq8_shape *shape, gq8_decoder **out)
     d->down.resize(L);
     d->inputNorm.resize(L);
     d->postNorm.resize(L);
+    // one allocation a tensor kind, the layers at a fixed 256-byte-aligned
+    // stride (the step kernel addresses a layer as base + l * stride)
+    auto stride_of = [](int64_t bytes) { return (bytes + 255) / 256 * 256; };
+    d->qkvStride = stride_of(gq8_int8_blocks_byte_count((int64_t) d->qkvWidth * W));
+    d->outStride = stride_of(gq8_int8_blocks_byte_count((int64_t) W * d->qWidth));
+    d->gateUpStride = stride_of(gq8_int8_blocks_byte_count(2 * (int64_t) s.intermediate * W));
+    d->downStride = stride_of(gq8_int8_blocks_byte_count((int64_t) W * s.intermediate));
+    d->normStride = stride_of((int64_t) W * sizeof(float)) / (int64_t) sizeof(float);
+    uint8_t *qkvBase = nullptr, *outBase = nullptr, *gateUpBase = nullptr, *downBase = nullptr;
+    float *inputNormBase = nullptr, *postNormBase = nullptr;
+    GQ8_ALLOC(qkvBase, d->qkvStride * L);
+    GQ8_ALLOC(outBase, d->outStride * L);
+    GQ8_ALLOC(gateUpBase, d->gateUpStride * L);
+    GQ8_ALLOC(downBase, d->downStride * L);
+    GQ8_ALLOC(inputNormBase, d->normStride * L * sizeof(float));
+    GQ8_ALLOC(postNormBase, d->normStride * L * sizeof(float));
     for (int l = 0; l < L; ++l) {
-        GQ8_ALLOC(d->qkv[l], gq8_int8_blocks_byte_count((int64_t) d->qkvWidth * W));
-        GQ8_ALLOC(d->out[l], gq8_int8_blocks_byte_count(W * d->qWidth));
-        GQ8_ALLOC(d->gateUp[l], gq8_int8_blocks_byte_count(2 * (int64_t) s.intermediate * W));
-        GQ8_ALLOC(d->down[l], gq8_int8_blocks_byte_count(W * s.intermediate));
-        GQ8_ALLOC(d->inputNorm[l], W * sizeof(float));
-        GQ8_ALLOC(d->postNorm[l], W * sizeof(float));
+        d->qkv[l] = qkvBase + d->qkvStride * l;
+        d->out[l] = outBase + d->outStride * l;
+        d->gateUp[l] = gateUpBase + d->gateUpStride * l;
+        d->down[l] = downBase + d->downStride * l;
+        d->inputNorm[l] = inputNormBase + d->normStride * l;
+        d->postNorm[l] = postNormBase + d->normStride * l;
     }
     GQ8_ALLOC(d->finalNorm, W * sizeof(float));
     d->present.assign(gq8_tensor_count(&s), 0);
@@ -679,6 +703,21 @@ extern "C" int gq8_decoder_create(const gq8_shape *shape, gq8_decoder **out)
     GQ8_ALLOC(d->debugNormalised, R * W * sizeof(float));
     GQ8_ALLOC(d->debugAttended, R * d->qWidth * sizeof(float));
     GQ8_ALLOC(d->debugActivated, R * (int64_t) s.intermediate * sizeof(float));
+    d->flowSupported = gq8::flow_decode_supported(s.width, s.heads, s.kv_heads, s.head_dim,
+                                                  s.intermediate, s.max_positions);
+    {
+        const int64_t words = [](int64_t n) { return n / 4 + n / gq8::kBlock; }(d->maxInner);
+        GQ8_ALLOC(d->flowAttnQ8, words * sizeof(uint32_t));
+        GQ8_ALLOC(d->flowActQ8, words * sizeof(uint32_t));
+        GQ8_ALLOC(d->flowHeadQ8, words * sizeof(uint32_t));
+        GQ8_ALLOC(d->flowCounters, (size_t) (gq8::kFlowPhases * L + gq8::kFlowExtraCounters) * gq8::kFlowCounterStride
+                                       * sizeof(int));
+        GQ8_ALLOC(d->flowError, 64 * sizeof(int));
+        if (hipMemset(d->flowCounters, 0, (size_t) (gq8::kFlowPhases * L + gq8::kFlowExtraCounters)
+                                              * gq8::kFlowCounterStride * sizeof(int)) != hipSuccess
+            || hipMemset(d->flowError, 0, sizeof(int)) != hipSuccess)
+            return cleanup(fail(GQ8_ERR_DEVICE, "flow counters: memset failed"));
+    }
     d->fusedSupported = gq8::fused_decode_supported(s.width, s.heads, s.kv_heads, s.head_dim,
                                                     s.intermediate, s.max_positions);
     {
@@ -913,6 +952,20 @@ extern "C" int gq8_decoder_position(const gq8_decoder *d)
     return d ? d->hostPosition : -1;
 }
 
+extern "C" int gq8_decoder_set_flow(gq8_decoder *d, int enabled)
+{
+    if (!d)
+        return fail(GQ8_ERR_ARGUMENT, "null decoder");
+    if (enabled && !d->flowSupported)
+        return fail(GQ8_ERR_SHAPE, "decoder_set_flow: the shape has no dataflow step");
+    d->useFlow = enabled != 0;
+    if (d->graph) { // a captured step follows the path it was captured with
+        (void) hipGraphExecDestroy(d->graph);
+        d->graph = nullptr;
+    }
+    return GQ8_OK;
+}
+
 extern "C" int gq8_decoder_set_fused(gq8_decoder *d, int enabled)
 {
     if (!d)
@@ -1010,6 +1063,80 @@ struct StageTimer {
         StageTimer timer_(d, stage);              \
         GQ8_LAUNCH(expr);                         \
     } while (0)
+
+// The one-token step as one dataflow launch (gq8_decode.hip).
+int encode_flow_token(gq8_decoder *d, float *logits, bool sample)
+{
+    const gq8_shape &s = d->shape;
+    gq8::FlowArgs a{};
+    a.layers = s.layers;
+    a.width = s.width;
+    a.heads = s.heads;
+    a.kv_heads = s.kv_heads;
+    a.head_dim = s.head_dim;
+    a.intermediate = s.intermediate;
+    a.vocab = s.vocab;
+    a.max_positions = s.max_positions;
+    a.epsilon = s.rms_epsilon;
+    a.embed_scale = s.embedding_scale;
+    a.attn_scale = 1.f / std::sqrt((float) s.head_dim);
+    a.embedding = d->embedding;
+    a.qkv = d->qkv[0];
+    a.qkv_stride = d->qkvStride;
+    a.out = d->out[0];
+    a.out_stride = d->outStride;
+    a.gate_up = d->gateUp[0];
+    a.gate_up_stride = d->gateUpStride;
+    a.down = d->down[0];
+    a.down_stride = d->downStride;
+    a.input_norm = d->inputNorm[0];
+    a.post_norm = d->postNorm[0];
+    a.norm_stride = d->normStride;
+    a.final_norm = d->finalNorm;
+    a.key_cache = d->keyCache;
+    a.value_cache = d->valueCache;
+    a.cosines = d->cosines;
+    a.sines = d->sines;
+    a.sequence = d->sequence;
+    a.position = d->position;
+    a.hidden = d->hidden;
+    a.query = d->qkvRows;
+    a.attn_q8 = d->flowAttnQ8;
+    a.act_q8 = d->flowActQ8;
+    a.head_q8 = d->flowHeadQ8;
+    a.normalised = d->normalisedRows;
+    a.logits = logits;
+    a.ws_o = d->decodeO;
+    a.ws_ml = d->decodeMl;
+    a.tickets = d->counters;
+    a.best = d->headBest;
+    a.counters = d->flowCounters;
+    a.error = d->flowError;
+    a.attn_splits = gq8::flow_attention_splits(s.max_positions);
+    a.sample = sample ? 1 : 0;
+    GQ8_STAGE(kStageLogits, gq8::launch_flow_step(a, d->stream));
+    return GQ8_OK;
+}
+
+// Reads and clears the dataflow step's error word; a set word means a step
+// gave up waiting, so the counters are reset as well.
+int check_flow_error(gq8_decoder *d)
+{
+    if (!d->flowSupported)
+        return GQ8_OK;
+    int error = 0;
+    GQ8_HIP(hipStreamSynchronize(d->stream));
+    GQ8_HIP(hipMemcpy(&error, d->flowError, sizeof(int), hipMemcpyDeviceToHost));
+    if (error == 0)
+        return GQ8_OK;
+    const int L = d->shape.layers;
+    GQ8_HIP(hipMemset(d->flowCounters, 0, (size_t) (gq8::kFlowPhases * L + gq8::kFlowExtraCounters)
+                                              * gq8::kFlowCounterStride * sizeof(int)));
+    GQ8_HIP(hipMemset(d->flowError, 0, sizeof(int)));
+    GQ8_HIP(hipMemset(d->counters, 0, gq8::kDecodeCounters * sizeof(int)));
+    GQ8_HIP(hipMemset(d->headBest, 0, gq8::kHeadSlots * gq8::kHeadSlotStride * sizeof(unsigned long long)));
+    return fail(GQ8_ERR_DEVICE, "dataflow step: a wait gave up (the step's results are invalid)");
+}
 
 // The one-token step through the fused kernels (gq8_decode.hip): five
 // launches a layer and one for the head, which also chooses the next id and
@@ -1132,6 +1259,9 @@ int encode_step(gq8_decoder *d, int rows, float *logits, int logitsRows, bool sa
     hipStream_t st = d->stream;
     const float attentionScale = 1.f / std::sqrt((float) s.head_dim);
     const bool dbg = d->debug;
+    if (rows == 1 && logits && logitsRows == 1 && d->useFlow && d->flowSupported
+        && !(d->debug && !d->capturing))
+        return encode_flow_token(d, logits, sample);
     if (rows == 1 && logits && logitsRows == 1 && d->useFused && d->fusedSupported)
         return encode_fused_token(d, logits, sample);
 
@@ -1232,6 +1362,9 @@ extern "C" int gq8_decoder_step(gq8_decoder *d, const uint32_t *tokens, int n, f
     if (int s = encode_step(d, n, logits, logits ? logits_rows : 0, false))
         return s;
     GQ8_HIP(hipStreamSynchronize(d->stream));
+    if (d->useFlow)
+        if (int s = check_flow_error(d))
+            return s;
     d->hostPosition += n;
     return GQ8_OK;
 }
@@ -1380,6 +1513,9 @@ extern "C" int gq8_generate(gq8_decoder *d, const int32_t *prompt, int prompt_le
             ++steps;
         }
         GQ8_HIP(hipStreamSynchronize(d->stream));
+        if (d->useFlow)
+            if (int st = check_flow_error(d))
+                return st;
         std::vector<uint32_t> ids(limit);
         GQ8_HIP(hipMemcpy(ids.data(), d->sequence + prompt_length, limit * sizeof(uint32_t),
                           hipMemcpyDeviceToHost));
@@ -1435,6 +1571,9 @@ extern "C" int gq8_generate(gq8_decoder *d, const int32_t *prompt, int prompt_le
             }
         }
         finish(GQ8_OK);
+        if (d->useFlow)
+            if (int st = check_flow_error(d))
+                return st;
     }
     local.decode_seconds = std::chrono::duration<double>(Clock::now() - decodeStart).count();
     local.step_count = steps;
@@ -1457,6 +1596,8 @@ extern "C" int gq8_decoder_decode(gq8_decoder *d, int steps, int use_graph)
         if (int st = decode_one(d, use_graph != 0))
             return st;
     GQ8_HIP(hipStreamSynchronize(d->stream));
+    if (d->useFlow)
+        return check_flow_error(d);
     return GQ8_OK;
 }
 

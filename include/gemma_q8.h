@@ -207,6 +207,13 @@ int gq8_decoder_step(gq8_decoder *decoder, const uint32_t *tokens, int n, float 
  * when the shape allows; 0 selects the unfused kernels (both compute the same
  * arithmetic).  On by default. */
 int gq8_decoder_set_fused(gq8_decoder *decoder, int enabled);
+/* One-token steps as one dataflow launch (every phase of every layer a set of
+ * workgroups that wait on the phase they read from) when the shape allows;
+ * the same arithmetic as the fused kernels.  Off by default.  A step that
+ * gave up waiting is reported by the next synchronous call as GQ8_ERR_DEVICE.
+ * No reference counterpart: it replaces the per-kernel dispatch of
+ * Decoder::step (Decoder.cpp:644-706) for one-token steps. */
+int gq8_decoder_set_flow(gq8_decoder *decoder, int enabled);
 /* Decoder::hiddenStates (Decoder.h:119-121): the last step's rows after the
  * final norm, [rows, width] fp32, copied to the host. */
 int gq8_decoder_hidden(gq8_decoder *decoder, float *host_out, int rows);
