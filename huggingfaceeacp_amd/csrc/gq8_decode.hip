@@ -865,10 +865,18 @@ __global__ __launch_bounds__(64) void head_finalize_kernel(HeadArgs a)
 // ends.  A wait is a bounded spin; giving up sets the error word, which every
 // other wait checks, so a failure ends the launch instead of hanging it.
 //
+// A phase counts its items on a tree (sub-counters of 16 arrivals, then a top
+// count): arrivals on one address serialize at about 15 ns each, so 512 items
+// on one counter would take 7 us.  The item that completes the tree raises 16
+// flags, and waiters poll the flag of their id modulo 16.
+//
 // Data that crosses items (hidden, q, the fp16 K/V row of the step, the Q8
 // rows, attention partials) is written and read with agent-scope accesses,
-// which the eight XCD L2s keep coherent; a workgroup waits for its stores to
-// complete before it counts itself done.  Weights are read-only and cached.
+// which the eight XCD L2s keep coherent (rows of it in 16-byte agent-coherent
+// buffer loads, staged through LDS when all waves need them); a workgroup
+// waits for its stores to complete before it counts itself done.  Weights and
+// the K/V rows of earlier steps were written before the launch: plain cached
+// loads, issued before the wait.
 constexpr int kFlowWaves = kFlowThreads / 64;
 constexpr int kFlowSpinLimit = 1 << 20;
 constexpr int kFlowQkvPairs = kFlowWaves * kPairsPerWave;   // 16 pairs (32 rows) an item
@@ -876,6 +884,8 @@ constexpr int kFlowORows = kFlowWaves * 2;                  // 16 rows an item
 constexpr int kFlowDownRows = kFlowWaves;                   // 8 rows an item
 constexpr int kFlowDownBlocks = 8;                          // blocks a lane (inner <= 16384)
 constexpr int kFlowHeadRows = kFlowWaves * kHeadRows;       // 64 rows an item
+constexpr int kFlowMaxInner = 64 * kBlock * kFlowDownBlocks;  // 16384
+constexpr int kFlowActWords = kFlowMaxInner / 4 + kFlowMaxInner / kBlock + 4; // a staged Q8 row
 
 enum { kPhaseQkv = 0, kPhaseAttention, kPhaseO, kPhaseGateUp, kPhaseDown };
 
@@ -908,25 +918,36 @@ __device__ inline void st_agent_i(int *p, int v)
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ inline int *flow_counter(const FlowArgs &a, int index)
+// 16 bytes at byte `offset` of a `bytes`-long buffer, with an agent-coherent
+// (sc1) buffer load; bytes past the end read as zero.
+constexpr int kCoherentLoad = 16; // the sc1 cache-policy bit of a buffer load
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+__device__ inline v4u ld_agent_16(const void *base, uint32_t offset, uint32_t bytes)
 {
-    return a.counters + index * kFlowCounterStride;
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int) bytes, 0x00020000);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int) offset, 0, kCoherentLoad);
 }
 
-// Waits until counter `index` reaches `target`; false after giving up.
-__device__ __forceinline__ bool flow_wait(const FlowArgs &a, int index, int target)
+__device__ inline int *flow_line(const FlowArgs &a, int counter, int line)
+{
+    return a.counters + ((int64_t) counter * kFlowCounterLines + line) * kFlowLineInts;
+}
+
+// Waits until counter `counter` has completed; false after giving up.
+__device__ __forceinline__ bool flow_wait(const FlowArgs &a, int counter)
 {
     __shared__ int sOk;
     if (threadIdx.x == 0) {
         int ok = 1, spins = 0;
-        const int *counter = flow_counter(a, index);
-        while (ld_agent_i(counter) < target) {
-            if (ld_agent_i(a.error) != 0 || ++spins > kFlowSpinLimit) {
+        const int *flag = flow_line(a, counter, 1 + (int) (blockIdx.x % kFlowFlagLines));
+        while (ld_agent_i(flag) == 0) {
+            if ((++spins & 63) == 0 && (ld_agent_i(a.error) != 0 || spins > kFlowSpinLimit)) {
                 __hip_atomic_fetch_or(a.error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 ok = 0;
                 break;
             }
-            __builtin_amdgcn_s_sleep(2);
+            __builtin_amdgcn_s_sleep(1);
         }
         sOk = ok;
     }
@@ -934,13 +955,53 @@ __device__ __forceinline__ bool flow_wait(const FlowArgs &a, int index, int targ
     return sOk != 0;
 }
 
-// Every thread's stores have completed; then the workgroup counts itself.
-__device__ __forceinline__ void flow_signal(const FlowArgs &a, int index)
+// One arrival on sub-counter `sub` (complete at `inSub` arrivals) of a counter
+// complete when `subs` sub-counters are; the arrival that completes it raises
+// the flags.  Completed lines go back to zero for the next launch.
+__device__ inline void flow_arrive(const FlowArgs &a, int counter, int sub, int inSub, int subs)
+{
+    int *subLine = flow_line(a, counter, 1 + kFlowFlagLines + sub);
+    if (__hip_atomic_fetch_add(subLine, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != inSub - 1)
+        return;
+    st_agent_i(subLine, 0);
+    int *top = flow_line(a, counter, 0);
+    if (__hip_atomic_fetch_add(top, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != subs - 1)
+        return;
+    st_agent_i(top, 0);
+    for (int k = 0; k < kFlowFlagLines; ++k)
+        st_agent_i(flow_line(a, counter, 1 + k), 1);
+}
+
+// Every thread's stores have completed; then item `index` of `count` arrives.
+__device__ __forceinline__ void flow_signal(const FlowArgs &a, int counter, int index, int count)
 {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (threadIdx.x == 0)
-        __hip_atomic_fetch_add(flow_counter(a, index), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) {
+        const int sub = index / kFlowFanIn;
+        flow_arrive(a, counter, sub, min(kFlowFanIn, count - sub * kFlowFanIn),
+                    (count + kFlowFanIn - 1) / kFlowFanIn);
+    }
+}
+
+// Copies a Q8 row in the word layout (inner / 4 words of bytes, then one
+// scale word a block) into LDS with 16-byte coherent loads.
+__device__ inline void flow_stage_q8(const uint32_t *q8, int inner, uint32_t *sAct)
+{
+    const int words = inner / 4 + inner / kBlock;
+    for (int p = threadIdx.x; p * 4 < words; p += kFlowThreads)
+        reinterpret_cast<v4u *>(sAct)[p] = ld_agent_16(q8, (uint32_t) p * 16, (uint32_t) words * 4);
+    __syncthreads();
+}
+
+// The activation block `block` of a Q8 row staged in LDS.
+__device__ inline void lds_act_block(const uint32_t *sAct, int inner, int block, int4 &a0, int4 &a1,
+                                     double &sa)
+{
+    const int4 *w = reinterpret_cast<const int4 *>(sAct + block * (kBlock / 4));
+    a0 = w[0];
+    a1 = w[1];
+    sa = (double) half_value((uint16_t) sAct[inner / 4 + block]);
 }
 
 // Four consecutive elements of the residual row (agent loads) or, on the
@@ -973,24 +1034,12 @@ __device__ __forceinline__ RowSlice<4> flow_row_slice(const FlowArgs &a, const f
             for (int k = 0; k < 4; ++k)
                 st_agent_f(a.hidden + i0 + k, r.v[k]);
     } else {
+        const v4u h = ld_agent_16(a.hidden, (uint32_t) i0 * 4, (uint32_t) a.width * 4);
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-            r.v[k] = ld_agent_f(a.hidden + i0 + k);
+            r.v[k] = __uint_as_float(h[k]);
     }
     return r;
-}
-
-// The activation block `block` of a Q8 row in the word layout (bytes, then
-// one scale word a block), read with agent loads.
-__device__ inline void flow_act_block(const uint32_t *q8, int inner, int block, int4 &a0, int4 &a1,
-                                      double &sa)
-{
-    const uint32_t *w = q8 + block * (kBlock / 4);
-    a0 = make_int4((int) ld_agent_u(w), (int) ld_agent_u(w + 1), (int) ld_agent_u(w + 2),
-                   (int) ld_agent_u(w + 3));
-    a1 = make_int4((int) ld_agent_u(w + 4), (int) ld_agent_u(w + 5), (int) ld_agent_u(w + 6),
-                   (int) ld_agent_u(w + 7));
-    sa = (double) half_value((uint16_t) ld_agent_u(q8 + inner / 4 + block));
 }
 
 // Packs the byte of each of four consecutive lanes into the first lane's
@@ -1032,7 +1081,7 @@ __device__ __forceinline__ void flow_qkv(const FlowArgs &a, int l, int item)
     }
     const int position = *a.position;
     __builtin_amdgcn_sched_barrier(0);
-    if (l > 0 && !flow_wait(a, (l - 1) * kFlowPhases + kPhaseDown, a.down_items))
+    if (l > 0 && !flow_wait(a, (l - 1) * kFlowPhases + kPhaseDown))
         return;
     const RowSlice<4> slice = flow_row_slice(a, a.input_norm + a.norm_stride * l, l == 0,
                                              l == 0 && item == 0,
@@ -1094,7 +1143,7 @@ __device__ __forceinline__ void flow_qkv(const FlowArgs &a, int l, int item)
             st_agent_u(reinterpret_cast<uint32_t *>(cache + c + half), wordHi);
         }
     }
-    flow_signal(a, l * kFlowPhases + kPhaseQkv);
+    flow_signal(a, l * kFlowPhases + kPhaseQkv, item, a.qkv_items);
 }
 
 // Attention plan of the flow kernel: whole 64-key rounds a split, at most
@@ -1144,31 +1193,22 @@ __device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int ite
 
     const int keyCount = *a.position + 1;
     const SplitPlan plan = flow_plan(keyCount, a.attn_splits);
+    const int groups = a.attn_items / a.attn_splits;
     if (split >= plan.splits) {
         // no work at this length; counted so that the finalize item (which
         // advances the position) knows every item has read the position
-        __syncthreads();
         if (t == 0)
-            __hip_atomic_fetch_add(flow_counter(a, a.layers * kFlowPhases + 2), 1, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+            flow_arrive(a, a.layers * kFlowPhases + 2, l * groups + group, a.attn_splits - plan.splits,
+                        a.layers * groups);
         return;
     }
-    if (!flow_wait(a, l * kFlowPhases + kPhaseQkv, a.qkv_items))
-        return;
 
     const bool active = lane * C < hd;
     const int c0 = active ? lane * C : 0;
     const uint32_t keep = active ? 0xFFFFFFFFu : 0u;
-    double q[G][C];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int i = 0; i < C; ++i)
-            q[g][i] = (double) __uint_as_float(
-                __float_as_uint(ld_agent_f(a.query + (h0 + g) * hd + c0 + i)) & keep);
-
     const int k0 = split * plan.perSplit;
     const int n = min(plan.perSplit, keyCount - k0);
+    const int newest = keyCount - 1 - k0; // this step's own row (not in this split when >= n)
     const int64_t layerBase = (int64_t) l * a.max_positions * kvWidth;
     const uint16_t *keys = a.key_cache + layerBase + (int64_t) k0 * kvWidth;
     const uint16_t *values = a.value_cache + layerBase + (int64_t) k0 * kvWidth;
@@ -1177,22 +1217,50 @@ __device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int ite
     for (int g = 0; g < G; ++g)
         kvOffset[g] = ((h0 + g) / perKv) * hd + c0;
 
+    // rows of earlier steps: plain loads, before the wait; this step's row (a
+    // wave-uniform case): a coherent load once the q|k|v items are done
     uint16_t kh[kScoreBatch][G][C], vh[kScoreBatch][G][C];
-    auto load_round = [&](const uint16_t *base, int r0, uint16_t (&dst)[kScoreBatch][G][C]) {
+    auto load_round = [&](const uint16_t *base, int r0, uint16_t (&dst)[kScoreBatch][G][C], bool waited) {
 #pragma unroll
         for (int b = 0; b < kScoreBatch; ++b) {
             const int j = min(r0 + wave + b * kAttnWaves, n - 1);
+            if (j != newest) {
 #pragma unroll
-            for (int g = 0; g < G; ++g)
-                load_halves_agent<C>(base + (int64_t) j * kvWidth + kvOffset[g], dst[b][g]);
+                for (int g = 0; g < G; ++g)
+                    load_halves<C>(base + (int64_t) j * kvWidth + kvOffset[g], dst[b][g]);
+            } else if (waited) {
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+                    load_halves_agent<C>(base + (int64_t) j * kvWidth + kvOffset[g], dst[b][g]);
+            }
         }
     };
-    load_round(keys, 0, kh);
-    load_round(values, 0, vh);
+    load_round(keys, 0, kh, false);
+    load_round(values, 0, vh, false);
+    if (!flow_wait(a, l * kFlowPhases + kPhaseQkv))
+        return;
+#pragma unroll
+    for (int b = 0; b < kScoreBatch; ++b) {
+        const int j = min(wave + b * kAttnWaves, n - 1);
+        if (j == newest) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                load_halves_agent<C>(keys + (int64_t) j * kvWidth + kvOffset[g], kh[b][g]);
+                load_halves_agent<C>(values + (int64_t) j * kvWidth + kvOffset[g], vh[b][g]);
+            }
+        }
+    }
+    double q[G][C];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int i = 0; i < C; ++i)
+            q[g][i] = (double) __uint_as_float(
+                __float_as_uint(ld_agent_f(a.query + (h0 + g) * hd + c0 + i)) & keep);
 
     for (int r0 = 0; r0 < n; r0 += kRoundKeys) {
         if (r0 > 0)
-            load_round(keys, r0, kh);
+            load_round(keys, r0, kh, true);
         double y[kRows];
 #pragma unroll
         for (int b = 0; b < kScoreBatch; ++b)
@@ -1239,7 +1307,7 @@ __device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int ite
             acc[g][i] = 0.0;
     for (int r0 = 0; r0 < n; r0 += kRoundKeys) {
         if (r0 > 0)
-            load_round(values, r0, vh);
+            load_round(values, r0, vh, true);
 #pragma unroll
         for (int b = 0; b < kScoreBatch; ++b) {
             const int j = r0 + wave + b * kAttnWaves;
@@ -1331,10 +1399,10 @@ __device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int ite
     flow_store_q8(a.attn_q8, qWidth, idx, byte, bits, live);
     if (t == 0)
         __hip_atomic_store(a.tickets + group, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    flow_signal(a, l * kFlowPhases + kPhaseAttention);
+    flow_signal(a, l * kFlowPhases + kPhaseAttention, group, groups);
 }
 
-__device__ __forceinline__ void flow_o(const FlowArgs &a, int l, int item)
+__device__ __forceinline__ void flow_o(const FlowArgs &a, int l, int item, uint32_t *sAct)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int W = a.width, qWidth = a.heads * a.head_dim, nb = qWidth / kBlock;
@@ -1345,11 +1413,12 @@ __device__ __forceinline__ void flow_o(const FlowArgs &a, int l, int item)
     for (int k = 0; k < 2; ++k)
         w[k] = load_block(a.out + a.out_stride * l, W, qWidth, r0 + k, lane, valid && r0 + k < W);
     __builtin_amdgcn_sched_barrier(0);
-    if (!flow_wait(a, l * kFlowPhases + kPhaseAttention, a.heads / (a.head_dim >= 32 ? 1 : 32 / a.head_dim)))
+    if (!flow_wait(a, l * kFlowPhases + kPhaseAttention))
         return;
+    flow_stage_q8(a.attn_q8, qWidth, sAct);
     int4 a0, a1;
     double sa;
-    flow_act_block(a.attn_q8, qWidth, valid ? lane : 0, a0, a1, sa);
+    lds_act_block(sAct, qWidth, valid ? lane : 0, a0, a1, sa);
     double y[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k)
@@ -1360,7 +1429,7 @@ __device__ __forceinline__ void flow_o(const FlowArgs &a, int l, int item)
         const double old = (double) ld_agent_f(a.hidden + row);
         st_agent_f(a.hidden + row, (float) (total + old));
     }
-    flow_signal(a, l * kFlowPhases + kPhaseO);
+    flow_signal(a, l * kFlowPhases + kPhaseO, item, a.o_items);
 }
 
 __device__ __forceinline__ void flow_gateup(const FlowArgs &a, int l, int item)
@@ -1382,7 +1451,7 @@ __device__ __forceinline__ void flow_gateup(const FlowArgs &a, int l, int item)
                                         lane, valid);
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (!flow_wait(a, l * kFlowPhases + kPhaseO, a.o_items))
+    if (!flow_wait(a, l * kFlowPhases + kPhaseO))
         return;
     const RowSlice<4> slice = flow_row_slice(a, a.post_norm + a.norm_stride * l, false, false, 0);
     norm_q8_finish<4>(slice, a.width, a.epsilon, row, sPartial, nullptr, nullptr);
@@ -1419,10 +1488,10 @@ __device__ __forceinline__ void flow_gateup(const FlowArgs &a, int l, int item)
         const uint8_t byte = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);
         flow_store_q8(a.act_q8, F, o, byte, bits, live);
     }
-    flow_signal(a, l * kFlowPhases + kPhaseGateUp);
+    flow_signal(a, l * kFlowPhases + kPhaseGateUp, item, a.gate_up_items);
 }
 
-__device__ __forceinline__ void flow_down(const FlowArgs &a, int l, int item)
+__device__ __forceinline__ void flow_down(const FlowArgs &a, int l, int item, uint32_t *sAct)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int W = a.width, F = a.intermediate, nb = F / kBlock;
@@ -1434,15 +1503,16 @@ __device__ __forceinline__ void flow_down(const FlowArgs &a, int l, int item)
         w[j] = load_block(a.down + a.down_stride * l, W, F, row, b, row < W && b < nb);
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (!flow_wait(a, l * kFlowPhases + kPhaseGateUp, a.gate_up_items))
+    if (!flow_wait(a, l * kFlowPhases + kPhaseGateUp))
         return;
+    flow_stage_q8(a.act_q8, F, sAct);
     double acc = 0.0;
 #pragma unroll
     for (int j = 0; j < kFlowDownBlocks; ++j) {
         const int b = lane + 64 * j;
         int4 a0, a1;
         double sa;
-        flow_act_block(a.act_q8, F, b < nb ? b : 0, a0, a1, sa);
+        lds_act_block(sAct, F, b < nb ? b : 0, a0, a1, sa);
         acc += block_term(w[j], a0, a1, sa);
     }
     const double total = wave_sum_d(acc);
@@ -1450,14 +1520,14 @@ __device__ __forceinline__ void flow_down(const FlowArgs &a, int l, int item)
         const double old = (double) ld_agent_f(a.hidden + row);
         st_agent_f(a.hidden + row, (float) (total + old));
     }
-    flow_signal(a, l * kFlowPhases + kPhaseDown);
+    flow_signal(a, l * kFlowPhases + kPhaseDown, item, a.down_items);
 }
 
 __device__ __forceinline__ void flow_final_norm(const FlowArgs &a)
 {
     __shared__ RowQ8 row;
     __shared__ double sPartial[kFlowWaves];
-    if (!flow_wait(a, (a.layers - 1) * kFlowPhases + kPhaseDown, a.down_items))
+    if (!flow_wait(a, (a.layers - 1) * kFlowPhases + kPhaseDown))
         return;
     const RowSlice<4> slice = flow_row_slice(a, a.final_norm, false, false, 0);
     norm_q8_finish<4>(slice, a.width, a.epsilon, row, sPartial, a.normalised, nullptr);
@@ -1469,10 +1539,10 @@ __device__ __forceinline__ void flow_final_norm(const FlowArgs &a)
     }
     if (t < a.width / kBlock)
         st_agent_u(a.head_q8 + a.width / 4 + t, half_bits((float) row.scale[t]));
-    flow_signal(a, a.layers * kFlowPhases);
+    flow_signal(a, a.layers * kFlowPhases, 0, 1);
 }
 
-__device__ __forceinline__ void flow_lmhead(const FlowArgs &a, int item)
+__device__ __forceinline__ void flow_lmhead(const FlowArgs &a, int item, uint32_t *sAct)
 {
     __shared__ unsigned long long sBest[kFlowWaves];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1485,11 +1555,12 @@ __device__ __forceinline__ void flow_lmhead(const FlowArgs &a, int item)
     for (int k = 0; k < kHeadRows; ++k)
         w[k] = load_block(a.embedding, V, a.width, r0 + k, lane, valid && r0 + k < V);
     __builtin_amdgcn_sched_barrier(0);
-    if (!flow_wait(a, a.layers * kFlowPhases, 1))
+    if (!flow_wait(a, a.layers * kFlowPhases))
         return;
+    flow_stage_q8(a.head_q8, a.width, sAct);
     int4 a0, a1;
     double sa;
-    flow_act_block(a.head_q8, a.width, valid ? lane : 0, a0, a1, sa);
+    lds_act_block(sAct, a.width, valid ? lane : 0, a0, a1, sa);
     double y[kHeadRows];
 #pragma unroll
     for (int k = 0; k < kHeadRows; ++k)
@@ -1513,7 +1584,7 @@ __device__ __forceinline__ void flow_lmhead(const FlowArgs &a, int item)
         if (c != 0)
             atomicMax(a.best + (item % kHeadSlots) * kHeadSlotStride, c);
     }
-    flow_signal(a, a.layers * kFlowPhases + 1);
+    flow_signal(a, a.layers * kFlowPhases + 1, item, a.head_items);
 }
 
 __device__ __forceinline__ void flow_finalize(const FlowArgs &a)
@@ -1523,8 +1594,7 @@ __device__ __forceinline__ void flow_finalize(const FlowArgs &a)
     const int position = *a.position;
     const int groups = a.attn_items / a.attn_splits;
     const int idle = a.layers * groups * (a.attn_splits - flow_plan(position + 1, a.attn_splits).splits);
-    if (!flow_wait(a, a.layers * kFlowPhases + 1, a.head_items)
-        || !flow_wait(a, a.layers * kFlowPhases + 2, idle))
+    if (!flow_wait(a, a.layers * kFlowPhases + 1) || (idle > 0 && !flow_wait(a, a.layers * kFlowPhases + 2)))
         return;
     const int t = threadIdx.x;
     if (t < 64) {
@@ -1541,16 +1611,18 @@ __device__ __forceinline__ void flow_finalize(const FlowArgs &a)
             *a.position = position + 1;
         }
     }
-    // every item has passed its wait: the counters start the next step at zero
-    const int counters = a.layers * kFlowPhases + kFlowExtraCounters;
-    for (int i = t; i < counters; i += kFlowThreads)
-        st_agent_i(flow_counter(a, i), 0);
+    // every item has passed its wait: the flags start the next step lowered
+    // (completed sub-counters and tops went back to zero as they completed)
+    const int flags = (a.layers * kFlowPhases + kFlowExtraCounters) * kFlowFlagLines;
+    for (int i = t; i < flags; i += kFlowThreads)
+        st_agent_i(flow_line(a, i / kFlowFlagLines, 1 + i % kFlowFlagLines), 0);
 }
 
 template <int C, int G>
 __global__ __launch_bounds__(kFlowThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void flow_step_kernel(FlowArgs a)
 {
+    __shared__ __attribute__((aligned(16))) uint32_t sAct[kFlowActWords];
     const int perLayer = a.qkv_items + a.attn_items + a.o_items + a.gate_up_items + a.down_items;
     int item = blockIdx.x;
     if (item < a.layers * perLayer) {
@@ -1563,18 +1635,18 @@ void flow_step_kernel(FlowArgs a)
             return flow_attention<C, G>(a, l, item);
         item -= a.attn_items;
         if (item < a.o_items)
-            return flow_o(a, l, item);
+            return flow_o(a, l, item, sAct);
         item -= a.o_items;
         if (item < a.gate_up_items)
             return flow_gateup(a, l, item);
         item -= a.gate_up_items;
-        return flow_down(a, l, item);
+        return flow_down(a, l, item, sAct);
     }
     item -= a.layers * perLayer;
     if (item == 0)
         return flow_final_norm(a);
     if (item <= a.head_items)
-        return flow_lmhead(a, item - 1);
+        return flow_lmhead(a, item - 1, sAct);
     flow_finalize(a);
 }
 
@@ -1599,15 +1671,18 @@ static bool attention_layout(int head_dim, int *channels, int *group)
     return false;
 }
 
-bool flow_decode_supported(int width, int heads, int kv_heads, int head_dim, int intermediate,
-                           int max_positions)
+bool flow_decode_supported(int layers, int width, int heads, int kv_heads, int head_dim, int intermediate,
+                           int vocab, int max_positions)
 {
     const int qWidth = heads * head_dim;
     int channels = 0, group = 0;
     return fused_decode_supported(width, heads, kv_heads, head_dim, intermediate, max_positions)
-           && attention_layout(head_dim, &channels, &group) && width % 4 == 0
+           && attention_layout(head_dim, &channels, &group)
+           && (int64_t) layers * (heads / group) <= kFlowSubLines            // idle-split sub-counters
+           && (vocab + kFlowHeadRows - 1) / kFlowHeadRows <= kFlowSubLines * kFlowFanIn
+           && intermediate / kBlock <= kFlowSubLines * kFlowFanIn && width % 4 == 0
            && width <= kFlowThreads * 4 && qWidth <= 64 * kBlock && width <= 64 * kBlock
-           && intermediate <= 64 * kBlock * kFlowDownBlocks && intermediate % kBlock == 0
+           && intermediate <= kFlowMaxInner && intermediate % kBlock == 0
            && (head_dim / 2) % 2 == 0
            && flow_attention_splits(max_positions) * kMaxSplitKeys >= max_positions;
 }

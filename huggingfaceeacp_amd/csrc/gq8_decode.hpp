@@ -85,8 +85,19 @@ struct HeadArgs {
 // agent-scope (cross-L2 coherent) stores before counting itself done.
 constexpr int kFlowThreads = 512;
 constexpr int kFlowPhases = 5;        // per layer: qkv, attention, o, gate|up, down
-constexpr int kFlowCounterStride = 32; // ints between counters (128 bytes)
 constexpr int kFlowExtraCounters = 3;  // after the layers: final norm, lm_head, idle attention splits
+// A counter is a tree of 128-byte lines: a top line, kFlowFlagLines completion
+// flags (waiters spread their polling over them) and kFlowSubLines
+// sub-counters of at most kFlowFanIn arrivals each.
+constexpr int kFlowLineInts = 32;
+constexpr int kFlowFanIn = 16;
+constexpr int kFlowFlagLines = 16;
+constexpr int kFlowSubLines = 1024;
+constexpr int kFlowCounterLines = 1 + kFlowFlagLines + kFlowSubLines;
+constexpr int64_t flow_counter_ints(int layers)
+{
+    return (int64_t) (kFlowPhases * layers + kFlowExtraCounters) * kFlowCounterLines * kFlowLineInts;
+}
 
 struct FlowArgs {
     int layers, width, heads, kv_heads, head_dim, intermediate, vocab, max_positions;
@@ -120,8 +131,8 @@ struct FlowArgs {
     int qkv_items, attn_items, o_items, gate_up_items, down_items, head_items;
 };
 
-bool flow_decode_supported(int width, int heads, int kv_heads, int head_dim, int intermediate,
-                           int max_positions);
+bool flow_decode_supported(int layers, int width, int heads, int kv_heads, int head_dim, int intermediate,
+                           int vocab, int max_positions);
 int flow_attention_splits(int max_positions);
 // Fills the item counts of a; returns the grid size.
 int flow_items(FlowArgs &a);

@@ -703,18 +703,16 @@ extern "C" int gq8_decoder_create(const gq8_shape *shape, gq8_decoder **out)
     GQ8_ALLOC(d->debugNormalised, R * W * sizeof(float));
     GQ8_ALLOC(d->debugAttended, R * d->qWidth * sizeof(float));
     GQ8_ALLOC(d->debugActivated, R * (int64_t) s.intermediate * sizeof(float));
-    d->flowSupported = gq8::flow_decode_supported(s.width, s.heads, s.kv_heads, s.head_dim,
-                                                  s.intermediate, s.max_positions);
+    d->flowSupported = gq8::flow_decode_supported(s.layers, s.width, s.heads, s.kv_heads, s.head_dim,
+                                                  s.intermediate, s.vocab, s.max_positions);
     {
         const int64_t words = [](int64_t n) { return n / 4 + n / gq8::kBlock; }(d->maxInner);
         GQ8_ALLOC(d->flowAttnQ8, words * sizeof(uint32_t));
         GQ8_ALLOC(d->flowActQ8, words * sizeof(uint32_t));
         GQ8_ALLOC(d->flowHeadQ8, words * sizeof(uint32_t));
-        GQ8_ALLOC(d->flowCounters, (size_t) (gq8::kFlowPhases * L + gq8::kFlowExtraCounters) * gq8::kFlowCounterStride
-                                       * sizeof(int));
+        GQ8_ALLOC(d->flowCounters, (size_t) gq8::flow_counter_ints(L) * sizeof(int));
         GQ8_ALLOC(d->flowError, 64 * sizeof(int));
-        if (hipMemset(d->flowCounters, 0, (size_t) (gq8::kFlowPhases * L + gq8::kFlowExtraCounters)
-                                              * gq8::kFlowCounterStride * sizeof(int)) != hipSuccess
+        if (hipMemset(d->flowCounters, 0, (size_t) gq8::flow_counter_ints(L) * sizeof(int)) != hipSuccess
             || hipMemset(d->flowError, 0, sizeof(int)) != hipSuccess)
             return cleanup(fail(GQ8_ERR_DEVICE, "flow counters: memset failed"));
     }
@@ -1130,8 +1128,7 @@ int check_flow_error(gq8_decoder *d)
     if (error == 0)
         return GQ8_OK;
     const int L = d->shape.layers;
-    GQ8_HIP(hipMemset(d->flowCounters, 0, (size_t) (gq8::kFlowPhases * L + gq8::kFlowExtraCounters)
-                                              * gq8::kFlowCounterStride * sizeof(int)));
+    GQ8_HIP(hipMemset(d->flowCounters, 0, (size_t) gq8::flow_counter_ints(L) * sizeof(int)));
     GQ8_HIP(hipMemset(d->flowError, 0, sizeof(int)));
     GQ8_HIP(hipMemset(d->counters, 0, gq8::kDecodeCounters * sizeof(int)));
     GQ8_HIP(hipMemset(d->headBest, 0, gq8::kHeadSlots * gq8::kHeadSlotStride * sizeof(unsigned long long)));
