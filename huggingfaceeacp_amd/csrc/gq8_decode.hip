@@ -865,18 +865,22 @@ __global__ __launch_bounds__(64) void head_finalize_kernel(HeadArgs a)
 // ends.  A wait is a bounded spin; giving up sets the error word, which every
 // other wait checks, so a failure ends the launch instead of hanging it.
 //
-// A phase counts its items on a tree (sub-counters of 16 arrivals, then a top
-// count): arrivals on one address serialize at about 15 ns each, so 512 items
-// on one counter would take 7 us.  The item that completes the tree raises 16
-// flags, and waiters poll the flag of their id modulo 16.
+// Items hand rows on in tagged words: one 64-bit store of a 32-bit value and
+// a 32-bit tag (the launch's epoch and the row's version), single-copy atomic.
+// A reader polls the words it needs until each carries the tag it expects, so
+// a hand-over is one trip through the memory system; a counter and a flag
+// would take four (the data, the count, the flag, the data again).  Readers
+// of a whole row first poll the word its last producer writes, then read the
+// row once.  Every version of a row is read only by items that the writer of
+// its next version depends on, so no version is overwritten while it is read.
+// Tagged words are written and read with agent-scope (sc1) accesses, which
+// the eight XCD L2s keep coherent.
 //
-// Data that crosses items (hidden, q, the fp16 K/V row of the step, the Q8
-// rows, attention partials) is written and read with agent-scope accesses,
-// which the eight XCD L2s keep coherent (rows of it in 16-byte agent-coherent
-// buffer loads, staged through LDS when all waves need them); a workgroup
-// waits for its stores to complete before it counts itself done.  Weights and
-// the K/V rows of earlier steps were written before the launch: plain cached
-// loads, issued before the wait.
+// Weights and the K/V rows of earlier steps were written before the launch:
+// plain cached loads, issued before the wait.  The lm_head items and the idle
+// attention splits count themselves on trees of counters (sub-counters of 16
+// arrivals, then a top count, then 16 flags that waiters spread their polls
+// over), which the finalize item waits on.
 constexpr int kFlowWaves = kFlowThreads / 64;
 constexpr int kFlowSpinLimit = 1 << 20;
 constexpr int kFlowQkvPairs = kFlowWaves * kPairsPerWave;   // 16 pairs (32 rows) an item
@@ -886,13 +890,13 @@ constexpr int kFlowDownBlocks = 8;                          // blocks a lane (in
 constexpr int kFlowHeadRows = kFlowWaves * kHeadRows;       // 64 rows an item
 constexpr int kFlowMaxInner = 64 * kBlock * kFlowDownBlocks;  // 16384
 constexpr int kFlowActWords = kFlowMaxInner / 4 + kFlowMaxInner / kBlock + 4; // a staged Q8 row
+constexpr int kFlowMergePieces = 8;    // partials a merging lane loads at once
+constexpr int kFlowStagePieces = (kFlowActWords / 2 + kFlowThreads - 1) / kFlowThreads; // 5
+constexpr int kFlowRowPieces = ((kFusedMaxWidth / 4 + kFusedMaxWidth / kBlock) / 2 + kFlowThreads - 1)
+                               / kFlowThreads; // a Q8 row of at most the fused width: 1
 
-enum { kPhaseQkv = 0, kPhaseAttention, kPhaseO, kPhaseGateUp, kPhaseDown };
+enum { kCounterHead = 0, kCounterIdle = 1 };
 
-__device__ inline float ld_agent_f(const float *p)
-{
-    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ inline uint32_t ld_agent_u(const uint32_t *p)
 {
     return __hip_atomic_load(const_cast<uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -904,14 +908,6 @@ __device__ inline uint64_t ld_agent_u64(const uint64_t *p)
 __device__ inline int ld_agent_i(const int *p)
 {
     return __hip_atomic_load(const_cast<int *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline void st_agent_f(float *p, float v)
-{
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline void st_agent_u(uint32_t *p, uint32_t v)
-{
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ inline void st_agent_i(int *p, int v)
 {
@@ -929,6 +925,147 @@ __device__ inline v4u ld_agent_16(const void *base, uint32_t offset, uint32_t by
     return __builtin_amdgcn_raw_buffer_load_b128(r, (int) offset, 0, kCoherentLoad);
 }
 
+// ---- tagged words -----------------------------------------------------------
+// tag = epoch << 8 | version.  Versions of the residual row: 0 the embedding
+// row, 2 l + 1 after layer l's o projection, 2 l + 2 after its down
+// projection; every other row has the layer as its version.
+__device__ inline uint32_t flow_tag(uint32_t epoch, int version)
+{
+    return (epoch << 8) | (uint32_t) version;
+}
+
+__device__ inline void ll_put(uint64_t *p, uint32_t value, uint32_t tag)
+{
+    __hip_atomic_store(p, ((uint64_t) tag << 32) | value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ inline bool flow_give_up(const int *error, int &spins)
+{
+    if ((++spins & 63) == 0 && (ld_agent_i(error) != 0 || spins > kFlowSpinLimit)) {
+        __hip_atomic_fetch_or(const_cast<int *>(error), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return true;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    return false;
+}
+
+// The value of word `p` once it carries `tag`; false after giving up.
+__device__ inline bool ll_get(const uint64_t *p, uint32_t tag, const int *error, uint32_t &value)
+{
+    int spins = 0;
+    for (;;) {
+        const uint64_t w = ld_agent_u64(p);
+        if ((uint32_t) (w >> 32) == tag) {
+            value = (uint32_t) w;
+            return true;
+        }
+        if (flow_give_up(error, spins))
+            return false;
+    }
+}
+
+// Words `word` and `word + 1` (word even) of a `words`-long row; a second word
+// past the end is not waited for.
+__device__ inline bool ll_get2(const uint64_t *row, int word, int words, uint32_t tag, const int *error,
+                               uint32_t &v0, uint32_t &v1)
+{
+    int spins = 0;
+    for (;;) {
+        const v4u w = ld_agent_16(row, (uint32_t) word * 8, (uint32_t) words * 8);
+        if (w.y == tag && (word + 1 >= words || w.w == tag)) {
+            v0 = w.x;
+            v1 = w.z;
+            return true;
+        }
+        if (flow_give_up(error, spins))
+            return false;
+    }
+}
+
+// N consecutive pieces (2 N words) from even word `word` of a `words`-long
+// row: every load issued first, then the words not yet tagged polled again.
+template <int N>
+__device__ inline bool ll_get_pieces(const uint64_t *row, int word, int words, uint32_t tag, const int *error,
+                                     uint32_t (&v)[2 * N])
+{
+    v4u w[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k)
+        w[k] = ld_agent_16(row, (uint32_t) (word + 2 * k) * 8, (uint32_t) words * 8);
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        v[2 * k] = w[k].x;
+        v[2 * k + 1] = w[k].z;
+        if (w[k].y != tag || (word + 2 * k + 1 < words && w[k].w != tag))
+            ok = ll_get2(row, word + 2 * k, words, tag, error, v[2 * k], v[2 * k + 1]) && ok;
+    }
+    return ok;
+}
+
+// The values of a `words`-long tagged row (at most 2 P words a thread) into
+// LDS; thread 0 first waits for word `sentinel` (the one its last producer
+// writes).  False for every thread after a wait gave up.
+template <int P>
+__device__ inline bool flow_stage_ll(const FlowArgs &a, const uint64_t *row, int words, int sentinel,
+                                     uint32_t tag, uint32_t *sDst)
+{
+    bool ok = true;
+    if (threadIdx.x == 0) {
+        uint32_t v;
+        ok = ll_get(row + sentinel, tag, a.error, v);
+    }
+    if (__syncthreads_or(!ok))
+        return false;
+    const int pieces = (words + 1) / 2;
+    v4u w[P];
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+        const int p = threadIdx.x + k * kFlowThreads;
+        if (p < pieces)
+            w[k] = ld_agent_16(row, (uint32_t) p * 16, (uint32_t) words * 8);
+    }
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+        const int p = threadIdx.x + k * kFlowThreads;
+        if (p < pieces) {
+            uint32_t v0 = w[k].x, v1 = w[k].z;
+            if (w[k].y != tag || (2 * p + 1 < words && w[k].w != tag))
+                ok = ll_get2(row, 2 * p, words, tag, a.error, v0, v1) && ok;
+            sDst[2 * p] = v0;
+            sDst[2 * p + 1] = v1;
+        }
+    }
+    return !__syncthreads_or(!ok);
+}
+
+// The Q8 byte of each of four consecutive lanes packed into the first lane's
+// word; lanes 32 k also put the block's scale word (the row's word layout:
+// inner / 4 words of bytes, then one scale word a block).
+__device__ inline void flow_put_q8(uint64_t *row, int inner, int idx, uint8_t byte, uint16_t bits, bool live,
+                                   uint32_t tag)
+{
+    const uint32_t b = byte;
+    const uint32_t w = b | ((uint32_t) __shfl_down((int) b, 1) << 8)
+                       | ((uint32_t) __shfl_down((int) b, 2) << 16)
+                       | ((uint32_t) __shfl_down((int) b, 3) << 24);
+    if (live && (idx & 3) == 0)
+        ll_put(row + idx / 4, w, tag);
+    if (live && (idx & 31) == 0)
+        ll_put(row + inner / 4 + idx / kBlock, bits, tag);
+}
+
+// The activation block `block` of a Q8 row staged in LDS.
+__device__ inline void lds_act_block(const uint32_t *sAct, int inner, int block, int4 &a0, int4 &a1,
+                                     double &sa)
+{
+    const int4 *w = reinterpret_cast<const int4 *>(sAct + block * (kBlock / 4));
+    a0 = w[0];
+    a1 = w[1];
+    sa = (double) half_value((uint16_t) sAct[inner / 4 + block]);
+}
+
+// ---- counter trees (lm_head items, idle attention splits) --------------------
 __device__ inline int *flow_line(const FlowArgs &a, int counter, int line)
 {
     return a.counters + ((int64_t) counter * kFlowCounterLines + line) * kFlowLineInts;
@@ -937,22 +1074,17 @@ __device__ inline int *flow_line(const FlowArgs &a, int counter, int line)
 // Waits until counter `counter` has completed; false after giving up.
 __device__ __forceinline__ bool flow_wait(const FlowArgs &a, int counter)
 {
-    __shared__ int sOk;
+    bool ok = true;
     if (threadIdx.x == 0) {
-        int ok = 1, spins = 0;
+        int spins = 0;
         const int *flag = flow_line(a, counter, 1 + (int) (blockIdx.x % kFlowFlagLines));
-        while (ld_agent_i(flag) == 0) {
-            if ((++spins & 63) == 0 && (ld_agent_i(a.error) != 0 || spins > kFlowSpinLimit)) {
-                __hip_atomic_fetch_or(a.error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                ok = 0;
+        while (ld_agent_i(flag) == 0)
+            if (flow_give_up(a.error, spins)) {
+                ok = false;
                 break;
             }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        sOk = ok;
     }
-    __syncthreads();
-    return sOk != 0;
+    return !__syncthreads_or(!ok);
 }
 
 // One arrival on sub-counter `sub` (complete at `inSub` arrivals) of a counter
@@ -984,80 +1116,64 @@ __device__ __forceinline__ void flow_signal(const FlowArgs &a, int counter, int 
     }
 }
 
-// Copies a Q8 row in the word layout (inner / 4 words of bytes, then one
-// scale word a block) into LDS with 16-byte coherent loads.
-__device__ inline void flow_stage_q8(const uint32_t *q8, int inner, uint32_t *sAct)
+// ---- rows into the norms -------------------------------------------------------
+// Thread t's four elements of the residual row at version `tag`, with their
+// norm weights; thread 0 first waits for the last element (its last writer).
+__device__ __forceinline__ bool flow_hidden_slice(const FlowArgs &a, const float *weight, uint32_t tag,
+                                                  RowSlice<4> &r)
 {
-    const int words = inner / 4 + inner / kBlock;
-    for (int p = threadIdx.x; p * 4 < words; p += kFlowThreads)
-        reinterpret_cast<v4u *>(sAct)[p] = ld_agent_16(q8, (uint32_t) p * 16, (uint32_t) words * 4);
-    __syncthreads();
+    const int t = threadIdx.x;
+    r.active = t * 4 < a.width;
+    const int i0 = r.active ? t * 4 : 0;
+    load4<4>(weight + i0, r.w);
+    bool ok = true;
+    if (t == 0) {
+        uint32_t v;
+        ok = ll_get(a.hidden_ll + a.width - 1, tag, a.error, v);
+    }
+    if (__syncthreads_or(!ok))
+        return false;
+    uint32_t v[4];
+    ok = ll_get_pieces<2>(a.hidden_ll, i0, a.width, tag, a.error, v);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        r.v[k] = __uint_as_float(v[k]);
+    return !__syncthreads_or(!ok);
 }
 
-// The activation block `block` of a Q8 row staged in LDS.
-__device__ inline void lds_act_block(const uint32_t *sAct, int inner, int block, int4 &a0, int4 &a1,
-                                     double &sa)
-{
-    const int4 *w = reinterpret_cast<const int4 *>(sAct + block * (kBlock / 4));
-    a0 = w[0];
-    a1 = w[1];
-    sa = (double) half_value((uint16_t) sAct[inner / 4 + block]);
-}
-
-// Four consecutive elements of the residual row (agent loads) or, on the
-// first layer, of the embedding row of sequence[position] (thread 0's item
-// 0 also publishes it as the residual row), with their norm weights.
-__device__ __forceinline__ RowSlice<4> flow_row_slice(const FlowArgs &a, const float *weight, bool embedding,
-                                      bool publish, int position)
+// Thread t's four elements of the embedding row of sequence[position] (scaled)
+// with their norm weights; with `publish`, also put as the residual row's
+// version 0.
+__device__ __forceinline__ RowSlice<4> flow_embed_slice(const FlowArgs &a, const float *weight, int position,
+                                                        bool publish, uint32_t tag)
 {
     RowSlice<4> r;
     const int t = threadIdx.x;
     r.active = t * 4 < a.width;
     const int i0 = r.active ? t * 4 : 0;
     load4<4>(weight + i0, r.w);
-    if (embedding) {
-        uint32_t id = a.sequence[position];
-        if (id >= (uint32_t) a.vocab) // ids are validated on the host; a guard, not a rule
-            id = 0;
-        const int64_t e0 = (int64_t) id * a.width + i0;
-        const int64_t V = a.vocab;
-        const uint16_t bits = reinterpret_cast<const uint16_t *>(a.embedding + V * a.width)[e0 / kBlock];
-        const float sc = half_value(bits);
-        const int packed = *reinterpret_cast<const int *>(a.embedding + e0);
-        int8_t b[4];
-        __builtin_memcpy(b, &packed, 4);
+    uint32_t id = a.sequence[position];
+    if (id >= (uint32_t) a.vocab) // ids are validated on the host; a guard, not a rule
+        id = 0;
+    const int64_t e0 = (int64_t) id * a.width + i0;
+    const int64_t V = a.vocab;
+    const uint16_t bits = reinterpret_cast<const uint16_t *>(a.embedding + V * a.width)[e0 / kBlock];
+    const float sc = half_value(bits);
+    const int packed = *reinterpret_cast<const int *>(a.embedding + e0);
+    int8_t b[4];
+    __builtin_memcpy(b, &packed, 4);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        r.v[k] = (float) ((double) a.embed_scale * (double) (sc * (float) b[k]));
+    if (publish && r.active)
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-            r.v[k] = (float) ((double) a.embed_scale * (double) (sc * (float) b[k]));
-        if (publish && r.active)
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                st_agent_f(a.hidden + i0 + k, r.v[k]);
-    } else {
-        const v4u h = ld_agent_16(a.hidden, (uint32_t) i0 * 4, (uint32_t) a.width * 4);
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            r.v[k] = __uint_as_float(h[k]);
-    }
+            ll_put(a.hidden_ll + i0 + k, __float_as_uint(r.v[k]), tag);
     return r;
 }
 
-// Packs the byte of each of four consecutive lanes into the first lane's
-// word and stores it (agent); lanes 32 k store the block's scale word.
-__device__ inline void flow_store_q8(uint32_t *q8, int inner, int idx, uint8_t byte, uint16_t bits,
-                                     bool live)
-{
-    const uint32_t b = byte;
-    const uint32_t w = b | ((uint32_t) __shfl_down((int) b, 1) << 8)
-                       | ((uint32_t) __shfl_down((int) b, 2) << 16)
-                       | ((uint32_t) __shfl_down((int) b, 3) << 24);
-    if (live && (idx & 3) == 0)
-        st_agent_u(q8 + idx / 4, w);
-    if (live && (idx & 31) == 0)
-        st_agent_u(q8 + inner / 4 + idx / kBlock, bits);
-}
-
-__device__ __forceinline__ void flow_qkv(const FlowArgs &a, int l, int item)
+// ---- items ----------------------------------------------------------------------
+__device__ __forceinline__ void flow_qkv(const FlowArgs &a, int l, int item, uint32_t epoch)
 {
     __shared__ RowQ8 row;
     __shared__ double sPartial[kFlowWaves];
@@ -1081,11 +1197,11 @@ __device__ __forceinline__ void flow_qkv(const FlowArgs &a, int l, int item)
     }
     const int position = *a.position;
     __builtin_amdgcn_sched_barrier(0);
-    if (l > 0 && !flow_wait(a, (l - 1) * kFlowPhases + kPhaseDown))
+    RowSlice<4> slice;
+    if (l == 0)
+        slice = flow_embed_slice(a, a.input_norm, position, item == 0, flow_tag(epoch, 0));
+    else if (!flow_hidden_slice(a, a.input_norm + a.norm_stride * l, flow_tag(epoch, 2 * l), slice))
         return;
-    const RowSlice<4> slice = flow_row_slice(a, a.input_norm + a.norm_stride * l, l == 0,
-                                             l == 0 && item == 0,
-                                             position);
     norm_q8_finish<4>(slice, a.width, a.epsilon, row, sPartial, nullptr, nullptr);
 
     int4 a0 = make_int4(0, 0, 0, 0), a1 = a0;
@@ -1108,8 +1224,9 @@ __device__ __forceinline__ void flow_qkv(const FlowArgs &a, int l, int item)
     for (int r = 0; r < kRows; ++r)
         rowTotal[r] = __shfl(total, lane_of_row<kRows>(r));
     // lane 0: the wave's two pairs are the consecutive elements (i, i + 1) and
-    // (i + half, i + half + 1) of one head: two-element stores
+    // (i + half, i + half + 1) of one head
     if (lane == 0 && firstPair < pairs) {
+        const uint32_t tag = flow_tag(epoch, l);
         const int head = firstPair / half, i = firstPair % half;
         const int rLo = head * hd + i;
         const bool second = firstPair + 1 < pairs;
@@ -1126,24 +1243,28 @@ __device__ __forceinline__ void flow_qkv(const FlowArgs &a, int l, int item)
             }
         }
         if (rLo < qWidth) {
-            st_agent_f(a.query + rLo, fLo[0]);
-            st_agent_f(a.query + rLo + half, fHi[0]);
+            ll_put(a.q_ll + rLo, __float_as_uint(fLo[0]), tag);
+            ll_put(a.q_ll + rLo + half, __float_as_uint(fHi[0]), tag);
             if (second) {
-                st_agent_f(a.query + rLo + 1, fLo[1]);
-                st_agent_f(a.query + rLo + half + 1, fHi[1]);
+                ll_put(a.q_ll + rLo + 1, __float_as_uint(fLo[1]), tag);
+                ll_put(a.q_ll + rLo + half + 1, __float_as_uint(fHi[1]), tag);
             }
         } else {
+            // the fp16 row into the cache (for later steps) and, tagged, for
+            // this step's attention: one word a pair of halves
             const bool isKey = rLo < qWidth + kvWidth;
             uint16_t *cache = (isKey ? a.key_cache : a.value_cache)
                               + ((int64_t) l * a.max_positions + position) * kvWidth;
+            uint64_t *fresh = isKey ? a.k_ll : a.v_ll;
             const int c = rLo - qWidth - (isKey ? 0 : kvWidth);
             const uint32_t wordLo = (uint32_t) half_bits(fLo[0]) | ((uint32_t) half_bits(fLo[1]) << 16);
             const uint32_t wordHi = (uint32_t) half_bits(fHi[0]) | ((uint32_t) half_bits(fHi[1]) << 16);
-            st_agent_u(reinterpret_cast<uint32_t *>(cache + c), wordLo);
-            st_agent_u(reinterpret_cast<uint32_t *>(cache + c + half), wordHi);
+            *reinterpret_cast<uint32_t *>(cache + c) = wordLo;
+            *reinterpret_cast<uint32_t *>(cache + c + half) = wordHi;
+            ll_put(fresh + c / 2, wordLo, tag);
+            ll_put(fresh + (c + half) / 2, wordHi, tag);
         }
     }
-    flow_signal(a, l * kFlowPhases + kPhaseQkv, item, a.qkv_items);
 }
 
 // Attention plan of the flow kernel: whole 64-key rounds a split, at most
@@ -1155,33 +1276,45 @@ __device__ inline SplitPlan flow_plan(int keyCount, int maxSplits)
     return {(keyCount + perSplit - 1) / perSplit, perSplit};
 }
 
+// Halves c .. c + C of this step's K or V row (tagged words of two halves).
 template <int C>
-__device__ inline void load_halves_agent(const uint16_t *p, uint16_t (&h)[C])
+__device__ inline bool ll_halves(const FlowArgs &a, const uint64_t *fresh, int c, uint32_t tag, uint16_t (&h)[C])
 {
-    if constexpr (C == 4) {
-        const uint64_t v = ld_agent_u64(reinterpret_cast<const uint64_t *>(p));
-        h[0] = (uint16_t) (v & 0xFFFFu); h[1] = (uint16_t) ((v >> 16) & 0xFFFFu);
-        h[2] = (uint16_t) ((v >> 32) & 0xFFFFu); h[3] = (uint16_t) (v >> 48);
+    if constexpr (C == 4) { // c is a multiple of 4: one piece
+        uint32_t w[2];
+        const bool ok = ll_get_pieces<1>(fresh, c / 2, a.kv_heads * a.head_dim / 2, tag, a.error, w);
+        h[0] = (uint16_t) (w[0] & 0xFFFFu); h[1] = (uint16_t) (w[0] >> 16);
+        h[2] = (uint16_t) (w[1] & 0xFFFFu); h[3] = (uint16_t) (w[1] >> 16);
+        return ok;
     } else if constexpr (C == 2) {
-        const uint32_t v = ld_agent_u(reinterpret_cast<const uint32_t *>(p));
-        h[0] = (uint16_t) (v & 0xFFFFu); h[1] = (uint16_t) (v >> 16);
+        uint32_t w0 = 0;
+        const bool ok = ll_get(fresh + c / 2, tag, a.error, w0);
+        h[0] = (uint16_t) (w0 & 0xFFFFu); h[1] = (uint16_t) (w0 >> 16);
+        return ok;
     } else {
-        // one half: the aligned word holding it
-        const uintptr_t at = reinterpret_cast<uintptr_t>(p);
-        const uint32_t v = ld_agent_u(reinterpret_cast<const uint32_t *>(at & ~(uintptr_t) 3));
-        h[0] = (uint16_t) ((at & 2) ? v >> 16 : v & 0xFFFFu);
+        uint32_t w0 = 0;
+        const bool ok = ll_get(fresh + c / 2, tag, a.error, w0);
+        h[0] = (uint16_t) ((c & 1) ? w0 >> 16 : w0 & 0xFFFFu);
+        return ok;
     }
 }
 
+// A double as two tagged words (low word first).
+__device__ inline void ll_put_double(uint64_t *p, double v, uint32_t tag)
+{
+    const uint64_t bits = (uint64_t) __double_as_longlong(v);
+    ll_put(p, (uint32_t) bits, tag);
+    ll_put(p + 1, (uint32_t) (bits >> 32), tag);
+}
+
 template <int C, int G>
-__device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int item)
+__device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int item, uint32_t epoch)
 {
     constexpr int kRows = kScoreBatch * G;
     __shared__ double sScore[G][kMaxSplitKeys];
     __shared__ double sAcc[kAttnWaves][kMaxGroupWidth];
     __shared__ double sMax[G], sSum[G];
     __shared__ double sSplitMax[G][kDecodeSplits], sSplitSum[G][kDecodeSplits];
-    __shared__ int sLast;
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int hd = a.head_dim, kvWidth = a.kv_heads * hd;
@@ -1198,10 +1331,10 @@ __device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int ite
         // no work at this length; counted so that the finalize item (which
         // advances the position) knows every item has read the position
         if (t == 0)
-            flow_arrive(a, a.layers * kFlowPhases + 2, l * groups + group, a.attn_splits - plan.splits,
-                        a.layers * groups);
+            flow_arrive(a, kCounterIdle, l * groups + group, a.attn_splits - plan.splits, a.layers * groups);
         return;
     }
+    const uint32_t tag = flow_tag(epoch, l);
 
     const bool active = lane * C < hd;
     const int c0 = active ? lane * C : 0;
@@ -1218,9 +1351,11 @@ __device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int ite
         kvOffset[g] = ((h0 + g) / perKv) * hd + c0;
 
     // rows of earlier steps: plain loads, before the wait; this step's row (a
-    // wave-uniform case): a coherent load once the q|k|v items are done
+    // wave-uniform case): its tagged words once the q|k|v items have put them
+    bool ok = true;
     uint16_t kh[kScoreBatch][G][C], vh[kScoreBatch][G][C];
-    auto load_round = [&](const uint16_t *base, int r0, uint16_t (&dst)[kScoreBatch][G][C], bool waited) {
+    auto load_round = [&](bool isKeys, int r0, uint16_t (&dst)[kScoreBatch][G][C], bool waited) {
+        const uint16_t *base = isKeys ? keys : values;
 #pragma unroll
         for (int b = 0; b < kScoreBatch; ++b) {
             const int j = min(r0 + wave + b * kAttnWaves, n - 1);
@@ -1231,36 +1366,40 @@ __device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int ite
             } else if (waited) {
 #pragma unroll
                 for (int g = 0; g < G; ++g)
-                    load_halves_agent<C>(base + (int64_t) j * kvWidth + kvOffset[g], dst[b][g]);
+                    ok = ll_halves<C>(a, isKeys ? a.k_ll : a.v_ll, kvOffset[g], tag, dst[b][g]) && ok;
             }
         }
     };
-    load_round(keys, 0, kh, false);
-    load_round(values, 0, vh, false);
-    if (!flow_wait(a, l * kFlowPhases + kPhaseQkv))
-        return;
+    load_round(true, 0, kh, false);
+    load_round(false, 0, vh, false);
+    __builtin_amdgcn_sched_barrier(0);
+    double q[G][C];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        uint32_t bits[C > 1 ? C : 2] = {};
+        if constexpr (C > 1) // c0 even: C / 2 pieces
+            ok = ll_get_pieces<C / 2>(a.q_ll, (h0 + g) * hd + c0, qWidth, tag, a.error, bits) && ok;
+        else
+            ok = ll_get(a.q_ll + (h0 + g) * hd + c0, tag, a.error, bits[0]) && ok;
+#pragma unroll
+        for (int i = 0; i < C; ++i)
+            q[g][i] = (double) __uint_as_float(bits[i] & keep);
+    }
 #pragma unroll
     for (int b = 0; b < kScoreBatch; ++b) {
         const int j = min(wave + b * kAttnWaves, n - 1);
         if (j == newest) {
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                load_halves_agent<C>(keys + (int64_t) j * kvWidth + kvOffset[g], kh[b][g]);
-                load_halves_agent<C>(values + (int64_t) j * kvWidth + kvOffset[g], vh[b][g]);
+                ok = ll_halves<C>(a, a.k_ll, kvOffset[g], tag, kh[b][g]) && ok;
+                ok = ll_halves<C>(a, a.v_ll, kvOffset[g], tag, vh[b][g]) && ok;
             }
         }
     }
-    double q[G][C];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int i = 0; i < C; ++i)
-            q[g][i] = (double) __uint_as_float(
-                __float_as_uint(ld_agent_f(a.query + (h0 + g) * hd + c0 + i)) & keep);
 
     for (int r0 = 0; r0 < n; r0 += kRoundKeys) {
         if (r0 > 0)
-            load_round(keys, r0, kh, true);
+            load_round(true, r0, kh, true);
         double y[kRows];
 #pragma unroll
         for (int b = 0; b < kScoreBatch; ++b)
@@ -1307,7 +1446,7 @@ __device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int ite
             acc[g][i] = 0.0;
     for (int r0 = 0; r0 < n; r0 += kRoundKeys) {
         if (r0 > 0)
-            load_round(values, r0, vh, true);
+            load_round(false, r0, vh, true);
 #pragma unroll
         for (int b = 0; b < kScoreBatch; ++b) {
             const int j = r0 + wave + b * kAttnWaves;
@@ -1328,33 +1467,43 @@ __device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int ite
 #pragma unroll
             for (int i = 0; i < C; ++i)
                 sAcc[wave][g * hd + c0 + i] = acc[g][i];
-    __syncthreads();
-    if (t < groupWidth) {
-        double o = 0.0;
-        for (int w = 0; w < kAttnWaves; ++w)
-            o += sAcc[w][t];
-        store_agent(a.ws_o + (int64_t) split * qWidth + h0 * hd + t, o);
-    }
-    if (t < G) {
-        store_agent(a.ws_ml + (split * heads + h0 + t) * 2, sMax[t]);
-        store_agent(a.ws_ml + (split * heads + h0 + t) * 2 + 1, sSum[t]);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (t == 0)
-        sLast = __hip_atomic_fetch_add(a.tickets + group, 1, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT) == plan.splits - 1;
-    __syncthreads();
-    if (!sLast)
+    if (__syncthreads_or(!ok))
         return;
+    double own = 0.0;
+    if (t < groupWidth)
+        for (int w = 0; w < kAttnWaves; ++w)
+            own += sAcc[w][t];
 
+    // every split but the last puts its partial (unnormalised output, max,
+    // sum); the last split, which holds this step's row, merges them
+    uint64_t *partO = a.part_ll + (int64_t) split * qWidth * 2;
+    uint64_t *partMl = a.part_ml_ll + (int64_t) split * heads * 4;
     const int splits = plan.splits;
+    if (split != splits - 1) {
+        if (t < groupWidth)
+            ll_put_double(partO + (h0 * hd + t) * 2, own, tag);
+        if (t < G) {
+            ll_put_double(partMl + (h0 + t) * 4, sMax[t], tag);
+            ll_put_double(partMl + (h0 + t) * 4 + 2, sSum[t], tag);
+        }
+        return;
+    }
+
     if (t < G * splits) {
         const int g = t / splits, sp = t % splits;
-        sSplitMax[g][sp] = load_agent(a.ws_ml + (sp * heads + h0 + g) * 2);
-        sSplitSum[g][sp] = load_agent(a.ws_ml + (sp * heads + h0 + g) * 2 + 1);
+        double m = sMax[g], s = sSum[g];
+        if (sp != split) {
+            const int ml = (sp * heads + h0 + g) * 4, mlWords = kDecodeSplits * heads * 4;
+            uint32_t w[4];
+            ok = ll_get_pieces<2>(a.part_ml_ll, ml, mlWords, tag, a.error, w);
+            m = __longlong_as_double((long long) (((uint64_t) w[1] << 32) | w[0]));
+            s = __longlong_as_double((long long) (((uint64_t) w[3] << 32) | w[2]));
+        }
+        sSplitMax[g][sp] = m;
+        sSplitSum[g][sp] = s;
     }
-    __syncthreads();
+    if (__syncthreads_or(!ok))
+        return;
     if (t < G) {
         double largest = -INFINITY;
         for (int sp = 0; sp < splits; ++sp)
@@ -1377,17 +1526,31 @@ __device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int ite
     const bool live = t < groupWidth;
     const int g = min(t / hd, G - 1);
     double weighted = 0.0;
-    for (int s0 = 0; s0 < splits; s0 += kMergeBatch) {
-        double part[kMergeBatch];
+    const int tt = live ? t : 0;
+    const uint32_t partBytes = (uint32_t) kDecodeSplits * qWidth * 16;
+    for (int s0 = 0; s0 < splits; s0 += kFlowMergePieces) {
+        v4u part[kFlowMergePieces]; // every lane loads (clamped), so the loads issue together
 #pragma unroll
-        for (int u = 0; u < kMergeBatch; ++u)
-            part[u] = (s0 + u < splits && live)
-                          ? load_agent(a.ws_o + (int64_t) (s0 + u) * qWidth + h0 * hd + t) : 0.0;
+        for (int u = 0; u < kFlowMergePieces; ++u) {
+            const int sp = min(s0 + u, splits - 1);
+            part[u] = ld_agent_16(a.part_ll, (uint32_t) (sp * qWidth + h0 * hd + tt) * 16, partBytes);
+        }
 #pragma unroll
-        for (int u = 0; u < kMergeBatch; ++u)
-            if (s0 + u < splits)
-                weighted += part[u] * sSplitMax[g][s0 + u];
+        for (int u = 0; u < kFlowMergePieces; ++u)
+            if (s0 + u < splits) {
+                double v = own;
+                if (s0 + u != split) {
+                    uint32_t lo = part[u].x, hi = part[u].z;
+                    if (part[u].y != tag || part[u].w != tag)
+                        ok = ll_get2(a.part_ll, ((s0 + u) * qWidth + h0 * hd + tt) * 2, kDecodeSplits * qWidth * 2,
+                                     tag, a.error, lo, hi) && ok;
+                    v = __longlong_as_double((long long) (((uint64_t) hi << 32) | lo));
+                }
+                weighted += (live ? v : 0.0) * sSplitMax[g][s0 + u];
+            }
     }
+    if (__syncthreads_or(!ok))
+        return;
     const int idx = h0 * hd + t;
     const float v = live ? (float) (weighted / sSum[g]) : 0.f;
     float amax = fabsf(v);
@@ -1396,13 +1559,10 @@ __device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int ite
     const uint16_t bits = scale_bits_from_amax(amax);
     const float sc = half_value(bits);
     const uint8_t byte = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);
-    flow_store_q8(a.attn_q8, qWidth, idx, byte, bits, live);
-    if (t == 0)
-        __hip_atomic_store(a.tickets + group, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    flow_signal(a, l * kFlowPhases + kPhaseAttention, group, groups);
+    flow_put_q8(a.attn_ll, qWidth, idx, byte, bits, live, tag);
 }
 
-__device__ __forceinline__ void flow_o(const FlowArgs &a, int l, int item, uint32_t *sAct)
+__device__ __forceinline__ void flow_o(const FlowArgs &a, int l, int item, uint32_t epoch, uint32_t *sAct)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int W = a.width, qWidth = a.heads * a.head_dim, nb = qWidth / kBlock;
@@ -1413,9 +1573,9 @@ __device__ __forceinline__ void flow_o(const FlowArgs &a, int l, int item, uint3
     for (int k = 0; k < 2; ++k)
         w[k] = load_block(a.out + a.out_stride * l, W, qWidth, r0 + k, lane, valid && r0 + k < W);
     __builtin_amdgcn_sched_barrier(0);
-    if (!flow_wait(a, l * kFlowPhases + kPhaseAttention))
+    const int words = qWidth / 4 + qWidth / kBlock;
+    if (!flow_stage_ll<kFlowRowPieces>(a, a.attn_ll, words, words - 1, flow_tag(epoch, l), sAct))
         return;
-    flow_stage_q8(a.attn_q8, qWidth, sAct);
     int4 a0, a1;
     double sa;
     lds_act_block(sAct, qWidth, valid ? lane : 0, a0, a1, sa);
@@ -1426,13 +1586,14 @@ __device__ __forceinline__ void flow_o(const FlowArgs &a, int l, int item, uint3
     const double total = reduce_rows<2>(y, lane);
     const int row = r0 + row_of_lane<2>(lane);
     if (stores_row<2>(lane) && row < W) {
-        const double old = (double) ld_agent_f(a.hidden + row);
-        st_agent_f(a.hidden + row, (float) (total + old));
+        uint32_t old;
+        if (ll_get(a.hidden_ll + row, flow_tag(epoch, 2 * l), a.error, old))
+            ll_put(a.hidden_ll + row, __float_as_uint((float) (total + (double) __uint_as_float(old))),
+                   flow_tag(epoch, 2 * l + 1));
     }
-    flow_signal(a, l * kFlowPhases + kPhaseO, item, a.o_items);
 }
 
-__device__ __forceinline__ void flow_gateup(const FlowArgs &a, int l, int item)
+__device__ __forceinline__ void flow_gateup(const FlowArgs &a, int l, int item, uint32_t epoch)
 {
     __shared__ RowQ8 row;
     __shared__ double sPartial[kFlowWaves];
@@ -1451,9 +1612,9 @@ __device__ __forceinline__ void flow_gateup(const FlowArgs &a, int l, int item)
                                         lane, valid);
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (!flow_wait(a, l * kFlowPhases + kPhaseO))
+    RowSlice<4> slice;
+    if (!flow_hidden_slice(a, a.post_norm + a.norm_stride * l, flow_tag(epoch, 2 * l + 1), slice))
         return;
-    const RowSlice<4> slice = flow_row_slice(a, a.post_norm + a.norm_stride * l, false, false, 0);
     norm_q8_finish<4>(slice, a.width, a.epsilon, row, sPartial, nullptr, nullptr);
     int4 a0 = make_int4(0, 0, 0, 0), a1 = a0;
     double sa = 0.0;
@@ -1486,12 +1647,11 @@ __device__ __forceinline__ void flow_gateup(const FlowArgs &a, int l, int item)
         const uint16_t bits = scale_bits_from_amax(amax);
         const float sc = half_value(bits);
         const uint8_t byte = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);
-        flow_store_q8(a.act_q8, F, o, byte, bits, live);
+        flow_put_q8(a.act_ll, F, o, byte, bits, live, flow_tag(epoch, l));
     }
-    flow_signal(a, l * kFlowPhases + kPhaseGateUp, item, a.gate_up_items);
 }
 
-__device__ __forceinline__ void flow_down(const FlowArgs &a, int l, int item, uint32_t *sAct)
+__device__ __forceinline__ void flow_down(const FlowArgs &a, int l, int item, uint32_t epoch, uint32_t *sAct)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int W = a.width, F = a.intermediate, nb = F / kBlock;
@@ -1503,9 +1663,9 @@ __device__ __forceinline__ void flow_down(const FlowArgs &a, int l, int item, ui
         w[j] = load_block(a.down + a.down_stride * l, W, F, row, b, row < W && b < nb);
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (!flow_wait(a, l * kFlowPhases + kPhaseGateUp))
+    const int words = F / 4 + F / kBlock;
+    if (!flow_stage_ll<kFlowStagePieces>(a, a.act_ll, words, words - 1, flow_tag(epoch, l), sAct))
         return;
-    flow_stage_q8(a.act_q8, F, sAct);
     double acc = 0.0;
 #pragma unroll
     for (int j = 0; j < kFlowDownBlocks; ++j) {
@@ -1517,32 +1677,33 @@ __device__ __forceinline__ void flow_down(const FlowArgs &a, int l, int item, ui
     }
     const double total = wave_sum_d(acc);
     if (lane == 0 && row < W) {
-        const double old = (double) ld_agent_f(a.hidden + row);
-        st_agent_f(a.hidden + row, (float) (total + old));
+        uint32_t old;
+        if (ll_get(a.hidden_ll + row, flow_tag(epoch, 2 * l + 1), a.error, old))
+            ll_put(a.hidden_ll + row, __float_as_uint((float) (total + (double) __uint_as_float(old))),
+                   flow_tag(epoch, 2 * l + 2));
     }
-    flow_signal(a, l * kFlowPhases + kPhaseDown, item, a.down_items);
 }
 
-__device__ __forceinline__ void flow_final_norm(const FlowArgs &a)
+__device__ __forceinline__ void flow_final_norm(const FlowArgs &a, uint32_t epoch)
 {
     __shared__ RowQ8 row;
     __shared__ double sPartial[kFlowWaves];
-    if (!flow_wait(a, (a.layers - 1) * kFlowPhases + kPhaseDown))
+    RowSlice<4> slice;
+    if (!flow_hidden_slice(a, a.final_norm, flow_tag(epoch, 2 * a.layers), slice))
         return;
-    const RowSlice<4> slice = flow_row_slice(a, a.final_norm, false, false, 0);
-    norm_q8_finish<4>(slice, a.width, a.epsilon, row, sPartial, a.normalised, nullptr);
+    norm_q8_finish<4>(slice, a.width, a.epsilon, row, sPartial, nullptr, nullptr);
     const int t = threadIdx.x;
+    const uint32_t tag = flow_tag(epoch, 0);
     if (t * 4 < a.width) {
         uint32_t word;
         __builtin_memcpy(&word, row.q + t * 4, 4);
-        st_agent_u(a.head_q8 + t, word);
+        ll_put(a.head_ll + t, word, tag);
     }
     if (t < a.width / kBlock)
-        st_agent_u(a.head_q8 + a.width / 4 + t, half_bits((float) row.scale[t]));
-    flow_signal(a, a.layers * kFlowPhases, 0, 1);
+        ll_put(a.head_ll + a.width / 4 + t, half_bits((float) row.scale[t]), tag);
 }
 
-__device__ __forceinline__ void flow_lmhead(const FlowArgs &a, int item, uint32_t *sAct)
+__device__ __forceinline__ void flow_lmhead(const FlowArgs &a, int item, uint32_t epoch, uint32_t *sAct)
 {
     __shared__ unsigned long long sBest[kFlowWaves];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1555,9 +1716,9 @@ __device__ __forceinline__ void flow_lmhead(const FlowArgs &a, int item, uint32_
     for (int k = 0; k < kHeadRows; ++k)
         w[k] = load_block(a.embedding, V, a.width, r0 + k, lane, valid && r0 + k < V);
     __builtin_amdgcn_sched_barrier(0);
-    if (!flow_wait(a, a.layers * kFlowPhases))
+    const int words = a.width / 4 + a.width / kBlock;
+    if (!flow_stage_ll<kFlowRowPieces>(a, a.head_ll, words, words - 1, flow_tag(epoch, 0), sAct))
         return;
-    flow_stage_q8(a.head_q8, a.width, sAct);
     int4 a0, a1;
     double sa;
     lds_act_block(sAct, a.width, valid ? lane : 0, a0, a1, sa);
@@ -1584,17 +1745,17 @@ __device__ __forceinline__ void flow_lmhead(const FlowArgs &a, int item, uint32_
         if (c != 0)
             atomicMax(a.best + (item % kHeadSlots) * kHeadSlotStride, c);
     }
-    flow_signal(a, a.layers * kFlowPhases + 1, item, a.head_items);
+    flow_signal(a, kCounterHead, item, a.head_items);
 }
 
-__device__ __forceinline__ void flow_finalize(const FlowArgs &a)
+__device__ __forceinline__ void flow_finalize(const FlowArgs &a, uint32_t epoch)
 {
-    // every other item has read the position: the lm_head items (whose wait
-    // chains back through every working item) and the idle attention splits
+    // every other item has read the position and the epoch: the lm_head items
+    // (whose inputs chain back through every working item) and the idle
+    // attention splits
     const int position = *a.position;
-    const int groups = a.attn_items / a.attn_splits;
-    const int idle = a.layers * groups * (a.attn_splits - flow_plan(position + 1, a.attn_splits).splits);
-    if (!flow_wait(a, a.layers * kFlowPhases + 1) || (idle > 0 && !flow_wait(a, a.layers * kFlowPhases + 2)))
+    const int idle = a.attn_splits - flow_plan(position + 1, a.attn_splits).splits;
+    if (!flow_wait(a, kCounterHead) || (idle > 0 && !flow_wait(a, kCounterIdle)))
         return;
     const int t = threadIdx.x;
     if (t < 64) {
@@ -1609,13 +1770,16 @@ __device__ __forceinline__ void flow_finalize(const FlowArgs &a)
             if (a.sample)
                 a.sequence[position + 1] = token;
             *a.position = position + 1;
+            // the next launch's tags (24 bits of epoch; zero is never used, so
+            // words cleared to zero never match)
+            const uint32_t next = (epoch + 1) & 0xFFFFFFu;
+            *a.epoch = next == 0 ? 1u : next;
         }
     }
-    // every item has passed its wait: the flags start the next step lowered
+    // every waiter has passed its wait: the flags start the next step lowered
     // (completed sub-counters and tops went back to zero as they completed)
-    const int flags = (a.layers * kFlowPhases + kFlowExtraCounters) * kFlowFlagLines;
-    for (int i = t; i < flags; i += kFlowThreads)
-        st_agent_i(flow_line(a, i / kFlowFlagLines, 1 + i % kFlowFlagLines), 0);
+    if (t < kFlowCounters * kFlowFlagLines)
+        st_agent_i(flow_line(a, t / kFlowFlagLines, 1 + t % kFlowFlagLines), 0);
 }
 
 template <int C, int G>
@@ -1623,31 +1787,32 @@ __global__ __launch_bounds__(kFlowThreads) __attribute__((amdgpu_waves_per_eu(4)
 void flow_step_kernel(FlowArgs a)
 {
     __shared__ __attribute__((aligned(16))) uint32_t sAct[kFlowActWords];
+    const uint32_t epoch = *a.epoch;
     const int perLayer = a.qkv_items + a.attn_items + a.o_items + a.gate_up_items + a.down_items;
     int item = blockIdx.x;
     if (item < a.layers * perLayer) {
         const int l = item / perLayer;
         item -= l * perLayer;
         if (item < a.qkv_items)
-            return flow_qkv(a, l, item);
+            return flow_qkv(a, l, item, epoch);
         item -= a.qkv_items;
         if (item < a.attn_items)
-            return flow_attention<C, G>(a, l, item);
+            return flow_attention<C, G>(a, l, item, epoch);
         item -= a.attn_items;
         if (item < a.o_items)
-            return flow_o(a, l, item, sAct);
+            return flow_o(a, l, item, epoch, sAct);
         item -= a.o_items;
         if (item < a.gate_up_items)
-            return flow_gateup(a, l, item);
+            return flow_gateup(a, l, item, epoch);
         item -= a.gate_up_items;
-        return flow_down(a, l, item, sAct);
+        return flow_down(a, l, item, epoch, sAct);
     }
     item -= a.layers * perLayer;
     if (item == 0)
-        return flow_final_norm(a);
+        return flow_final_norm(a, epoch);
     if (item <= a.head_items)
-        return flow_lmhead(a, item - 1, sAct);
-    flow_finalize(a);
+        return flow_lmhead(a, item - 1, epoch, sAct);
+    flow_finalize(a, epoch);
 }
 
 } // namespace
@@ -1678,6 +1843,7 @@ bool flow_decode_supported(int layers, int width, int heads, int kv_heads, int h
     int channels = 0, group = 0;
     return fused_decode_supported(width, heads, kv_heads, head_dim, intermediate, max_positions)
            && attention_layout(head_dim, &channels, &group)
+           && layers <= kFlowMaxLayers
            && (int64_t) layers * (heads / group) <= kFlowSubLines            // idle-split sub-counters
            && (vocab + kFlowHeadRows - 1) / kFlowHeadRows <= kFlowSubLines * kFlowFanIn
            && intermediate / kBlock <= kFlowSubLines * kFlowFanIn && width % 4 == 0

@@ -84,8 +84,7 @@ struct HeadArgs {
 // reads from has finished, computes and publishes its outputs with
 // agent-scope (cross-L2 coherent) stores before counting itself done.
 constexpr int kFlowThreads = 512;
-constexpr int kFlowPhases = 5;        // per layer: qkv, attention, o, gate|up, down
-constexpr int kFlowExtraCounters = 3;  // after the layers: final norm, lm_head, idle attention splits
+constexpr int kFlowCounters = 2;       // the lm_head items, the idle attention splits
 // A counter is a tree of 128-byte lines: a top line, kFlowFlagLines completion
 // flags (waiters spread their polling over them) and kFlowSubLines
 // sub-counters of at most kFlowFanIn arrivals each.
@@ -94,10 +93,8 @@ constexpr int kFlowFanIn = 16;
 constexpr int kFlowFlagLines = 16;
 constexpr int kFlowSubLines = 1024;
 constexpr int kFlowCounterLines = 1 + kFlowFlagLines + kFlowSubLines;
-constexpr int64_t flow_counter_ints(int layers)
-{
-    return (int64_t) (kFlowPhases * layers + kFlowExtraCounters) * kFlowCounterLines * kFlowLineInts;
-}
+constexpr int64_t kFlowCounterInts = (int64_t) kFlowCounters * kFlowCounterLines * kFlowLineInts;
+constexpr int kFlowMaxLayers = 127;    // residual-row versions 0 .. 2 layers fit a tag's 8 bits
 
 struct FlowArgs {
     int layers, width, heads, kv_heads, head_dim, intermediate, vocab, max_positions;
@@ -114,17 +111,17 @@ struct FlowArgs {
     const float *cosines, *sines;
     uint32_t *sequence;
     int *position;
-    float *hidden;                            // the residual row
-    float *query;                             // the rotated q row
-    uint32_t *attn_q8;                        // Q8 of the attention row: bytes, then one word a block
-    uint32_t *act_q8;                         // Q8 of the GeGLU row: the same layout
-    uint32_t *head_q8;                        // Q8 of the final-norm row: the same layout
-    float *normalised;                        // the final-norm row
+    uint32_t *epoch;                          // the launch's tag epoch (never 0)
+    // rows handed between items, one tagged word (value | tag << 32) an element
+    uint64_t *hidden_ll;                      // the residual row [width]
+    uint64_t *q_ll;                           // the rotated q row [heads * head_dim]
+    uint64_t *k_ll, *v_ll;                    // this step's fp16 K and V rows, two halves a word
+    uint64_t *part_ll;                        // attention partial outputs [kDecodeSplits][q width] doubles
+    uint64_t *part_ml_ll;                     // their max and sum [kDecodeSplits][heads] double pairs
+    uint64_t *attn_ll, *act_ll, *head_ll;     // Q8 rows: bytes (four a word), then one scale word a block
     float *logits;
-    double *ws_o, *ws_ml;                     // attention partials (kDecodeSplits splits)
-    int *tickets;                             // attention head-group tickets
     unsigned long long *best;                 // argmax slots
-    int *counters;                            // kFlowPhases * layers + 2 counters, strided
+    int *counters;                            // kFlowCounters counter trees
     int *error;                               // nonzero after a wait gave up
     int attn_splits;                          // attention split items a head group
     int sample;                               // nonzero: the id goes to sequence[position + 1]

@@ -426,7 +426,12 @@ struct gq8_decoder {
     // the dataflow step (one launch a token)
     bool useFlow = false;
     bool flowSupported = false;
-    uint32_t *flowAttnQ8 = nullptr, *flowActQ8 = nullptr, *flowHeadQ8 = nullptr;
+    uint64_t *flowTagged = nullptr;  // the tagged rows, one allocation
+    size_t flowTaggedBytes = 0;
+    uint64_t *flowHidden = nullptr, *flowQ = nullptr, *flowK = nullptr, *flowV = nullptr;
+    uint64_t *flowPart = nullptr, *flowPartMl = nullptr, *flowAttn = nullptr, *flowAct = nullptr,
+             *flowHead = nullptr;
+    uint32_t *flowEpoch = nullptr;
     int *flowCounters = nullptr;
     int *flowError = nullptr;
     double *decodeO = nullptr, *decodeMl = nullptr;
@@ -706,15 +711,33 @@ extern "C" int gq8_decoder_create(const gq8_shape *shape, gq8_decoder **out)
     d->flowSupported = gq8::flow_decode_supported(s.layers, s.width, s.heads, s.kv_heads, s.head_dim,
                                                   s.intermediate, s.vocab, s.max_positions);
     {
-        const int64_t words = [](int64_t n) { return n / 4 + n / gq8::kBlock; }(d->maxInner);
-        GQ8_ALLOC(d->flowAttnQ8, words * sizeof(uint32_t));
-        GQ8_ALLOC(d->flowActQ8, words * sizeof(uint32_t));
-        GQ8_ALLOC(d->flowHeadQ8, words * sizeof(uint32_t));
-        GQ8_ALLOC(d->flowCounters, (size_t) gq8::flow_counter_ints(L) * sizeof(int));
+        // tagged rows (one 8-byte word an element), carved from one allocation
+        const auto q8Words = [](int64_t n) { return n / 4 + n / gq8::kBlock + 2; };
+        const int64_t sizes[] = {
+            W, d->qWidth, d->kvWidth / 2 + 2, d->kvWidth / 2 + 2,
+            (int64_t) gq8::kDecodeSplits * d->qWidth * 2, (int64_t) gq8::kDecodeSplits * s.heads * 4,
+            q8Words(d->qWidth), q8Words(s.intermediate), q8Words(W)};
+        int64_t total = 0;
+        for (int64_t n : sizes)
+            total += (n + 1) / 2 * 2; // 16-byte aligned parts
+        d->flowTaggedBytes = (size_t) total * sizeof(uint64_t);
+        GQ8_ALLOC(d->flowTagged, d->flowTaggedBytes);
+        uint64_t *part = d->flowTagged;
+        uint64_t **dst[] = {&d->flowHidden, &d->flowQ, &d->flowK, &d->flowV, &d->flowPart,
+                            &d->flowPartMl, &d->flowAttn, &d->flowAct, &d->flowHead};
+        for (int k = 0; k < 9; ++k) {
+            *dst[k] = part;
+            part += (sizes[k] + 1) / 2 * 2;
+        }
+        GQ8_ALLOC(d->flowEpoch, 64 * sizeof(uint32_t));
+        GQ8_ALLOC(d->flowCounters, (size_t) gq8::kFlowCounterInts * sizeof(int));
         GQ8_ALLOC(d->flowError, 64 * sizeof(int));
-        if (hipMemset(d->flowCounters, 0, (size_t) gq8::flow_counter_ints(L) * sizeof(int)) != hipSuccess
+        const uint32_t one = 1;
+        if (hipMemset(d->flowTagged, 0, d->flowTaggedBytes) != hipSuccess
+            || hipMemcpy(d->flowEpoch, &one, sizeof(one), hipMemcpyHostToDevice) != hipSuccess
+            || hipMemset(d->flowCounters, 0, (size_t) gq8::kFlowCounterInts * sizeof(int)) != hipSuccess
             || hipMemset(d->flowError, 0, sizeof(int)) != hipSuccess)
-            return cleanup(fail(GQ8_ERR_DEVICE, "flow counters: memset failed"));
+            return cleanup(fail(GQ8_ERR_DEVICE, "flow state: initialisation failed"));
     }
     d->fusedSupported = gq8::fused_decode_supported(s.width, s.heads, s.kv_heads, s.head_dim,
                                                     s.intermediate, s.max_positions);
@@ -1097,16 +1120,17 @@ int encode_flow_token(gq8_decoder *d, float *logits, bool sample)
     a.sines = d->sines;
     a.sequence = d->sequence;
     a.position = d->position;
-    a.hidden = d->hidden;
-    a.query = d->qkvRows;
-    a.attn_q8 = d->flowAttnQ8;
-    a.act_q8 = d->flowActQ8;
-    a.head_q8 = d->flowHeadQ8;
-    a.normalised = d->normalisedRows;
+    a.epoch = d->flowEpoch;
+    a.hidden_ll = d->flowHidden;
+    a.q_ll = d->flowQ;
+    a.k_ll = d->flowK;
+    a.v_ll = d->flowV;
+    a.part_ll = d->flowPart;
+    a.part_ml_ll = d->flowPartMl;
+    a.attn_ll = d->flowAttn;
+    a.act_ll = d->flowAct;
+    a.head_ll = d->flowHead;
     a.logits = logits;
-    a.ws_o = d->decodeO;
-    a.ws_ml = d->decodeMl;
-    a.tickets = d->counters;
     a.best = d->headBest;
     a.counters = d->flowCounters;
     a.error = d->flowError;
@@ -1116,8 +1140,9 @@ int encode_flow_token(gq8_decoder *d, float *logits, bool sample)
     return GQ8_OK;
 }
 
-// Reads and clears the dataflow step's error word; a set word means a step
-// gave up waiting, so the counters are reset as well.
+// Reads and clears the dataflow step's error word.  A set word means a step
+// gave up waiting: the counters and tagged rows are cleared and the epoch
+// moves on, so that nothing the failed step put is taken as current.
 int check_flow_error(gq8_decoder *d)
 {
     if (!d->flowSupported)
@@ -1127,8 +1152,14 @@ int check_flow_error(gq8_decoder *d)
     GQ8_HIP(hipMemcpy(&error, d->flowError, sizeof(int), hipMemcpyDeviceToHost));
     if (error == 0)
         return GQ8_OK;
-    const int L = d->shape.layers;
-    GQ8_HIP(hipMemset(d->flowCounters, 0, (size_t) gq8::flow_counter_ints(L) * sizeof(int)));
+    uint32_t epoch = 0;
+    GQ8_HIP(hipMemcpy(&epoch, d->flowEpoch, sizeof(epoch), hipMemcpyDeviceToHost));
+    epoch = (epoch + 1) & 0xFFFFFFu;
+    if (epoch == 0)
+        epoch = 1;
+    GQ8_HIP(hipMemcpy(d->flowEpoch, &epoch, sizeof(epoch), hipMemcpyHostToDevice));
+    GQ8_HIP(hipMemset(d->flowTagged, 0, d->flowTaggedBytes));
+    GQ8_HIP(hipMemset(d->flowCounters, 0, (size_t) gq8::kFlowCounterInts * sizeof(int)));
     GQ8_HIP(hipMemset(d->flowError, 0, sizeof(int)));
     GQ8_HIP(hipMemset(d->counters, 0, gq8::kDecodeCounters * sizeof(int)));
     GQ8_HIP(hipMemset(d->headBest, 0, gq8::kHeadSlots * gq8::kHeadSlotStride * sizeof(unsigned long long)));
