@@ -69,25 +69,31 @@ __device__ inline int dot32(const int4 &w0, const int4 &w1, const int4 &a0, cons
 // and adds the partner lane's share of them.  Returns the total of row
 // row_of_lane(lane) (every lane holds one; lanes whose low bits are zero are
 // the ones that store).
+// One halving step a lane bit, every index fixed at compile time (a runtime
+// row count turns v[i] into select chains over the whole array).
+template <int N, int Mask, int U>
+__device__ inline void reduce_halving(double (&v)[U], int lane)
+{
+    if constexpr (N > 1) {
+        const bool upper = (lane & Mask) != 0;
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i) {
+            const double keep = upper ? v[i + N / 2] : v[i];
+            const double send = upper ? v[i] : v[i + N / 2];
+            v[i] = keep + __shfl_xor(send, Mask);
+        }
+        reduce_halving<N / 2, Mask / 2, U>(v, lane);
+    } else if constexpr (Mask >= 1) {
+        v[0] += __shfl_xor(v[0], Mask);
+        reduce_halving<1, Mask / 2, U>(v, lane);
+    }
+}
+
 template <int U>
 __device__ inline double reduce_rows(double (&v)[U], int lane)
 {
-    int n = U;
-#pragma unroll
-    for (int mask = 32; mask >= 1; mask >>= 1) {
-        if (n > 1) {
-            const bool upper = (lane & mask) != 0;
-#pragma unroll
-            for (int i = 0; i < n / 2; ++i) {
-                const double keep = upper ? v[i + n / 2] : v[i];
-                const double send = upper ? v[i] : v[i + n / 2];
-                v[i] = keep + __shfl_xor(send, mask);
-            }
-            n /= 2;
-        } else {
-            v[0] += __shfl_xor(v[0], mask);
-        }
-    }
+    static_assert(U >= 1 && U <= 64 && (U & (U - 1)) == 0, "a power of two rows");
+    reduce_halving<U, 32, U>(v, lane);
     return v[0];
 }
 
@@ -498,6 +504,29 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
         for (int i = 0; i < C; ++i)
             q[g][i] = (double) __uint_as_float(__float_as_uint(a.query[(h0 + g) * hd + c0 + i]) & keep);
 
+    int kvOffset[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+        kvOffset[g] = ((h0 + g) / perKv) * hd + c0;
+
+    // While at most kDecodeSplits rounds of keys are attended, split s is the
+    // one round [64 s, 64 s + 64): its rows are loaded before the position
+    // arrives (rows past the position are read, inside the cache, and never
+    // used), so the two loads do not wait on each other.
+    uint16_t kh[kScoreBatch][G][C], vh[kScoreBatch][G][C];
+#pragma unroll
+    for (int b = 0; b < kScoreBatch; ++b) {
+        const int j = min(split * kRoundKeys + wave + b * kAttnWaves, a.max_positions - 1);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            load_halves<C>(a.key_cache + (int64_t) j * kvWidth + kvOffset[g], kh[b][g]);
+            load_halves<C>(a.value_cache + (int64_t) j * kvWidth + kvOffset[g], vh[b][g]);
+        }
+    }
+    // keeps the loads above the position-dependent exit: the compiler would
+    // otherwise sink them below it, after the position's own round trip
+    asm volatile("" ::: "memory");
+
     const int keyCount = *a.position + 1;
     const SplitPlan plan = plan_splits(keyCount);
     if (split >= plan.splits)
@@ -506,14 +535,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
     const int n = min(plan.perSplit, keyCount - k0);
     const uint16_t *keys = a.key_cache + (int64_t) k0 * kvWidth;
     const uint16_t *values = a.value_cache + (int64_t) k0 * kvWidth;
-    int kvOffset[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-        kvOffset[g] = ((h0 + g) / perKv) * hd + c0;
 
     // a round's rows for this wave: keys r0 + wave + 8 b, clamped into range
     // (the clamped duplicates are masked where they are used)
-    uint16_t kh[kScoreBatch][G][C], vh[kScoreBatch][G][C];
     auto load_round = [&](const uint16_t *base, int r0, uint16_t (&dst)[kScoreBatch][G][C]) {
 #pragma unroll
         for (int b = 0; b < kScoreBatch; ++b) {
@@ -523,8 +547,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
                 load_halves<C>(base + (int64_t) j * kvWidth + kvOffset[g], dst[b][g]);
         }
     };
-    load_round(keys, 0, kh);
-    load_round(values, 0, vh);
+    if (plan.perSplit != kRoundKeys) { // longer splits: the first round again, from k0
+        load_round(keys, 0, kh);
+        load_round(values, 0, vh);
+    }
 
     for (int r0 = 0; r0 < n; r0 += kRoundKeys) {
         if (r0 > 0)
@@ -612,6 +638,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
         store_agent(a.ws_ml + (split * heads + h0 + t) * 2, sMax[t]);
         store_agent(a.ws_ml + (split * heads + h0 + t) * 2 + 1, sSum[t]);
     }
+    if (a.partials_only)
+        return; // o_merge_kernel merges them after this launch
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // the stores have completed
     __syncthreads();
     if (t == 0)
@@ -679,6 +707,149 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
     }
     if (t == 0) // ready for the next launch
         __hip_atomic_store(a.counter + group, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---- o_proj with the attention merge ---------------------------------------------
+// A workgroup of eight waves owns 16 rows of o (two a wave).  It issues its
+// weight loads, then merges the attention splits of every head exactly as the
+// attention kernel's last workgroup would (MultiQueryAttention.h:43-49: the
+// splits rescaled to the row maximum, in split order, the sums divided by the
+// total), quantizes the attention row into LDS (thread t owns elements
+// 4 t .. 4 t + 3, eight threads a 32-block) and takes its rows of the product
+// (Linear.h:284-298, + residual).  Every workgroup repeats the merge; it
+// saves the attention kernel's ticket, its last workgroup's reads and a
+// dependent round of stores.
+constexpr int kOMergeThreads = 512;
+constexpr int kOMergeRows = 16;
+constexpr int kOMergeBatch = 8; // splits a thread loads at once
+
+__global__ __launch_bounds__(kOMergeThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void o_merge_kernel(OMergeArgs a)
+{
+    __shared__ RowQ8 row;
+    __shared__ double sFactor[kOMergeMaxHeads][kDecodeSplits];
+    __shared__ double sPart[kOMergeMaxHeads][kDecodeSplits];
+    __shared__ double sTotal[kOMergeMaxHeads];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int hd = a.head_dim, heads = a.heads, qWidth = heads * hd, nb = qWidth / kBlock;
+    const int W = a.width;
+    const int r0 = blockIdx.x * kOMergeRows + wave * 2;
+    const bool valid = lane < nb;
+    // loads in the order they are consumed (a wave's loads complete in
+    // order): the (max, sum) pairs, the partials, then the o rows
+    // thread t's four elements of the attention row: the partials of the first
+    // kOMergeBatch splits and four (max, sum) pairs are loaded before the
+    // position (so the split count) arrives; unused ones are never read
+    const bool live = t * 4 < qWidth;
+    const int e0 = live ? t * 4 : 0;
+    const int h = e0 / hd;
+    double2 part[kOMergeBatch][2]; // the partials were stored by the previous launch
+    auto load_batch = [&](int s0, int last) {
+#pragma unroll
+        for (int u = 0; u < kOMergeBatch; ++u) {
+            const int sp = min(s0 + u, last);
+            const double2 *src = reinterpret_cast<const double2 *>(a.ws_o + (int64_t) sp * qWidth + e0);
+            part[u][0] = src[0];
+            part[u][1] = src[1];
+        }
+    };
+    const int allPairs = kDecodeSplits * heads; // (split, head) pairs, split-major as stored
+    double2 ml[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        ml[k] = *reinterpret_cast<const double2 *>(a.ws_ml + min(t + k * kOMergeThreads, allPairs - 1) * 2);
+    load_batch(0, kDecodeSplits - 1);
+    WeightBlock w[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+        w[k] = load_block(a.weights, W, qWidth, r0 + k, lane, valid && r0 + k < W);
+    __builtin_amdgcn_sched_barrier(0);
+    const int splits = plan_splits(*a.position + 1).splits;
+    const int pairs = heads * splits;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = t + k * kOMergeThreads;
+        if (i < pairs) {
+            sFactor[i % heads][i / heads] = ml[k].x;
+            sPart[i % heads][i / heads] = ml[k].y;
+        }
+    }
+    __syncthreads();
+    // each head's maximum, the splits' factors and the total, in split order
+    __shared__ double sMaxH[kOMergeMaxHeads];
+    if (t < heads) {
+        double largest = -INFINITY;
+        for (int sp = 0; sp < splits; ++sp)
+            largest = fmax(largest, sFactor[t][sp]);
+        sMaxH[t] = largest;
+    }
+    __syncthreads();
+    for (int i = t; i < pairs; i += kOMergeThreads) {
+        const int hh = i / splits, sp = i % splits;
+        sFactor[hh][sp] = exp(sFactor[hh][sp] - sMaxH[hh]);
+    }
+    __syncthreads();
+    if (t < heads) {
+        double total = 0.0;
+        for (int sp = 0; sp < splits; ++sp)
+            total += sPart[t][sp] * sFactor[t][sp];
+        sTotal[t] = total;
+    }
+    __syncthreads();
+
+    // the merged elements, then their Q8
+    double weighted[4] = {0.0, 0.0, 0.0, 0.0};
+    for (int s0 = 0; s0 < splits; s0 += kOMergeBatch) {
+        if (s0 > 0)
+            load_batch(s0, splits - 1);
+#pragma unroll
+        for (int u = 0; u < kOMergeBatch; ++u)
+            if (s0 + u < splits) {
+                const double f = sFactor[h][s0 + u];
+                weighted[0] += part[u][0].x * f;
+                weighted[1] += part[u][0].y * f;
+                weighted[2] += part[u][1].x * f;
+                weighted[3] += part[u][1].y * f;
+            }
+    }
+    float v[4];
+    float amax = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        v[k] = live ? (float) (weighted[k] / sTotal[h]) : 0.f;
+        amax = fmaxf(amax, fabsf(v[k]));
+    }
+    for (int mask = 1; mask < kBlock / 4; mask <<= 1)
+        amax = fmaxf(amax, __shfl_xor(amax, mask));
+    const uint16_t bits = scale_bits_from_amax(amax);
+    const float sc = half_value(bits);
+    const float inverse = bits ? 1.0f / sc : 0.f;
+    if (live) {
+        int packed = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            packed |= ((bits ? quantize_value(v[k], sc, inverse) : 0) & 0xFF) << (8 * k);
+        __builtin_memcpy(row.q + e0, &packed, 4);
+        if ((t & 7) == 0)
+            row.scale[e0 / kBlock] = (double) sc;
+    }
+    __syncthreads();
+
+    int4 a0 = make_int4(0, 0, 0, 0), a1 = a0;
+    double sa = 0.0;
+    if (valid) {
+        a0 = reinterpret_cast<const int4 *>(row.q + lane * kBlock)[0];
+        a1 = reinterpret_cast<const int4 *>(row.q + lane * kBlock)[1];
+        sa = row.scale[lane];
+    }
+    double y[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+        y[k] = block_term(w[k], a0, a1, sa);
+    const double total = reduce_rows<2>(y, lane);
+    const int r = r0 + row_of_lane<2>(lane);
+    if (stores_row<2>(lane) && r < W)
+        a.hidden[r] = (float) (total + (double) a.hidden[r]);
 }
 
 // ---- gate|up + GeGLU + Q8 -----------------------------------------------------------
@@ -1939,6 +2110,22 @@ hipError_t launch_attention(const AttentionArgs &a, hipStream_t stream)
         hipLaunchKernelGGL((attention_kernel<1, 1>), grid, dim3(kAttnThreads), 0, stream, a);
     else
         hipLaunchKernelGGL((attention_kernel<1, 2>), grid, dim3(kAttnThreads), 0, stream, a);
+    return hipGetLastError();
+}
+
+bool o_merge_supported(int heads, int head_dim)
+{
+    const int qWidth = heads * head_dim;
+    return heads <= kOMergeMaxHeads && qWidth % kBlock == 0 && qWidth <= kFusedMaxWidth
+           && qWidth <= 4 * kOMergeThreads && head_dim % 4 == 0;
+}
+
+hipError_t launch_o_merge(const OMergeArgs &a, hipStream_t stream)
+{
+    if (!o_merge_supported(a.heads, a.head_dim) || a.width <= 0)
+        return hipErrorInvalidValue;
+    const int grid = (a.width + kOMergeRows - 1) / kOMergeRows;
+    hipLaunchKernelGGL(o_merge_kernel, dim3(grid), dim3(kOMergeThreads), 0, stream, a);
     return hipGetLastError();
 }
 

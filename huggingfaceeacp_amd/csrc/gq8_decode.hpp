@@ -40,12 +40,27 @@ struct AttentionArgs {
     const float *query;
     const uint16_t *key_cache, *value_cache;
     int heads, kv_heads, head_dim;
+    int max_positions;        // rows of the cache (the bound of speculative reads)
     const int *position;      // keys [0, *position] are attended
     float scale;
     double *ws_o, *ws_ml;     // kDecodeSplits partials
     int *counter;             // one a head group (kDecodeCounters), zero between launches
     float *out;               // optional fp32 row
     uint8_t *q8;              // Q8 row for o_proj
+    int partials_only;        // nonzero: store the split partials and stop (o_merge merges them)
+};
+
+// o_proj fed by the attention partials: every workgroup merges the splits
+// itself (the same arithmetic as the attention kernel's merge), quantizes the
+// attention row into LDS and takes its rows of the product (+ residual).
+constexpr int kOMergeMaxHeads = 32;
+struct OMergeArgs {
+    const double *ws_o, *ws_ml;  // the attention kernel's partials
+    const int *position;
+    int heads, head_dim;
+    const uint8_t *weights;      // o, Int8Blocks [width, heads * head_dim]
+    int width;
+    float *hidden;               // residual row, updated in place
 };
 
 struct GateUpArgs {
@@ -141,6 +156,8 @@ size_t decode_workspace_bytes(int heads, int head_dim);
 
 hipError_t launch_qkv_rope(const QkvArgs &a, hipStream_t stream);
 hipError_t launch_attention(const AttentionArgs &a, hipStream_t stream);
+bool o_merge_supported(int heads, int head_dim);
+hipError_t launch_o_merge(const OMergeArgs &a, hipStream_t stream);
 hipError_t launch_gateup_geglu(const GateUpArgs &a, hipStream_t stream);
 hipError_t launch_final_norm(const HeadArgs &a, hipStream_t stream);    // one workgroup
 hipError_t launch_lmhead_argmax(const HeadArgs &a, hipStream_t stream); // logits + packed maximum

@@ -1216,6 +1216,7 @@ int encode_fused_token(gq8_decoder *d, float *logits, bool sample)
         at.heads = s.heads;
         at.kv_heads = s.kv_heads;
         at.head_dim = s.head_dim;
+        at.max_positions = s.max_positions;
         at.position = d->position;
         at.scale = 1.f / std::sqrt((float) s.head_dim);
         at.ws_o = d->decodeO;
@@ -1223,12 +1224,29 @@ int encode_fused_token(gq8_decoder *d, float *logits, bool sample)
         at.counter = d->counters;
         at.out = debugValues(1, l);
         at.q8 = d->x8;
+        // the o product merges the attention splits itself, except for the
+        // debug views, which need the merged row
+        const bool merged = !dbg && gq8::o_merge_supported(s.heads, s.head_dim);
+        at.partials_only = merged ? 1 : 0;
         GQ8_STAGE(kStageAttention, gq8::launch_attention(at, st));
         if (dbg && copy_last_q8_row(d, d->x8, 1, d->qWidth, debugQ8(1, l)))
             return GQ8_ERR_DEVICE;
 
-        GQ8_STAGE(kStageO, gq8::launch_q8_product(d->x8, 1, 0, 1, d->out[l], d->qWidth, W,
-                                                  d->hidden, W, 1, st));
+        if (merged) {
+            gq8::OMergeArgs om{};
+            om.ws_o = d->decodeO;
+            om.ws_ml = d->decodeMl;
+            om.position = d->position;
+            om.heads = s.heads;
+            om.head_dim = s.head_dim;
+            om.weights = d->out[l];
+            om.width = W;
+            om.hidden = d->hidden;
+            GQ8_STAGE(kStageO, gq8::launch_o_merge(om, st));
+        } else {
+            GQ8_STAGE(kStageO, gq8::launch_q8_product(d->x8, 1, 0, 1, d->out[l], d->qWidth, W,
+                                                      d->hidden, W, 1, st));
+        }
 
         gq8::GateUpArgs g{};
         g.hidden = d->hidden;
