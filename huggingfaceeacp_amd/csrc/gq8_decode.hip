@@ -30,6 +30,8 @@
 
 #include <cfloat>
 
+#include "gq8_lanes.hpp"
+
 namespace gq8 {
 namespace {
 
@@ -38,16 +40,25 @@ constexpr int kWaves = kThreads / 64;
 
 __device__ inline double wave_sum_d(double v)
 {
-    for (int mask = 32; mask >= 1; mask >>= 1)
-        v += __shfl_xor(v, mask);
-    return v;
+    return sum_lanes<32>(v);
 }
 
 __device__ inline double wave_max_d(double v)
 {
-    for (int mask = 32; mask >= 1; mask >>= 1)
-        v = fmax(v, __shfl_xor(v, mask));
-    return v;
+    return max_lanes<32>(v);
+}
+
+// The merge weights of one head's key splits (MultiQueryAttention.h:43-49),
+// one split a lane: lane sp < splits holds split sp's (max, sum).  Returns
+// the split's factor exp(max - row max) and leaves the row's total, the sum
+// of sum x factor, in `total` (every lane).  Every merge of split partials
+// uses this, so they all agree bit for bit.
+__device__ inline double merge_factor(double m, double s, bool live, double &total)
+{
+    const double rowMax = wave_max_d(live ? m : -INFINITY);
+    const double f = live ? exp(m - rowMax) : 0.0;
+    total = wave_sum_d(live ? s * f : 0.0);
+    return f;
 }
 
 __device__ inline int dot32(const int4 &w0, const int4 &w1, const int4 &a0, const int4 &a1)
@@ -80,11 +91,11 @@ __device__ inline void reduce_halving(double (&v)[U], int lane)
         for (int i = 0; i < N / 2; ++i) {
             const double keep = upper ? v[i + N / 2] : v[i];
             const double send = upper ? v[i] : v[i + N / 2];
-            v[i] = keep + __shfl_xor(send, Mask);
+            v[i] = keep + xor_lane<Mask>(send);
         }
         reduce_halving<N / 2, Mask / 2, U>(v, lane);
     } else if constexpr (Mask >= 1) {
-        v[0] += __shfl_xor(v[0], Mask);
+        v[0] += xor_lane<Mask>(v[0]);
         reduce_halving<1, Mask / 2, U>(v, lane);
     }
 }
@@ -253,8 +264,7 @@ __device__ void norm_q8_finish(const RowSlice<E> &r, int width, float epsilon, R
         n[k] = r.active ? norm_value(v[k], scale, r.w[k]) : 0.f;
         amax = fmaxf(amax, fabsf(n[k]));
     }
-    for (int mask = 1; mask < kBlock / E; mask <<= 1)
-        amax = fmaxf(amax, __shfl_xor(amax, mask));
+    amax = max_lanes<kBlock / E / 2>(amax);
     const uint16_t bits = scale_bits_from_amax(amax);
     const float s = half_value(bits);
     const float inverse = bits ? 1.0f / s : 0.f;
@@ -375,7 +385,7 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a)
     double rowTotal[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; ++r)
-        rowTotal[r] = __shfl(total, lane_of_row<kRows>(r));
+        rowTotal[r] = lane_value(total, lane_of_row<kRows>(r));
 #pragma unroll
     for (int p = 0; p < kPairsPerWave; ++p) {
         const double yLo = rowTotal[2 * p], yHi = rowTotal[2 * p + 1];
@@ -480,7 +490,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
     __shared__ double sScore[G][kMaxSplitKeys];
     __shared__ double sAcc[kAttnWaves][kMaxGroupWidth];
     __shared__ double sMax[G], sSum[G];
-    __shared__ double sSplitMax[G][kDecodeSplits], sSplitSum[G][kDecodeSplits];
+    __shared__ double sSplitMax[G][kDecodeSplits];
     __shared__ int sLast;
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -649,31 +659,19 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
     if (!sLast)
         return;
 
-    // the merge of the group's splits
+    // the merge of the group's splits: wave g takes head h0 + g
     const int splits = plan.splits;
-    if (t < G * splits) {
-        const int g = t / splits, sp = t % splits;
-        sSplitMax[g][sp] = load_agent(a.ws_ml + (sp * heads + h0 + g) * 2);
-        sSplitSum[g][sp] = load_agent(a.ws_ml + (sp * heads + h0 + g) * 2 + 1);
-    }
-    __syncthreads();
-    if (t < G) {
-        double largest = -INFINITY;
-        for (int sp = 0; sp < splits; ++sp)
-            largest = fmax(largest, sSplitMax[t][sp]);
-        sMax[t] = largest;
-    }
-    __syncthreads();
-    if (t < G * splits) {
-        const int g = t / splits, sp = t % splits;
-        sSplitMax[g][sp] = exp(sSplitMax[g][sp] - sMax[g]); // now the split's factor
-    }
-    __syncthreads();
-    if (t < G) {
-        double total = 0.0;
-        for (int sp = 0; sp < splits; ++sp)
-            total += sSplitSum[t][sp] * sSplitMax[t][sp];
-        sSum[t] = total;
+    if (wave < G) {
+        const bool liveSplit = lane < splits;
+        const int sp = liveSplit ? lane : 0;
+        const double m = load_agent(a.ws_ml + (sp * heads + h0 + wave) * 2);
+        const double sum = load_agent(a.ws_ml + (sp * heads + h0 + wave) * 2 + 1);
+        double total;
+        const double f = merge_factor(m, sum, liveSplit, total);
+        if (liveSplit)
+            sSplitMax[wave][sp] = f; // now the split's factor
+        if (lane == 0)
+            sSum[wave] = total;
     }
     __syncthreads();
     if (t >= ((groupWidth + 63) / 64) * 64)
@@ -696,8 +694,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
     if (a.out && t < groupWidth)
         a.out[idx] = v;
     float amax = fabsf(v);
-    for (int mask = 16; mask >= 1; mask >>= 1)
-        amax = fmaxf(amax, __shfl_xor(amax, mask));
+    amax = max_lanes<16>(amax);
     if (t < groupWidth) { // whole 32-blocks: groupWidth is a multiple of 32
         const uint16_t bits = scale_bits_from_amax(amax);
         const float sc = half_value(bits);
@@ -728,7 +725,6 @@ void o_merge_kernel(OMergeArgs a)
 {
     __shared__ RowQ8 row;
     __shared__ double sFactor[kOMergeMaxHeads][kDecodeSplits];
-    __shared__ double sPart[kOMergeMaxHeads][kDecodeSplits];
     __shared__ double sTotal[kOMergeMaxHeads];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int hd = a.head_dim, heads = a.heads, qWidth = heads * hd, nb = qWidth / kBlock;
@@ -736,9 +732,9 @@ void o_merge_kernel(OMergeArgs a)
     const int r0 = blockIdx.x * kOMergeRows + wave * 2;
     const bool valid = lane < nb;
     // loads in the order they are consumed (a wave's loads complete in
-    // order): the (max, sum) pairs, the partials, then the o rows
-    // thread t's four elements of the attention row: the partials of the first
-    // kOMergeBatch splits and four (max, sum) pairs are loaded before the
+    // order): the (max, sum) pairs, the partials, the o rows, the residual.
+    // Thread t's four elements of the attention row: the partials of the first
+    // kOMergeBatch splits, and every split's (max, sum), are loaded before the
     // position (so the split count) arrives; unused ones are never read
     const bool live = t * 4 < qWidth;
     const int e0 = live ? t * 4 : 0;
@@ -753,47 +749,34 @@ void o_merge_kernel(OMergeArgs a)
             part[u][1] = src[1];
         }
     };
-    const int allPairs = kDecodeSplits * heads; // (split, head) pairs, split-major as stored
-    double2 ml[4];
+    // wave w takes heads w, w + 8, ...: lane sp holds split sp's (max, sum)
+    constexpr int kHeadsPerWave = kOMergeMaxHeads / (kOMergeThreads / 64);
+    double2 ml[kHeadsPerWave];
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-        ml[k] = *reinterpret_cast<const double2 *>(a.ws_ml + min(t + k * kOMergeThreads, allPairs - 1) * 2);
+    for (int k = 0; k < kHeadsPerWave; ++k) {
+        const int hh = min(wave + k * (kOMergeThreads / 64), heads - 1);
+        ml[k] = *reinterpret_cast<const double2 *>(a.ws_ml + (lane * heads + hh) * 2);
+    }
     load_batch(0, kDecodeSplits - 1);
     WeightBlock w[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k)
         w[k] = load_block(a.weights, W, qWidth, r0 + k, lane, valid && r0 + k < W);
+    const int r = r0 + row_of_lane<2>(lane);
+    const bool stores = stores_row<2>(lane) && r < W;
+    const float old = a.hidden[stores ? r : 0]; // the residual, read with the rest
     __builtin_amdgcn_sched_barrier(0);
     const int splits = plan_splits(*a.position + 1).splits;
-    const int pairs = heads * splits;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int i = t + k * kOMergeThreads;
-        if (i < pairs) {
-            sFactor[i % heads][i / heads] = ml[k].x;
-            sPart[i % heads][i / heads] = ml[k].y;
+    for (int k = 0; k < kHeadsPerWave; ++k) {
+        const int hh = wave + k * (kOMergeThreads / 64);
+        if (hh < heads) {
+            double total;
+            const double f = merge_factor(ml[k].x, ml[k].y, lane < splits, total);
+            sFactor[hh][lane] = f;
+            if (lane == 0)
+                sTotal[hh] = total;
         }
-    }
-    __syncthreads();
-    // each head's maximum, the splits' factors and the total, in split order
-    __shared__ double sMaxH[kOMergeMaxHeads];
-    if (t < heads) {
-        double largest = -INFINITY;
-        for (int sp = 0; sp < splits; ++sp)
-            largest = fmax(largest, sFactor[t][sp]);
-        sMaxH[t] = largest;
-    }
-    __syncthreads();
-    for (int i = t; i < pairs; i += kOMergeThreads) {
-        const int hh = i / splits, sp = i % splits;
-        sFactor[hh][sp] = exp(sFactor[hh][sp] - sMaxH[hh]);
-    }
-    __syncthreads();
-    if (t < heads) {
-        double total = 0.0;
-        for (int sp = 0; sp < splits; ++sp)
-            total += sPart[t][sp] * sFactor[t][sp];
-        sTotal[t] = total;
     }
     __syncthreads();
 
@@ -819,8 +802,7 @@ void o_merge_kernel(OMergeArgs a)
         v[k] = live ? (float) (weighted[k] / sTotal[h]) : 0.f;
         amax = fmaxf(amax, fabsf(v[k]));
     }
-    for (int mask = 1; mask < kBlock / 4; mask <<= 1)
-        amax = fmaxf(amax, __shfl_xor(amax, mask));
+    amax = max_lanes<kBlock / 4 / 2>(amax);
     const uint16_t bits = scale_bits_from_amax(amax);
     const float sc = half_value(bits);
     const float inverse = bits ? 1.0f / sc : 0.f;
@@ -847,9 +829,8 @@ void o_merge_kernel(OMergeArgs a)
     for (int k = 0; k < 2; ++k)
         y[k] = block_term(w[k], a0, a1, sa);
     const double total = reduce_rows<2>(y, lane);
-    const int r = r0 + row_of_lane<2>(lane);
-    if (stores_row<2>(lane) && r < W)
-        a.hidden[r] = (float) (total + (double) a.hidden[r]);
+    if (stores)
+        a.hidden[r] = (float) (total + (double) old);
 }
 
 // ---- gate|up + GeGLU + Q8 -----------------------------------------------------------
@@ -911,8 +892,7 @@ void gateup_geglu_kernel(GateUpArgs a)
         if (a.debug_activated)
             a.debug_activated[o] = v;
         float amax = fabsf(v);
-        for (int mask = 16; mask >= 1; mask >>= 1)
-            amax = fmaxf(amax, __shfl_xor(amax, mask));
+        amax = max_lanes<16>(amax);
         const uint16_t bits = scale_bits_from_amax(amax);
         const float sc = half_value(bits);
         a.q8[o] = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);
@@ -948,11 +928,7 @@ __device__ inline unsigned long long candidate_key(float value, uint32_t index)
 
 __device__ inline unsigned long long fold_wave_max(unsigned long long c)
 {
-    for (int mask = 32; mask >= 1; mask >>= 1) {
-        const unsigned long long other = __shfl_xor(c, mask);
-        c = other > c ? other : c;
-    }
-    return c;
+    return max_lanes<32>(c);
 }
 
 __global__ __launch_bounds__(kThreads) void final_norm_kernel(HeadArgs a)
@@ -1393,7 +1369,7 @@ __device__ __forceinline__ void flow_qkv(const FlowArgs &a, int l, int item, uin
     double rowTotal[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; ++r)
-        rowTotal[r] = __shfl(total, lane_of_row<kRows>(r));
+        rowTotal[r] = lane_value(total, lane_of_row<kRows>(r));
     // lane 0: the wave's two pairs are the consecutive elements (i, i + 1) and
     // (i + half, i + half + 1) of one head
     if (lane == 0 && firstPair < pairs) {
@@ -1485,7 +1461,7 @@ __device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int ite
     __shared__ double sScore[G][kMaxSplitKeys];
     __shared__ double sAcc[kAttnWaves][kMaxGroupWidth];
     __shared__ double sMax[G], sSum[G];
-    __shared__ double sSplitMax[G][kDecodeSplits], sSplitSum[G][kDecodeSplits];
+    __shared__ double sSplitMax[G][kDecodeSplits];
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int hd = a.head_dim, kvWidth = a.kv_heads * hd;
@@ -1660,40 +1636,25 @@ __device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int ite
         return;
     }
 
-    if (t < G * splits) {
-        const int g = t / splits, sp = t % splits;
-        double m = sMax[g], s = sSum[g];
-        if (sp != split) {
-            const int ml = (sp * heads + h0 + g) * 4, mlWords = kDecodeSplits * heads * 4;
+    if (wave < G) { // wave g takes head h0 + g, one split a lane
+        const bool liveSplit = lane < splits;
+        double m = sMax[wave], sum = sSum[wave];
+        if (liveSplit && lane != split) {
+            const int ml = (lane * heads + h0 + wave) * 4, mlWords = kDecodeSplits * heads * 4;
             uint32_t w[4];
             ok = ll_get_pieces<2>(a.part_ml_ll, ml, mlWords, tag, a.error, w);
             m = __longlong_as_double((long long) (((uint64_t) w[1] << 32) | w[0]));
-            s = __longlong_as_double((long long) (((uint64_t) w[3] << 32) | w[2]));
+            sum = __longlong_as_double((long long) (((uint64_t) w[3] << 32) | w[2]));
         }
-        sSplitMax[g][sp] = m;
-        sSplitSum[g][sp] = s;
+        double total;
+        const double f = merge_factor(m, sum, liveSplit, total);
+        if (liveSplit)
+            sSplitMax[wave][lane] = f;
+        if (lane == 0)
+            sSum[wave] = total;
     }
     if (__syncthreads_or(!ok))
         return;
-    if (t < G) {
-        double largest = -INFINITY;
-        for (int sp = 0; sp < splits; ++sp)
-            largest = fmax(largest, sSplitMax[t][sp]);
-        sMax[t] = largest;
-    }
-    __syncthreads();
-    if (t < G * splits) {
-        const int g = t / splits, sp = t % splits;
-        sSplitMax[g][sp] = exp(sSplitMax[g][sp] - sMax[g]);
-    }
-    __syncthreads();
-    if (t < G) {
-        double total = 0.0;
-        for (int sp = 0; sp < splits; ++sp)
-            total += sSplitSum[t][sp] * sSplitMax[t][sp];
-        sSum[t] = total;
-    }
-    __syncthreads();
     const bool live = t < groupWidth;
     const int g = min(t / hd, G - 1);
     double weighted = 0.0;
@@ -1725,8 +1686,7 @@ __device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int ite
     const int idx = h0 * hd + t;
     const float v = live ? (float) (weighted / sSum[g]) : 0.f;
     float amax = fabsf(v);
-    for (int mask = 16; mask >= 1; mask >>= 1)
-        amax = fmaxf(amax, __shfl_xor(amax, mask));
+    amax = max_lanes<16>(amax);
     const uint16_t bits = scale_bits_from_amax(amax);
     const float sc = half_value(bits);
     const uint8_t byte = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);
@@ -1813,8 +1773,7 @@ __device__ __forceinline__ void flow_gateup(const FlowArgs &a, int l, int item, 
         const int o = item * kBlock + (live ? threadIdx.x : 0);
         const float v = live ? geglu(sGate[threadIdx.x & 31], sUp[threadIdx.x & 31]) : 0.f;
         float amax = fabsf(v);
-        for (int mask = 16; mask >= 1; mask >>= 1)
-            amax = fmaxf(amax, __shfl_xor(amax, mask));
+        amax = max_lanes<16>(amax);
         const uint16_t bits = scale_bits_from_amax(amax);
         const float sc = half_value(bits);
         const uint8_t byte = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);

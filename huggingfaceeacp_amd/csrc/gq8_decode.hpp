@@ -53,7 +53,7 @@ struct AttentionArgs {
 // o_proj fed by the attention partials: every workgroup merges the splits
 // itself (the same arithmetic as the attention kernel's merge), quantizes the
 // attention row into LDS and takes its rows of the product (+ residual).
-constexpr int kOMergeMaxHeads = 32;
+constexpr int kOMergeMaxHeads = 16;
 struct OMergeArgs {
     const double *ws_o, *ws_ml;  // the attention kernel's partials
     const int *position;

@@ -7,6 +7,7 @@
 // the CPU oracle is in gq8_numerics.hpp.
 #include "gq8_kernels.hpp"
 #include "gq8_numerics.hpp"
+#include "gq8_lanes.hpp"
 
 #include <algorithm>
 #include <cfloat>
@@ -44,18 +45,15 @@ __device__ inline void quantize_in_group(float value, int lane32, uint8_t *byte,
         *scaleSlot = bits;
 }
 
+// whole-wave butterflies (every caller is a whole wave)
 __device__ inline double wave_sum(double v)
 {
-    for (int mask = 32; mask >= 1; mask >>= 1)
-        v += __shfl_xor(v, mask);
-    return v;
+    return sum_lanes<32>(v);
 }
 
 __device__ inline double wave_max(double v)
 {
-    for (int mask = 32; mask >= 1; mask >>= 1)
-        v = fmax(v, __shfl_xor(v, mask));
-    return v;
+    return max_lanes<32>(v);
 }
 
 // ---- quantization of fp32 rows --------------------------------------------
