@@ -167,6 +167,8 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true", help="launch steps without hipGraph replay")
     ap.add_argument("--flow", action="store_true",
                     help="decode steps as one dataflow launch a token")
+    ap.add_argument("--persistent", action="store_true",
+                    help="decode steps as one persistent launch a token (one workgroup a compute unit)")
     ap.add_argument("--mode", choices=("decode", "prefill"), default="decode",
                     help="decode: the headline decode loop; prefill: the 2048-token prefill "
                          "(use with --prompt 2048)")
@@ -208,6 +210,7 @@ def main() -> int:
     prompt = G.prompt_ids(0xC0FFEE + 2, shape.vocab, args.prompt)
     use_graph = not args.no_graph
     decoder.set_flow(args.flow)
+    decoder.set_persistent(args.persistent)
 
     # warmup: its own sequence (graph instantiation, first launches)
     decoder.generate(prompt, args.warmup + 1, eos=-1, use_graph=use_graph)
@@ -233,6 +236,7 @@ def main() -> int:
     # events on the decoder's stream (the event packets add about a
     # microsecond to each bracket)
     decoder.set_flow(False)
+    decoder.set_persistent(False)
     decoder.generate(prompt, 1, eos=-1, use_graph=False)
     decoder.set_timing(True)
     decoder.decode(args.steps, use_graph=False)
@@ -274,7 +278,8 @@ def main() -> int:
                                f"{args.prompt}-token prompt, {args.steps} timed decode steps, "
                                "fp16 KV cache, batch 1",
                    "layers": args.layers, "prompt_tokens": args.prompt,
-                   "decode_steps": args.steps, "graph": use_graph, "flow": args.flow},
+                   "decode_steps": args.steps, "graph": use_graph, "flow": args.flow,
+                   "persistent": args.persistent},
         "step_hbm": {"bytes_per_token": int(step_bytes), "achieved_gbs": round(step_gbs, 1),
                      "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
         "roofline": roofline,

@@ -26,6 +26,7 @@
 // RoPE.h, Linear.h, MultiQueryAttention.h, GeGLU.h, Argmax.h.  The arithmetic
 // is gq8_numerics.hpp's, identical to the unfused kernels'.
 #include "gq8_decode.hpp"
+#include "gq8_device.hpp"
 #include "gq8_numerics.hpp"
 
 #include <cfloat>
@@ -37,122 +38,6 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-
-__device__ inline double wave_sum_d(double v)
-{
-    return sum_lanes<32>(v);
-}
-
-__device__ inline double wave_max_d(double v)
-{
-    return max_lanes<32>(v);
-}
-
-// The merge weights of one head's key splits (MultiQueryAttention.h:43-49),
-// one split a lane: lane sp < splits holds split sp's (max, sum).  Returns
-// the split's factor exp(max - row max) and leaves the row's total, the sum
-// of sum x factor, in `total` (every lane).  Every merge of split partials
-// uses this, so they all agree bit for bit.
-__device__ inline double merge_factor(double m, double s, bool live, double &total)
-{
-    const double rowMax = wave_max_d(live ? m : -INFINITY);
-    const double f = live ? exp(m - rowMax) : 0.0;
-    total = wave_sum_d(live ? s * f : 0.0);
-    return f;
-}
-
-__device__ inline int dot32(const int4 &w0, const int4 &w1, const int4 &a0, const int4 &a1)
-{
-    int d = 0;
-    d = __builtin_amdgcn_sdot4(w0.x, a0.x, d, false);
-    d = __builtin_amdgcn_sdot4(w0.y, a0.y, d, false);
-    d = __builtin_amdgcn_sdot4(w0.z, a0.z, d, false);
-    d = __builtin_amdgcn_sdot4(w0.w, a0.w, d, false);
-    d = __builtin_amdgcn_sdot4(w1.x, a1.x, d, false);
-    d = __builtin_amdgcn_sdot4(w1.y, a1.y, d, false);
-    d = __builtin_amdgcn_sdot4(w1.z, a1.z, d, false);
-    d = __builtin_amdgcn_sdot4(w1.w, a1.w, d, false);
-    return d;
-}
-
-// Sums U per-lane values (one per row) across the 64 lanes with U - 1 + 6 -
-// log2(U) shuffles instead of 6 U: each halving step keeps half of the rows
-// and adds the partner lane's share of them.  Returns the total of row
-// row_of_lane(lane) (every lane holds one; lanes whose low bits are zero are
-// the ones that store).
-// One halving step a lane bit, every index fixed at compile time (a runtime
-// row count turns v[i] into select chains over the whole array).
-template <int N, int Mask, int U>
-__device__ inline void reduce_halving(double (&v)[U], int lane)
-{
-    if constexpr (N > 1) {
-        const bool upper = (lane & Mask) != 0;
-#pragma unroll
-        for (int i = 0; i < N / 2; ++i) {
-            const double keep = upper ? v[i + N / 2] : v[i];
-            const double send = upper ? v[i] : v[i + N / 2];
-            v[i] = keep + xor_lane<Mask>(send);
-        }
-        reduce_halving<N / 2, Mask / 2, U>(v, lane);
-    } else if constexpr (Mask >= 1) {
-        v[0] += xor_lane<Mask>(v[0]);
-        reduce_halving<1, Mask / 2, U>(v, lane);
-    }
-}
-
-template <int U>
-__device__ inline double reduce_rows(double (&v)[U], int lane)
-{
-    static_assert(U >= 1 && U <= 64 && (U & (U - 1)) == 0, "a power of two rows");
-    reduce_halving<U, 32, U>(v, lane);
-    return v[0];
-}
-
-// The row whose total reduce_rows<U> leaves in `lane`: the halving steps
-// consume lane bits 5, 4, ... in turn, the upper half of the rows going to
-// the lanes with the bit set.
-template <int U>
-__device__ inline int row_of_lane(int lane)
-{
-    int row = 0, n = U, bit = 32;
-    while (n > 1) {
-        n /= 2;
-        if (lane & bit)
-            row += n;
-        bit >>= 1;
-    }
-    return row;
-}
-
-// Whether `lane` is the one that stores its row's total (the lowest lane
-// holding it).
-template <int U>
-__device__ inline bool stores_row(int lane)
-{
-    int bits = 0, n = U, bit = 32;
-    while (n > 1) {
-        n /= 2;
-        bits |= bit;
-        bit >>= 1;
-    }
-    return (lane & ~bits) == 0;
-}
-
-// The lowest lane holding row r's total after reduce_rows<U>.
-template <int U>
-__device__ inline int lane_of_row(int r)
-{
-    int lane = 0, n = U, bit = 32;
-    while (n > 1) {
-        n /= 2;
-        if (r >= n) {
-            lane |= bit;
-            r -= n;
-        }
-        bit >>= 1;
-    }
-    return lane;
-}
 
 // The Q8 form of one normalised row, shared by a workgroup.
 struct RowQ8 {
@@ -292,42 +177,6 @@ __device__ void norm_q8_finish(const RowSlice<E> &r, int width, float epsilon, R
         }
     }
     __syncthreads();
-}
-
-// The 32-byte weight block and fp16 scale of (row, block) in an Int8Blocks
-// tensor of `rows` x `inner`.  The loads are unconditional (an invalid pair
-// reads block 0 of row 0 with its scale masked to zero) and the scale comes in the
-// aligned 32-bit word holding it, so the compiler neither branches around the
-// loads nor packs 16-bit results: every load of a wave is in flight before
-// the first wait.
-struct WeightBlock {
-    int4 w0, w1;
-    uint32_t scalePair; // the fp16 scale is the high half when `high`
-    bool high;
-};
-
-__device__ inline WeightBlock load_block(const uint8_t *w8, int64_t rows, int inner, int64_t row,
-                                         int block, bool valid)
-{
-    WeightBlock b;
-    const int64_t r = valid ? row : 0;
-    const int c = valid ? block : 0;
-    const int4 *p = reinterpret_cast<const int4 *>(w8 + r * inner + (int64_t) c * kBlock);
-    b.w0 = p[0];
-    b.w1 = p[1];
-    const int64_t index = r * (inner / kBlock) + c;
-    // masking (not selecting) the word keeps the load unconditional; a zero
-    // scale zeroes the term
-    b.scalePair = reinterpret_cast<const uint32_t *>(w8 + rows * inner)[index >> 1]
-                  & (valid ? 0xFFFFFFFFu : 0u);
-    b.high = (index & 1) != 0;
-    return b;
-}
-
-__device__ inline double block_term(const WeightBlock &b, const int4 &a0, const int4 &a1, double sa)
-{
-    const uint16_t bits = (uint16_t) (b.high ? b.scalePair >> 16 : b.scalePair & 0xFFFFu);
-    return (double) dot32(b.w0, b.w1, a0, a1) * ((double) half_value(bits) * sa);
 }
 
 // ---- q|k|v + RoPE + fp16 KV ---------------------------------------------------
@@ -915,22 +764,6 @@ void gateup_geglu_kernel(GateUpArgs a)
 // after the position, advances the position and clears the slots.
 constexpr int kHeadRows = 8;
 
-// Larger floats give larger keys; NaN gives 0, below every ordered value, so
-// it is never chosen (a NaN logit never compares greater in the scan either).
-__device__ inline unsigned long long candidate_key(float value, uint32_t index)
-{
-    const uint32_t bits = __float_as_uint(value);
-    uint32_t key = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
-    if (value != value)
-        key = 0;
-    return ((unsigned long long) key << 32) | (unsigned long long) (0xFFFFFFFFu - index);
-}
-
-__device__ inline unsigned long long fold_wave_max(unsigned long long c)
-{
-    return max_lanes<32>(c);
-}
-
 __global__ __launch_bounds__(kThreads) void final_norm_kernel(HeadArgs a)
 {
     __shared__ RowQ8 row;
@@ -1029,7 +862,6 @@ __global__ __launch_bounds__(64) void head_finalize_kernel(HeadArgs a)
 // arrivals, then a top count, then 16 flags that waiters spread their polls
 // over), which the finalize item waits on.
 constexpr int kFlowWaves = kFlowThreads / 64;
-constexpr int kFlowSpinLimit = 1 << 20;
 constexpr int kFlowQkvPairs = kFlowWaves * kPairsPerWave;   // 16 pairs (32 rows) an item
 constexpr int kFlowORows = kFlowWaves * 2;                  // 16 rows an item
 constexpr int kFlowDownRows = kFlowWaves;                   // 8 rows an item
@@ -1043,91 +875,6 @@ constexpr int kFlowRowPieces = ((kFusedMaxWidth / 4 + kFusedMaxWidth / kBlock) /
                                / kFlowThreads; // a Q8 row of at most the fused width: 1
 
 enum { kCounterHead = 0, kCounterIdle = 1 };
-
-__device__ inline uint32_t ld_agent_u(const uint32_t *p)
-{
-    return __hip_atomic_load(const_cast<uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline uint64_t ld_agent_u64(const uint64_t *p)
-{
-    return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline int ld_agent_i(const int *p)
-{
-    return __hip_atomic_load(const_cast<int *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline void st_agent_i(int *p, int v)
-{
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// 16 bytes at byte `offset` of a `bytes`-long buffer, with an agent-coherent
-// (sc1) buffer load; bytes past the end read as zero.
-constexpr int kCoherentLoad = 16; // the sc1 cache-policy bit of a buffer load
-typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-__device__ inline v4u ld_agent_16(const void *base, uint32_t offset, uint32_t bytes)
-{
-    const __amdgpu_buffer_rsrc_t r =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int) bytes, 0x00020000);
-    return __builtin_amdgcn_raw_buffer_load_b128(r, (int) offset, 0, kCoherentLoad);
-}
-
-// ---- tagged words -----------------------------------------------------------
-// tag = epoch << 8 | version.  Versions of the residual row: 0 the embedding
-// row, 2 l + 1 after layer l's o projection, 2 l + 2 after its down
-// projection; every other row has the layer as its version.
-__device__ inline uint32_t flow_tag(uint32_t epoch, int version)
-{
-    return (epoch << 8) | (uint32_t) version;
-}
-
-__device__ inline void ll_put(uint64_t *p, uint32_t value, uint32_t tag)
-{
-    __hip_atomic_store(p, ((uint64_t) tag << 32) | value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ inline bool flow_give_up(const int *error, int &spins)
-{
-    if ((++spins & 63) == 0 && (ld_agent_i(error) != 0 || spins > kFlowSpinLimit)) {
-        __hip_atomic_fetch_or(const_cast<int *>(error), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return true;
-    }
-    __builtin_amdgcn_s_sleep(1);
-    return false;
-}
-
-// The value of word `p` once it carries `tag`; false after giving up.
-__device__ inline bool ll_get(const uint64_t *p, uint32_t tag, const int *error, uint32_t &value)
-{
-    int spins = 0;
-    for (;;) {
-        const uint64_t w = ld_agent_u64(p);
-        if ((uint32_t) (w >> 32) == tag) {
-            value = (uint32_t) w;
-            return true;
-        }
-        if (flow_give_up(error, spins))
-            return false;
-    }
-}
-
-// Words `word` and `word + 1` (word even) of a `words`-long row; a second word
-// past the end is not waited for.
-__device__ inline bool ll_get2(const uint64_t *row, int word, int words, uint32_t tag, const int *error,
-                               uint32_t &v0, uint32_t &v1)
-{
-    int spins = 0;
-    for (;;) {
-        const v4u w = ld_agent_16(row, (uint32_t) word * 8, (uint32_t) words * 8);
-        if (w.y == tag && (word + 1 >= words || w.w == tag)) {
-            v0 = w.x;
-            v1 = w.z;
-            return true;
-        }
-        if (flow_give_up(error, spins))
-            return false;
-    }
-}
 
 // N consecutive pieces (2 N words) from even word `word` of a `words`-long
 // row: every load issued first, then the words not yet tagged polled again.
@@ -1226,7 +973,7 @@ __device__ __forceinline__ bool flow_wait(const FlowArgs &a, int counter)
         int spins = 0;
         const int *flag = flow_line(a, counter, 1 + (int) (blockIdx.x % kFlowFlagLines));
         while (ld_agent_i(flag) == 0)
-            if (flow_give_up(a.error, spins)) {
+            if (wait_give_up(a.error, spins)) {
                 ok = false;
                 break;
             }
@@ -1346,8 +1093,8 @@ __device__ __forceinline__ void flow_qkv(const FlowArgs &a, int l, int item, uin
     __builtin_amdgcn_sched_barrier(0);
     RowSlice<4> slice;
     if (l == 0)
-        slice = flow_embed_slice(a, a.input_norm, position, item == 0, flow_tag(epoch, 0));
-    else if (!flow_hidden_slice(a, a.input_norm + a.norm_stride * l, flow_tag(epoch, 2 * l), slice))
+        slice = flow_embed_slice(a, a.input_norm, position, item == 0, word_tag(epoch, 0));
+    else if (!flow_hidden_slice(a, a.input_norm + a.norm_stride * l, word_tag(epoch, 2 * l), slice))
         return;
     norm_q8_finish<4>(slice, a.width, a.epsilon, row, sPartial, nullptr, nullptr);
 
@@ -1373,7 +1120,7 @@ __device__ __forceinline__ void flow_qkv(const FlowArgs &a, int l, int item, uin
     // lane 0: the wave's two pairs are the consecutive elements (i, i + 1) and
     // (i + half, i + half + 1) of one head
     if (lane == 0 && firstPair < pairs) {
-        const uint32_t tag = flow_tag(epoch, l);
+        const uint32_t tag = word_tag(epoch, l);
         const int head = firstPair / half, i = firstPair % half;
         const int rLo = head * hd + i;
         const bool second = firstPair + 1 < pairs;
@@ -1481,7 +1228,7 @@ __device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int ite
             flow_arrive(a, kCounterIdle, l * groups + group, a.attn_splits - plan.splits, a.layers * groups);
         return;
     }
-    const uint32_t tag = flow_tag(epoch, l);
+    const uint32_t tag = word_tag(epoch, l);
 
     const bool active = lane * C < hd;
     const int c0 = active ? lane * C : 0;
@@ -1705,7 +1452,7 @@ __device__ __forceinline__ void flow_o(const FlowArgs &a, int l, int item, uint3
         w[k] = load_block(a.out + a.out_stride * l, W, qWidth, r0 + k, lane, valid && r0 + k < W);
     __builtin_amdgcn_sched_barrier(0);
     const int words = qWidth / 4 + qWidth / kBlock;
-    if (!flow_stage_ll<kFlowRowPieces>(a, a.attn_ll, words, words - 1, flow_tag(epoch, l), sAct))
+    if (!flow_stage_ll<kFlowRowPieces>(a, a.attn_ll, words, words - 1, word_tag(epoch, l), sAct))
         return;
     int4 a0, a1;
     double sa;
@@ -1718,9 +1465,9 @@ __device__ __forceinline__ void flow_o(const FlowArgs &a, int l, int item, uint3
     const int row = r0 + row_of_lane<2>(lane);
     if (stores_row<2>(lane) && row < W) {
         uint32_t old;
-        if (ll_get(a.hidden_ll + row, flow_tag(epoch, 2 * l), a.error, old))
+        if (ll_get(a.hidden_ll + row, word_tag(epoch, 2 * l), a.error, old))
             ll_put(a.hidden_ll + row, __float_as_uint((float) (total + (double) __uint_as_float(old))),
-                   flow_tag(epoch, 2 * l + 1));
+                   word_tag(epoch, 2 * l + 1));
     }
 }
 
@@ -1744,7 +1491,7 @@ __device__ __forceinline__ void flow_gateup(const FlowArgs &a, int l, int item, 
     }
     __builtin_amdgcn_sched_barrier(0);
     RowSlice<4> slice;
-    if (!flow_hidden_slice(a, a.post_norm + a.norm_stride * l, flow_tag(epoch, 2 * l + 1), slice))
+    if (!flow_hidden_slice(a, a.post_norm + a.norm_stride * l, word_tag(epoch, 2 * l + 1), slice))
         return;
     norm_q8_finish<4>(slice, a.width, a.epsilon, row, sPartial, nullptr, nullptr);
     int4 a0 = make_int4(0, 0, 0, 0), a1 = a0;
@@ -1777,7 +1524,7 @@ __device__ __forceinline__ void flow_gateup(const FlowArgs &a, int l, int item, 
         const uint16_t bits = scale_bits_from_amax(amax);
         const float sc = half_value(bits);
         const uint8_t byte = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);
-        flow_put_q8(a.act_ll, F, o, byte, bits, live, flow_tag(epoch, l));
+        flow_put_q8(a.act_ll, F, o, byte, bits, live, word_tag(epoch, l));
     }
 }
 
@@ -1794,7 +1541,7 @@ __device__ __forceinline__ void flow_down(const FlowArgs &a, int l, int item, ui
     }
     __builtin_amdgcn_sched_barrier(0);
     const int words = F / 4 + F / kBlock;
-    if (!flow_stage_ll<kFlowStagePieces>(a, a.act_ll, words, words - 1, flow_tag(epoch, l), sAct))
+    if (!flow_stage_ll<kFlowStagePieces>(a, a.act_ll, words, words - 1, word_tag(epoch, l), sAct))
         return;
     double acc = 0.0;
 #pragma unroll
@@ -1808,9 +1555,9 @@ __device__ __forceinline__ void flow_down(const FlowArgs &a, int l, int item, ui
     const double total = wave_sum_d(acc);
     if (lane == 0 && row < W) {
         uint32_t old;
-        if (ll_get(a.hidden_ll + row, flow_tag(epoch, 2 * l + 1), a.error, old))
+        if (ll_get(a.hidden_ll + row, word_tag(epoch, 2 * l + 1), a.error, old))
             ll_put(a.hidden_ll + row, __float_as_uint((float) (total + (double) __uint_as_float(old))),
-                   flow_tag(epoch, 2 * l + 2));
+                   word_tag(epoch, 2 * l + 2));
     }
 }
 
@@ -1819,11 +1566,11 @@ __device__ __forceinline__ void flow_final_norm(const FlowArgs &a, uint32_t epoc
     __shared__ RowQ8 row;
     __shared__ double sPartial[kFlowWaves];
     RowSlice<4> slice;
-    if (!flow_hidden_slice(a, a.final_norm, flow_tag(epoch, 2 * a.layers), slice))
+    if (!flow_hidden_slice(a, a.final_norm, word_tag(epoch, 2 * a.layers), slice))
         return;
     norm_q8_finish<4>(slice, a.width, a.epsilon, row, sPartial, nullptr, nullptr);
     const int t = threadIdx.x;
-    const uint32_t tag = flow_tag(epoch, 0);
+    const uint32_t tag = word_tag(epoch, 0);
     if (t * 4 < a.width) {
         uint32_t word;
         __builtin_memcpy(&word, row.q + t * 4, 4);
@@ -1847,7 +1594,7 @@ __device__ __forceinline__ void flow_lmhead(const FlowArgs &a, int item, uint32_
         w[k] = load_block(a.embedding, V, a.width, r0 + k, lane, valid && r0 + k < V);
     __builtin_amdgcn_sched_barrier(0);
     const int words = a.width / 4 + a.width / kBlock;
-    if (!flow_stage_ll<kFlowRowPieces>(a, a.head_ll, words, words - 1, flow_tag(epoch, 0), sAct))
+    if (!flow_stage_ll<kFlowRowPieces>(a, a.head_ll, words, words - 1, word_tag(epoch, 0), sAct))
         return;
     int4 a0, a1;
     double sa;

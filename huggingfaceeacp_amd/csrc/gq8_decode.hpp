@@ -143,6 +143,60 @@ struct FlowArgs {
     int qkv_items, attn_items, o_items, gate_up_items, down_items, head_items;
 };
 
+// ---- the persistent decode step: one launch a token, one workgroup a CU -------
+// Every workgroup runs the whole step's program on its share of every phase
+// (gq8_persist.hip).  Four prefetch waves stream its share of the gate|up,
+// down and lm_head weights into an LDS ring; four compute waves run the
+// dependent chain and hand rows on in tagged words.
+constexpr int kPersistThreads = 512;
+constexpr int kPersistMaxSplits = 64;   // attention key splits of a row
+constexpr int kPersistMaxLayers = 127;  // residual-row versions 0 .. 2 layers fit a tag's 8 bits
+
+struct PersistArgs {
+    int layers, width, heads, kv_heads, head_dim, intermediate, vocab, max_positions;
+    float epsilon, embed_scale, attn_scale;
+    const uint8_t *embedding;                 // Int8Blocks [vocab, width], also the lm_head
+    // layer l of a kind at base + l * stride (bytes for the Int8Blocks
+    // tensors, floats for the norms)
+    const uint8_t *qkv, *out, *gate_up, *down;
+    int64_t qkv_stride, out_stride, gate_up_stride, down_stride;
+    const float *input_norm, *post_norm;
+    int64_t norm_stride;
+    const float *final_norm;
+    uint16_t *key_cache, *value_cache;        // [layers][max_positions][kv_heads * head_dim]
+    const float *cosines, *sines;
+    uint32_t *sequence;
+    int *position;
+    uint32_t *epoch;                          // the launch's tag epoch (never 0)
+    // tagged rows (value | tag << 32, one element a word)
+    uint64_t *hid_ll;                         // the residual row [width]
+    uint64_t *q_ll;                           // the rotated q row [heads * head_dim]
+    uint64_t *kv_ll;                          // this step's k then v row, fp16 bits [2 kv width]
+    uint64_t *part_ll;                        // attention partials [split][head][head_dim], doubles as
+                                              // (low, high) word pairs
+    uint64_t *ml_ll;                          // their (max, sum) [split][head], four words
+    uint64_t *attn_ll, *act_ll;               // Q8 rows: bytes four a word, then a scale word a block
+    uint64_t *cand_ll;                        // a workgroup's argmax candidate, two words
+    float *logits;                            // fp32 [vocab]
+    int *error;                               // nonzero after a wait gave up
+    int sample;                               // nonzero: the id goes to sequence[position + 1]
+    int grid;                                 // workgroups: one a compute unit, all resident
+};
+
+// Tagged words the persistent step needs, by row (the runtime carves them
+// from one allocation).
+struct PersistWords {
+    int64_t hid, q, kv, part, ml, attn, act, cand;
+};
+PersistWords persist_words(int width, int heads, int kv_heads, int head_dim, int intermediate, int grid);
+// Whether the shape fits the persistent step's partition on `grid` workgroups.
+bool persist_decode_supported(int layers, int width, int heads, int kv_heads, int head_dim,
+                              int intermediate, int vocab, int max_positions, int grid);
+// The workgroups of the persistent step on `device` (its compute units, when
+// one workgroup fits a unit), or 0.
+int persist_grid(int device);
+hipError_t launch_persist_step(const PersistArgs &a, hipStream_t stream);
+
 bool flow_decode_supported(int layers, int width, int heads, int kv_heads, int head_dim, int intermediate,
                            int vocab, int max_positions);
 int flow_attention_splits(int max_positions);

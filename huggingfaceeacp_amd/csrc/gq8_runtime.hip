@@ -434,6 +434,16 @@ struct gq8_decoder {
     uint32_t *flowEpoch = nullptr;
     int *flowCounters = nullptr;
     int *flowError = nullptr;
+    // the persistent step (one launch a token, one workgroup a compute unit)
+    bool usePersist = false;
+    bool persistSupported = false;
+    int persistGrid = 0;
+    uint64_t *persistTagged = nullptr; // the tagged rows, one allocation
+    size_t persistTaggedBytes = 0;
+    uint64_t *persistHid = nullptr, *persistQ = nullptr, *persistKv = nullptr, *persistPart = nullptr,
+             *persistMl = nullptr, *persistAttn = nullptr, *persistAct = nullptr, *persistCand = nullptr;
+    uint32_t *persistEpoch = nullptr;
+    int *persistError = nullptr;
     double *decodeO = nullptr, *decodeMl = nullptr;
     int *counters = nullptr; // attention head-group tickets
     unsigned long long *headBest = nullptr; // the lm_head argmax slots
@@ -739,6 +749,39 @@ extern "C" int gq8_decoder_create(const gq8_shape *shape, gq8_decoder **out)
             || hipMemset(d->flowError, 0, sizeof(int)) != hipSuccess)
             return cleanup(fail(GQ8_ERR_DEVICE, "flow state: initialisation failed"));
     }
+    {
+        int device = 0;
+        if (hipGetDevice(&device) != hipSuccess)
+            return cleanup(fail(GQ8_ERR_DEVICE, "persistent step: no current device"));
+        d->persistGrid = gq8::persist_grid(device);
+        d->persistSupported = d->persistGrid > 0
+                              && gq8::persist_decode_supported(s.layers, s.width, s.heads, s.kv_heads,
+                                                               s.head_dim, s.intermediate, s.vocab,
+                                                               s.max_positions, d->persistGrid);
+        const int grid = d->persistGrid > 0 ? d->persistGrid : 1;
+        const gq8::PersistWords pw = gq8::persist_words(s.width, s.heads, s.kv_heads, s.head_dim,
+                                                        s.intermediate, grid);
+        const int64_t sizes[] = {pw.hid, pw.q, pw.kv, pw.part, pw.ml, pw.attn, pw.act, pw.cand};
+        int64_t total = 0;
+        for (int64_t n : sizes)
+            total += (n + 1) / 2 * 2; // 16-byte aligned parts
+        d->persistTaggedBytes = (size_t) total * sizeof(uint64_t);
+        GQ8_ALLOC(d->persistTagged, d->persistTaggedBytes);
+        uint64_t *part = d->persistTagged;
+        uint64_t **dst[] = {&d->persistHid, &d->persistQ, &d->persistKv, &d->persistPart,
+                            &d->persistMl, &d->persistAttn, &d->persistAct, &d->persistCand};
+        for (int k = 0; k < 8; ++k) {
+            *dst[k] = part;
+            part += (sizes[k] + 1) / 2 * 2;
+        }
+        GQ8_ALLOC(d->persistEpoch, 64 * sizeof(uint32_t));
+        GQ8_ALLOC(d->persistError, 64 * sizeof(int));
+        const uint32_t one = 1;
+        if (hipMemset(d->persistTagged, 0, d->persistTaggedBytes) != hipSuccess
+            || hipMemcpy(d->persistEpoch, &one, sizeof(one), hipMemcpyHostToDevice) != hipSuccess
+            || hipMemset(d->persistError, 0, sizeof(int)) != hipSuccess)
+            return cleanup(fail(GQ8_ERR_DEVICE, "persistent step state: initialisation failed"));
+    }
     d->fusedSupported = gq8::fused_decode_supported(s.width, s.heads, s.kv_heads, s.head_dim,
                                                     s.intermediate, s.max_positions);
     {
@@ -987,6 +1030,20 @@ extern "C" int gq8_decoder_set_flow(gq8_decoder *d, int enabled)
     return GQ8_OK;
 }
 
+extern "C" int gq8_decoder_set_persistent(gq8_decoder *d, int enabled)
+{
+    if (!d)
+        return fail(GQ8_ERR_ARGUMENT, "null decoder");
+    if (enabled && !d->persistSupported)
+        return fail(GQ8_ERR_SHAPE, "decoder_set_persistent: the shape or device has no persistent step");
+    d->usePersist = enabled != 0;
+    if (d->graph) { // a captured step follows the path it was captured with
+        (void) hipGraphExecDestroy(d->graph);
+        d->graph = nullptr;
+    }
+    return GQ8_OK;
+}
+
 extern "C" int gq8_decoder_set_fused(gq8_decoder *d, int enabled)
 {
     if (!d)
@@ -1137,6 +1194,93 @@ int encode_flow_token(gq8_decoder *d, float *logits, bool sample)
     a.attn_splits = gq8::flow_attention_splits(s.max_positions);
     a.sample = sample ? 1 : 0;
     GQ8_STAGE(kStageLogits, gq8::launch_flow_step(a, d->stream));
+    return GQ8_OK;
+}
+
+// The one-token step as one persistent launch (gq8_persist.hip).
+int encode_persist_token(gq8_decoder *d, float *logits, bool sample)
+{
+    const gq8_shape &s = d->shape;
+    gq8::PersistArgs a{};
+    a.layers = s.layers;
+    a.width = s.width;
+    a.heads = s.heads;
+    a.kv_heads = s.kv_heads;
+    a.head_dim = s.head_dim;
+    a.intermediate = s.intermediate;
+    a.vocab = s.vocab;
+    a.max_positions = s.max_positions;
+    a.epsilon = s.rms_epsilon;
+    a.embed_scale = s.embedding_scale;
+    a.attn_scale = 1.f / std::sqrt((float) s.head_dim);
+    a.embedding = d->embedding;
+    a.qkv = d->qkv[0];
+    a.qkv_stride = d->qkvStride;
+    a.out = d->out[0];
+    a.out_stride = d->outStride;
+    a.gate_up = d->gateUp[0];
+    a.gate_up_stride = d->gateUpStride;
+    a.down = d->down[0];
+    a.down_stride = d->downStride;
+    a.input_norm = d->inputNorm[0];
+    a.post_norm = d->postNorm[0];
+    a.norm_stride = d->normStride;
+    a.final_norm = d->finalNorm;
+    a.key_cache = d->keyCache;
+    a.value_cache = d->valueCache;
+    a.cosines = d->cosines;
+    a.sines = d->sines;
+    a.sequence = d->sequence;
+    a.position = d->position;
+    a.epoch = d->persistEpoch;
+    a.hid_ll = d->persistHid;
+    a.q_ll = d->persistQ;
+    a.kv_ll = d->persistKv;
+    a.part_ll = d->persistPart;
+    a.ml_ll = d->persistMl;
+    a.attn_ll = d->persistAttn;
+    a.act_ll = d->persistAct;
+    a.cand_ll = d->persistCand;
+    a.logits = logits;
+    a.error = d->persistError;
+    a.sample = sample ? 1 : 0;
+    a.grid = d->persistGrid;
+    GQ8_STAGE(kStageLogits, gq8::launch_persist_step(a, d->stream));
+    return GQ8_OK;
+}
+
+// Reads and clears the persistent step's error word, as check_flow_error does
+// for the dataflow step.
+int check_persist_error(gq8_decoder *d)
+{
+    if (!d->persistSupported)
+        return GQ8_OK;
+    int error = 0;
+    GQ8_HIP(hipStreamSynchronize(d->stream));
+    GQ8_HIP(hipMemcpy(&error, d->persistError, sizeof(int), hipMemcpyDeviceToHost));
+    if (error == 0)
+        return GQ8_OK;
+    uint32_t epoch = 0;
+    GQ8_HIP(hipMemcpy(&epoch, d->persistEpoch, sizeof(epoch), hipMemcpyDeviceToHost));
+    epoch = (epoch + 1) & 0xFFFFFFu;
+    if (epoch == 0)
+        epoch = 1;
+    GQ8_HIP(hipMemcpy(d->persistEpoch, &epoch, sizeof(epoch), hipMemcpyHostToDevice));
+    GQ8_HIP(hipMemset(d->persistTagged, 0, d->persistTaggedBytes));
+    GQ8_HIP(hipMemset(d->persistError, 0, sizeof(int)));
+    return fail(GQ8_ERR_DEVICE, "persistent step: a wait gave up (the step's results are invalid)");
+}
+
+int check_flow_error(gq8_decoder *d);
+
+// The error word of whichever one-launch step is on.
+int check_step_error(gq8_decoder *d)
+{
+    if (d->usePersist)
+        if (int s = check_persist_error(d))
+            return s;
+    if (d->useFlow)
+        return check_flow_error(d);
     return GQ8_OK;
 }
 
@@ -1305,6 +1449,9 @@ int encode_step(gq8_decoder *d, int rows, float *logits, int logitsRows, bool sa
     hipStream_t st = d->stream;
     const float attentionScale = 1.f / std::sqrt((float) s.head_dim);
     const bool dbg = d->debug;
+    if (rows == 1 && logits && logitsRows == 1 && d->usePersist && d->persistSupported
+        && !(d->debug && !d->capturing))
+        return encode_persist_token(d, logits, sample);
     if (rows == 1 && logits && logitsRows == 1 && d->useFlow && d->flowSupported
         && !(d->debug && !d->capturing))
         return encode_flow_token(d, logits, sample);
@@ -1408,9 +1555,8 @@ extern "C" int gq8_decoder_step(gq8_decoder *d, const uint32_t *tokens, int n, f
     if (int s = encode_step(d, n, logits, logits ? logits_rows : 0, false))
         return s;
     GQ8_HIP(hipStreamSynchronize(d->stream));
-    if (d->useFlow)
-        if (int s = check_flow_error(d))
-            return s;
+    if (int s = check_step_error(d))
+        return s;
     d->hostPosition += n;
     return GQ8_OK;
 }
@@ -1559,9 +1705,8 @@ extern "C" int gq8_generate(gq8_decoder *d, const int32_t *prompt, int prompt_le
             ++steps;
         }
         GQ8_HIP(hipStreamSynchronize(d->stream));
-        if (d->useFlow)
-            if (int st = check_flow_error(d))
-                return st;
+        if (int st = check_step_error(d))
+            return st;
         std::vector<uint32_t> ids(limit);
         GQ8_HIP(hipMemcpy(ids.data(), d->sequence + prompt_length, limit * sizeof(uint32_t),
                           hipMemcpyDeviceToHost));
@@ -1617,9 +1762,8 @@ extern "C" int gq8_generate(gq8_decoder *d, const int32_t *prompt, int prompt_le
             }
         }
         finish(GQ8_OK);
-        if (d->useFlow)
-            if (int st = check_flow_error(d))
-                return st;
+        if (int st = check_step_error(d))
+            return st;
     }
     local.decode_seconds = std::chrono::duration<double>(Clock::now() - decodeStart).count();
     local.step_count = steps;
@@ -1642,9 +1786,7 @@ extern "C" int gq8_decoder_decode(gq8_decoder *d, int steps, int use_graph)
         if (int st = decode_one(d, use_graph != 0))
             return st;
     GQ8_HIP(hipStreamSynchronize(d->stream));
-    if (d->useFlow)
-        return check_flow_error(d);
-    return GQ8_OK;
+    return check_step_error(d);
 }
 
 extern "C" int gq8_decoder_tokens(gq8_decoder *d, int first, int count, int32_t *host_out)

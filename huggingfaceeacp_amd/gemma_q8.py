@@ -113,6 +113,7 @@ def library() -> ctypes.CDLL:
         "gq8_decoder_set_debug": (i32, [P, i32]),
         "gq8_decoder_set_fused": (i32, [P, i32]),
         "gq8_decoder_set_flow": (i32, [P, i32]),
+        "gq8_decoder_set_persistent": (i32, [P, i32]),
         "gq8_decoder_debug": (i32, [P, i32, i32, P, P]),
         "gq8_generate": (i32, [P, P, i32, i32, i32, i32, P, ctypes.POINTER(_RunStats)]),
         "gq8_decoder_decode": (i32, [P, i32, i32]),
@@ -360,6 +361,11 @@ class Decoder:
     def set_flow(self, enabled: bool) -> None:
         """Run one-token steps as one dataflow launch (off by default)."""
         check(library().gq8_decoder_set_flow(self.handle, int(enabled)))
+
+    def set_persistent(self, enabled: bool) -> None:
+        """Run one-token steps as one persistent launch (one workgroup a compute
+        unit); raises when the shape or device has no persistent step."""
+        check(library().gq8_decoder_set_persistent(self.handle, int(enabled)))
 
     def set_fused(self, enabled: bool) -> None:
         """Choose the fused one-token kernels (default) or the unfused ones."""

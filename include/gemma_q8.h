@@ -214,6 +214,16 @@ int gq8_decoder_set_fused(gq8_decoder *decoder, int enabled);
  * No reference counterpart: it replaces the per-kernel dispatch of
  * Decoder::step (Decoder.cpp:644-706) for one-token steps. */
 int gq8_decoder_set_flow(gq8_decoder *decoder, int enabled);
+/* One-token steps as one persistent launch when the shape and the device
+ * allow: one workgroup a compute unit runs the whole step, prefetch waves
+ * streaming the gate|up, down and lm_head weights into LDS while compute waves
+ * run the dependent chain.  The products have the fused kernels' arithmetic
+ * and summation order; attention splits its keys its own way (double sums
+ * throughout).  A step that gave up waiting is reported by the next
+ * synchronous call as GQ8_ERR_DEVICE.  No reference counterpart: it replaces
+ * the per-kernel dispatch of Decoder::step (Decoder.cpp:644-706) for
+ * one-token steps.  GQ8_ERR_SHAPE when the shape or device has none. */
+int gq8_decoder_set_persistent(gq8_decoder *decoder, int enabled);
 /* Decoder::hiddenStates (Decoder.h:119-121): the last step's rows after the
  * final norm, [rows, width] fp32, copied to the host. */
 int gq8_decoder_hidden(gq8_decoder *decoder, float *host_out, int rows);
