@@ -9,11 +9,11 @@
 //
 //   prefetch waves (4-7)  stream the workgroup's share of every gate|up, down
 //                         and lm_head weight row into a ring of four LDS slots
-//                         of 34 KB, with direct-to-LDS loads (global_load_lds),
-//                         in the order the compute waves consume them.  They
-//                         wait only for a slot to be consumed, never on
-//                         another workgroup, so these weights stream while the
-//                         step's latency-bound links run;
+//                         of 34 KB, each wave holding its slot's next stage in
+//                         registers, in the order the compute waves consume
+//                         them.  They wait only for a slot to be consumed,
+//                         never on another workgroup, so these weights stream
+//                         while the step's latency-bound links run;
 //   compute waves (0-3)   run the chain: q|k|v + RoPE (weights loaded into
 //                         registers before the input row arrives), attention
 //                         over key splits, the split merge, o (+ residual),
@@ -70,8 +70,6 @@ constexpr int kMaxSplitKeys = 256;
 
 static_assert(kRowBufBytes >= kMaxWidth * 4, "the row buffer holds an fp32 residual row");
 
-typedef __attribute__((address_space(3))) void *LdsPtr;
-
 struct Shared {
     uint8_t ring[kSlots][kSlotBytes];
     uint8_t row[kRowBufBytes];                // fp32 residual row, or a Q8 row with scale words
@@ -83,6 +81,11 @@ struct Shared {
     int blockArrivals[kMaxWgBlocks];
     int bestArrivals;
 };
+
+// The workgroup's LDS, at file scope so that the out-of-line helpers (shared
+// by several phases, to keep the step's code within the instruction cache)
+// address it directly.
+__shared__ __attribute__((aligned(16))) Shared g_sh;
 
 // ---- the workgroup's share of each phase ----------------------------------------
 struct Plan {
@@ -139,12 +142,24 @@ __device__ __forceinline__ int opaque_lane()
 }
 
 // ---- waits inside the workgroup (LDS counters) ---------------------------------
+// A wait on an LDS counter polls the LDS only; the error word (a device-scope
+// load that costs microseconds while the HBM streams) is read once every
+// kLdsErrorCheck polls, so a wave does not sit in that load when the counter
+// moves.  A wait gives up after kWaitSpinLimit error checks.
+constexpr int kLdsErrorCheck = 1 << 14;
+
 __device__ __forceinline__ bool lds_wait(int *counter, int target, const int *error)
 {
-    int spins = 0;
-    while (__hip_atomic_load(counter, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target)
-        if (wait_give_up(error, spins))
-            return false;
+    int spins = 0, checks = 0;
+    while (__hip_atomic_load(counter, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+        if ((++spins & (kLdsErrorCheck - 1)) == 0) {
+            if (ld_agent_i(error) != 0 || ++checks > kWaitSpinLimit / kLdsErrorCheck) {
+                __hip_atomic_fetch_or(const_cast<int *>(error), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                return false;
+            }
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
     return true;
 }
 
@@ -169,36 +184,48 @@ __device__ __forceinline__ void lds_writes_done()
 }
 
 // ---- tagged rows ---------------------------------------------------------------
-// Words [w0, w1) (w0 even) of a `words`-long tagged row into dst as 32-bit
-// values, once each carries `tag`: a batch of 16-byte loads, then every piece
-// not yet tagged polled again.
-__device__ __forceinline__ bool stage_words(const uint64_t *row, int words, int w0, int w1, uint32_t tag,
-                                   uint32_t *dst, const int *error)
+// Words [w0, w1) (w0 even) of a `words`-long tagged row into the row buffer as 32-bit
+// values, once each carries `tag`: a lane's batch of 16-byte loads is issued
+// at once and re-issued whole until every piece is tagged (one copy of the
+// code; re-reading a piece that was already there costs nothing).
+__device__ __attribute__((noinline)) bool stage_words(const uint64_t *row, int words, int w0, int w1, uint32_t tag,
+                                                      const int *error)
 {
-    constexpr int kBatch = 8;
+    uint32_t *dst = reinterpret_cast<uint32_t *>(g_sh.row);
+    constexpr int kBatch = 10; // a quarter of a 16384-wide Q8 row (1152 words) in one batch
     const int lane = opaque_lane();
-    bool ok = true;
     for (int base = w0; base < w1; base += 2 * 64 * kBatch) {
-        v4u v[kBatch];
+        int spins = 0;
+        for (;;) {
+            v4u v[kBatch];
 #pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-            const int w = base + 2 * (lane + 64 * k);
-            v[k] = ld_agent_16(row, (uint32_t) min(w, words - 1) * 8, (uint32_t) words * 8);
-        }
-#pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-            const int w = base + 2 * (lane + 64 * k);
-            if (w < w1) {
-                uint32_t v0 = v[k].x, v1 = v[k].z;
-                if (v[k].y != tag || (w + 1 < words && v[k].w != tag))
-                    ok = ll_get2(row, w, words, tag, error, v0, v1) && ok;
-                dst[w] = v0;
-                if (w + 1 < w1)
-                    dst[w + 1] = v1;
+            for (int k = 0; k < kBatch; ++k) {
+                const int w = base + 2 * (lane + 64 * k);
+                v[k] = ld_agent_16(row, (uint32_t) min(w, words - 1) * 8, (uint32_t) words * 8);
             }
+            bool ok = true;
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                const int w = base + 2 * (lane + 64 * k);
+                ok = ok && (w >= w1 || (v[k].y == tag && (w + 1 >= words || v[k].w == tag)));
+            }
+            if (ok) {
+#pragma unroll
+                for (int k = 0; k < kBatch; ++k) {
+                    const int w = base + 2 * (lane + 64 * k);
+                    if (w < w1) {
+                        dst[w] = v[k].x;
+                        if (w + 1 < w1)
+                            dst[w + 1] = v[k].z;
+                    }
+                }
+                break;
+            }
+            if (wait_give_up(error, spins))
+                return false;
         }
     }
-    return ok;
+    return true;
 }
 
 // This compute wave's quarter of a tagged row (boundaries even).
@@ -248,30 +275,73 @@ __device__ __forceinline__ bool get_pair(const uint64_t *row, int word, int word
     return ll_get2(row, word, words, tag, error, v0, v1);
 }
 
-// ---- norm of a staged fp32 row ---------------------------------------------------
-// norm_q8_finish's arithmetic with 64 * V threads of E elements (thread t owns
-// [E t, E t + E)); lane l plays thread l of each of V virtual waves.  The
-// scale is the same double in every lane.
-template <int E, int V>
-__device__ __forceinline__ double staged_norm_scale(const float *row, int width, float epsilon)
+// N 16-byte pieces (word pairs from even indices) of a tagged row: every load
+// issued before the first wait, then each piece not yet tagged polled again,
+// so N pieces that are already there cost one round trip, not N.
+// Piece k comes from word word[k] of row rows[k] (words[k] words long); the
+// batch is re-issued whole until every piece is tagged.
+template <int N>
+__device__ __forceinline__ bool get_pieces(const uint64_t *const (&rows)[N], const int (&word)[N],
+                                           const int (&words)[N], uint32_t tag, const int *error,
+                                           uint32_t (&lo)[N], uint32_t (&hi)[N])
 {
-    const int lane = opaque_lane();
-    double total = 0.0;
+    int spins = 0;
+    for (;;) {
+        v4u v[N];
 #pragma unroll
-    for (int vw = 0; vw < V; ++vw) {
-        const int e0 = (64 * vw + lane) * E;
-        double squares = 0.0;
-        if (e0 < width)
+        for (int k = 0; k < N; ++k)
+            v[k] = ld_agent_16(rows[k], (uint32_t) word[k] * 8, (uint32_t) words[k] * 8);
+        bool ok = true;
 #pragma unroll
-            for (int k = 0; k < E; ++k) {
-                const float x = row[e0 + k];
-                squares += (double) x * (double) x;
-            }
-        total += wave_sum_d(squares);
+        for (int k = 0; k < N; ++k) {
+            lo[k] = v[k].x;
+            hi[k] = v[k].z;
+            ok = ok && v[k].y == tag && (word[k] + 1 >= words[k] || v[k].w == tag);
+        }
+        if (ok)
+            return true;
+        if (wait_give_up(error, spins))
+            return false;
     }
-    return norm_scale(total, width, epsilon);
 }
 
+// N pieces of one row.
+template <int N>
+__device__ __forceinline__ bool get_pairs(const uint64_t *row, const int (&word)[N], int words, uint32_t tag,
+                                          const int *error, uint32_t (&lo)[N], uint32_t (&hi)[N])
+{
+    const uint64_t *rows[N];
+    int sizes[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        rows[k] = row;
+        sizes[k] = words;
+    }
+    return get_pieces<N>(rows, word, sizes, tag, error, lo, hi);
+}
+
+// C consecutive words from word w (w even unless C == 1) of a tagged row,
+// with M more pieces of another row in the same batch.
+template <int C>
+struct Words {
+    static constexpr int kPieces = C == 1 ? 1 : C / 2;
+    int piece[kPieces];
+    __device__ __forceinline__ void at(int w)
+    {
+#pragma unroll
+        for (int k = 0; k < kPieces; ++k)
+            piece[k] = C == 1 ? (w & ~1) : w + 2 * k;
+    }
+    __device__ __forceinline__ uint32_t value(int w, int i, const uint32_t (&lo)[kPieces],
+                                              const uint32_t (&hi)[kPieces]) const
+    {
+        if (C == 1)
+            return (w & 1) ? hi[0] : lo[0];
+        return (i & 1) ? hi[i / 2] : lo[i / 2];
+    }
+};
+
+// ---- norm of a staged fp32 row ---------------------------------------------------
 // The Q8 row of a normalised row, a quarter of its 32-blocks a compute wave:
 // lane l of wave cw takes elements [32 b + 8 (l % 4), + 8) of block
 // b = cw * ceil(nb / 4) + l / 4 (norm_q8_finish's thread layout), so the bytes
@@ -343,21 +413,59 @@ __device__ __forceinline__ void lane_block(const uint8_t *qBytes, const uint16_t
 constexpr int kRowQ8Offset = kMaxWidth * 4;
 static_assert(kRowQ8Offset + kMaxWidth + kMaxWidth / kBlock * 2 <= kRowBufBytes, "the Q8 row fits");
 
-// The staged row's norm (every wave sums the squares itself, in the fused
-// kernels' order) and its Q8 row (a quarter a wave, then a compute-wave
-// barrier), ending with lane l's block in registers.
-template <int E, int V>
-__device__ __forceinline__ bool norm_q8_row(const PersistArgs &a, Shared &sh, const NormQuarter &q, int nb,
-                                            int &bar, int4 &a0, int4 &a1, double &sa)
+// The staged row's norm (every wave sums the squares itself, in
+// norm_q8_finish's order for 64 V threads of E elements) and this wave's
+// quarter of its Q8 row, into the row buffer after the fp32 row.  One copy for
+// every norm of the step.
+__device__ __attribute__((noinline)) void norm_q8_quarter(NormQuarter q, int width, float epsilon, int E, int V)
 {
-    const float *row = reinterpret_cast<const float *>(sh.row);
-    uint8_t *qBytes = sh.row + kRowQ8Offset;
-    uint16_t *qScales = reinterpret_cast<uint16_t *>(qBytes + kMaxWidth);
-    const double scale = staged_norm_scale<E, V>(row, a.width, a.epsilon);
-    quarter_q8(row, q, scale, qBytes, qScales);
+    const float *row = reinterpret_cast<const float *>(g_sh.row);
+    const int lane = opaque_lane();
+    // a lane's 32 elements in 8 loads issued together: thread 64 vw + lane of
+    // E = 4 owns float4 vw; of E = 8, float4s 2 vw and 2 vw + 1
+    float4 x[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int e0 = E == 4 ? (64 * i + lane) * 4 : (64 * (i / 2) + lane) * 8 + 4 * (i % 2);
+        x[i] = e0 < width ? *reinterpret_cast<const float4 *>(row + e0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    double total = 0.0;
+    if (E == 4) {
+#pragma unroll
+        for (int vw = 0; vw < 8; ++vw) {
+            const float4 v = x[vw];
+            const double squares = (((0.0 + (double) v.x * (double) v.x) + (double) v.y * (double) v.y)
+                                    + (double) v.z * (double) v.z) + (double) v.w * (double) v.w;
+            total += wave_sum_d(squares);
+        }
+    } else {
+        // a thread's eight squares in order: its first float4's, then its second's
+#pragma unroll
+        for (int vw = 0; vw < 4; ++vw) {
+            const float4 v = x[2 * vw], u = x[2 * vw + 1];
+            const double squares =
+                (((((((0.0 + (double) v.x * (double) v.x) + (double) v.y * (double) v.y) + (double) v.z * (double) v.z)
+                     + (double) v.w * (double) v.w) + (double) u.x * (double) u.x) + (double) u.y * (double) u.y)
+                  + (double) u.z * (double) u.z) + (double) u.w * (double) u.w;
+            total += wave_sum_d(squares);
+        }
+    }
+    (void) V;
+    const double scale = norm_scale(total, width, epsilon);
+    uint8_t *qBytes = g_sh.row + kRowQ8Offset;
+    quarter_q8(row, q, scale, qBytes, reinterpret_cast<uint16_t *>(qBytes + kMaxWidth));
+}
+
+// The norm and Q8 row of the staged row (E elements a thread over V waves, as
+// the fused kernel of the same norm), ending with lane l's block in registers.
+__device__ __forceinline__ bool norm_q8_row(const PersistArgs &a, Shared &sh, const NormQuarter &q, int nb, int E,
+                                            int V, int &bar, int4 &a0, int4 &a1, double &sa)
+{
+    norm_q8_quarter(q, a.width, a.epsilon, E, V);
     if (!compute_sync(sh, bar, a.error))
         return false;
-    lane_block(qBytes, qScales, nb, a0, a1, sa);
+    const uint8_t *qBytes = sh.row + kRowQ8Offset;
+    lane_block(qBytes, reinterpret_cast<const uint16_t *>(qBytes + kMaxWidth), nb, a0, a1, sa);
     return true;
 }
 
@@ -371,28 +479,29 @@ __device__ __forceinline__ double lds_term(const uint8_t *bytes, const uint16_t 
 }
 
 // ---- the prefetch program ----------------------------------------------------------
-// 16-byte (bytes) and 4-byte (scales) direct-to-LDS copies; lane i of a load
-// writes bytes [size i, size i + size) past the load's LDS address.
-__device__ __forceinline__ void dma16(const uint8_t *src, uint8_t *dst, int bytes)
-{
-    const int lane = opaque_lane();
-    for (int c = 0; c < bytes; c += 1024)
-        if (c + lane * 16 < bytes)
-            __builtin_amdgcn_global_load_lds(src + c + lane * 16, (LdsPtr) (dst + c), 16, 0, 0);
-}
+// A stage is at most 32 KB of weight bytes (whole rows, in at most two
+// regions) and 2 KB of their fp16 scales (at most two regions), laid out in
+// its slot as bytes from offset 0 and scales from kSlotScales.  A prefetch wave
+// loads the next stage of its slot into registers (32 16-byte pieces and 8
+// scale words a lane) while the slot's current stage is being consumed, then
+// writes it into the slot: two stages a wave in hand, eight a workgroup.  Its
+// loads go out kLoadBurst at a time, which keeps the HBM busy while leaving the
+// memory queues short for the compute waves' latency-bound loads.
+constexpr int kStagePieces = 32;
+constexpr int kStageScaleWords = 8;
+constexpr int kLoadBurst = 8;
 
-__device__ __forceinline__ void dma4(const uint8_t *src, uint8_t *dst, int bytes)
-{
-    const int lane = opaque_lane();
-    for (int c = 0; c < bytes; c += 256)
-        if (c + lane * 4 < bytes)
-            __builtin_amdgcn_global_load_lds(src + c + lane * 4, (LdsPtr) (dst + c), 4, 0, 0);
-}
+struct StageRegions {
+    const uint8_t *bytes[2];
+    int byteLen[2];
+    const uint8_t *scales[2];
+    int scaleLen[2];
+};
 
-// Stage s of the workgroup into `slot`.
-__device__ __forceinline__ void issue_stage(const PersistArgs &a, const Plan &p, int s, uint8_t *slot)
+__device__ __forceinline__ StageRegions stage_regions(const PersistArgs &a, const Plan &p, int s)
 {
     const int W = a.width, F = a.intermediate;
+    StageRegions r;
     if (s < a.layers * p.perLayer) {
         const int l = s / p.perLayer, j = s % p.perLayer;
         if (j < p.nG) {
@@ -400,35 +509,112 @@ __device__ __forceinline__ void issue_stage(const PersistArgs &a, const Plan &p,
             const int o0 = (p.gb0 + j / (kBlock / kGateActs)) * kBlock + (j % (kBlock / kGateActs)) * kGateActs;
             const uint8_t *base = a.gate_up + (int64_t) l * a.gate_up_stride;
             const uint8_t *scales = base + (int64_t) 2 * F * W;
-            dma16(base + (int64_t) o0 * W, slot, kGateActs * W);
-            dma16(base + (int64_t) (F + o0) * W, slot + kGateActs * W, kGateActs * W);
-            dma4(scales + (int64_t) o0 * p.nb * 2, slot + kSlotScales, kGateActs * p.nb * 2);
-            dma4(scales + (int64_t) (F + o0) * p.nb * 2, slot + kSlotScales + kGateActs * p.nb * 2,
-                 kGateActs * p.nb * 2);
+            r.bytes[0] = base + (int64_t) o0 * W;
+            r.bytes[1] = base + (int64_t) (F + o0) * W;
+            r.byteLen[0] = r.byteLen[1] = kGateActs * W;
+            r.scales[0] = scales + (int64_t) o0 * p.nb * 2;
+            r.scales[1] = scales + (int64_t) (F + o0) * p.nb * 2;
+            r.scaleLen[0] = r.scaleLen[1] = kGateActs * p.nb * 2;
         } else {
             const int q0 = p.r0 + (j - p.nG) * kDownStageRows;
             const int nr = min(kDownStageRows, p.r1 - q0);
             const uint8_t *base = a.down + (int64_t) l * a.down_stride;
-            dma16(base + (int64_t) q0 * F, slot, nr * F);
-            dma4(base + (int64_t) W * F + (int64_t) q0 * p.nbF * 2, slot + kSlotScales, nr * p.nbF * 2);
+            r.bytes[0] = r.bytes[1] = base + (int64_t) q0 * F;
+            r.byteLen[0] = nr * F;
+            r.byteLen[1] = 0;
+            r.scales[0] = r.scales[1] = base + (int64_t) W * F + (int64_t) q0 * p.nbF * 2;
+            r.scaleLen[0] = nr * p.nbF * 2;
+            r.scaleLen[1] = 0;
         }
     } else {
         const int q0 = p.hr0 + (s - a.layers * p.perLayer) * kHeadStageRows;
         const int nr = min(kHeadStageRows, p.hr1 - q0);
         const int64_t V = a.vocab;
-        dma16(a.embedding + (int64_t) q0 * W, slot, nr * W);
-        dma4(a.embedding + V * W + (int64_t) q0 * p.nb * 2, slot + kSlotScales, nr * p.nb * 2);
+        r.bytes[0] = r.bytes[1] = a.embedding + (int64_t) q0 * W;
+        r.byteLen[0] = nr * W;
+        r.byteLen[1] = 0;
+        r.scales[0] = r.scales[1] = a.embedding + V * W + (int64_t) q0 * p.nb * 2;
+        r.scaleLen[0] = nr * p.nb * 2;
+        r.scaleLen[1] = 0;
+    }
+    return r;
+}
+
+struct StageRegs {
+    int4 piece[kStagePieces];
+    uint32_t scale[kStageScaleWords];
+};
+
+// A region as a raw buffer: loads past its end read as zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t region_buffer(const uint8_t *base, int bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0, bytes, 0x00020000);
+}
+
+// Stage regions into registers.  Byte piece i is slot bytes [1024 i + 16 lane,
+// + 16): whole-row regions are multiples of 1024 bytes, so a piece lies in one
+// region (a uniform choice).  A scale word may straddle the two scale regions
+// (rows of fewer than 16 blocks), so it is the OR of both regions' reads, one
+// of which is past its region and reads zero.
+__device__ __forceinline__ void load_stage(const StageRegions &r, StageRegs &g)
+{
+    const int lane = opaque_lane();
+    const __amdgpu_buffer_rsrc_t b0 = region_buffer(r.bytes[0], r.byteLen[0]);
+    const __amdgpu_buffer_rsrc_t b1 = region_buffer(r.bytes[1], r.byteLen[1]);
+    const __amdgpu_buffer_rsrc_t s0 = region_buffer(r.scales[0], r.scaleLen[0]);
+    const __amdgpu_buffer_rsrc_t s1 = region_buffer(r.scales[1], r.scaleLen[1]);
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    int issued = 0;
+#pragma unroll
+    for (int i = 0; i < kStagePieces; ++i) {
+        const bool first = 1024 * i < r.byteLen[0];
+        const v4i v = __builtin_amdgcn_raw_buffer_load_b128(first ? b0 : b1, 16 * lane,
+                                                            first ? 1024 * i : 1024 * i - r.byteLen[0], 0);
+        g.piece[i] = make_int4(v.x, v.y, v.z, v.w);
+        if (++issued % kLoadBurst == 0)
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+#pragma unroll
+    for (int j = 0; j < kStageScaleWords; ++j) {
+        const int off = 256 * j + 4 * lane;
+        // an offset before the second region becomes its length: past its end
+        const int off1 = off >= r.scaleLen[0] ? off - r.scaleLen[0] : r.scaleLen[1];
+        g.scale[j] = __builtin_amdgcn_raw_buffer_load_b32(s0, off, 0, 0)
+                     | __builtin_amdgcn_raw_buffer_load_b32(s1, off1, 0, 0);
+        if (++issued % kLoadBurst == 0)
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+}
+
+__device__ __forceinline__ void write_stage(const StageRegions &r, const StageRegs &g, uint8_t *slot)
+{
+    const int lane = opaque_lane();
+    const int bytes = r.byteLen[0] + r.byteLen[1], scales = r.scaleLen[0] + r.scaleLen[1];
+#pragma unroll
+    for (int i = 0; i < kStagePieces; ++i) {
+        const int off = 1024 * i + 16 * lane;
+        if (off < bytes)
+            *reinterpret_cast<int4 *>(slot + off) = g.piece[i];
+    }
+#pragma unroll
+    for (int j = 0; j < kStageScaleWords; ++j) {
+        const int off = 256 * j + 4 * lane;
+        if (off < scales)
+            *reinterpret_cast<uint32_t *>(slot + kSlotScales + off) = g.scale[j];
     }
 }
 
 __device__ __forceinline__ void prefetch_program(const PersistArgs &a, const Plan &p, Shared &sh, int pw)
 {
     const int stages = a.layers * p.perLayer + p.nH;
+    StageRegs g;
     for (int s = pw, k = 0; s < stages; s += kSlots, ++k) {
-        if (!lds_wait(&sh.consumed[pw], k, a.error))
+        const StageRegions r = stage_regions(a, p, s);
+        load_stage(r, g);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // stage s is in registers
+        if (!lds_wait(&sh.consumed[pw], k, a.error))    // its slot has given back stage s - 4
             return;
-        issue_stage(a, p, s, sh.ring[pw]);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // the slot's bytes are in LDS
+        write_stage(r, g, sh.ring[pw]);
         lds_release(&sh.ready[pw], k + 1);
     }
 }
@@ -505,8 +691,7 @@ __device__ __forceinline__ bool phase_qkv(const PersistArgs &a, const Plan &p, S
     } else if (wgWork) {
         int w0, w1;
         quarter(W, cw, w0, w1);
-        if (!stage_words(a.hid_ll, W, w0, w1, word_tag(epoch, 2 * l), reinterpret_cast<uint32_t *>(row),
-                         a.error))
+        if (!stage_words(a.hid_ll, W, w0, w1, word_tag(epoch, 2 * l), a.error))
             return false;
     }
     if (l == 0 || wgWork) {
@@ -523,7 +708,7 @@ __device__ __forceinline__ bool phase_qkv(const PersistArgs &a, const Plan &p, S
         return true;
     int4 a0, a1;
     double sa;
-    if (!norm_q8_row<8, 4>(a, sh, nq, p.nb, bar, a0, a1, sa))
+    if (!norm_q8_row(a, sh, nq, p.nb, 8, 4, bar, a0, a1, sa))
         return false;
     if (!waveWork)
         return true;
@@ -660,47 +845,84 @@ __device__ __forceinline__ bool attention_task(const PersistArgs &a, int l, int 
 #pragma unroll
     for (int i = 0; i < C; ++i)
         acc[i] = 0.0;
-    double q[C];
-    bool haveQ = false;
-    for (int j0 = 0; j0 < n; j0 += kChunkKeys) {
-        // the chunk's cached keys and values (positions before pos; rows past
-        // the split are read in range and never weighted), then q
-        HalfRow<C> kh[kChunkKeys], vh[kChunkKeys];
+    // the first chunk's cached keys and values are loaded before q arrives
+    HalfRow<C> kh[kChunkKeys], vh[kChunkKeys];
+    auto load_chunk = [&](int j0) {
 #pragma unroll
         for (int jj = 0; jj < kChunkKeys; ++jj) {
             const int key = min(k0 + j0 + jj, max(pos - 1, 0));
             kh[jj] = load_half_row<C>(keys + (size_t) key * kvWidth);
             vh[jj] = load_half_row<C>(values + (size_t) key * kvWidth);
         }
-        if (!haveQ) {
-            uint32_t qb[C];
-            if constexpr (C == 1) {
-                if (!ll_get(a.q_ll + h * hd + c0, tag, a.error, qb[0]))
-                    return false;
-            } else {
+    };
+    load_chunk(0);
+    // q, and this step's key and value if the split holds the position (from
+    // the q|k|v phase's tagged rows): one batch of polls
+    const bool freshHere = pos >= k0 && pos < k0 + n;
+    Words<C> qw, kw, vw;
+    qw.at(h * hd + c0);
+    kw.at(kvh * hd + c0);
+    vw.at(kvWidth + kvh * hd + c0);
+    constexpr int P = Words<C>::kPieces;
+    int word[3 * P];
+    uint32_t lo[3 * P], hi[3 * P];
 #pragma unroll
-                for (int i = 0; i < C; i += 2)
-                    if (!get_pair(a.q_ll, h * hd + c0 + i, qWidth, tag, a.error, qb[i], qb[i + 1]))
-                        return false;
-            }
+    for (int k = 0; k < P; ++k) {
+        word[k] = qw.piece[k];
+        word[P + k] = kw.piece[k];
+        word[2 * P + k] = vw.piece[k];
+    }
+    double q[C];
+    HalfRow<C> fk = kh[0], fv = vh[0];
+    if (freshHere) {
+        const uint64_t *rows[3 * P];
+        int sizes[3 * P];
 #pragma unroll
-            for (int i = 0; i < C; ++i)
-                q[i] = active ? (double) __uint_as_float(qb[i]) : 0.0;
-            haveQ = true;
+        for (int k = 0; k < 3 * P; ++k) {
+            rows[k] = k < P ? a.q_ll : a.kv_ll;
+            sizes[k] = k < P ? qWidth : 2 * kvWidth;
         }
-        // this step's key and value come from the q|k|v phase's tagged row
+        if (!get_pieces<3 * P>(rows, word, sizes, tag, a.error, lo, hi))
+            return false;
+    } else {
+        int wq[P];
+        uint32_t ql[P], qh[P];
+#pragma unroll
+        for (int k = 0; k < P; ++k)
+            wq[k] = word[k];
+        if (!get_pairs<P>(a.q_ll, wq, qWidth, tag, a.error, ql, qh))
+            return false;
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            lo[k] = ql[k];
+            hi[k] = qh[k];
+        }
+    }
+    {
+        uint32_t ql[P], qh[P], kl[P], khi[P], vl[P], vhi[P];
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            ql[k] = lo[k];
+            qh[k] = hi[k];
+            kl[k] = lo[P + k];
+            khi[k] = hi[P + k];
+            vl[k] = lo[2 * P + k];
+            vhi[k] = hi[2 * P + k];
+        }
+#pragma unroll
+        for (int i = 0; i < C; ++i) {
+            q[i] = active ? (double) __uint_as_float(qw.value(h * hd + c0, i, ql, qh)) : 0.0;
+            if (freshHere) {
+                set_half<C>(fk, i, (uint16_t) kw.value(kvh * hd + c0, i, kl, khi));
+                set_half<C>(fv, i, (uint16_t) vw.value(kvWidth + kvh * hd + c0, i, vl, vhi));
+            }
+        }
+    }
+    for (int j0 = 0; j0 < n; j0 += kChunkKeys) {
+        if (j0 > 0)
+            load_chunk(j0);
         const int fresh = pos - k0 - j0; // its place in the chunk, if any
         if (fresh >= 0 && fresh < kChunkKeys) {
-            HalfRow<C> fk, fv;
-#pragma unroll
-            for (int i = 0; i < C; ++i) {
-                uint32_t kb, vb;
-                if (!ll_get(a.kv_ll + kvh * hd + c0 + i, tag, a.error, kb)
-                    || !ll_get(a.kv_ll + kvWidth + kvh * hd + c0 + i, tag, a.error, vb))
-                    return false;
-                set_half<C>(fk, i, (uint16_t) kb);
-                set_half<C>(fv, i, (uint16_t) vb);
-            }
 #pragma unroll
             for (int jj = 0; jj < kChunkKeys; ++jj)
                 if (jj == fresh) {
@@ -761,7 +983,7 @@ __device__ __forceinline__ bool attention_task(const PersistArgs &a, int l, int 
 // sp's (max, sum); every split's partials completed before it, so then one
 // batch of loads finds them: lanes c and c + 32 take channel c's first and
 // second half of the splits (in split order), added in that order.
-constexpr int kMergeBatch = 16;
+constexpr int kMergeBatch = 24;
 
 __device__ __forceinline__ bool merge_task(const PersistArgs &a, int l, int h, int cb, const AttnPlan &plan,
                                            uint32_t epoch)
@@ -773,10 +995,11 @@ __device__ __forceinline__ bool merge_task(const PersistArgs &a, int l, int h, i
     const int mlWords = kPersistMaxSplits * a.heads * 4;
     const int partWords = kPersistMaxSplits * qWidth * 2;
     const int sp = lane < splits ? lane : 0;
-    uint32_t m0, m1, s0, s1;
-    if (!get_pair(a.ml_ll, (sp * a.heads + h) * 4, mlWords, tag, a.error, m0, m1)
-        || !get_pair(a.ml_ll, (sp * a.heads + h) * 4 + 2, mlWords, tag, a.error, s0, s1))
+    const int mlWord[2] = {(sp * a.heads + h) * 4, (sp * a.heads + h) * 4 + 2};
+    uint32_t mlLo[2], mlHi[2];
+    if (!get_pairs<2>(a.ml_ll, mlWord, mlWords, tag, a.error, mlLo, mlHi))
         return false;
+    const uint32_t m0 = mlLo[0], m1 = mlHi[0], s0 = mlLo[1], s1 = mlHi[1];
     double total;
     const double f = merge_factor(join_double(m0, m1), join_double(s0, s1), lane < splits, total);
     const int c = lane & (kBlock - 1);
@@ -786,24 +1009,13 @@ __device__ __forceinline__ bool merge_task(const PersistArgs &a, int l, int h, i
     const int sEnd = lane < kBlock ? firstHalf : splits;
     double weighted = 0.0;
     for (int s = 0; s < firstHalf; s += kMergeBatch) {
+        int word[kMergeBatch];
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u)
+            word[u] = (int) (((int64_t) min(sBegin + s + u, splits - 1) * qWidth + ch) * 2);
         uint32_t lo[kMergeBatch], hi[kMergeBatch];
-        v4u v[kMergeBatch];
-#pragma unroll
-        for (int u = 0; u < kMergeBatch; ++u) {
-            const int split = min(sBegin + s + u, splits - 1);
-            v[u] = ld_agent_16(a.part_ll, (uint32_t) (((int64_t) split * qWidth + ch) * 2 * 8),
-                               (uint32_t) partWords * 8);
-        }
-#pragma unroll
-        for (int u = 0; u < kMergeBatch; ++u) {
-            const int split = sBegin + s + u;
-            lo[u] = v[u].x;
-            hi[u] = v[u].z;
-            if (split < sEnd && (v[u].y != tag || v[u].w != tag))
-                if (!get_pair(a.part_ll, (int) (((int64_t) split * qWidth + ch) * 2), partWords, tag, a.error,
-                              lo[u], hi[u]))
-                    return false;
-        }
+        if (!get_pairs<kMergeBatch>(a.part_ll, word, partWords, tag, a.error, lo, hi))
+            return false;
 #pragma unroll
         for (int u = 0; u < kMergeBatch; ++u) {
             // split s + u's factor for the first half, firstHalf + s + u's for
@@ -843,15 +1055,15 @@ __device__ __forceinline__ bool phase_o(const PersistArgs &a, const Plan &p, Sha
         w[k] = load_block(wOut, a.width, qWidth, rBase + k, lane, lane < p.nbQ && rBase + k < p.r1);
     const uint32_t tag = word_tag(epoch, l);
     const int words = qWidth / 4 + p.nbQ;
-    uint32_t bw[8];
-    uint32_t scaleBits = 0;
     const int b = lane < p.nbQ ? lane : 0;
-#pragma unroll
-    for (int k = 0; k < 8; k += 2)
-        if (!get_pair(a.attn_ll, b * 8 + k, words, tag, a.error, bw[k], bw[k + 1]))
-            return false;
-    if (!ll_get(a.attn_ll + qWidth / 4 + b, tag, a.error, scaleBits))
+    // the block's eight byte words and the piece holding its scale word: one batch
+    const int scaleWord = qWidth / 4 + b;
+    const int word[5] = {b * 8, b * 8 + 2, b * 8 + 4, b * 8 + 6, scaleWord & ~1};
+    uint32_t lo[5], hi[5];
+    if (!get_pairs<5>(a.attn_ll, word, words, tag, a.error, lo, hi))
         return false;
+    const uint32_t bw[8] = {lo[0], hi[0], lo[1], hi[1], lo[2], hi[2], lo[3], hi[3]};
+    const uint32_t scaleBits = (scaleWord & 1) ? hi[4] : lo[4];
     const int4 a0 = make_int4((int) bw[0], (int) bw[1], (int) bw[2], (int) bw[3]);
     const int4 a1 = make_int4((int) bw[4], (int) bw[5], (int) bw[6], (int) bw[7]);
     const double sa = lane < p.nbQ ? (double) half_value((uint16_t) scaleBits) : 0.0;
@@ -883,14 +1095,13 @@ __device__ __forceinline__ bool phase_gateup(const PersistArgs &a, const Plan &p
     float *row = reinterpret_cast<float *>(sh.row);
     int w0, w1;
     quarter(W, cw, w0, w1);
-    if (!stage_words(a.hid_ll, W, w0, w1, word_tag(epoch, 2 * l + 1), reinterpret_cast<uint32_t *>(row),
-                     a.error))
+    if (!stage_words(a.hid_ll, W, w0, w1, word_tag(epoch, 2 * l + 1), a.error))
         return false;
     if (!compute_sync(sh, bar, a.error))
         return false;
     int4 a0, a1;
     double sa;
-    if (!norm_q8_row<4, 8>(a, sh, nq, p.nb, bar, a0, a1, sa))
+    if (!norm_q8_row(a, sh, nq, p.nb, 4, 8, bar, a0, a1, sa))
         return false;
     const uint32_t tag = word_tag(epoch, l);
     constexpr int kStagesPerBlock = kBlock / kGateActs;
@@ -960,7 +1171,7 @@ __device__ __forceinline__ bool phase_down(const PersistArgs &a, const Plan &p, 
     int w0, w1;
     quarter(words, cw, w0, w1);
     uint32_t *staged = reinterpret_cast<uint32_t *>(sh.row);
-    if (!stage_words(a.act_ll, words, w0, w1, word_tag(epoch, l), staged, a.error))
+    if (!stage_words(a.act_ll, words, w0, w1, word_tag(epoch, l), a.error))
         return false;
     if (!compute_sync(sh, bar, a.error))
         return false;
@@ -1039,14 +1250,13 @@ __device__ __forceinline__ bool phase_head(const PersistArgs &a, const Plan &p, 
     float *row = reinterpret_cast<float *>(sh.row);
     int w0, w1;
     quarter(W, cw, w0, w1);
-    if (!stage_words(a.hid_ll, W, w0, w1, word_tag(epoch, 2 * a.layers), reinterpret_cast<uint32_t *>(row),
-                     a.error))
+    if (!stage_words(a.hid_ll, W, w0, w1, word_tag(epoch, 2 * a.layers), a.error))
         return false;
     if (!compute_sync(sh, bar, a.error))
         return false;
     int4 a0, a1;
     double sa;
-    if (!norm_q8_row<8, 4>(a, sh, nq, p.nb, bar, a0, a1, sa))
+    if (!norm_q8_row(a, sh, nq, p.nb, 8, 4, bar, a0, a1, sa))
         return false;
     const int headBase = a.layers * p.perLayer;
     unsigned long long best = 0;
@@ -1103,12 +1313,19 @@ __device__ __forceinline__ bool phase_head(const PersistArgs &a, const Plan &p, 
         return true;
     // workgroup 0: every workgroup's candidate, the id, the position, the epoch
     unsigned long long winner = 0;
-    for (int k = lane; k < p.P; k += 64) {
-        uint32_t lo, hi;
-        if (!get_pair(a.cand_ll, 2 * k, 2 * p.P, tag, a.error, lo, hi))
+    for (int k0 = 0; k0 < p.P; k0 += 4 * 64) {
+        int word[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            word[j] = 2 * min(k0 + lane + 64 * j, p.P - 1);
+        uint32_t lo[4], hi[4];
+        if (!get_pairs<4>(a.cand_ll, word, 2 * p.P, tag, a.error, lo, hi))
             return false;
-        const unsigned long long v = ((unsigned long long) hi << 32) | lo;
-        winner = v > winner ? v : winner;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const unsigned long long v = ((unsigned long long) hi[j] << 32) | lo[j];
+            winner = v > winner ? v : winner; // repeats of the last candidate change nothing
+        }
     }
     winner = fold_wave_max(winner);
     if (lane == 0) {
@@ -1158,7 +1375,7 @@ __device__ __forceinline__ void compute_program(const PersistArgs &a, const Plan
 template <int C>
 __global__ __launch_bounds__(kPersistThreads, 1) void persist_step_kernel(PersistArgs a)
 {
-    __shared__ __attribute__((aligned(16))) Shared sh;
+    Shared &sh = g_sh;
     if (threadIdx.x < kSlots) {
         sh.ready[threadIdx.x] = 0;
         sh.consumed[threadIdx.x] = 0;
@@ -1207,7 +1424,8 @@ bool persist_decode_supported(int layers, int width, int heads, int kv_heads, in
     if (grid < 1 || layers < 1 || layers > kPersistMaxLayers || heads < 1 || kv_heads < 1
         || heads % kv_heads != 0 || vocab < 1)
         return false;
-    if (width % 64 != 0 || width > kMaxWidth || intermediate % 64 != 0 || intermediate > kMaxInner)
+    // whole-row byte regions of a stage are multiples of 1024 bytes (eight rows)
+    if (width % 128 != 0 || width > kMaxWidth || intermediate % 64 != 0 || intermediate > kMaxInner)
         return false;
     if (head_dim != 64 && head_dim != 128 && head_dim != 256)
         return false;
