@@ -153,6 +153,104 @@ def prefill_bench(args, G, torch) -> dict:
     }
 
 
+BATCH_METRIC = "Gemma-2B Q8_0 lockstep decode tok/s (16 sequences x (1024 prompt + 128 decode))"
+
+
+def batch_stage_bytes(shape, stage: str, rows: int) -> int:
+    """Algorithmic HBM bytes of one lockstep product launch: the Int8Blocks
+    weights once, the rows' Q8 inputs and fp32 outputs (read and written for
+    a residual)."""
+    w, f, v = shape.width, shape.intermediate, shape.vocab
+    q8 = lambda n: n * 17 // 16  # noqa: E731
+    if stage == "gate_up":
+        return q8(2 * f * w) + rows * (q8(w) + 2 * f * 4)
+    if stage == "lm_head":
+        return q8(v * w) + rows * (q8(w) + v * 4)
+    if stage == "down":
+        return q8(f * w) + rows * (q8(f) + 2 * w * 4)
+    raise ValueError(stage)
+
+
+def batch_bench(args, G, torch) -> dict:
+    """The lockstep workload: S sequences of seeded 1024-token prompts
+    (prefilled one by one, untimed), W untimed lockstep steps, then the
+    sequences are prefilled again and exactly K lockstep steps are timed."""
+    S, prompt_len = args.sequences, args.prompt
+    steps = args.steps
+    shape = G.DecoderShape.gemma_2b(layers=args.layers, max_positions=prompt_len + steps + args.warmup + 1,
+                                    max_step_rows=256)
+    decoder = G.Decoder(shape)
+    threads = args.threads if args.threads > 0 else (os.cpu_count() or 1)
+    decoder.fill_synthetic(threads)
+    batch = G.Batch(decoder, S)
+    prompts = [G.prompt_ids(0xC0FFEE + 5 + 1000 * s, shape.vocab, prompt_len) for s in range(S)]
+
+    def prefill_all():
+        t = time.perf_counter()
+        for s, prompt in enumerate(prompts):
+            batch.prefill(s, prompt)
+        return time.perf_counter() - t
+
+    prefill_all()
+    batch.decode(args.warmup, use_graph=True)
+    prefill_s = prefill_all()
+    log(f"prefill of {S} x {prompt_len} tokens: {prefill_s * 1e3:.1f} ms")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    batch.decode(steps, use_graph=True)
+    torch.cuda.synchronize()
+    seconds = time.perf_counter() - t0
+    tok_s = S * steps / seconds
+    step_bytes = sum(G.algorithmic_batch_step_bytes(shape, [prompt_len + k + 1] * S)
+                     for k in range(steps)) / steps
+    step_gbs = step_bytes * steps / seconds / 1e9
+    log(f"lockstep: {tok_s:.1f} tok/s, {seconds / steps * 1e3:.3f} ms/step, {step_gbs:.0f} GB/s of "
+        f"{step_bytes / 1e9:.4f} GB/step; sequence 0 ids {list(batch.tokens(0, prompt_len, 6))}")
+
+    # stage breakdown and the dominant product's launch duration: eager steps
+    # with every launch group bracketed by HIP events
+    prefill_all()
+    timed = min(steps, 32)
+    decoder.set_timing(True)
+    batch.decode(timed, use_graph=False)
+    timing = decoder.timing()
+    decoder.set_timing(False)
+    total_ms = sum(ms for ms, _ in timing.values())
+    for name, (ms, n) in sorted(timing.items(), key=lambda kv: -kv[1][0]):
+        if n:
+            log(f"  {name:10s} {ms / timed * 1e3:8.1f} us/step  {n // timed:3d} launches/step"
+                f"  {100 * ms / total_ms:5.1f} %")
+    dominant = max(("gate_up", "lm_head", "down"), key=lambda k: timing[k][0])
+    ms, launches = timing[dominant]
+    per_launch_s = ms / launches / 1e3
+    launch_bytes = batch_stage_bytes(shape, dominant, S)
+    achieved = launch_bytes / per_launch_s / 1e9
+    labels = {"gate_up": "q8_rows_kernel (gate|up 2048 -> 2x16384, 16 rows)",
+              "lm_head": "q8_rows_kernel (tied lm_head 2048 -> 256000, 16 rows)",
+              "down": "q8_rows_kernel (down 16384 -> 2048 + residual, 16 rows)"}
+    batch.close()
+    return {
+        "metric": BATCH_METRIC, "value": round(tok_s, 1), "unit": "tok/s",
+        "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": round(seconds / steps * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic: seeded N(0,0.02) weights / N(0,0.1) norms quantized to Int8Blocks, "
+                "seeded uniform prompt ids",
+        "config": {"workload": f"Gemma-2B Int8Blocks lockstep greedy decode, {args.layers} layers, "
+                               f"{S} sequences x ({prompt_len} prompt + {steps} timed steps), "
+                               "fp16 KV caches",
+                   "layers": args.layers, "sequences": S, "prompt_tokens": prompt_len,
+                   "decode_steps": steps, "graph": True},
+        "step_hbm": {"bytes_per_step": int(step_bytes), "achieved_gbs": round(step_gbs, 1),
+                     "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "kernel": labels[dominant], "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "bytes_per_launch": launch_bytes,
+                     "avg_launch_us": round(per_launch_s * 1e6, 2)},
+        "cpu_baseline": None,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -169,9 +267,11 @@ def main() -> int:
                     help="decode steps as one dataflow launch a token")
     ap.add_argument("--persistent", action="store_true",
                     help="decode steps as one persistent launch a token (one workgroup a compute unit)")
-    ap.add_argument("--mode", choices=("decode", "prefill"), default="decode",
+    ap.add_argument("--mode", choices=("decode", "prefill", "batch"), default="decode",
                     help="decode: the headline decode loop; prefill: the 2048-token prefill "
-                         "(use with --prompt 2048)")
+                         "(use with --prompt 2048); batch: lockstep decode of --sequences "
+                         "sequences (use with --prompt 1024 --steps 128)")
+    ap.add_argument("--sequences", type=int, default=16, help="sequences of --mode batch")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first copy MIB MiB device-to-device three times (a kernel of known "
                          "bytes to scale the FETCH_SIZE / WRITE_SIZE counters by)")
@@ -190,6 +290,9 @@ def main() -> int:
         return 1
     if args.mode == "prefill":
         print(json.dumps(prefill_bench(args, G, torch)), flush=True)
+        return 0
+    if args.mode == "batch":
+        print(json.dumps(batch_bench(args, G, torch)), flush=True)
         return 0
     threads = args.threads if args.threads > 0 else (os.cpu_count() or 1)
     if args.copy_probe > 0:

@@ -69,8 +69,13 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_kernel(const float *__
 }
 
 // ---- embedding gather (Embed.h:45-82) ------------------------------------
+// Row r embeds tokens[*pos_ptr + r] (one sequence), or with row_positions
+// tokens[r * slot_stride + row_positions[r]] (row r of a lockstep batch, each
+// sequence's slots slot_stride apart).
 __global__ __launch_bounds__(kThreads) void embed_kernel(const uint32_t *__restrict__ tokens,
                                                          const int *pos_ptr,
+                                                         const int *row_positions,
+                                                         int64_t slot_stride,
                                                          const uint8_t *__restrict__ table,
                                                          int64_t vocab, int width, float scale,
                                                          float *__restrict__ out)
@@ -79,8 +84,9 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const uint32_t *__restr
     const int c = blockIdx.x * kThreads + threadIdx.x;
     if (c >= width)
         return;
-    const int base = pos_ptr ? *pos_ptr : 0;
-    uint32_t token = tokens[base + row];
+    const int64_t slot = row_positions ? row * slot_stride + row_positions[row]
+                                       : (int64_t) (pos_ptr ? *pos_ptr : 0) + row;
+    uint32_t token = tokens[slot];
     if (token >= (uint32_t) vocab) // ids are validated on the host; a guard, not a rule
         token = 0;
     const int64_t e = (int64_t) token * width + c;
@@ -101,10 +107,29 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restri
     const int row = blockIdx.x;
     const float *xr = x + (int64_t) row * width;
 
+    // rows up to kThreads * kNormHeld wide are loaded once, all at once
+    constexpr int kNormHeld = 16;
+    const bool held = width <= kThreads * kNormHeld;
+    float xv[kNormHeld], wv[kNormHeld];
+    if (held) {
+#pragma unroll
+        for (int k = 0; k < kNormHeld; ++k) {
+            const int i = min(threadIdx.x + k * kThreads, width - 1); // clamped; masked below
+            xv[k] = xr[i];
+            wv[k] = weight[i];
+        }
+    }
     double squares = 0.0;
-    for (int i = threadIdx.x; i < width; i += kThreads) {
-        const double v = (double) xr[i];
-        squares += v * v; // the square is exact in double
+    if (held) {
+#pragma unroll
+        for (int k = 0; k < kNormHeld; ++k)
+            if (threadIdx.x + k * kThreads < width)
+                squares += (double) xv[k] * (double) xv[k]; // the square is exact in double
+    } else {
+        for (int i = threadIdx.x; i < width; i += kThreads) {
+            const double v = (double) xr[i];
+            squares += v * v;
+        }
     }
     squares = wave_sum(squares);
     if ((threadIdx.x & 63) == 0)
@@ -116,6 +141,22 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restri
     const double scale = norm_scale(total, width, epsilon);
 
     const int64_t elements = (int64_t) rows * width;
+    if (held) {
+#pragma unroll
+        for (int k = 0; k < kNormHeld; ++k) {
+            const int i = threadIdx.x + k * kThreads;
+            if (i >= width) // whole 32-element groups drop out together
+                break;
+            const int64_t at = (int64_t) row * width + i;
+            const float v = norm_value(xv[k], scale, wv[k]);
+            if (y)
+                y[at] = v;
+            if (q8)
+                quantize_in_group(v, threadIdx.x & 31, q8 + at,
+                                  reinterpret_cast<uint16_t *>(q8 + elements) + at / kBlock);
+        }
+        return;
+    }
     for (int i = threadIdx.x; i < width; i += kThreads) {
         const int64_t at = (int64_t) row * width + i;
         const float v = norm_value(xr[i], scale, weight[i]);
@@ -150,19 +191,24 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(float *__restrict__ x, i
 
 // The step's q|k|v rows: q rotated in place, k rotated and stored fp16 in the
 // key cache, v stored fp16 in the value cache (Decoder.cpp:459-548).
+// Row r sits at position base + r of one sequence's caches, or with
+// row_positions at row_positions[r] of sequence r's caches (cache_stride
+// elements apart: the rows of a lockstep batch).
 __global__ __launch_bounds__(kThreads) void rope_kv_kernel(
     float *__restrict__ qkv, int qkv_stride, int heads, int kv_heads, int head_dim,
-    const int *pos_ptr, int pos_value, const float *__restrict__ cosines,
-    const float *__restrict__ sines, uint16_t *__restrict__ key_cache,
-    uint16_t *__restrict__ value_cache)
+    const int *pos_ptr, int pos_value, const int *row_positions, int64_t cache_stride,
+    const float *__restrict__ cosines, const float *__restrict__ sines,
+    uint16_t *__restrict__ key_cache, uint16_t *__restrict__ value_cache)
 {
     const int row = blockIdx.x;
     const int half = head_dim / 2;
     const int qWidth = heads * head_dim, kvWidth = kv_heads * head_dim;
-    const int position = (pos_ptr ? *pos_ptr : 0) + pos_value + row;
+    const int position =
+        row_positions ? row_positions[row] : (pos_ptr ? *pos_ptr : 0) + pos_value + row;
+    const int64_t cache = row_positions ? row * cache_stride : 0;
     float *r = qkv + (int64_t) row * qkv_stride;
-    uint16_t *keys = key_cache + (int64_t) position * kvWidth;
-    uint16_t *values = value_cache + (int64_t) position * kvWidth;
+    uint16_t *keys = key_cache + cache + (int64_t) position * kvWidth;
+    uint16_t *values = value_cache + cache + (int64_t) position * kvWidth;
 
     for (int idx = threadIdx.x; idx < (heads + kv_heads) * half; idx += kThreads) {
         const int head = idx / half, pair = idx % half;
@@ -760,7 +806,20 @@ hipError_t launch_embed(const uint32_t *tokens, const int *pos_ptr, int rows,
     if (rows <= 0 || width <= 0 || width % kBlock != 0)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(embed_kernel, dim3(blocks_for(width, kThreads), rows), dim3(kThreads), 0,
-                       stream, tokens, pos_ptr, table, (int64_t) vocab, width, scale, out);
+                       stream, tokens, pos_ptr, nullptr, (int64_t) 0, table, (int64_t) vocab, width,
+                       scale, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_slots(const uint32_t *slots, int64_t slot_stride, const int *positions,
+                              int rows, const uint8_t *table, int vocab, int width, float scale,
+                              float *out, hipStream_t stream)
+{
+    if (rows <= 0 || width <= 0 || width % kBlock != 0 || !positions || slot_stride <= 0)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(embed_kernel, dim3(blocks_for(width, kThreads), rows), dim3(kThreads), 0,
+                       stream, slots, nullptr, positions, slot_stride, table, (int64_t) vocab,
+                       width, scale, out);
     return hipGetLastError();
 }
 
@@ -793,8 +852,22 @@ hipError_t launch_rope_kv(float *qkv, int qkv_stride, int heads, int kv_heads, i
     if (rows <= 0 || heads <= 0 || kv_heads <= 0 || head_dim % 2 != 0)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(rope_kv_kernel, dim3(rows), dim3(kThreads), 0, stream, qkv, qkv_stride,
-                       heads, kv_heads, head_dim, pos_ptr, pos_value, cosines, sines, key_cache,
-                       value_cache);
+                       heads, kv_heads, head_dim, pos_ptr, pos_value, nullptr, (int64_t) 0,
+                       cosines, sines, key_cache, value_cache);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_kv_rows(float *qkv, int qkv_stride, int heads, int kv_heads, int head_dim,
+                               const int *positions, int rows, const float *cosines,
+                               const float *sines, uint16_t *key_cache, uint16_t *value_cache,
+                               int64_t cache_stride, hipStream_t stream)
+{
+    if (rows <= 0 || heads <= 0 || kv_heads <= 0 || head_dim % 2 != 0 || !positions
+        || cache_stride <= 0)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rope_kv_kernel, dim3(rows), dim3(kThreads), 0, stream, qkv, qkv_stride,
+                       heads, kv_heads, head_dim, nullptr, 0, positions, cache_stride, cosines,
+                       sines, key_cache, value_cache);
     return hipGetLastError();
 }
 

@@ -96,4 +96,67 @@ hipError_t launch_argmax(const float *logits, const float *mask, int rows, int l
 
 hipError_t launch_advance(int *pos_ptr, int amount, hipStream_t stream);
 
+// ---- lockstep sequences (one step of up to kBatchRows independent sequences
+// over one weight set) ----------------------------------------------------------
+// Row r: sequence r, at position positions[r]; its token slots start at
+// slots + r * slot_stride and its caches at key_cache / value_cache +
+// r * cache_stride.
+constexpr int kBatchRows = 16;
+
+hipError_t launch_embed_slots(const uint32_t *slots, int64_t slot_stride, const int *positions,
+                              int rows, const uint8_t *table, int vocab, int width, float scale,
+                              float *out, hipStream_t stream);
+
+hipError_t launch_rope_kv_rows(float *qkv, int qkv_stride, int heads, int kv_heads, int head_dim,
+                               const int *positions, int rows, const float *cosines,
+                               const float *sines, uint16_t *key_cache, uint16_t *value_cache,
+                               int64_t cache_stride, hipStream_t stream);
+
+// y[m, n] (+)= the Int8Blocks product of up to kBatchRows activation rows (a
+// Q8 row buffer of x_rows rows, rows [0, rows) used) on int8 MFMA.  Products
+// too small to fill the chip split their blocks over several workgroups:
+// partials (rows_workspace_bytes) and tickets (rows_ticket_count ints, zero
+// between launches) carry the split.
+size_t rows_workspace_bytes(int inner, int outputs);
+int rows_ticket_count(int outputs);
+hipError_t launch_q8_rows(const uint8_t *x8, int x_rows, int rows, const uint8_t *w8, int inner,
+                          int outputs, float *y, int y_stride, int residual, double *partials,
+                          size_t partial_bytes, int *tickets, hipStream_t stream);
+
+// Attention of the lockstep rows with the step's RoPE and cache append
+// (multi-query: one KV head).  qkv row r holds sequence r's unrotated
+// q | k | v; the keys [0, positions[r]] of sequence r's caches (the layer's
+// base for sequence 0, cache_stride elements a sequence) are attended after
+// the new key and value are appended at positions[r].  The merged row goes to
+// row r of a Q8 row buffer of q8_rows rows.  per_split is
+// rows_attention_split_keys(max_positions); ws_o / ws_ml hold
+// rows_attention_workspace_doubles; tickets (one a row) are zero between
+// launches.
+constexpr int kRowsMaxSplits = 32;
+struct RowsAttentionArgs {
+    const float *qkv;
+    int qkv_stride;
+    const int *positions;
+    const float *cosines, *sines;
+    uint16_t *key_cache, *value_cache;
+    int64_t cache_stride;
+    int heads, head_dim;
+    float scale;
+    int per_split;
+    double *ws_o, *ws_ml;
+    int *tickets;
+    uint8_t *q8;
+    int q8_rows;
+};
+bool rows_attention_supported(int heads, int kv_heads, int head_dim, int max_positions);
+int rows_attention_split_keys(int max_positions);
+size_t rows_attention_workspace_doubles(int rows, int heads, int head_dim);
+hipError_t launch_rows_attention(const RowsAttentionArgs &a, int rows, int max_positions,
+                                 hipStream_t stream);
+
+// After the argmax of a step: slot positions[r] + 1 of sequence r takes
+// chosen[r], and positions[r] advances by one.
+hipError_t launch_batch_advance(const uint32_t *chosen, uint32_t *slots, int64_t slot_stride,
+                                int *positions, int rows, hipStream_t stream);
+
 } // namespace gq8

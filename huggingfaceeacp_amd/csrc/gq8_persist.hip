@@ -1092,7 +1092,6 @@ __device__ __forceinline__ bool phase_gateup(const PersistArgs &a, const Plan &p
         return true;
     const int W = a.width, F = a.intermediate;
     const NormQuarter nq = load_norm_quarter(a.post_norm + (int64_t) l * a.norm_stride, p.nb, cw);
-    float *row = reinterpret_cast<float *>(sh.row);
     int w0, w1;
     quarter(W, cw, w0, w1);
     if (!stage_words(a.hid_ll, W, w0, w1, word_tag(epoch, 2 * l + 1), a.error))
@@ -1247,7 +1246,6 @@ __device__ __forceinline__ bool phase_head(const PersistArgs &a, const Plan &p, 
     const int lane = opaque_lane();
     const int W = a.width;
     const NormQuarter nq = load_norm_quarter(a.final_norm, p.nb, cw);
-    float *row = reinterpret_cast<float *>(sh.row);
     int w0, w1;
     quarter(W, cw, w0, w1);
     if (!stage_words(a.hid_ll, W, w0, w1, word_tag(epoch, 2 * a.layers), a.error))

@@ -1903,3 +1903,386 @@ extern "C" int gq8_decoder_timing(gq8_decoder *d, double *milliseconds, int *lau
     d->marks.clear();
     return GQ8_OK;
 }
+
+// ==== lockstep sequences ======================================================
+// S sequences (S <= 16) decoded in lockstep over one decoder's weights: the
+// reference's S separate greedy loops (Gemma.cpp:459-543), each with its own
+// cache and token slots.  A prompt is prefilled through the decoder's own step
+// path with the decoder pointed at the sequence's cache, slots and position
+// (the prefill arithmetic is the one-sequence path's); a lockstep step then
+// carries one row per sequence: the products run all rows against one read of
+// the weights (q8_rows_kernel), RoPE, the cache append and attention take
+// each row's own position and cache.
+
+struct gq8_batch {
+    gq8_decoder *d = nullptr;
+    int sequences = 0;
+    int64_t cacheStride = 0; // elements between two sequences' caches
+    int64_t slotStride = 0;  // slots a sequence (max_positions + 1)
+    uint16_t *keyCache = nullptr, *valueCache = nullptr;
+    uint32_t *slots = nullptr;
+    int *positions = nullptr; // device: the position each sequence's next step takes
+    std::vector<int> hostPositions;
+    float *hidden = nullptr, *qkvRows = nullptr, *fused = nullptr, *logits = nullptr;
+    uint8_t *x8 = nullptr;
+    uint32_t *chosen = nullptr;
+    double *attnO = nullptr, *attnMl = nullptr;
+    int *attnCounters = nullptr;
+    double *partials = nullptr;
+    size_t partialBytes = 0;
+    int *tickets = nullptr;
+    void *argmaxWorkspace = nullptr;
+    size_t argmaxWorkspaceBytes = 0;
+    hipGraphExec_t graph = nullptr;
+    std::vector<void *> allocations;
+};
+
+namespace {
+
+int batch_alloc(gq8_batch *b, void **out, size_t bytes)
+{
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+        (void) hipGetLastError();
+        return fail(GQ8_ERR_MEMORY, "hipMalloc of " + std::to_string(bytes) + " bytes failed");
+    }
+    b->allocations.push_back(p);
+    *out = p;
+    return GQ8_OK;
+}
+
+template <typename T>
+int batch_alloc_as(gq8_batch *b, T **out, size_t bytes)
+{
+    void *p = nullptr;
+    const int s = batch_alloc(b, &p, bytes);
+    *out = reinterpret_cast<T *>(p);
+    return s;
+}
+
+// The decoder pointed at one sequence of a batch for the length of a prefill.
+struct SequenceLoan {
+    gq8_decoder *d;
+    uint16_t *keyCache, *valueCache;
+    uint32_t *sequence;
+    int *position;
+    int hostPosition;
+    SequenceLoan(gq8_decoder *decoder, gq8_batch *b, int s)
+        : d(decoder), keyCache(d->keyCache), valueCache(d->valueCache), sequence(d->sequence),
+          position(d->position), hostPosition(d->hostPosition)
+    {
+        d->keyCache = b->keyCache + s * b->cacheStride;
+        d->valueCache = b->valueCache + s * b->cacheStride;
+        d->sequence = b->slots + s * b->slotStride;
+        d->position = b->positions + s;
+        d->hostPosition = 0;
+    }
+    ~SequenceLoan()
+    {
+        d->keyCache = keyCache;
+        d->valueCache = valueCache;
+        d->sequence = sequence;
+        d->position = position;
+        d->hostPosition = hostPosition;
+    }
+};
+
+int batch_product(gq8_batch *b, int inner, int outputs, const uint8_t *w, float *y, int yStride,
+                  int residual)
+{
+    GQ8_LAUNCH(gq8::launch_q8_rows(b->x8, b->sequences, b->sequences, w, inner, outputs, y, yStride,
+                                   residual, b->partials, b->partialBytes, b->tickets,
+                                   b->d->stream));
+    return GQ8_OK;
+}
+
+#define GQ8_BATCH_STAGE(stage, expr)         \
+    do {                                     \
+        StageTimer timer_(d, stage);         \
+        if (int status_ = (expr))            \
+            return status_;                  \
+    } while (0)
+
+// One lockstep step: every sequence's token at its position, its argmax into
+// the next slot, every position advanced by one.
+int encode_batch_step(gq8_batch *b)
+{
+    gq8_decoder *d = b->d;
+    const gq8_shape &s = d->shape;
+    const int S = b->sequences, W = s.width, F = s.intermediate;
+    hipStream_t st = d->stream;
+
+    GQ8_STAGE(kStageEmbed, gq8::launch_embed_slots(b->slots, b->slotStride, b->positions, S,
+                                                   d->embedding, s.vocab, W, s.embedding_scale,
+                                                   b->hidden, st));
+    for (int l = 0; l < s.layers; ++l) {
+        const int64_t layerCache = (int64_t) l * s.max_positions * d->kvWidth;
+        GQ8_STAGE(kStageNorm, gq8::launch_rmsnorm(b->hidden, d->inputNorm[l], S, W, s.rms_epsilon,
+                                                  nullptr, b->x8, st));
+        GQ8_BATCH_STAGE(kStageQkv, batch_product(b, W, d->qkvWidth, d->qkv[l], b->qkvRows,
+                                                 d->qkvWidth, 0));
+        gq8::RowsAttentionArgs at{};
+        at.qkv = b->qkvRows;
+        at.qkv_stride = d->qkvWidth;
+        at.positions = b->positions;
+        at.cosines = d->cosines;
+        at.sines = d->sines;
+        at.key_cache = b->keyCache + layerCache;
+        at.value_cache = b->valueCache + layerCache;
+        at.cache_stride = b->cacheStride;
+        at.heads = s.heads;
+        at.head_dim = s.head_dim;
+        at.scale = 1.f / std::sqrt((float) s.head_dim);
+        at.per_split = gq8::rows_attention_split_keys(s.max_positions);
+        at.ws_o = b->attnO;
+        at.ws_ml = b->attnMl;
+        at.tickets = b->attnCounters;
+        at.q8 = b->x8;
+        at.q8_rows = S;
+        GQ8_STAGE(kStageAttention, gq8::launch_rows_attention(at, S, s.max_positions, st));
+        GQ8_BATCH_STAGE(kStageO, batch_product(b, d->qWidth, W, d->out[l], b->hidden, W, 1));
+        GQ8_STAGE(kStageNorm, gq8::launch_rmsnorm(b->hidden, d->postNorm[l], S, W, s.rms_epsilon,
+                                                  nullptr, b->x8, st));
+        GQ8_BATCH_STAGE(kStageGateUp, batch_product(b, W, 2 * F, d->gateUp[l], b->fused, 2 * F, 0));
+        GQ8_STAGE(kStageGeglu, gq8::launch_geglu(b->fused, S, F, nullptr, b->x8, st));
+        GQ8_BATCH_STAGE(kStageDown, batch_product(b, F, W, d->down[l], b->hidden, W, 1));
+    }
+    GQ8_STAGE(kStageNorm, gq8::launch_rmsnorm(b->hidden, d->finalNorm, S, W, s.rms_epsilon, nullptr,
+                                              b->x8, st));
+    GQ8_BATCH_STAGE(kStageLogits, batch_product(b, W, s.vocab, d->embedding, b->logits, s.vocab, 0));
+    GQ8_STAGE(kStageArgmax, gq8::launch_argmax(b->logits, nullptr, S, s.vocab, b->chosen, nullptr, 0,
+                                               b->argmaxWorkspace, b->argmaxWorkspaceBytes, st));
+    GQ8_LAUNCH(gq8::launch_batch_advance(b->chosen, b->slots, b->slotStride, b->positions, S, st));
+    return GQ8_OK;
+}
+
+int ensure_batch_graph(gq8_batch *b)
+{
+    if (b->graph)
+        return GQ8_OK;
+    gq8_decoder *d = b->d;
+    hipGraph_t graph = nullptr;
+    GQ8_HIP(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
+    d->capturing = true;
+    const int status = encode_batch_step(b);
+    d->capturing = false;
+    hipError_t end = hipStreamEndCapture(d->stream, &graph);
+    if (status != GQ8_OK) {
+        if (graph)
+            (void) hipGraphDestroy(graph);
+        return status;
+    }
+    if (end != hipSuccess)
+        return fail(GQ8_ERR_DEVICE, std::string("hipStreamEndCapture: ") + hipGetErrorString(end));
+    hipError_t inst = hipGraphInstantiate(&b->graph, graph, nullptr, nullptr, 0);
+    (void) hipGraphDestroy(graph);
+    if (inst != hipSuccess) {
+        b->graph = nullptr;
+        return fail(GQ8_ERR_DEVICE, std::string("hipGraphInstantiate: ") + hipGetErrorString(inst));
+    }
+    return GQ8_OK;
+}
+
+int check_sequence(const gq8_batch *b, int sequence)
+{
+    if (sequence < 0 || sequence >= b->sequences)
+        return fail(GQ8_ERR_ARGUMENT, "sequence " + std::to_string(sequence) + " is outside a batch of "
+                                          + std::to_string(b->sequences));
+    return GQ8_OK;
+}
+
+} // namespace
+
+extern "C" void gq8_batch_destroy(gq8_batch *b)
+{
+    if (!b)
+        return;
+    if (b->d && b->d->stream)
+        (void) hipStreamSynchronize(b->d->stream);
+    if (b->graph)
+        (void) hipGraphExecDestroy(b->graph);
+    for (void *p : b->allocations)
+        (void) hipFree(p);
+    delete b;
+}
+
+extern "C" int gq8_batch_create(gq8_decoder *d, int sequences, gq8_batch **out)
+{
+    if (!d || !out)
+        return fail(GQ8_ERR_ARGUMENT, "batch_create: null argument");
+    *out = nullptr;
+    if (sequences <= 0 || sequences > gq8::kBatchRows)
+        return fail(GQ8_ERR_ARGUMENT, "a lockstep batch holds 1 to " + std::to_string(gq8::kBatchRows)
+                                          + " sequences, not " + std::to_string(sequences));
+    const gq8_shape &s = d->shape;
+    if (!gq8::rows_attention_supported(s.heads, s.kv_heads, s.head_dim, s.max_positions))
+        return fail(GQ8_ERR_SHAPE, "lockstep decode takes multi-query attention (one KV head) "
+                                   "with 2, 4 or 8 query heads of width 64, 128 or 256");
+    auto *b = new gq8_batch();
+    b->d = d;
+    b->sequences = sequences;
+    b->cacheStride = (int64_t) s.layers * s.max_positions * d->kvWidth;
+    b->slotStride = (int64_t) s.max_positions + 1;
+    b->hostPositions.assign(sequences, 0);
+    auto cleanup = [&](int status) {
+        gq8_batch_destroy(b);
+        return status;
+    };
+    const int S = sequences, W = s.width, F = s.intermediate;
+    int st = GQ8_OK;
+#define GQ8_BATCH_ALLOC(ptr, bytes)                                \
+    if ((st = batch_alloc_as(b, &(ptr), (size_t) (bytes))) != 0)   \
+        return cleanup(st)
+    GQ8_BATCH_ALLOC(b->keyCache, b->cacheStride * S * sizeof(uint16_t));
+    GQ8_BATCH_ALLOC(b->valueCache, b->cacheStride * S * sizeof(uint16_t));
+    GQ8_BATCH_ALLOC(b->slots, b->slotStride * S * sizeof(uint32_t));
+    GQ8_BATCH_ALLOC(b->positions, S * sizeof(int));
+    GQ8_BATCH_ALLOC(b->hidden, (size_t) S * W * sizeof(float));
+    GQ8_BATCH_ALLOC(b->qkvRows, (size_t) S * d->qkvWidth * sizeof(float));
+    GQ8_BATCH_ALLOC(b->fused, (size_t) S * 2 * F * sizeof(float));
+    GQ8_BATCH_ALLOC(b->logits, (size_t) S * s.vocab * sizeof(float));
+    GQ8_BATCH_ALLOC(b->x8, gq8::q8_bytes(S, d->maxInner));
+    GQ8_BATCH_ALLOC(b->chosen, S * sizeof(uint32_t));
+    GQ8_BATCH_ALLOC(b->attnO, gq8::rows_attention_workspace_doubles(S, s.heads, s.head_dim)
+                                  * sizeof(double));
+    b->attnMl = b->attnO + (size_t) S * gq8::kRowsMaxSplits * d->qWidth;
+    GQ8_BATCH_ALLOC(b->attnCounters, (size_t) S * sizeof(int));
+    {
+        const int products[5][2] = {{W, d->qkvWidth}, {d->qWidth, W}, {W, 2 * F}, {F, W},
+                                    {W, s.vocab}};
+        size_t bytes = 0;
+        int tickets = 0;
+        for (auto &p : products) {
+            bytes = std::max(bytes, gq8::rows_workspace_bytes(p[0], p[1]));
+            tickets = std::max(tickets, gq8::rows_ticket_count(p[1]));
+        }
+        b->partialBytes = bytes;
+        if (bytes)
+            GQ8_BATCH_ALLOC(b->partials, bytes);
+        GQ8_BATCH_ALLOC(b->tickets, (size_t) tickets * sizeof(int));
+        if (hipMemset(b->tickets, 0, (size_t) tickets * sizeof(int)) != hipSuccess)
+            return cleanup(fail(GQ8_ERR_DEVICE, "batch tickets: initialisation failed"));
+    }
+    b->argmaxWorkspaceBytes = gq8::argmax_workspace_bytes(S, s.vocab);
+    if (b->argmaxWorkspaceBytes)
+        GQ8_BATCH_ALLOC(b->argmaxWorkspace, b->argmaxWorkspaceBytes);
+#undef GQ8_BATCH_ALLOC
+    if (hipMemset(b->attnCounters, 0, (size_t) S * sizeof(int)) != hipSuccess
+        || hipMemset(b->positions, 0, S * sizeof(int)) != hipSuccess
+        || hipMemset(b->slots, 0, b->slotStride * S * sizeof(uint32_t)) != hipSuccess)
+        return cleanup(fail(GQ8_ERR_DEVICE, "batch state: initialisation failed"));
+    *out = b;
+    return GQ8_OK;
+}
+
+extern "C" int gq8_batch_prefill(gq8_batch *b, int sequence, const int32_t *prompt,
+                                 int prompt_length)
+{
+    if (!b || !prompt)
+        return fail(GQ8_ERR_ARGUMENT, "batch_prefill: null argument");
+    if (int st = check_sequence(b, sequence))
+        return st;
+    gq8_decoder *d = b->d;
+    const gq8_shape &s = d->shape;
+    if (prompt_length <= 0)
+        return fail(GQ8_ERR_EMPTY, "a run needs at least one prompt token");
+    if (prompt_length > s.max_positions)
+        return fail(GQ8_ERR_WINDOW, "the prompt is longer than the window");
+    for (int i = 0; i < prompt_length; ++i)
+        if (prompt[i] < 0 || prompt[i] >= s.vocab)
+            return fail(GQ8_ERR_TOKEN, "prompt token " + std::to_string(prompt[i])
+                                           + " is outside a vocabulary of "
+                                           + std::to_string(s.vocab));
+    for (size_t i = 0; i < d->present.size(); ++i)
+        if (!d->present[i])
+            return fail(GQ8_ERR_NOT_PREPARED, "tensor " + std::to_string(i) + " was never loaded");
+    GQ8_HIP(hipStreamSynchronize(d->stream));
+    uint32_t *slots = b->slots + sequence * b->slotStride;
+    GQ8_HIP(hipMemsetAsync(b->positions + sequence, 0, sizeof(int), d->stream));
+    GQ8_HIP(hipMemcpyAsync(slots, prompt, prompt_length * sizeof(uint32_t), hipMemcpyHostToDevice,
+                           d->stream));
+    b->hostPositions[sequence] = 0;
+    {
+        SequenceLoan loan(d, b, sequence);
+        // the prefill in blocks of the step capacity (Gemma.cpp:350-380); the
+        // last row's argmax goes to slot prompt_length
+        for (int first = 0; first < prompt_length; first += d->capacity) {
+            const int rows = std::min(d->capacity, prompt_length - first);
+            const bool last = first + rows >= prompt_length;
+            if (int st = encode_step(d, rows, last ? d->logits : nullptr, last ? 1 : 0, last))
+                return st;
+            d->hostPosition += rows;
+        }
+        GQ8_HIP(hipStreamSynchronize(d->stream));
+        if (int st = check_step_error(d))
+            return st;
+    }
+    b->hostPositions[sequence] = prompt_length;
+    return GQ8_OK;
+}
+
+extern "C" int gq8_batch_decode(gq8_batch *b, int steps, int use_graph)
+{
+    if (!b || steps < 0)
+        return fail(GQ8_ERR_ARGUMENT, "batch_decode: bad arguments");
+    const gq8_shape &s = b->d->shape;
+    for (int i = 0; i < b->sequences; ++i) {
+        if (b->hostPositions[i] == 0)
+            return fail(GQ8_ERR_NOT_PREPARED, "sequence " + std::to_string(i) + " has no prompt");
+        if (b->hostPositions[i] + steps > s.max_positions)
+            return fail(GQ8_ERR_WINDOW, "sequence " + std::to_string(i) + " would pass the window of "
+                                            + std::to_string(s.max_positions));
+    }
+    if (steps == 0)
+        return GQ8_OK;
+    if (use_graph)
+        if (int st = ensure_batch_graph(b))
+            return st;
+    for (int i = 0; i < steps; ++i) {
+        if (use_graph)
+            GQ8_HIP(hipGraphLaunch(b->graph, b->d->stream));
+        else if (int st = encode_batch_step(b))
+            return st;
+    }
+    for (int &p : b->hostPositions)
+        p += steps;
+    GQ8_HIP(hipStreamSynchronize(b->d->stream));
+    return GQ8_OK;
+}
+
+extern "C" int gq8_batch_sequences(const gq8_batch *b)
+{
+    return b ? b->sequences : fail(GQ8_ERR_ARGUMENT, "batch_sequences: null batch");
+}
+
+extern "C" int gq8_batch_position(const gq8_batch *b, int sequence)
+{
+    if (!b)
+        return fail(GQ8_ERR_ARGUMENT, "batch_position: null batch");
+    if (int st = check_sequence(b, sequence))
+        return st;
+    return b->hostPositions[sequence];
+}
+
+extern "C" int gq8_batch_tokens(gq8_batch *b, int sequence, int first, int count,
+                                int32_t *host_out)
+{
+    if (!b || !host_out || first < 0 || count < 0 || first + count > b->slotStride)
+        return fail(GQ8_ERR_ARGUMENT, "batch_tokens: bad range");
+    if (int st = check_sequence(b, sequence))
+        return st;
+    GQ8_HIP(hipStreamSynchronize(b->d->stream));
+    GQ8_HIP(hipMemcpy(host_out, b->slots + sequence * b->slotStride + first,
+                      count * sizeof(uint32_t), hipMemcpyDeviceToHost));
+    return GQ8_OK;
+}
+
+extern "C" int gq8_batch_logits(gq8_batch *b, float *host_out)
+{
+    if (!b || !host_out)
+        return fail(GQ8_ERR_ARGUMENT, "batch_logits: null argument");
+    GQ8_HIP(hipStreamSynchronize(b->d->stream));
+    GQ8_HIP(hipMemcpy(host_out, b->logits, (size_t) b->sequences * b->d->shape.vocab * sizeof(float),
+                      hipMemcpyDeviceToHost));
+    return GQ8_OK;
+}

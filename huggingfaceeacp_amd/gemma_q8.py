@@ -123,6 +123,14 @@ def library() -> ctypes.CDLL:
         "gq8_decoder_set_timing": (i32, [P, i32]),
         "gq8_decoder_timing": (i32, [P, P, P]),
         "gq8_decoder_time_kernel": (i32, [P, i32, i32, ctypes.POINTER(f64), ctypes.POINTER(i32)]),
+        "gq8_batch_create": (i32, [P, i32, ctypes.POINTER(P)]),
+        "gq8_batch_destroy": (None, [P]),
+        "gq8_batch_prefill": (i32, [P, i32, P, i32]),
+        "gq8_batch_decode": (i32, [P, i32, i32]),
+        "gq8_batch_sequences": (i32, [P]),
+        "gq8_batch_position": (i32, [P, i32]),
+        "gq8_batch_tokens": (i32, [P, i32, i32, i32, P]),
+        "gq8_batch_logits": (i32, [P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -431,6 +439,53 @@ class Decoder:
                                             stats.step_count, stats.generated)
 
 
+class Batch:
+    """Up to 16 independent sequences decoded in lockstep over one Decoder's
+    weights: S separate greedy loops (Gemma.cpp:459-543) in one step a token.
+    The decoder must stay open while the batch is."""
+
+    def __init__(self, decoder: Decoder, sequences: int):
+        self.decoder = decoder
+        handle = ctypes.c_void_p()
+        check(library().gq8_batch_create(decoder.handle, sequences, ctypes.byref(handle)))
+        self.handle = handle
+        self.sequences = sequences
+
+    def close(self) -> None:
+        if self.handle:
+            library().gq8_batch_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def prefill(self, sequence: int, prompt) -> None:
+        """Restart one sequence with `prompt`; its first chosen id fills slot len(prompt)."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        check(library().gq8_batch_prefill(self.handle, sequence, _host(prompt), prompt.size))
+
+    def decode(self, steps: int, use_graph: bool = True) -> None:
+        """`steps` lockstep steps (every sequence one token a step, no EOS check)."""
+        check(library().gq8_batch_decode(self.handle, steps, int(use_graph)))
+
+    def position(self, sequence: int) -> int:
+        return check(library().gq8_batch_position(self.handle, sequence))
+
+    def tokens(self, sequence: int, first: int, count: int) -> np.ndarray:
+        out = np.empty(count, dtype=np.int32)
+        check(library().gq8_batch_tokens(self.handle, sequence, first, count, _host(out)))
+        return out
+
+    def logits(self) -> np.ndarray:
+        """The last lockstep step's logits, [sequences, vocab]."""
+        out = np.empty((self.sequences, self.decoder.shape.vocab), dtype=np.float32)
+        check(library().gq8_batch_logits(self.handle, _host(out)))
+        return out
+
+
 def normal_fill_host(seed: int, sigma: float, count: int) -> np.ndarray:
     """The synthetic-weight generator for one tensor (host threads)."""
     out = np.empty(count, dtype=np.float32)
@@ -472,6 +527,17 @@ def algorithmic_decode_bytes(shape: DecoderShape, attended_length: int) -> int:
     embed_row = w + w // 16
     kv_row = shape.layers * 2 * shape.kv_width * 2
     return q8 + norms + embed_row + kv_row * attended_length + kv_row
+
+
+def algorithmic_batch_step_bytes(shape: DecoderShape, attended_lengths) -> int:
+    """Bytes one lockstep step must move: the weights and norms once, and per
+    sequence its embedding row, its K+V read over its attended length and
+    its own K+V write."""
+    w = shape.width
+    embed_row = w + w // 16
+    kv_row = shape.layers * 2 * shape.kv_width * 2
+    shared = algorithmic_decode_bytes(shape, 0) - embed_row - kv_row
+    return shared + sum(embed_row + kv_row * L + kv_row for L in attended_lengths)
 
 
 def log2ceil(n: int) -> int:

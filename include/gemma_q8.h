@@ -283,6 +283,40 @@ int gq8_decoder_timing(gq8_decoder *decoder, double *milliseconds, int *launches
 int gq8_decoder_time_kernel(gq8_decoder *decoder, int stage, int repeats, double *milliseconds,
                             int *launches);
 
+/* ======================================================================= */
+/* Lockstep decode of up to 16 independent sequences over one decoder's     */
+/* weights.  The reference has no batch dimension: a batch stands for S     */
+/* separate HF::Decoders (Decoder.h:69-319, one sequence and one cache      */
+/* each) run by S greedy loops (Gemma.cpp:459-543), and every sequence's     */
+/* ids equal its own one-sequence run's.                                    */
+/* ======================================================================= */
+typedef struct gq8_batch gq8_batch;
+/* S in [1, 16] sequences, each with its own fp16 cache and max_positions + 1
+ * token slots; the decoder's weights are shared, so the decoder must outlive
+ * the batch.  GQ8_ERR_SHAPE where the one-token attention layout does not
+ * cover the decoder's shape. */
+int gq8_batch_create(gq8_decoder *decoder, int sequences, gq8_batch **out);
+void gq8_batch_destroy(gq8_batch *batch);
+/* Gemma::generate's prefill (Gemma.cpp:350-380, 402-424) of one sequence,
+ * restarting it: the prompt goes through the decoder's own step path in
+ * blocks of max_step_rows, and the last row's argmax fills slot
+ * prompt_length.  Refusals as gq8_generate's.  Synchronous. */
+int gq8_batch_prefill(gq8_batch *batch, int sequence, const int32_t *prompt, int prompt_length);
+/* `steps` lockstep steps: each takes every sequence's token at its position,
+ * writes its argmax into the next slot and advances the position (the
+ * greedy loop's step, Gemma.cpp:320-333, for every sequence at once); no EOS
+ * check.  GQ8_ERR_NOT_PREPARED if a sequence has no prompt, GQ8_ERR_WINDOW if
+ * one would pass max_positions.  use_graph != 0 replays one captured step.
+ * Synchronous. */
+int gq8_batch_decode(gq8_batch *batch, int steps, int use_graph);
+int gq8_batch_sequences(const gq8_batch *batch);
+/* The position of the sequence's next step (prompt length + steps so far). */
+int gq8_batch_position(const gq8_batch *batch, int sequence);
+/* Slots [first, first + count) of one sequence (prompt, then generated ids). */
+int gq8_batch_tokens(gq8_batch *batch, int sequence, int first, int count, int32_t *host_out);
+/* The last lockstep step's logits, [S, vocab] fp32, copied to the host. */
+int gq8_batch_logits(gq8_batch *batch, float *host_out);
+
 #ifdef __cplusplus
 }
 #endif
