@@ -13,18 +13,19 @@
 //
 // q8_rows_kernel: one v_mfma_i32_16x16x32_i8 per block covers 16 sequences x
 // 16 weight rows.  Lane l supplies 8 bytes of sequence (l % 16)'s block and 8
-// bytes of weight row (l % 16)'s block, both at byte 8 (l / 16) of the block,
-// straight from memory (the activation rows stay in L2 across workgroups);
+// bytes of weight row (l % 16)'s block, both at byte 8 (l / 16) of the block;
 // the result D[m][n] lands in lane 16 (m / 4) + n, element m % 4.  A
-// workgroup of four waves owns one 16-row tile of the outputs; its waves take
-// consecutive ranges of blocks and add their 16 x 16 double tiles in LDS in
-// wave (= block) order.  Products with too few tiles to fill the chip split
-// the blocks over several workgroups: each stores its double tile, and the
-// last of a tile's workgroups (a ticket per tile) adds them in split order.
+// workgroup stages its range of the activation blocks in LDS in that fragment
+// order (and their scales as fp32), so each wave streams only weight rows
+// from HBM, two chunks of 8 blocks in flight.  Products with too few tiles to
+// fill the chip split the blocks over several workgroups: each stores its
+// double tile, and the last of a column's workgroups (a ticket each) adds
+// them in split order.
 //
 // attention_rows_kernel: one workgroup per (sequence, key split) scores all
 // the query heads against one read of the split's keys (the single KV head of
-// multi-query attention), so every key and value row is read once a layer.
+// multi-query attention), so every key and value row is read once a layer;
+// four waves take 16 keys of each 64-key tile, every head in registers.
 // It also takes the step's RoPE and cache append: each workgroup rotates the
 // sequence's query row itself, and the workgroup whose split holds the new
 // position rotates the new key, appends it (and the value) to the cache and
@@ -34,6 +35,8 @@
 #include "gq8_kernels.hpp"
 #include "gq8_numerics.hpp"
 
+#include <algorithm>
+
 namespace gq8 {
 namespace {
 
@@ -41,31 +44,50 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kRowsThreads = 256;
 constexpr int kRowsWaves = kRowsThreads / 64;
-constexpr int kRowsTile = 16;         // outputs a workgroup
-constexpr int kChunkBlocks = 8;       // blocks a wave loads at once
-constexpr int kTargetWorkgroups = 512;
+constexpr int kRowsTile = 16;         // outputs a tile (a wave's MFMA columns)
+constexpr int kChunkBlocks = 8;       // blocks a wave's weight loads cover at once
+constexpr int kRowsMaxRange = 128;    // blocks of the activation rows a workgroup stages
+constexpr int kRowsManyTiles = 1024;  // products this wide give each wave whole rows
 
+// A workgroup stages `range` blocks of the activation rows in LDS and its
+// waves stream weight rows against them.  Wide products (tiles >= 1024: gate
+// | up, the lm_head) give a workgroup four tiles and each wave a tile's whole
+// rows (WPT 1); narrow ones give a workgroup one tile, its four waves
+// consecutive quarters of the staged blocks (WPT 4), and split the blocks over
+// `splits` workgroups until the chip has about 512.
 struct RowsPlan {
+    int wpt;    // waves a tile: 1 or 4
     int per;    // blocks a wave takes
     int splits; // workgroups over one tile's blocks
+    int range() const { return wpt * per; }
 };
 
-// Whole chunks a wave while the tiles alone leave the chip short of
-// workgroups; the split count follows.
 RowsPlan rows_plan(int inner, int outputs)
 {
     const int nb = inner / kBlock;
     const int tiles = (outputs + kRowsTile - 1) / kRowsTile;
+    if (tiles >= kRowsManyTiles) {
+        const int per = std::min(nb, kRowsMaxRange);
+        return {1, per, (nb + per - 1) / per};
+    }
     int per = (nb + kRowsWaves - 1) / kRowsWaves;
     if (per > kChunkBlocks)
         per = (per + kChunkBlocks - 1) / kChunkBlocks * kChunkBlocks;
-    int splits = 1;
-    while ((int64_t) tiles * splits < kTargetWorkgroups && per > kChunkBlocks
-           && per % (2 * kChunkBlocks) == 0) {
+    while (kRowsWaves * per > kRowsMaxRange)
+        per /= 2;
+    int splits = (nb + kRowsWaves * per - 1) / (kRowsWaves * per);
+    while (tiles * splits < 512 && per >= 2 * kChunkBlocks && per % (2 * kChunkBlocks) == 0) {
         per /= 2;
         splits = (nb + kRowsWaves * per - 1) / (kRowsWaves * per);
     }
-    return {per, splits};
+    return {kRowsWaves, per, splits};
+}
+
+size_t rows_lds_bytes(const RowsPlan &p)
+{
+    // fragments [block][lane] 8 bytes, scales [block][row] fp32, the tiles' partial sums
+    return (size_t) p.range() * 64 * 8 + (size_t) p.range() * kBatchRows * 4
+           + (size_t) kRowsWaves * kBatchRows * (kRowsTile + 1) * 8;
 }
 
 struct RowsArgs {
@@ -76,7 +98,8 @@ struct RowsArgs {
     float *y;
     int y_stride, residual;
     double *partials; // [splits][kBatchRows][outputs]
-    int *tickets;     // one a tile
+    int *tickets;     // one a workgroup column
+    uint8_t *geglu8;  // non-null: outputs are gate | up rows; GeGLU's Q8 rows land here
 };
 
 __device__ inline void store_agent_d(double *p, double v)
@@ -94,107 +117,216 @@ __device__ inline float half_of(uint32_t word, int upper)
     return half_value((uint16_t) (upper ? word >> 16 : word & 0xFFFFu));
 }
 
-// V: the scales of a chunk load as one 16-byte vector per row (the block
-// count and every wave's first block are multiples of 8).
+// One chunk of a wave's weight rows: 8 blocks' bytes at this lane's 8-byte
+// slice, and their fp16 scales.
+struct WeightChunk {
+    long w[kChunkBlocks];
+    uint32_t s[kChunkBlocks / 2];
+};
+
+// V: whole chunks (the block count and every range a multiple of 8), the
+// scales one 16-byte load; else blocks past `end` are loaded clamped.
 template <bool V>
+__device__ inline void load_weight_chunk(WeightChunk &c, const uint8_t *wRow, const uint16_t *wScale,
+                                         int c0, int end)
+{
+#pragma unroll
+    for (int k = 0; k < kChunkBlocks; ++k) {
+        const int b = V ? c0 + k : min(c0 + k, end - 1);
+        c.w[k] = *reinterpret_cast<const long *>(wRow + (int64_t) b * kBlock);
+    }
+    if constexpr (V) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(wScale + c0);
+        c.s[0] = v.x; c.s[1] = v.y; c.s[2] = v.z; c.s[3] = v.w;
+    } else {
+#pragma unroll
+        for (int k = 0; k < kChunkBlocks; k += 2) {
+            const uint32_t lo = wScale[min(c0 + k, end - 1)];
+            const uint32_t hi = wScale[min(c0 + k + 1, end - 1)];
+            c.s[k / 2] = lo | (hi << 16);
+        }
+    }
+}
+
+// The chunk against the staged activation blocks: one MFMA a block, then
+// acc[r] (sequence 4 (lane / 16) + r, output lane % 16) += dot * (sw * sx)
+// (the scale product exact in fp32, the product exact in double).
+template <bool V>
+__device__ inline void chunk_products(const WeightChunk &c, const long *sX, const float *sSx,
+                                      int rb, int c0, int end, int lane, double (&acc)[4])
+{
+    const int grp = lane >> 4;
+#pragma unroll
+    for (int k = 0; k < kChunkBlocks; ++k) {
+        const int kb = V ? rb + k : min(rb + k, rb + (end - 1 - c0));
+        const long xa = sX[kb * 64 + lane];
+        const float4 sx = *reinterpret_cast<const float4 *>(sSx + kb * kBatchRows + 4 * grp);
+        const float sw = (V || c0 + k < end) ? half_of(c.s[k / 2], k & 1) : 0.f;
+        const v4i zero = {0, 0, 0, 0};
+        const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa, c.w[k], zero, 0, 0, 0);
+        acc[0] = fma((double) d[0], (double) (sw * sx.x), acc[0]);
+        acc[1] = fma((double) d[1], (double) (sw * sx.y), acc[1]);
+        acc[2] = fma((double) d[2], (double) (sw * sx.z), acc[2]);
+        acc[3] = fma((double) d[3], (double) (sw * sx.w), acc[3]);
+    }
+}
+
+// NC > 0: every wave takes exactly NC whole chunks (the loop unrolled, so
+// each chunk's wait counts only the loads before it); NC == 0: any range.
+template <int WPT, int NC>
 __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
 {
-    __shared__ double sPart[kRowsWaves][kBatchRows][kRowsTile + 1];
+    constexpr bool V = NC > 0;
+    constexpr int kTiles = kRowsWaves / WPT; // tiles a workgroup
+    extern __shared__ __attribute__((aligned(16))) unsigned char rowsLds[];
+    const int range = WPT * a.per;
+    long *sX = reinterpret_cast<long *>(rowsLds);
+    float *sSx = reinterpret_cast<float *>(rowsLds + (size_t) range * 64 * 8);
+    double *sPart = reinterpret_cast<double *>(rowsLds + (size_t) range * 64 * 8
+                                               + (size_t) range * kBatchRows * 4);
     __shared__ int sLast;
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int nb = a.inner / kBlock;
-    const int col = lane & 15, grp = lane >> 4;
-    const int n0 = blockIdx.x * kRowsTile;
-    // operand rows of this lane, clamped into range (their results are never stored)
+    const int col = lane & 15;
+    // GeGLU's pairing (four tiles a workgroup): waves 0 and 1 take gate
+    // tiles 2 x, 2 x + 1, waves 2 and 3 the up tiles of the same outputs
+    const int upTiles = a.outputs / (2 * kRowsTile);
+    const int tile = a.geglu8 ? (wave >> 1) * upTiles + 2 * blockIdx.x + (wave & 1)
+                              : blockIdx.x * kTiles + wave / WPT;
+    const int part = wave % WPT;
+    const int n0 = tile * kRowsTile;
+    const int r0 = blockIdx.y * range;             // the workgroup's first block
+    const int rEnd = min(r0 + range, nb);
+    const int b0 = r0 + part * a.per;              // this wave's blocks
+    const int b1 = min(b0 + a.per, nb);
+
+    // this wave's weight rows (clamped into range; never stored)
     const int n = min(n0 + col, a.outputs - 1);
-    const int xr = min(col, a.rows - 1);
-    const uint8_t *wRow = a.w8 + (int64_t) n * a.inner + grp * 8;
-    const uint8_t *xRow = a.x8 + (int64_t) xr * a.inner + grp * 8;
+    const uint8_t *wRow = a.w8 + (int64_t) n * a.inner + (lane >> 4) * 8;
     const uint16_t *wScale = reinterpret_cast<const uint16_t *>(a.w8 + (int64_t) a.outputs * a.inner)
                              + (int64_t) n * nb;
-    const uint16_t *xScales = reinterpret_cast<const uint16_t *>(a.x8 + (int64_t) a.x_rows * a.inner);
-    const uint16_t *xScale[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-        xScale[r] = xScales + (int64_t) min(4 * grp + r, a.rows - 1) * nb;
+    WeightChunk bufA, bufB;
+    if (b0 < b1)
+        load_weight_chunk<V>(bufA, wRow, wScale, b0, b1);
 
-    const int b0 = (blockIdx.y * kRowsWaves + wave) * a.per;
-    const int b1 = min(b0 + a.per, nb);
+    // stage the workgroup's activation blocks in MFMA fragment order (lane l
+    // of block b: sequence l % 16, bytes 8 (l / 16) .. + 8) and their scales
+    const uint16_t *xScales = reinterpret_cast<const uint16_t *>(a.x8 + (int64_t) a.x_rows * a.inner);
+    // every load first (clamped into range), then the LDS writes
+    constexpr int kPieces = kRowsMaxRange * kBatchRows * 2 / kRowsThreads; // 16-byte pieces
+    constexpr int kScales = kRowsMaxRange * kBatchRows / kRowsThreads;
+    const int pieces = (rEnd - r0) * kBatchRows * 2, scales = (rEnd - r0) * kBatchRows;
+    uint4 piece[kPieces];
+    uint16_t scaleBits[kScales];
+#pragma unroll
+    for (int i = 0; i < kPieces; ++i) {
+        const int p = min(t + i * kRowsThreads, pieces - 1);
+        const int rb = p >> 5, m = (p >> 1) & 15, h = p & 1;
+        piece[i] = *reinterpret_cast<const uint4 *>(a.x8 + (int64_t) min(m, a.rows - 1) * a.inner
+                                                    + (int64_t) (r0 + rb) * kBlock + h * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < kScales; ++i) {
+        const int e = min(t + i * kRowsThreads, scales - 1);
+        scaleBits[i] = xScales[(int64_t) min(e & 15, a.rows - 1) * nb + r0 + (e >> 4)];
+    }
+#pragma unroll
+    for (int i = 0; i < kPieces; ++i) {
+        const int p = t + i * kRowsThreads;
+        if (p < pieces) {
+            const int rb = p >> 5, m = (p >> 1) & 15, h = p & 1;
+            uint2 *dst = reinterpret_cast<uint2 *>(sX) + rb * 64 + m;
+            dst[(2 * h) * 16] = make_uint2(piece[i].x, piece[i].y);
+            dst[(2 * h + 1) * 16] = make_uint2(piece[i].z, piece[i].w);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kScales; ++i) {
+        const int e = t + i * kRowsThreads;
+        if (e < scales)
+            sSx[e] = half_value(scaleBits[i]);
+    }
+    __syncthreads();
+
     double acc[4] = {0.0, 0.0, 0.0, 0.0};
-    for (int c0 = b0; c0 < b1; c0 += kChunkBlocks) {
-        long wv[kChunkBlocks], xv[kChunkBlocks];
+    // two weight buffers: the next chunk's loads are in flight while this
+    // one computes
+    if constexpr (V) {
+        if (b0 < b1) { // the last split's waves may have no blocks
 #pragma unroll
-        for (int k = 0; k < kChunkBlocks; ++k) {
-            const int b = min(c0 + k, b1 - 1);
-            wv[k] = *reinterpret_cast<const long *>(wRow + (int64_t) b * kBlock);
-            xv[k] = *reinterpret_cast<const long *>(xRow + (int64_t) b * kBlock);
-        }
-        float sw[kChunkBlocks], sx[4][kChunkBlocks];
-        if constexpr (V) {
-            const uint4 w4 = *reinterpret_cast<const uint4 *>(wScale + c0);
-            const uint32_t ww[4] = {w4.x, w4.y, w4.z, w4.w};
-#pragma unroll
-            for (int k = 0; k < kChunkBlocks; ++k)
-                sw[k] = half_of(ww[k / 2], k & 1);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint4 x4 = *reinterpret_cast<const uint4 *>(xScale[r] + c0);
-                const uint32_t xw[4] = {x4.x, x4.y, x4.z, x4.w};
-#pragma unroll
-                for (int k = 0; k < kChunkBlocks; ++k)
-                    sx[r][k] = half_of(xw[k / 2], k & 1);
-            }
-        } else {
-            // blocks past the wave's range were loaded clamped; a zero scale
-            // drops them (0 * dot adds an exact zero)
-#pragma unroll
-            for (int k = 0; k < kChunkBlocks; ++k) {
-                const int b = min(c0 + k, b1 - 1);
-                sw[k] = c0 + k < b1 ? half_value(wScale[b]) : 0.f;
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    sx[r][k] = half_value(xScale[r][b]);
+            for (int i = 0; i < NC; ++i) {
+                WeightChunk &cur = (i & 1) ? bufB : bufA;
+                WeightChunk &next = (i & 1) ? bufA : bufB;
+                if (i + 1 < NC)
+                    load_weight_chunk<true>(next, wRow, wScale, b0 + (i + 1) * kChunkBlocks, b1);
+                __builtin_amdgcn_sched_barrier(0);
+                chunk_products<true>(cur, sX, sSx, b0 - r0 + i * kChunkBlocks,
+                                     b0 + i * kChunkBlocks, b1, lane, acc);
             }
         }
-        // no branch between the loads and the arithmetic, and no arithmetic
-        // scheduled among the loads: every load of the chunk is in flight
-        // before the first product waits
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int k = 0; k < kChunkBlocks; ++k) {
-            const v4i zero = {0, 0, 0, 0};
-            const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(xv[k], wv[k], zero, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) // the scale product is exact in fp32
-                acc[r] = fma((double) d[r], (double) (sw[k] * sx[r][k]), acc[r]);
+    } else {
+        for (int c0 = b0; c0 < b1; c0 += kChunkBlocks) {
+            if (c0 > b0)
+                load_weight_chunk<false>(bufA, wRow, wScale, c0, b1);
+            chunk_products<false>(bufA, sX, sSx, c0 - r0, c0, b1, lane, acc);
         }
     }
 
+    // a tile's sum over its waves (in block order), one (sequence, output)
+    // cell a thread; tile k of the workgroup lands in sPart[k]
+    const int grp = lane >> 4;
+    double *mine = sPart + (size_t) wave * kBatchRows * (kRowsTile + 1);
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-        sPart[wave][4 * grp + r][col] = acc[r];
+        mine[(4 * grp + r) * (kRowsTile + 1) + col] = acc[r];
     __syncthreads();
-    const int m = t >> 4, c = t & 15; // 256 threads: one (sequence, output) cell each
-    double sum = sPart[0][m][c];
+    if (WPT == 1 && a.geglu8) {
+        // the products' fp32 outputs, GeGLU, and the 32-element block's Q8
+        // (a row's 32 outputs in 32 consecutive lanes)
+        const int F = a.outputs / 2;
+        uint16_t *scales = reinterpret_cast<uint16_t *>(a.geglu8 + (int64_t) a.x_rows * F);
 #pragma unroll
-    for (int w = 1; w < kRowsWaves; ++w)
-        sum += sPart[w][m][c];
-    const int on = n0 + c;
-    const bool live = m < a.rows && on < a.outputs;
-    if (gridDim.y == 1) {
-        if (live) {
-            float *dst = a.y + (int64_t) m * a.y_stride + on;
-            const double old = a.residual ? (double) *dst : 0.0;
-            *dst = (float) (sum + old);
+        for (int i = 0; i < 2; ++i) {
+            const int cell = t + i * kRowsThreads;
+            const int m = cell >> 5, jj = cell & 31;
+            const double *gate = sPart + (size_t) (jj >> 4) * kBatchRows * (kRowsTile + 1);
+            const double *up = sPart + (size_t) (2 + (jj >> 4)) * kBatchRows * (kRowsTile + 1);
+            const float v = geglu((float) gate[m * (kRowsTile + 1) + (jj & 15)],
+                                  (float) up[m * (kRowsTile + 1) + (jj & 15)]);
+            const float amax = max_lanes<16>(fabsf(v));
+            const uint16_t bits = scale_bits_from_amax(amax);
+            const float sc = half_value(bits);
+            const int j = blockIdx.x * 2 * kRowsTile + jj;
+            if (m < a.rows) {
+                a.geglu8[(int64_t) m * F + j] = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);
+                if (jj == 0)
+                    scales[(int64_t) m * (F / kBlock) + j / kBlock] = bits;
+            }
         }
         return;
     }
-
-    // the blocks are split over gridDim.y workgroups: agent-scope stores
-    // (coherent across the L2s), completed before the ticket is taken
-    if (live)
-        store_agent_d(a.partials + ((int64_t) blockIdx.y * kBatchRows + m) * a.outputs + on, sum);
+    for (int cell = t; cell < kTiles * kBatchRows * kRowsTile; cell += kRowsThreads) {
+        const int k = cell >> 8, m = (cell >> 4) & 15, c = cell & 15;
+        double sum = 0.0;
+#pragma unroll
+        for (int w = 0; w < WPT; ++w)
+            sum += sPart[((size_t) (k * WPT + w) * kBatchRows + m) * (kRowsTile + 1) + c];
+        const int on = (blockIdx.x * kTiles + k) * kRowsTile + c;
+        if (m >= a.rows || on >= a.outputs)
+            continue;
+        if (gridDim.y == 1) {
+            float *dst = a.y + (int64_t) m * a.y_stride + on;
+            const double old = a.residual ? (double) *dst : 0.0;
+            *dst = (float) (sum + old);
+        } else {
+            // the blocks are split over gridDim.y workgroups: agent-scope
+            // stores (coherent across the L2s), completed before the ticket
+            store_agent_d(a.partials + ((int64_t) blockIdx.y * kBatchRows + m) * a.outputs + on, sum);
+        }
+    }
+    if (gridDim.y == 1)
+        return;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (t == 0)
@@ -203,7 +335,11 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
     __syncthreads();
     if (!sLast)
         return;
-    if (live) {
+    for (int cell = t; cell < kTiles * kBatchRows * kRowsTile; cell += kRowsThreads) {
+        const int k = cell >> 8, m = (cell >> 4) & 15, c = cell & 15;
+        const int on = (blockIdx.x * kTiles + k) * kRowsTile + c;
+        if (m >= a.rows || on >= a.outputs)
+            continue;
         double total = 0.0;
         for (int s = 0; s < (int) gridDim.y; ++s)
             total += load_agent_d(a.partials + ((int64_t) s * kBatchRows + m) * a.outputs + on);
@@ -245,25 +381,26 @@ __device__ inline Halves<C> load_channels(const uint16_t *p)
     return h;
 }
 
-// C channels a lane (head width 64 C), HW heads a wave, HG head groups: four
-// key waves per head group, 256 HG threads.
-template <int C, int HW, int HG>
-__global__ __launch_bounds__(256 * HG) void attention_rows_kernel(RowsAttentionArgs a)
+// C channels a lane (head width 64 C), H heads: four waves, each scoring
+// every head against its 16 keys of a 64-key tile.
+template <int C, int H>
+__global__ __launch_bounds__(kRowsThreads) void attention_rows_kernel(RowsAttentionArgs a)
 {
-    constexpr int H = HW * HG, kWaves = 4 * HG, kThreadsAll = 256 * HG;
     constexpr int hd = 64 * C, half = hd / 2, qW = H * hd;
-    constexpr int R = 16 / HW; // keys a scoring round: 16 (key, head) rows a reduction
-    static_assert(HW * R == 16 && kRowsWaveKeys % R == 0, "rounds");
+    constexpr int R = 16 / H;          // keys a scoring round: 16 (key, head) rows a reduction
+    constexpr int kAccHeads = 4;       // heads a pass of the waves' LDS sum
+    constexpr int kRopePairs = ((H + 1) * half + kRowsThreads - 1) / kRowsThreads;
+    constexpr int kOut = (qW + kRowsThreads - 1) / kRowsThreads; // merged outputs a thread
+    static_assert(H * R == 16 && kRowsWaveKeys % R == 0, "layout");
     __shared__ float sQ[qW];
     __shared__ __attribute__((aligned(8))) uint16_t sKnew[hd], sVnew[hd];
     __shared__ double sS[H][kRowsTileKeys];
     __shared__ double sMax[H], sSum[H], sF[H];
-    __shared__ double sAcc[kWaves][HW * hd];
+    __shared__ double sAcc[kRowsWaves][kAccHeads * hd];
     __shared__ double sMerge[H][kRowsMaxSplits];
     __shared__ int sLast;
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int g = wave >> 2, kw = wave & 3;
     const int seq = blockIdx.y, split = blockIdx.x;
     const int pos = a.positions[seq];
     const int keyCount = pos + 1;
@@ -276,64 +413,79 @@ __global__ __launch_bounds__(256 * HG) void attention_rows_kernel(RowsAttentionA
     uint16_t *keys = a.key_cache + seq * a.cache_stride;
     uint16_t *values = a.value_cache + seq * a.cache_stride;
 
-    // RoPE (rope_kv_kernel's arithmetic): the query heads, and the new key
-    // where this split holds it; the new value rounded to fp16
-    for (int idx = t; idx < (H + 1) * half; idx += kThreadsAll) {
-        const int head = idx / half, i = idx % half;
-        if (head == H && !holdsNew)
-            break;
-        const float *base = row + head * hd; // head H: the key, right after the queries
-        const int64_t angle = (int64_t) pos * half + i;
-        float lo, hi;
-        rotate_pair(base[i], base[i + half], a.cosines[angle], a.sines[angle], &lo, &hi);
-        if (head < H) {
-            sQ[head * hd + i] = lo;
-            sQ[head * hd + i + half] = hi;
-        } else {
-            sKnew[i] = half_bits(lo);
-            sKnew[i + half] = half_bits(hi);
+    // RoPE (rope_kv_kernel's arithmetic) of the query heads and, in the
+    // split holding it, of the new key (head H, right after the queries); the
+    // new value rounded to fp16.  Every load first, clamped into the row.
+    {
+        float lo[kRopePairs], hi[kRopePairs], cs[kRopePairs], sn[kRopePairs];
+#pragma unroll
+        for (int k = 0; k < kRopePairs; ++k) {
+            const int idx = min(t + k * kRowsThreads, (H + 1) * half - 1);
+            const int head = idx / half, i = idx % half;
+            const int64_t angle = (int64_t) pos * half + i;
+            lo[k] = row[head * hd + i];
+            hi[k] = row[head * hd + i + half];
+            cs[k] = a.cosines[angle];
+            sn[k] = a.sines[angle];
         }
+        float v = 0.f;
+        if (holdsNew && t < hd)
+            v = row[qW + hd + t];
+#pragma unroll
+        for (int k = 0; k < kRopePairs; ++k) {
+            const int idx = t + k * kRowsThreads;
+            if (idx >= (H + 1) * half)
+                break;
+            const int head = idx / half, i = idx % half;
+            float rl, rh;
+            rotate_pair(lo[k], hi[k], cs[k], sn[k], &rl, &rh);
+            if (head < H) {
+                sQ[head * hd + i] = rl;
+                sQ[head * hd + i + half] = rh;
+            } else {
+                sKnew[i] = half_bits(rl);
+                sKnew[i + half] = half_bits(rh);
+            }
+        }
+        if (holdsNew && t < hd)
+            sVnew[t] = half_bits(v);
     }
-    if (holdsNew)
-        for (int i = t; i < hd; i += kThreadsAll)
-            sVnew[i] = half_bits(row[qW + hd + i]);
     if (t < H) {
         sMax[t] = -INFINITY;
         sSum[t] = 0.0;
     }
     __syncthreads();
-    if (holdsNew)
-        for (int i = t; i < hd; i += kThreadsAll) {
-            keys[(int64_t) pos * hd + i] = sKnew[i];
-            values[(int64_t) pos * hd + i] = sVnew[i];
-        }
+    if (holdsNew && t < hd) {
+        keys[(int64_t) pos * hd + t] = sKnew[t];
+        values[(int64_t) pos * hd + t] = sVnew[t];
+    }
 
     const int c0 = lane * C;
-    double q[HW][C], acc[HW][C];
+    double q[H][C], acc[H][C];
 #pragma unroll
-    for (int h = 0; h < HW; ++h)
+    for (int h = 0; h < H; ++h)
 #pragma unroll
         for (int c = 0; c < C; ++c) {
-            q[h][c] = (double) sQ[(g * HW + h) * hd + c0 + c];
+            q[h][c] = (double) sQ[h * hd + c0 + c];
             acc[h][c] = 0.0;
         }
 
     for (int t0 = k0; t0 < k1; t0 += kRowsTileKeys) {
         const int nk = min(kRowsTileKeys, k1 - t0);
-        // this wave's keys t0 + 16 kw + i, clamped into the tile (the
-        // duplicates are masked), the new position's row from LDS
         const bool tileHoldsNew = holdsNew && t0 + nk == keyCount;
+        // this wave's keys t0 + 16 wave + i, clamped into the tile (the
+        // duplicates are masked), the new position's row from LDS
         Halves<C> kh[kRowsWaveKeys], vh[kRowsWaveKeys];
 #pragma unroll
         for (int i = 0; i < kRowsWaveKeys; ++i) {
-            const int j = t0 + min(kw * kRowsWaveKeys + i, nk - 1);
+            const int j = t0 + min(wave * kRowsWaveKeys + i, nk - 1);
             kh[i] = load_channels<C>(keys + (int64_t) j * hd + c0);
         }
         if (tileHoldsNew) {
             const Halves<C> kn = load_channels<C>(sKnew + c0);
 #pragma unroll
             for (int i = 0; i < kRowsWaveKeys; ++i)
-                if (t0 + min(kw * kRowsWaveKeys + i, nk - 1) == pos)
+                if (t0 + min(wave * kRowsWaveKeys + i, nk - 1) == pos)
                     kh[i] = kn;
         }
 #pragma unroll
@@ -342,38 +494,37 @@ __global__ __launch_bounds__(256 * HG) void attention_rows_kernel(RowsAttentionA
 #pragma unroll
             for (int i = 0; i < R; ++i)
 #pragma unroll
-                for (int h = 0; h < HW; ++h) {
+                for (int h = 0; h < H; ++h) {
                     double p = 0.0;
 #pragma unroll
                     for (int c = 0; c < C; ++c)
                         p += q[h][c] * (double) kh[r0 + i].at(c);
-                    y[i * HW + h] = p;
+                    y[i * H + h] = p;
                 }
             const double total = reduce_rows<16>(y, lane);
             if (stores_row<16>(lane)) {
                 const int rr = row_of_lane<16>(lane);
-                const int jj = kw * kRowsWaveKeys + r0 + rr / HW;
-                sS[g * HW + rr % HW][jj] = jj < nk ? (double) a.scale * total : -INFINITY;
+                const int jj = wave * kRowsWaveKeys + r0 + rr / H;
+                sS[rr % H][jj] = jj < nk ? (double) a.scale * total : -INFINITY;
             }
             __builtin_amdgcn_sched_barrier(0); // one round's conversions at a time
         }
         // the values, in flight during the softmax
 #pragma unroll
         for (int i = 0; i < kRowsWaveKeys; ++i) {
-            const int j = t0 + min(kw * kRowsWaveKeys + i, nk - 1);
+            const int j = t0 + min(wave * kRowsWaveKeys + i, nk - 1);
             vh[i] = load_channels<C>(values + (int64_t) j * hd + c0);
         }
         if (tileHoldsNew) {
             const Halves<C> vn = load_channels<C>(sVnew + c0);
 #pragma unroll
             for (int i = 0; i < kRowsWaveKeys; ++i)
-                if (t0 + min(kw * kRowsWaveKeys + i, nk - 1) == pos)
+                if (t0 + min(wave * kRowsWaveKeys + i, nk - 1) == pos)
                     vh[i] = vn;
         }
         __syncthreads();
-        // the tile's softmax against the running maximum, one wave a head
-        if (wave < H) {
-            const int h = wave;
+        // the tile's softmax against the running maximum, a wave a head
+        for (int h = wave; h < H; h += kRowsWaves) {
             const double sc = lane < nk ? sS[h][lane] : -INFINITY;
             const double tileMax = wave_max_d(sc);
             const double previous = sMax[h];
@@ -389,13 +540,15 @@ __global__ __launch_bounds__(256 * HG) void attention_rows_kernel(RowsAttentionA
             }
         }
         __syncthreads();
-        // this wave's keys in order for every head (weights past the tile are zero)
-        double part[HW][C];
+        // rescaled running sums plus this wave's keys in order (weights past
+        // the tile are zero)
 #pragma unroll
-        for (int h = 0; h < HW; ++h)
+        for (int h = 0; h < H; ++h) {
+            const double f = sF[h];
 #pragma unroll
             for (int c = 0; c < C; ++c)
-                part[h][c] = 0.0;
+                acc[h][c] *= f;
+        }
 #pragma unroll
         for (int i = 0; i < kRowsWaveKeys; ++i) {
             double v[C];
@@ -403,38 +556,37 @@ __global__ __launch_bounds__(256 * HG) void attention_rows_kernel(RowsAttentionA
             for (int c = 0; c < C; ++c)
                 v[c] = (double) vh[i].at(c);
 #pragma unroll
-            for (int h = 0; h < HW; ++h) {
-                const double wi = sS[g * HW + h][kw * kRowsWaveKeys + i];
+            for (int h = 0; h < H; ++h) {
+                const double wi = sS[h][wave * kRowsWaveKeys + i];
 #pragma unroll
                 for (int c = 0; c < C; ++c)
-                    part[h][c] += wi * v[c];
+                    acc[h][c] += wi * v[c];
             }
-        }
-#pragma unroll
-        for (int h = 0; h < HW; ++h) {
-            const double f = sF[g * HW + h];
-#pragma unroll
-            for (int c = 0; c < C; ++c)
-                acc[h][c] = acc[h][c] * f + part[h][c];
         }
         __syncthreads(); // the next tile rewrites the scores
     }
 
-    // the split's partial: the four key waves of each head in order
-#pragma unroll
-    for (int h = 0; h < HW; ++h)
-#pragma unroll
-        for (int c = 0; c < C; ++c)
-            sAcc[wave][h * hd + c0 + c] = acc[h][c];
-    __syncthreads();
+    // the split's partial: the four waves' sums in wave order, kAccHeads
+    // heads a pass
     const int64_t slot = (int64_t) seq * kRowsMaxSplits + split;
-    for (int o = t; o < qW; o += kThreadsAll) {
-        const int head = o / hd, gg = head / HW, within = o - gg * HW * hd;
-        double v = sAcc[gg * 4][within];
 #pragma unroll
-        for (int w = 1; w < 4; ++w)
-            v += sAcc[gg * 4 + w][within];
-        store_agent_d(a.ws_o + slot * qW + o, v);
+    for (int h0 = 0; h0 < H; h0 += kAccHeads) {
+        if (h0 > 0)
+            __syncthreads();
+#pragma unroll
+        for (int h = 0; h < kAccHeads && h0 + h < H; ++h)
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+                sAcc[wave][h * hd + c0 + c] = acc[h0 + h][c];
+        __syncthreads();
+        const int width = min(kAccHeads, H - h0) * hd;
+        for (int o = t; o < width; o += kRowsThreads) {
+            double v = sAcc[0][o];
+#pragma unroll
+            for (int w = 1; w < kRowsWaves; ++w)
+                v += sAcc[w][o];
+            store_agent_d(a.ws_o + slot * qW + h0 * hd + o, v);
+        }
     }
     if (t < H) {
         store_agent_d(a.ws_ml + (slot * H + t) * 2, sMax[t]);
@@ -452,35 +604,48 @@ __global__ __launch_bounds__(256 * HG) void attention_rows_kernel(RowsAttentionA
 
     // the merge: split weights per head (one split a lane), then the row
     const int64_t first = (int64_t) seq * kRowsMaxSplits;
-    if (wave < H) {
+    for (int h = wave; h < H; h += kRowsWaves) {
         const bool live = lane < splits;
         const int sp = live ? lane : 0;
-        const double m = load_agent_d(a.ws_ml + ((first + sp) * H + wave) * 2);
-        const double sum = load_agent_d(a.ws_ml + ((first + sp) * H + wave) * 2 + 1);
+        const double m = load_agent_d(a.ws_ml + ((first + sp) * H + h) * 2);
+        const double sum = load_agent_d(a.ws_ml + ((first + sp) * H + h) * 2 + 1);
         double total;
         const double f = merge_factor(m, sum, live, total);
         if (live)
-            sMerge[wave][sp] = f;
+            sMerge[h][sp] = f;
         if (lane == 0)
-            sSum[wave] = total;
+            sSum[h] = total;
     }
     __syncthreads();
+    // thread t's outputs t + 256 k, every split's partials of a batch loaded at once
+    constexpr int kMergeSplits = 8;
+    double weighted[kOut];
+#pragma unroll
+    for (int k = 0; k < kOut; ++k)
+        weighted[k] = 0.0;
+    for (int s0 = 0; s0 < splits; s0 += kMergeSplits) {
+        double part[kMergeSplits][kOut];
+#pragma unroll
+        for (int u = 0; u < kMergeSplits; ++u)
+#pragma unroll
+            for (int k = 0; k < kOut; ++k)
+                part[u][k] = load_agent_d(a.ws_o + (first + min(s0 + u, splits - 1)) * qW
+                                          + min(t + k * kRowsThreads, qW - 1));
+#pragma unroll
+        for (int u = 0; u < kMergeSplits; ++u)
+            if (s0 + u < splits)
+#pragma unroll
+                for (int k = 0; k < kOut; ++k)
+                    weighted[k] += part[u][k] * sMerge[min(t + k * kRowsThreads, qW - 1) / hd][s0 + u];
+    }
     uint16_t *scales = reinterpret_cast<uint16_t *>(a.q8 + (int64_t) a.q8_rows * qW)
                        + (int64_t) seq * (qW / kBlock);
-    for (int o = t; o < qW; o += kThreadsAll) { // whole waves: qW is a multiple of 64
-        const int head = o / hd;
-        double weighted = 0.0;
-        for (int s0 = 0; s0 < splits; s0 += 8) {
-            double part[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
-                part[u] = s0 + u < splits ? load_agent_d(a.ws_o + (first + s0 + u) * qW + o) : 0.0;
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (s0 + u < splits)
-                    weighted += part[u] * sMerge[head][s0 + u];
-        }
-        const float v = (float) (weighted / sSum[head]);
+    for (int k = 0; k < kOut; ++k) { // whole waves: a 32-block is 32 consecutive lanes
+        const int o = t + k * kRowsThreads;
+        if (o >= qW) // whole waves (qW is a multiple of 64)
+            break;
+        const float v = (float) (weighted[k] / sSum[o / hd]);
         const float amax = max_lanes<16>(fabsf(v));
         const uint16_t bits = scale_bits_from_amax(amax);
         const float sc = half_value(bits);
@@ -518,6 +683,10 @@ int rows_ticket_count(int outputs)
     return (outputs + kRowsTile - 1) / kRowsTile;
 }
 
+namespace {
+hipError_t launch_rows(const RowsArgs &a, const RowsPlan &plan, hipStream_t stream);
+}
+
 hipError_t launch_q8_rows(const uint8_t *x8, int x_rows, int rows, const uint8_t *w8, int inner,
                           int outputs, float *y, int y_stride, int residual, double *partials,
                           size_t partial_bytes, int *tickets, hipStream_t stream)
@@ -529,20 +698,67 @@ hipError_t launch_q8_rows(const uint8_t *x8, int x_rows, int rows, const uint8_t
     if (plan.splits > 1
         && (!partials || !tickets || partial_bytes < rows_workspace_bytes(inner, outputs)))
         return hipErrorInvalidValue;
-    RowsArgs a{x8, x_rows, rows, w8, inner, outputs, plan.per, y, y_stride, residual, partials,
-               tickets};
+    const RowsArgs a{x8, x_rows, rows, w8, inner, outputs, plan.per, y, y_stride, residual,
+                     partials, tickets, nullptr};
+    return launch_rows(a, plan, stream);
+}
+
+bool rows_geglu_supported(int inner, int intermediate)
+{
+    if (inner <= 0 || inner % kBlock != 0 || intermediate <= 0 || intermediate % (2 * kRowsTile) != 0)
+        return false;
+    const RowsPlan plan = rows_plan(inner, 2 * intermediate);
+    return plan.wpt == 1 && plan.splits == 1;
+}
+
+hipError_t launch_q8_rows_geglu(const uint8_t *x8, int x_rows, int rows, const uint8_t *w8,
+                                int inner, int intermediate, uint8_t *geglu8, hipStream_t stream)
+{
+    if (rows <= 0 || rows > kBatchRows || x_rows < rows || !geglu8
+        || !rows_geglu_supported(inner, intermediate))
+        return hipErrorInvalidValue;
+    const RowsPlan plan = rows_plan(inner, 2 * intermediate);
+    const RowsArgs a{x8, x_rows, rows, w8, inner, 2 * intermediate, plan.per, nullptr, 0, 0,
+                     nullptr, nullptr, geglu8};
+    return launch_rows(a, plan, stream);
+}
+
+namespace {
+hipError_t launch_rows(const RowsArgs &a, const RowsPlan &plan, hipStream_t stream)
+{
+    const int inner = a.inner, outputs = a.outputs;
+    const uint8_t *w8 = a.w8;
     const int nb = inner / kBlock;
     const uintptr_t wScales = reinterpret_cast<uintptr_t>(w8) + (uintptr_t) outputs * inner;
-    const uintptr_t xScales = reinterpret_cast<uintptr_t>(x8) + (uintptr_t) x_rows * inner;
-    const bool vec = nb % kChunkBlocks == 0 && plan.per % kChunkBlocks == 0 && wScales % 16 == 0
-                     && xScales % 16 == 0;
-    const dim3 grid(rows_ticket_count(outputs), plan.splits);
-    if (vec)
-        hipLaunchKernelGGL(q8_rows_kernel<true>, grid, dim3(kRowsThreads), 0, stream, a);
-    else
-        hipLaunchKernelGGL(q8_rows_kernel<false>, grid, dim3(kRowsThreads), 0, stream, a);
+    // whole chunks: every wave's range a multiple of 8 blocks inside the row
+    // (the last split's waves may hold fewer, or none: nb a multiple of per)
+    const int nc = plan.per / kChunkBlocks;
+    const bool whole = plan.per % kChunkBlocks == 0 && nb % plan.per == 0 && wScales % 16 == 0
+                       && (nc == 1 || nc == 2 || nc == 4 || nc == 8 || nc == 16);
+    const int tilesPerGroup = kRowsWaves / plan.wpt;
+    const dim3 grid((rows_ticket_count(outputs) + tilesPerGroup - 1) / tilesPerGroup, plan.splits);
+    const size_t lds = rows_lds_bytes(plan);
+#define GQ8_ROWS(W, N)                                                                         \
+    hipLaunchKernelGGL((q8_rows_kernel<W, N>), grid, dim3(kRowsThreads), lds, stream, a)
+#define GQ8_ROWS_NC(W)                                                                         \
+    switch (whole ? nc : 0) {                                                                  \
+    case 1: GQ8_ROWS(W, 1); break;                                                             \
+    case 2: GQ8_ROWS(W, 2); break;                                                             \
+    case 4: GQ8_ROWS(W, 4); break;                                                             \
+    case 8: GQ8_ROWS(W, 8); break;                                                             \
+    case 16: GQ8_ROWS(W, 16); break;                                                           \
+    default: GQ8_ROWS(W, 0); break;                                                            \
+    }
+    if (plan.wpt == 1) {
+        GQ8_ROWS_NC(1);
+    } else {
+        GQ8_ROWS_NC(kRowsWaves);
+    }
+#undef GQ8_ROWS_NC
+#undef GQ8_ROWS
     return hipGetLastError();
 }
+} // namespace
 
 bool rows_attention_supported(int heads, int kv_heads, int head_dim, int max_positions)
 {
@@ -571,17 +787,18 @@ hipError_t launch_rows_attention(const RowsAttentionArgs &a, int rows, int max_p
         return hipErrorInvalidValue;
     const dim3 grid((max_positions + a.per_split - 1) / a.per_split, rows);
     const int C = a.head_dim / 64;
-#define GQ8_ROWS_ATTENTION(CC, HW, HG)                                                              hipLaunchKernelGGL((attention_rows_kernel<CC, HW, HG>), grid, dim3(256 * HG), 0, stream, a)
+#define GQ8_ROWS_ATTENTION(CC, HH)                                                              \
+    hipLaunchKernelGGL((attention_rows_kernel<CC, HH>), grid, dim3(kRowsThreads), 0, stream, a)
     switch (a.heads * 8 + C) {
-    case 2 * 8 + 1: GQ8_ROWS_ATTENTION(1, 2, 1); break;
-    case 2 * 8 + 2: GQ8_ROWS_ATTENTION(2, 2, 1); break;
-    case 2 * 8 + 4: GQ8_ROWS_ATTENTION(4, 2, 1); break;
-    case 4 * 8 + 1: GQ8_ROWS_ATTENTION(1, 4, 1); break;
-    case 4 * 8 + 2: GQ8_ROWS_ATTENTION(2, 4, 1); break;
-    case 4 * 8 + 4: GQ8_ROWS_ATTENTION(4, 4, 1); break;
-    case 8 * 8 + 1: GQ8_ROWS_ATTENTION(1, 4, 2); break;
-    case 8 * 8 + 2: GQ8_ROWS_ATTENTION(2, 4, 2); break;
-    case 8 * 8 + 4: GQ8_ROWS_ATTENTION(4, 4, 2); break;
+    case 2 * 8 + 1: GQ8_ROWS_ATTENTION(1, 2); break;
+    case 2 * 8 + 2: GQ8_ROWS_ATTENTION(2, 2); break;
+    case 2 * 8 + 4: GQ8_ROWS_ATTENTION(4, 2); break;
+    case 4 * 8 + 1: GQ8_ROWS_ATTENTION(1, 4); break;
+    case 4 * 8 + 2: GQ8_ROWS_ATTENTION(2, 4); break;
+    case 4 * 8 + 4: GQ8_ROWS_ATTENTION(4, 4); break;
+    case 8 * 8 + 1: GQ8_ROWS_ATTENTION(1, 8); break;
+    case 8 * 8 + 2: GQ8_ROWS_ATTENTION(2, 8); break;
+    case 8 * 8 + 4: GQ8_ROWS_ATTENTION(4, 8); break;
     default: return hipErrorInvalidValue;
     }
 #undef GQ8_ROWS_ATTENTION

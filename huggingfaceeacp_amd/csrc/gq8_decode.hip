@@ -333,7 +333,7 @@ __device__ inline double load_agent(const double *p)
 }
 
 template <int C, int G>
-__global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs args)
+__global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a)
 {
     constexpr int kRows = kScoreBatch * G; // reduce_rows width: (key, head) pairs
     __shared__ double sScore[G][kMaxSplitKeys];
@@ -343,25 +343,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
     __shared__ int sLast;
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int hd = args.head_dim, kvWidth = args.kv_heads * hd;
-    const int heads = args.heads, qWidth = heads * hd;
-    const int perKv = heads / args.kv_heads;
+    const int hd = a.head_dim, kvWidth = a.kv_heads * hd;
+    const int heads = a.heads, qWidth = heads * hd;
+    const int perKv = heads / a.kv_heads;
     const int group = blockIdx.y, h0 = group * G;
-    // this sequence's query, caches, position, partials, tickets and rows
-    const int seq = blockIdx.z;
-    AttentionArgs a = args;
-    a.query += seq * a.query_stride;
-    a.key_cache += seq * a.cache_stride;
-    a.value_cache += seq * a.cache_stride;
-    a.position += seq;
-    a.ws_o += (int64_t) seq * kDecodeSplits * qWidth;
-    a.ws_ml += (int64_t) seq * kDecodeSplits * heads * 2;
-    a.counter += seq * kDecodeCounters;
-    if (a.out)
-        a.out += (int64_t) seq * qWidth;
-    uint16_t *q8Scales = reinterpret_cast<uint16_t *>(a.q8 + (int64_t) max(a.q8_rows, 1) * qWidth)
-                         + (int64_t) seq * (qWidth / kBlock);
-    a.q8 += (int64_t) seq * qWidth;
     const int groupWidth = G * hd;
     const int split = blockIdx.x;
 
@@ -564,7 +549,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
         const float sc = half_value(bits);
         a.q8[idx] = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);
         if ((t & 31) == 0)
-            q8Scales[idx / kBlock] = bits;
+            reinterpret_cast<uint16_t *>(a.q8 + qWidth)[idx / kBlock] = bits;
     }
     if (t == 0) // ready for the next launch
         __hip_atomic_store(a.counter + group, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1822,7 +1807,7 @@ hipError_t launch_attention(const AttentionArgs &a, hipStream_t stream)
     int channels = 0, group = 0;
     if (!attention_layout(a.head_dim, &channels, &group) || a.heads % group != 0)
         return hipErrorInvalidValue;
-    const dim3 grid(kDecodeSplits, a.heads / group, a.rows > 1 ? a.rows : 1);
+    const dim3 grid(kDecodeSplits, a.heads / group);
     if (channels == 4)
         hipLaunchKernelGGL((attention_kernel<4, 1>), grid, dim3(kAttnThreads), 0, stream, a);
     else if (channels == 2)

@@ -48,13 +48,6 @@ struct AttentionArgs {
     float *out;               // optional fp32 row
     uint8_t *q8;              // Q8 row for o_proj
     int partials_only;        // nonzero: store the split partials and stop (o_merge merges them)
-    // lockstep sequences (grid z = rows; 0 means one): row r takes query
-    // row r, the caches at r * cache_stride, position[r], its own partials
-    // (kDecodeSplits each) and tickets (kDecodeCounters each), and writes
-    // row r of a Q8 row buffer of q8_rows rows (and of out)
-    int rows;
-    int64_t query_stride, cache_stride;
-    int q8_rows;
 };
 
 // o_proj fed by the attention partials: every workgroup merges the splits

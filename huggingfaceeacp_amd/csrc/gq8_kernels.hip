@@ -191,24 +191,19 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(float *__restrict__ x, i
 
 // The step's q|k|v rows: q rotated in place, k rotated and stored fp16 in the
 // key cache, v stored fp16 in the value cache (Decoder.cpp:459-548).
-// Row r sits at position base + r of one sequence's caches, or with
-// row_positions at row_positions[r] of sequence r's caches (cache_stride
-// elements apart: the rows of a lockstep batch).
 __global__ __launch_bounds__(kThreads) void rope_kv_kernel(
     float *__restrict__ qkv, int qkv_stride, int heads, int kv_heads, int head_dim,
-    const int *pos_ptr, int pos_value, const int *row_positions, int64_t cache_stride,
-    const float *__restrict__ cosines, const float *__restrict__ sines,
-    uint16_t *__restrict__ key_cache, uint16_t *__restrict__ value_cache)
+    const int *pos_ptr, int pos_value, const float *__restrict__ cosines,
+    const float *__restrict__ sines, uint16_t *__restrict__ key_cache,
+    uint16_t *__restrict__ value_cache)
 {
     const int row = blockIdx.x;
     const int half = head_dim / 2;
     const int qWidth = heads * head_dim, kvWidth = kv_heads * head_dim;
-    const int position =
-        row_positions ? row_positions[row] : (pos_ptr ? *pos_ptr : 0) + pos_value + row;
-    const int64_t cache = row_positions ? row * cache_stride : 0;
+    const int position = (pos_ptr ? *pos_ptr : 0) + pos_value + row;
     float *r = qkv + (int64_t) row * qkv_stride;
-    uint16_t *keys = key_cache + cache + (int64_t) position * kvWidth;
-    uint16_t *values = value_cache + cache + (int64_t) position * kvWidth;
+    uint16_t *keys = key_cache + (int64_t) position * kvWidth;
+    uint16_t *values = value_cache + (int64_t) position * kvWidth;
 
     for (int idx = threadIdx.x; idx < (heads + kv_heads) * half; idx += kThreads) {
         const int head = idx / half, pair = idx % half;
@@ -852,22 +847,8 @@ hipError_t launch_rope_kv(float *qkv, int qkv_stride, int heads, int kv_heads, i
     if (rows <= 0 || heads <= 0 || kv_heads <= 0 || head_dim % 2 != 0)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(rope_kv_kernel, dim3(rows), dim3(kThreads), 0, stream, qkv, qkv_stride,
-                       heads, kv_heads, head_dim, pos_ptr, pos_value, nullptr, (int64_t) 0,
-                       cosines, sines, key_cache, value_cache);
-    return hipGetLastError();
-}
-
-hipError_t launch_rope_kv_rows(float *qkv, int qkv_stride, int heads, int kv_heads, int head_dim,
-                               const int *positions, int rows, const float *cosines,
-                               const float *sines, uint16_t *key_cache, uint16_t *value_cache,
-                               int64_t cache_stride, hipStream_t stream)
-{
-    if (rows <= 0 || heads <= 0 || kv_heads <= 0 || head_dim % 2 != 0 || !positions
-        || cache_stride <= 0)
-        return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rope_kv_kernel, dim3(rows), dim3(kThreads), 0, stream, qkv, qkv_stride,
-                       heads, kv_heads, head_dim, nullptr, 0, positions, cache_stride, cosines,
-                       sines, key_cache, value_cache);
+                       heads, kv_heads, head_dim, pos_ptr, pos_value, cosines, sines, key_cache,
+                       value_cache);
     return hipGetLastError();
 }
 

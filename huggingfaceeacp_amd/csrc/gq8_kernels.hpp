@@ -99,18 +99,12 @@ hipError_t launch_advance(int *pos_ptr, int amount, hipStream_t stream);
 // ---- lockstep sequences (one step of up to kBatchRows independent sequences
 // over one weight set) ----------------------------------------------------------
 // Row r: sequence r, at position positions[r]; its token slots start at
-// slots + r * slot_stride and its caches at key_cache / value_cache +
-// r * cache_stride.
+// slots + r * slot_stride.
 constexpr int kBatchRows = 16;
 
 hipError_t launch_embed_slots(const uint32_t *slots, int64_t slot_stride, const int *positions,
                               int rows, const uint8_t *table, int vocab, int width, float scale,
                               float *out, hipStream_t stream);
-
-hipError_t launch_rope_kv_rows(float *qkv, int qkv_stride, int heads, int kv_heads, int head_dim,
-                               const int *positions, int rows, const float *cosines,
-                               const float *sines, uint16_t *key_cache, uint16_t *value_cache,
-                               int64_t cache_stride, hipStream_t stream);
 
 // y[m, n] (+)= the Int8Blocks product of up to kBatchRows activation rows (a
 // Q8 row buffer of x_rows rows, rows [0, rows) used) on int8 MFMA.  Products
@@ -153,6 +147,13 @@ int rows_attention_split_keys(int max_positions);
 size_t rows_attention_workspace_doubles(int rows, int heads, int head_dim);
 hipError_t launch_rows_attention(const RowsAttentionArgs &a, int rows, int max_positions,
                                  hipStream_t stream);
+
+// The gate | up product with GeGLU fused: w8 is the stacked [gate; up]
+// tensor (2 intermediate rows), and GeGLU of row m's products goes, as Q8, to
+// row m of geglu8 (a Q8 row buffer of x_rows rows of intermediate).
+bool rows_geglu_supported(int inner, int intermediate);
+hipError_t launch_q8_rows_geglu(const uint8_t *x8, int x_rows, int rows, const uint8_t *w8,
+                                int inner, int intermediate, uint8_t *geglu8, hipStream_t stream);
 
 // After the argmax of a step: slot positions[r] + 1 of sequence r takes
 // chosen[r], and positions[r] advances by one.

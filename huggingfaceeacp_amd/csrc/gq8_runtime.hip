@@ -1924,7 +1924,8 @@ struct gq8_batch {
     int *positions = nullptr; // device: the position each sequence's next step takes
     std::vector<int> hostPositions;
     float *hidden = nullptr, *qkvRows = nullptr, *fused = nullptr, *logits = nullptr;
-    uint8_t *x8 = nullptr;
+    uint8_t *x8 = nullptr;  // Q8 rows of the norms and of attention
+    uint8_t *x8b = nullptr; // Q8 rows of GeGLU (gate | up reads x8 while they are written)
     uint32_t *chosen = nullptr;
     double *attnO = nullptr, *attnMl = nullptr;
     int *attnCounters = nullptr;
@@ -2043,9 +2044,15 @@ int encode_batch_step(gq8_batch *b)
         GQ8_BATCH_STAGE(kStageO, batch_product(b, d->qWidth, W, d->out[l], b->hidden, W, 1));
         GQ8_STAGE(kStageNorm, gq8::launch_rmsnorm(b->hidden, d->postNorm[l], S, W, s.rms_epsilon,
                                                   nullptr, b->x8, st));
-        GQ8_BATCH_STAGE(kStageGateUp, batch_product(b, W, 2 * F, d->gateUp[l], b->fused, 2 * F, 0));
-        GQ8_STAGE(kStageGeglu, gq8::launch_geglu(b->fused, S, F, nullptr, b->x8, st));
-        GQ8_BATCH_STAGE(kStageDown, batch_product(b, F, W, d->down[l], b->hidden, W, 1));
+        if (gq8::rows_geglu_supported(W, F)) { // GeGLU in the gate | up product's epilogue
+            GQ8_STAGE(kStageGateUp, gq8::launch_q8_rows_geglu(b->x8, S, S, d->gateUp[l], W, F,
+                                                               b->x8b, st));
+        } else {
+            GQ8_BATCH_STAGE(kStageGateUp, batch_product(b, W, 2 * F, d->gateUp[l], b->fused, 2 * F, 0));
+            GQ8_STAGE(kStageGeglu, gq8::launch_geglu(b->fused, S, F, nullptr, b->x8b, st));
+        }
+        GQ8_STAGE(kStageDown, gq8::launch_q8_rows(b->x8b, S, S, d->down[l], F, W, b->hidden, W, 1,
+                                                  b->partials, b->partialBytes, b->tickets, st));
     }
     GQ8_STAGE(kStageNorm, gq8::launch_rmsnorm(b->hidden, d->finalNorm, S, W, s.rms_epsilon, nullptr,
                                               b->x8, st));
@@ -2142,6 +2149,7 @@ extern "C" int gq8_batch_create(gq8_decoder *d, int sequences, gq8_batch **out)
     GQ8_BATCH_ALLOC(b->fused, (size_t) S * 2 * F * sizeof(float));
     GQ8_BATCH_ALLOC(b->logits, (size_t) S * s.vocab * sizeof(float));
     GQ8_BATCH_ALLOC(b->x8, gq8::q8_bytes(S, d->maxInner));
+    GQ8_BATCH_ALLOC(b->x8b, gq8::q8_bytes(S, F));
     GQ8_BATCH_ALLOC(b->chosen, S * sizeof(uint32_t));
     GQ8_BATCH_ALLOC(b->attnO, gq8::rows_attention_workspace_doubles(S, s.heads, s.head_dim)
                                   * sizeof(double));
