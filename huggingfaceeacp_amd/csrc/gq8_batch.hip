@@ -24,13 +24,12 @@
 //
 // attention_rows_kernel: one workgroup per (sequence, key split) scores all
 // the query heads against one read of the split's keys (the single KV head of
-// multi-query attention), so every key and value row is read once a layer;
-// four waves take 16 keys of each 64-key tile, every head in registers.
+// multi-query attention), so every key and value row is read once a layer.
 // It also takes the step's RoPE and cache append: each workgroup rotates the
 // sequence's query row itself, and the workgroup whose split holds the new
 // position rotates the new key, appends it (and the value) to the cache and
-// uses it for that position.  The last split of a sequence to finish merges
-// the splits (MultiQueryAttention.h:43-49) and quantizes the row for o_proj.
+// uses it for that position.  A second launch merges each row's splits
+// (MultiQueryAttention.h:43-49) and quantizes the row for o_proj.
 #include "gq8_device.hpp"
 #include "gq8_kernels.hpp"
 #include "gq8_numerics.hpp"
@@ -48,13 +47,14 @@ constexpr int kRowsTile = 16;         // outputs a tile (a wave's MFMA columns)
 constexpr int kChunkBlocks = 8;       // blocks a wave's weight loads cover at once
 constexpr int kRowsMaxRange = 128;    // blocks of the activation rows a workgroup stages
 constexpr int kRowsManyTiles = 1024;  // products this wide give each wave whole rows
+constexpr int kRowsPrefetch = 2;      // weight chunks in flight a wave
 
 // A workgroup stages `range` blocks of the activation rows in LDS and its
 // waves stream weight rows against them.  Wide products (tiles >= 1024: gate
 // | up, the lm_head) give a workgroup four tiles and each wave a tile's whole
-// rows (WPT 1); narrow ones give a workgroup one tile, its four waves
-// consecutive quarters of the staged blocks (WPT 4), and split the blocks over
-// `splits` workgroups until the chip has about 512.
+// rows (WPT 1); narrow ones give a workgroup one tile, its four waves consecutive
+// quarters of the staged blocks (WPT 4), and split the blocks over `splits`
+// workgroups until the chip has about 512.
 struct RowsPlan {
     int wpt;    // waves a tile: 1 or 4
     int per;    // blocks a wave takes
@@ -85,9 +85,10 @@ RowsPlan rows_plan(int inner, int outputs)
 
 size_t rows_lds_bytes(const RowsPlan &p)
 {
-    // fragments [block][lane] 8 bytes, scales [block][row] fp32, the tiles' partial sums
-    return (size_t) p.range() * 64 * 8 + (size_t) p.range() * kBatchRows * 4
-           + (size_t) kRowsWaves * kBatchRows * (kRowsTile + 1) * 8;
+    // fragments [block][lane] 8 bytes and scales [block][row] fp32; the
+    // tiles' partial sums later reuse the fragments' space
+    const size_t staged = (size_t) p.range() * 64 * 8 + (size_t) p.range() * kBatchRows * 4;
+    return std::max(staged, (size_t) kRowsWaves * kBatchRows * (kRowsTile + 1) * 8);
 }
 
 struct RowsArgs {
@@ -168,6 +169,9 @@ __device__ inline void chunk_products(const WeightChunk &c, const long *sX, cons
         acc[1] = fma((double) d[1], (double) (sw * sx.y), acc[1]);
         acc[2] = fma((double) d[2], (double) (sw * sx.z), acc[2]);
         acc[3] = fma((double) d[3], (double) (sw * sx.w), acc[3]);
+        // one block at a time: the results of hoisted products would hold
+        // accumulation registers that cost occupancy
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -182,8 +186,7 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
     const int range = WPT * a.per;
     long *sX = reinterpret_cast<long *>(rowsLds);
     float *sSx = reinterpret_cast<float *>(rowsLds + (size_t) range * 64 * 8);
-    double *sPart = reinterpret_cast<double *>(rowsLds + (size_t) range * 64 * 8
-                                               + (size_t) range * kBatchRows * 4);
+    double *sPart = reinterpret_cast<double *>(rowsLds); // over the fragments, once they are read
     __shared__ int sLast;
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -206,16 +209,24 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
     const uint8_t *wRow = a.w8 + (int64_t) n * a.inner + (lane >> 4) * 8;
     const uint16_t *wScale = reinterpret_cast<const uint16_t *>(a.w8 + (int64_t) a.outputs * a.inner)
                              + (int64_t) n * nb;
-    WeightChunk bufA, bufB;
-    if (b0 < b1)
-        load_weight_chunk<V>(bufA, wRow, wScale, b0, b1);
+    // up to kRowsPrefetch chunks of weights in flight a wave (issued before
+    // the staging below, so the first ones overlap it)
+    constexpr int P = V ? (NC < kRowsPrefetch ? NC : kRowsPrefetch) : 1;
+    WeightChunk buf[P];
+    if (b0 < b1) {
+#pragma unroll
+        for (int i = 0; i < P; ++i)
+            load_weight_chunk<V>(buf[i], wRow, wScale, V ? b0 + i * kChunkBlocks : b0, b1);
+    }
 
     // stage the workgroup's activation blocks in MFMA fragment order (lane l
     // of block b: sequence l % 16, bytes 8 (l / 16) .. + 8) and their scales
     const uint16_t *xScales = reinterpret_cast<const uint16_t *>(a.x8 + (int64_t) a.x_rows * a.inner);
-    // every load first (clamped into range), then the LDS writes
-    constexpr int kPieces = kRowsMaxRange * kBatchRows * 2 / kRowsThreads; // 16-byte pieces
-    constexpr int kScales = kRowsMaxRange * kBatchRows / kRowsThreads;
+    // every load first (clamped into range), then the LDS writes; with whole
+    // chunks the range is WPT NC chunks, so WPT NC pieces a thread
+    constexpr int kMaxRange = V ? WPT * NC * kChunkBlocks : kRowsMaxRange;
+    constexpr int kPieces = kMaxRange * kBatchRows * 2 / kRowsThreads; // 16-byte pieces
+    constexpr int kScales = (kMaxRange * kBatchRows + kRowsThreads - 1) / kRowsThreads;
     const int pieces = (rEnd - r0) * kBatchRows * 2, scales = (rEnd - r0) * kBatchRows;
     uint4 piece[kPieces];
     uint16_t scaleBits[kScales];
@@ -256,26 +267,30 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
         if (b0 < b1) { // the last split's waves may have no blocks
 #pragma unroll
             for (int i = 0; i < NC; ++i) {
-                WeightChunk &cur = (i & 1) ? bufB : bufA;
-                WeightChunk &next = (i & 1) ? bufA : bufB;
-                if (i + 1 < NC)
-                    load_weight_chunk<true>(next, wRow, wScale, b0 + (i + 1) * kChunkBlocks, b1);
+                // memory clobbers keep each chunk's loads where they are
+                // issued (hoisting them all would cost occupancy)
+                asm volatile("" ::: "memory");
                 __builtin_amdgcn_sched_barrier(0);
-                chunk_products<true>(cur, sX, sSx, b0 - r0 + i * kChunkBlocks,
+                chunk_products<true>(buf[i % P], sX, sSx, b0 - r0 + i * kChunkBlocks,
                                      b0 + i * kChunkBlocks, b1, lane, acc);
+                __builtin_amdgcn_sched_barrier(0);
+                asm volatile("" ::: "memory");
+                if (i + P < NC) // the buffer just consumed takes the chunk P ahead
+                    load_weight_chunk<true>(buf[i % P], wRow, wScale, b0 + (i + P) * kChunkBlocks, b1);
             }
         }
     } else {
         for (int c0 = b0; c0 < b1; c0 += kChunkBlocks) {
             if (c0 > b0)
-                load_weight_chunk<false>(bufA, wRow, wScale, c0, b1);
-            chunk_products<false>(bufA, sX, sSx, c0 - r0, c0, b1, lane, acc);
+                load_weight_chunk<false>(buf[0], wRow, wScale, c0, b1);
+            chunk_products<false>(buf[0], sX, sSx, c0 - r0, c0, b1, lane, acc);
         }
     }
 
     // a tile's sum over its waves (in block order), one (sequence, output)
     // cell a thread; tile k of the workgroup lands in sPart[k]
     const int grp = lane >> 4;
+    __syncthreads(); // every wave has read its fragments
     double *mine = sPart + (size_t) wave * kBatchRows * (kRowsTile + 1);
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -381,56 +396,91 @@ __device__ inline Halves<C> load_channels(const uint16_t *p)
     return h;
 }
 
-// C channels a lane (head width 64 C), H heads: four waves, each scoring
-// every head against its 16 keys of a 64-key tile.
+// C channels a lane (head width 64 C), H heads.  Scores: lane l takes key
+// t0 + l of a 64-key tile and wave w a quarter of the channels, every head
+// (no cross-lane sums; the query comes from LDS as doubles, the four
+// quarters are added in LDS).  Values: lane l takes channels C l .. C l + C - 1
+// and wave w keys t0 + 16 w .. + 15, every head.
 template <int C, int H>
 __global__ __launch_bounds__(kRowsThreads) void attention_rows_kernel(RowsAttentionArgs a)
 {
     constexpr int hd = 64 * C, half = hd / 2, qW = H * hd;
-    constexpr int R = 16 / H;          // keys a scoring round: 16 (key, head) rows a reduction
-    constexpr int kAccHeads = 4;       // heads a pass of the waves' LDS sum
+    constexpr int hq = hd / kRowsWaves;        // channels a wave scores
+    constexpr int kKeyWords = hq / 2;          // their fp16 pairs
+    constexpr int kAccHeads = 4;               // heads a pass of the waves' LDS sum
     constexpr int kRopePairs = ((H + 1) * half + kRowsThreads - 1) / kRowsThreads;
-    constexpr int kOut = (qW + kRowsThreads - 1) / kRowsThreads; // merged outputs a thread
-    static_assert(H * R == 16 && kRowsWaveKeys % R == 0, "layout");
-    __shared__ float sQ[qW];
-    __shared__ __attribute__((aligned(8))) uint16_t sKnew[hd], sVnew[hd];
+    static_assert(hq % 8 == 0, "16-byte key loads");
+    __shared__ double sQd[H][hd];
+    __shared__ __attribute__((aligned(16))) uint16_t sKnew[hd], sVnew[hd];
+    __shared__ double sP[kRowsWaves][H][kRowsTileKeys];
     __shared__ double sS[H][kRowsTileKeys];
     __shared__ double sMax[H], sSum[H], sF[H];
     __shared__ double sAcc[kRowsWaves][kAccHeads * hd];
-    __shared__ double sMerge[H][kRowsMaxSplits];
-    __shared__ int sLast;
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int seq = blockIdx.y, split = blockIdx.x;
-    const int pos = a.positions[seq];
-    const int keyCount = pos + 1;
     const int k0 = split * a.per_split;
-    if (k0 >= keyCount)
-        return;
-    const int k1 = min(k0 + a.per_split, keyCount);
-    const bool holdsNew = k1 == keyCount; // this split ends at the new position
+    // the position first: its wait then counts only the loads before it
+    const int pos = a.positions[seq];
+    asm volatile("" ::: "memory");
+    const int c0 = lane * C;
     const float *row = a.qkv + (int64_t) seq * a.qkv_stride;
     uint16_t *keys = a.key_cache + seq * a.cache_stride;
     uint16_t *values = a.value_cache + seq * a.cache_stride;
 
+    // Loads that do not need the position go first: the query and new key
+    // pairs, the new value, and the first tile's key and value rows (rows
+    // past the position are read inside the cache and never used).  Their
+    // round trip overlaps the position's.
+    float lo[kRopePairs], hi[kRopePairs];
+#pragma unroll
+    for (int k = 0; k < kRopePairs; ++k) {
+        const int idx = min(t + k * kRowsThreads, (H + 1) * half - 1);
+        const int head = idx / half, i = idx % half;
+        lo[k] = row[head * hd + i];
+        hi[k] = row[head * hd + i + half];
+    }
+    const float newValue = row[qW + hd + min(t, hd - 1)];
+    uint32_t kq[kKeyWords];
+    Halves<C> vh[kRowsWaveKeys];
+    auto load_keys = [&](int t0) {
+        const int j = min(t0 + lane, a.max_positions - 1);
+        const uint4 *src = reinterpret_cast<const uint4 *>(keys + (int64_t) j * hd + wave * hq);
+#pragma unroll
+        for (int v = 0; v < kKeyWords / 4; ++v) {
+            const uint4 w = src[v];
+            kq[4 * v] = w.x; kq[4 * v + 1] = w.y; kq[4 * v + 2] = w.z; kq[4 * v + 3] = w.w;
+        }
+    };
+    auto load_values = [&](int t0) {
+#pragma unroll
+        for (int i = 0; i < kRowsWaveKeys; ++i) {
+            const int j = min(t0 + wave * kRowsWaveKeys + i, a.max_positions - 1);
+            vh[i] = load_channels<C>(values + (int64_t) j * hd + c0);
+        }
+    };
+    load_keys(k0);
+    load_values(k0);
+    asm volatile("" ::: "memory"); // keeps the loads above the position-dependent exit
+
+    const int keyCount = pos + 1;
+    if (k0 >= keyCount)
+        return;
+    const int k1 = min(k0 + a.per_split, keyCount);
+    const bool holdsNew = k1 == keyCount; // this split ends at the new position
+
     // RoPE (rope_kv_kernel's arithmetic) of the query heads and, in the
     // split holding it, of the new key (head H, right after the queries); the
-    // new value rounded to fp16.  Every load first, clamped into the row.
+    // new value rounded to fp16
     {
-        float lo[kRopePairs], hi[kRopePairs], cs[kRopePairs], sn[kRopePairs];
+        float cs[kRopePairs], sn[kRopePairs];
 #pragma unroll
         for (int k = 0; k < kRopePairs; ++k) {
             const int idx = min(t + k * kRowsThreads, (H + 1) * half - 1);
-            const int head = idx / half, i = idx % half;
-            const int64_t angle = (int64_t) pos * half + i;
-            lo[k] = row[head * hd + i];
-            hi[k] = row[head * hd + i + half];
+            const int64_t angle = (int64_t) pos * half + idx % half;
             cs[k] = a.cosines[angle];
             sn[k] = a.sines[angle];
         }
-        float v = 0.f;
-        if (holdsNew && t < hd)
-            v = row[qW + hd + t];
 #pragma unroll
         for (int k = 0; k < kRopePairs; ++k) {
             const int idx = t + k * kRowsThreads;
@@ -440,15 +490,15 @@ __global__ __launch_bounds__(kRowsThreads) void attention_rows_kernel(RowsAttent
             float rl, rh;
             rotate_pair(lo[k], hi[k], cs[k], sn[k], &rl, &rh);
             if (head < H) {
-                sQ[head * hd + i] = rl;
-                sQ[head * hd + i + half] = rh;
+                sQd[head][i] = (double) rl;
+                sQd[head][i + half] = (double) rh;
             } else {
                 sKnew[i] = half_bits(rl);
                 sKnew[i + half] = half_bits(rh);
             }
         }
         if (holdsNew && t < hd)
-            sVnew[t] = half_bits(v);
+            sVnew[t] = half_bits(newValue);
     }
     if (t < H) {
         sMax[t] = -INFINITY;
@@ -460,72 +510,60 @@ __global__ __launch_bounds__(kRowsThreads) void attention_rows_kernel(RowsAttent
         values[(int64_t) pos * hd + t] = sVnew[t];
     }
 
-    const int c0 = lane * C;
-    double q[H][C], acc[H][C];
+    double acc[H][C];
 #pragma unroll
     for (int h = 0; h < H; ++h)
 #pragma unroll
-        for (int c = 0; c < C; ++c) {
-            q[h][c] = (double) sQ[h * hd + c0 + c];
+        for (int c = 0; c < C; ++c)
             acc[h][c] = 0.0;
-        }
 
     for (int t0 = k0; t0 < k1; t0 += kRowsTileKeys) {
         const int nk = min(kRowsTileKeys, k1 - t0);
-        const bool tileHoldsNew = holdsNew && t0 + nk == keyCount;
-        // this wave's keys t0 + 16 wave + i, clamped into the tile (the
-        // duplicates are masked), the new position's row from LDS
-        Halves<C> kh[kRowsWaveKeys], vh[kRowsWaveKeys];
-#pragma unroll
-        for (int i = 0; i < kRowsWaveKeys; ++i) {
-            const int j = t0 + min(wave * kRowsWaveKeys + i, nk - 1);
-            kh[i] = load_channels<C>(keys + (int64_t) j * hd + c0);
+        if (t0 > k0) { // the first tile's rows are already in
+            load_keys(t0);
+            load_values(t0);
         }
-        if (tileHoldsNew) {
-            const Halves<C> kn = load_channels<C>(sKnew + c0);
+        if (holdsNew && t0 + nk == keyCount) { // the new position's rows from LDS
+            if (t0 + lane == pos) {
+                const uint4 *src = reinterpret_cast<const uint4 *>(sKnew + wave * hq);
 #pragma unroll
-            for (int i = 0; i < kRowsWaveKeys; ++i)
-                if (t0 + min(wave * kRowsWaveKeys + i, nk - 1) == pos)
-                    kh[i] = kn;
-        }
-#pragma unroll
-        for (int r0 = 0; r0 < kRowsWaveKeys; r0 += R) {
-            double y[16];
-#pragma unroll
-            for (int i = 0; i < R; ++i)
-#pragma unroll
-                for (int h = 0; h < H; ++h) {
-                    double p = 0.0;
-#pragma unroll
-                    for (int c = 0; c < C; ++c)
-                        p += q[h][c] * (double) kh[r0 + i].at(c);
-                    y[i * H + h] = p;
+                for (int v = 0; v < kKeyWords / 4; ++v) {
+                    const uint4 w = src[v];
+                    kq[4 * v] = w.x; kq[4 * v + 1] = w.y; kq[4 * v + 2] = w.z; kq[4 * v + 3] = w.w;
                 }
-            const double total = reduce_rows<16>(y, lane);
-            if (stores_row<16>(lane)) {
-                const int rr = row_of_lane<16>(lane);
-                const int jj = wave * kRowsWaveKeys + r0 + rr / H;
-                sS[rr % H][jj] = jj < nk ? (double) a.scale * total : -INFINITY;
             }
-            __builtin_amdgcn_sched_barrier(0); // one round's conversions at a time
-        }
-        // the values, in flight during the softmax
-#pragma unroll
-        for (int i = 0; i < kRowsWaveKeys; ++i) {
-            const int j = t0 + min(wave * kRowsWaveKeys + i, nk - 1);
-            vh[i] = load_channels<C>(values + (int64_t) j * hd + c0);
-        }
-        if (tileHoldsNew) {
             const Halves<C> vn = load_channels<C>(sVnew + c0);
 #pragma unroll
             for (int i = 0; i < kRowsWaveKeys; ++i)
-                if (t0 + min(wave * kRowsWaveKeys + i, nk - 1) == pos)
+                if (t0 + wave * kRowsWaveKeys + i == pos)
                     vh[i] = vn;
         }
+        // this lane's key against every head over this wave's channels
+        double p[H];
+#pragma unroll
+        for (int h = 0; h < H; ++h)
+            p[h] = 0.0;
+#pragma unroll
+        for (int w = 0; w < kKeyWords; ++w) {
+            const double ka = (double) half_value((uint16_t) (kq[w] & 0xFFFFu));
+            const double kb = (double) half_value((uint16_t) (kq[w] >> 16));
+#pragma unroll
+            for (int h = 0; h < H; ++h) {
+                const double2 qq = *reinterpret_cast<const double2 *>(&sQd[h][wave * hq + 2 * w]);
+                p[h] = fma(qq.x, ka, p[h]);
+                p[h] = fma(qq.y, kb, p[h]);
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < H; ++h)
+            sP[wave][h][lane] = p[h];
         __syncthreads();
-        // the tile's softmax against the running maximum, a wave a head
+        // the tile's softmax against the running maximum, a wave a head; the
+        // four channel quarters added in order
         for (int h = wave; h < H; h += kRowsWaves) {
-            const double sc = lane < nk ? sS[h][lane] : -INFINITY;
+            const double sc = lane < nk ? (double) a.scale * (((sP[0][h][lane] + sP[1][h][lane])
+                                                               + sP[2][h][lane]) + sP[3][h][lane])
+                                        : -INFINITY;
             const double tileMax = wave_max_d(sc);
             const double previous = sMax[h];
             const double largest = fmax(previous, tileMax);
@@ -540,8 +578,7 @@ __global__ __launch_bounds__(kRowsThreads) void attention_rows_kernel(RowsAttent
             }
         }
         __syncthreads();
-        // rescaled running sums plus this wave's keys in order (weights past
-        // the tile are zero)
+        // rescaled running sums plus this wave's keys in order
 #pragma unroll
         for (int h = 0; h < H; ++h) {
             const double f = sF[h];
@@ -551,6 +588,8 @@ __global__ __launch_bounds__(kRowsThreads) void attention_rows_kernel(RowsAttent
         }
 #pragma unroll
         for (int i = 0; i < kRowsWaveKeys; ++i) {
+            if (wave * kRowsWaveKeys + i >= nk) // rows past the position may hold anything
+                break;
             double v[C];
 #pragma unroll
             for (int c = 0; c < C; ++c)
@@ -585,76 +624,59 @@ __global__ __launch_bounds__(kRowsThreads) void attention_rows_kernel(RowsAttent
 #pragma unroll
             for (int w = 1; w < kRowsWaves; ++w)
                 v += sAcc[w][o];
-            store_agent_d(a.ws_o + slot * qW + h0 * hd + o, v);
+            a.ws_o[slot * qW + h0 * hd + o] = v;
         }
     }
     if (t < H) {
-        store_agent_d(a.ws_ml + (slot * H + t) * 2, sMax[t]);
-        store_agent_d(a.ws_ml + (slot * H + t) * 2 + 1, sSum[t]);
+        a.ws_ml[(slot * H + t) * 2] = sMax[t];
+        a.ws_ml[(slot * H + t) * 2 + 1] = sSum[t];
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // the stores have completed
-    __syncthreads();
-    const int splits = (keyCount + a.per_split - 1) / a.per_split;
-    if (t == 0)
-        sLast = __hip_atomic_fetch_add(a.tickets + seq, 1, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
-    __syncthreads();
-    if (!sLast)
-        return;
+}
 
-    // the merge: split weights per head (one split a lane), then the row
+// The merge of a row's key splits, one workgroup a (head, sequence), one
+// channel a thread: every split rescaled to the row maximum, in split order,
+// the sum divided by the total (MultiQueryAttention.h:43-49), rounded to fp32
+// and quantized in 32-channel blocks for o_proj.  Every split's partial is
+// loaded at once.
+__global__ __launch_bounds__(kRowsThreads) void attention_merge_rows_kernel(RowsAttentionArgs a)
+{
+    __shared__ double sF[kRowsMaxSplits];
+    __shared__ double sTotal;
+    const int head = blockIdx.x, seq = blockIdx.y, t = threadIdx.x;
+    const int hd = a.head_dim, H = a.heads, qW = H * hd;
+    const int splits = (a.positions[seq] + a.per_split) / a.per_split; // keys: position + 1
     const int64_t first = (int64_t) seq * kRowsMaxSplits;
-    for (int h = wave; h < H; h += kRowsWaves) {
-        const bool live = lane < splits;
-        const int sp = live ? lane : 0;
-        const double m = load_agent_d(a.ws_ml + ((first + sp) * H + h) * 2);
-        const double sum = load_agent_d(a.ws_ml + ((first + sp) * H + h) * 2 + 1);
+    const int o = head * hd + t;
+    double part[kRowsMaxSplits];
+#pragma unroll
+    for (int u = 0; u < kRowsMaxSplits; ++u)
+        part[u] = a.ws_o[(first + min(u, splits - 1)) * qW + o];
+    if (t < 64) {
+        const bool live = t < splits;
+        const int sp = live ? t : 0;
+        const double m = a.ws_ml[((first + sp) * H + head) * 2];
+        const double sum = a.ws_ml[((first + sp) * H + head) * 2 + 1];
         double total;
         const double f = merge_factor(m, sum, live, total);
         if (live)
-            sMerge[h][sp] = f;
-        if (lane == 0)
-            sSum[h] = total;
+            sF[sp] = f;
+        if (t == 0)
+            sTotal = total;
     }
     __syncthreads();
-    // thread t's outputs t + 256 k, every split's partials of a batch loaded at once
-    constexpr int kMergeSplits = 8;
-    double weighted[kOut];
+    double weighted = 0.0;
 #pragma unroll
-    for (int k = 0; k < kOut; ++k)
-        weighted[k] = 0.0;
-    for (int s0 = 0; s0 < splits; s0 += kMergeSplits) {
-        double part[kMergeSplits][kOut];
-#pragma unroll
-        for (int u = 0; u < kMergeSplits; ++u)
-#pragma unroll
-            for (int k = 0; k < kOut; ++k)
-                part[u][k] = load_agent_d(a.ws_o + (first + min(s0 + u, splits - 1)) * qW
-                                          + min(t + k * kRowsThreads, qW - 1));
-#pragma unroll
-        for (int u = 0; u < kMergeSplits; ++u)
-            if (s0 + u < splits)
-#pragma unroll
-                for (int k = 0; k < kOut; ++k)
-                    weighted[k] += part[u][k] * sMerge[min(t + k * kRowsThreads, qW - 1) / hd][s0 + u];
-    }
-    uint16_t *scales = reinterpret_cast<uint16_t *>(a.q8 + (int64_t) a.q8_rows * qW)
-                       + (int64_t) seq * (qW / kBlock);
-#pragma unroll
-    for (int k = 0; k < kOut; ++k) { // whole waves: a 32-block is 32 consecutive lanes
-        const int o = t + k * kRowsThreads;
-        if (o >= qW) // whole waves (qW is a multiple of 64)
-            break;
-        const float v = (float) (weighted[k] / sSum[o / hd]);
-        const float amax = max_lanes<16>(fabsf(v));
-        const uint16_t bits = scale_bits_from_amax(amax);
-        const float sc = half_value(bits);
-        a.q8[(int64_t) seq * qW + o] = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);
-        if ((o & 31) == 0)
-            scales[o / kBlock] = bits;
-    }
-    if (t == 0) // ready for the next launch
-        __hip_atomic_store(a.tickets + seq, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int u = 0; u < kRowsMaxSplits; ++u)
+        if (u < splits)
+            weighted += part[u] * sF[u];
+    const float v = (float) (weighted / sTotal);
+    const float amax = max_lanes<16>(fabsf(v)); // a 32-block is 32 consecutive lanes
+    const uint16_t bits = scale_bits_from_amax(amax);
+    const float sc = half_value(bits);
+    a.q8[(int64_t) seq * qW + o] = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);
+    if ((t & 31) == 0)
+        reinterpret_cast<uint16_t *>(a.q8 + (int64_t) a.q8_rows * qW)[(int64_t) seq * (qW / kBlock)
+                                                                      + o / kBlock] = bits;
 }
 
 __global__ void batch_advance_kernel(const uint32_t *__restrict__ chosen, uint32_t *slots,
@@ -783,7 +805,7 @@ hipError_t launch_rows_attention(const RowsAttentionArgs &a, int rows, int max_p
 {
     if (rows <= 0 || rows > kBatchRows || a.q8_rows < rows
         || !rows_attention_supported(a.heads, 1, a.head_dim, max_positions)
-        || a.per_split != rows_attention_split_keys(max_positions))
+        || a.per_split != rows_attention_split_keys(max_positions) || a.max_positions != max_positions)
         return hipErrorInvalidValue;
     const dim3 grid((max_positions + a.per_split - 1) / a.per_split, rows);
     const int C = a.head_dim / 64;
@@ -802,6 +824,10 @@ hipError_t launch_rows_attention(const RowsAttentionArgs &a, int rows, int max_p
     default: return hipErrorInvalidValue;
     }
 #undef GQ8_ROWS_ATTENTION
+    if (hipError_t e = hipGetLastError(); e != hipSuccess)
+        return e;
+    hipLaunchKernelGGL(attention_merge_rows_kernel, dim3(a.heads, rows), dim3(a.head_dim), 0, stream,
+                       a);
     return hipGetLastError();
 }
 

@@ -124,8 +124,7 @@ hipError_t launch_q8_rows(const uint8_t *x8, int x_rows, int rows, const uint8_t
 // the new key and value are appended at positions[r].  The merged row goes to
 // row r of a Q8 row buffer of q8_rows rows.  per_split is
 // rows_attention_split_keys(max_positions); ws_o / ws_ml hold
-// rows_attention_workspace_doubles; tickets (one a row) are zero between
-// launches.
+// rows_attention_workspace_doubles.
 constexpr int kRowsMaxSplits = 32;
 struct RowsAttentionArgs {
     const float *qkv;
@@ -134,11 +133,11 @@ struct RowsAttentionArgs {
     const float *cosines, *sines;
     uint16_t *key_cache, *value_cache;
     int64_t cache_stride;
+    int max_positions;        // rows of each cache (the bound of speculative reads)
     int heads, head_dim;
     float scale;
     int per_split;
     double *ws_o, *ws_ml;
-    int *tickets;
     uint8_t *q8;
     int q8_rows;
 };

@@ -1928,7 +1928,6 @@ struct gq8_batch {
     uint8_t *x8b = nullptr; // Q8 rows of GeGLU (gate | up reads x8 while they are written)
     uint32_t *chosen = nullptr;
     double *attnO = nullptr, *attnMl = nullptr;
-    int *attnCounters = nullptr;
     double *partials = nullptr;
     size_t partialBytes = 0;
     int *tickets = nullptr;
@@ -2031,13 +2030,13 @@ int encode_batch_step(gq8_batch *b)
         at.key_cache = b->keyCache + layerCache;
         at.value_cache = b->valueCache + layerCache;
         at.cache_stride = b->cacheStride;
+        at.max_positions = s.max_positions;
         at.heads = s.heads;
         at.head_dim = s.head_dim;
         at.scale = 1.f / std::sqrt((float) s.head_dim);
         at.per_split = gq8::rows_attention_split_keys(s.max_positions);
         at.ws_o = b->attnO;
         at.ws_ml = b->attnMl;
-        at.tickets = b->attnCounters;
         at.q8 = b->x8;
         at.q8_rows = S;
         GQ8_STAGE(kStageAttention, gq8::launch_rows_attention(at, S, s.max_positions, st));
@@ -2154,7 +2153,6 @@ extern "C" int gq8_batch_create(gq8_decoder *d, int sequences, gq8_batch **out)
     GQ8_BATCH_ALLOC(b->attnO, gq8::rows_attention_workspace_doubles(S, s.heads, s.head_dim)
                                   * sizeof(double));
     b->attnMl = b->attnO + (size_t) S * gq8::kRowsMaxSplits * d->qWidth;
-    GQ8_BATCH_ALLOC(b->attnCounters, (size_t) S * sizeof(int));
     {
         const int products[5][2] = {{W, d->qkvWidth}, {d->qWidth, W}, {W, 2 * F}, {F, W},
                                     {W, s.vocab}};
@@ -2175,8 +2173,7 @@ extern "C" int gq8_batch_create(gq8_decoder *d, int sequences, gq8_batch **out)
     if (b->argmaxWorkspaceBytes)
         GQ8_BATCH_ALLOC(b->argmaxWorkspace, b->argmaxWorkspaceBytes);
 #undef GQ8_BATCH_ALLOC
-    if (hipMemset(b->attnCounters, 0, (size_t) S * sizeof(int)) != hipSuccess
-        || hipMemset(b->positions, 0, S * sizeof(int)) != hipSuccess
+    if (hipMemset(b->positions, 0, S * sizeof(int)) != hipSuccess
         || hipMemset(b->slots, 0, b->slotStride * S * sizeof(uint32_t)) != hipSuccess)
         return cleanup(fail(GQ8_ERR_DEVICE, "batch state: initialisation failed"));
     *out = b;
