@@ -1,0 +1,72 @@
+"""The long-context workload: an 8064-token seeded prompt and greedy decode to
+the end of the 8192-position window (Gemma-2B dims, 2 layers, fp16 cache).
+
+The oracle's full prefill at this length is minutes of CPU time, so parity
+here rests on properties the window fixes and on independent GPU paths:
+- the run returns exactly max_positions - prompt = 128 ids (Gemma.cpp:395-400)
+  and the window's last position is refused after the run's last step;
+- the plain loop, hipGraph replay and the one-launch persistent step give the
+  same ids;
+- the logits of the window's last position agree between the one-token
+  decode kernels (split-key attention over 8191 keys) and a multi-row step
+  (prefill attention on fp64 MFMA and the int8 MFMA GEMM) that recomputes the
+  last rows from the cache, to the double-sum order (1e-6 relative, >= 99 %
+  bit-identical).
+The oracle pins the same kernels at shorter lengths (test_gpu_decoder.py,
+test_gpu_persist.py)."""
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_helpers import exact_fraction, worst_error
+from huggingfaceeacp_amd import gemma_q8 as G
+from test_gpu_decoder import gemma_pair, gpu_step
+
+pytestmark = pytest.mark.gpu
+
+WINDOW, PROMPT = 8192, 8064
+
+
+def test_long_context_window(torch_cuda):
+    torch = torch_cuda
+    shape, decoder, _ = gemma_pair(2, WINDOW, max_step_rows=512)
+    prompt = O.prompt_ids(0xC0FFEE + 4, shape.vocab, PROMPT)
+    print("long_context: 8064 + 128, 2 layers", flush=True)
+    runs = {}
+    for label, persistent, graph in (("graph", False, True), ("plain", False, False),
+                                     ("persistent", True, True)):
+        decoder.set_persistent(persistent)
+        tokens, stats = decoder.generate(prompt, 1000, eos=-1, use_graph=graph)
+        runs[label] = list(tokens)
+        print(f"  {label}: {len(tokens)} ids, decode {stats.decode_seconds * 1e3:.1f} ms", flush=True)
+    decoder.set_persistent(False)
+    assert len(runs["graph"]) == WINDOW - PROMPT
+    assert runs["graph"] == runs["plain"] == runs["persistent"]
+
+    # the run's last step left the position at 8191: one more step fills the
+    # window's extra slot, a second is refused
+    assert decoder.position == WINDOW - 1
+    decoder.decode(1)
+    with pytest.raises(G.Gq8Error) as e:
+        decoder.decode(1)
+    assert e.value.status == G.ERR_WINDOW
+
+    # the window's last position: one-token kernels against a multi-row step
+    history = np.concatenate([prompt, np.asarray(runs["graph"], dtype=prompt.dtype)])
+    assert len(history) == WINDOW
+    decoder.begin_sequence()
+    capacity = shape.step_capacity()
+    for start in range(0, WINDOW - 1, capacity):
+        gpu_step(torch, decoder, history[start:min(start + capacity, WINDOW - 1)], 1)
+    one_token = gpu_step(torch, decoder, history[-1:])[0]
+    assert int(np.argmax(one_token)) == int(decoder.tokens(WINDOW, 1)[0])
+    decoder.begin_sequence()
+    tail = 48  # the last rows as one multi-row step over the cached prefix
+    for start in range(0, WINDOW - tail, capacity):
+        gpu_step(torch, decoder, history[start:min(start + capacity, WINDOW - tail)], 1)
+    multi_row = gpu_step(torch, decoder, history[WINDOW - tail:], 1)[0]
+    err = worst_error(one_token, multi_row)
+    exact = exact_fraction(one_token, multi_row)
+    print(f"  position 8191 logits, one-token vs multi-row: worst {err:.3g}, exact {exact:.4f}")
+    assert err <= 1e-6
+    assert exact >= 0.99
