@@ -162,8 +162,8 @@ def batch_stage_bytes(shape, stage: str, rows: int) -> int:
     a residual)."""
     w, f, v = shape.width, shape.intermediate, shape.vocab
     q8 = lambda n: n * 17 // 16  # noqa: E731
-    if stage == "gate_up":
-        return q8(2 * f * w) + rows * (q8(w) + 2 * f * 4)
+    if stage == "gate_up":  # GeGLU fused: Q8 rows in, GeGLU's Q8 rows out
+        return q8(2 * f * w) + rows * (q8(w) + q8(f))
     if stage == "lm_head":
         return q8(v * w) + rows * (q8(w) + v * 4)
     if stage == "down":
@@ -225,7 +225,7 @@ def batch_bench(args, G, torch) -> dict:
     per_launch_s = ms / launches / 1e3
     launch_bytes = batch_stage_bytes(shape, dominant, S)
     achieved = launch_bytes / per_launch_s / 1e9
-    labels = {"gate_up": "q8_rows_kernel (gate|up 2048 -> 2x16384, 16 rows)",
+    labels = {"gate_up": "q8_rows_kernel (gate|up 2048 -> 2x16384 + GeGLU + Q8, 16 rows)",
               "lm_head": "q8_rows_kernel (tied lm_head 2048 -> 256000, 16 rows)",
               "down": "q8_rows_kernel (down 16384 -> 2048 + residual, 16 rows)"}
     batch.close()
