@@ -4,6 +4,7 @@
 // Gemma.cpp).  Host C++ over the HIP runtime; every device buffer is owned
 // here and every refusal is checked before anything is launched.
 #include "gemma_q8.h"
+#include "gq8_checkpoint.hpp"
 #include "gq8_decode.hpp"
 #include "gq8_kernels.hpp"
 #include "gq8_numerics.hpp"
@@ -129,6 +130,11 @@ void normal_chunk(uint64_t tensorSeed, double sigma, int64_t chunk, int64_t coun
 // ============================================================================
 // Status and format helpers
 // ============================================================================
+int gq8::report(int status, const std::string &message)
+{
+    return fail(status, message);
+}
+
 extern "C" const char *gq8_status_string(int status)
 {
     switch (status) {
@@ -143,6 +149,7 @@ extern "C" const char *gq8_status_string(int status)
     case GQ8_ERR_EMPTY: return "no tokens";
     case GQ8_ERR_DEVICE: return "HIP error";
     case GQ8_ERR_MEMORY: return "device allocation failed";
+    case GQ8_ERR_FORMAT: return "malformed or mismatched checkpoint file";
     default: return "unknown status";
     }
 }
@@ -916,6 +923,111 @@ extern "C" int gq8_decoder_load_tensor_q8(gq8_decoder *d, int index, const uint8
     GQ8_HIP(hipMemcpy(p.q, host_bytes, p.elements, hipMemcpyHostToDevice));
     GQ8_HIP(hipMemcpy(p.scales, host_bytes + p.elements, p.elements / 16, hipMemcpyHostToDevice));
     return mark_present(d, index);
+}
+
+namespace {
+// The checkpoint's name for catalogue entry `index` (GemmaTensors.h:29-44).
+std::string checkpoint_name(const gq8_shape &s, int index)
+{
+    if (index == 0)
+        return "model.embed_tokens.weight";
+    if (is_final_norm(&s, index))
+        return "model.norm.weight";
+    static const char *const suffix[kPerLayer] = {
+        "self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
+        "self_attn.o_proj.weight", "mlp.gate_proj.weight", "mlp.up_proj.weight",
+        "mlp.down_proj.weight", "input_layernorm.weight", "post_attention_layernorm.weight"};
+    return "model.layers." + std::to_string((index - 1) / kPerLayer) + "." + suffix[(index - 1) % kPerLayer];
+}
+
+// HuggingFace stores a linear weight as [outputs, inputs] (GemmaTensors.h:13-16).
+std::vector<int64_t> checkpoint_dims(const gq8_shape &s, int index)
+{
+    const int64_t w = s.width, q = (int64_t) s.heads * s.head_dim,
+                  kv = (int64_t) s.kv_heads * s.head_dim, f = s.intermediate;
+    if (index == 0)
+        return {s.vocab, w};
+    if (is_final_norm(&s, index))
+        return {w};
+    switch ((index - 1) % kPerLayer) {
+    case kQ: return {q, w};
+    case kK: case kV: return {kv, w};
+    case kO: return {w, q};
+    case kGate: case kUp: return {f, w};
+    case kDown: return {w, f};
+    default: return {w};
+    }
+}
+
+std::string dims_text(const std::vector<int64_t> &dims)
+{
+    std::string t = "[";
+    for (size_t i = 0; i < dims.size(); ++i)
+        t += (i ? ", " : "") + std::to_string(dims[i]);
+    return t + "]";
+}
+} // namespace
+
+extern "C" int gq8_decoder_load_safetensors(gq8_decoder *d, gq8_safetensors *const *shards,
+                                            int shard_count)
+{
+    if (!d || !shards || shard_count <= 0)
+        return fail(GQ8_ERR_ARGUMENT, "load_safetensors: bad arguments");
+    const gq8_shape &s = d->shape;
+    const int count = gq8_tensor_count(&s);
+    // every tensor found and checked before a byte is uploaded
+    std::vector<std::pair<const gq8::SafeTensorsFile *, const gq8::TensorInfo *>> found(count);
+    for (int i = 0; i < count; ++i) {
+        const std::string name = checkpoint_name(s, i);
+        for (int k = 0; k < shard_count && !found[i].first; ++k) {
+            const gq8::SafeTensorsFile *f = gq8::file_of(shards[k]);
+            if (!f)
+                return fail(GQ8_ERR_ARGUMENT, "load_safetensors: null shard");
+            const int at = f->find(name);
+            if (at >= 0)
+                found[i] = {f, &f->tensors()[at]};
+        }
+        if (!found[i].first)
+            return fail(GQ8_ERR_FORMAT, "the checkpoint has no tensor '" + name + "'");
+        const gq8::TensorInfo &t = *found[i].second;
+        const std::vector<int64_t> want = checkpoint_dims(s, i);
+        if (t.shape != want)
+            return fail(GQ8_ERR_FORMAT, "tensor '" + name + "' is " + dims_text(t.shape)
+                                            + ", the config implies " + dims_text(want));
+        if (t.dtype != gq8::kF32 && t.dtype != gq8::kF16 && t.dtype != gq8::kBF16
+            && t.dtype != gq8::kF64)
+            return fail(GQ8_ERR_FORMAT, "tensor '" + name + "' is " + gq8::dtype_name(t.dtype)
+                                            + ", not a floating-point tensor");
+    }
+    const int64_t piece = int64_t(16) << 20; // elements a piece (a multiple of the block)
+    float *host = nullptr, *staging = nullptr;
+    if (hipHostMalloc(reinterpret_cast<void **>(&host), piece * sizeof(float)) != hipSuccess) {
+        (void) hipGetLastError();
+        return fail(GQ8_ERR_MEMORY, "load_safetensors: pinned staging allocation failed");
+    }
+    int status = GQ8_OK;
+    if (hipMalloc(&staging, piece * sizeof(float)) != hipSuccess) {
+        (void) hipGetLastError();
+        status = fail(GQ8_ERR_MEMORY, "load_safetensors: device staging allocation failed");
+    }
+    for (int i = 0; i < count && status == GQ8_OK; ++i) {
+        const gq8::TensorInfo &t = *found[i].second;
+        const int64_t elements = t.elements();
+        for (int64_t first = 0; first < elements && status == GQ8_OK; first += piece) {
+            const int64_t n = std::min(piece, elements - first);
+            status = found[i].first->read_floats(t, first, n, host);
+            if (status == GQ8_OK)
+                status = upload_values(d, i, host, first, n, staging);
+            if (status == GQ8_OK && hipStreamSynchronize(d->stream) != hipSuccess)
+                status = fail(GQ8_ERR_DEVICE, "load_safetensors: synchronize failed");
+        }
+        if (status == GQ8_OK)
+            mark_present(d, i);
+    }
+    if (staging)
+        (void) hipFree(staging);
+    (void) hipHostFree(host);
+    return status;
 }
 
 extern "C" int gq8_decoder_fill_synthetic(gq8_decoder *d, int threads)

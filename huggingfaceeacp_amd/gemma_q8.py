@@ -25,6 +25,11 @@ LIBRARY_PATH = os.path.join(HERE, "libgemma_q8.so")
 OK = 0
 ERR_ARGUMENT, ERR_SHAPE, ERR_CAPACITY, ERR_WINDOW, ERR_TOKEN = -1, -2, -3, -4, -5
 ERR_UNQUANTIZABLE, ERR_NOT_PREPARED, ERR_EMPTY, ERR_DEVICE, ERR_MEMORY = -6, -7, -8, -9, -10
+ERR_FORMAT = -11
+
+# safetensors dtype tags (TensorType.h:12-27 order)
+DTYPES = ["BOOL", "U8", "I8", "U16", "I16", "F16", "BF16", "U32", "I32", "F32", "U64", "I64",
+          "F64"]
 
 # GemmaTensors::all order (GemmaTensors.cpp:30-57)
 T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN, T_INPUT_NORM, T_POST_NORM = range(9)
@@ -52,6 +57,10 @@ class _Shape(ctypes.Structure):
         ("max_step_rows", ctypes.c_int), ("rms_epsilon", ctypes.c_float),
         ("rope_theta", ctypes.c_double), ("embedding_scale", ctypes.c_float),
     ]
+
+
+class _TokenIds(ctypes.Structure):
+    _fields_ = [("bos", ctypes.c_int), ("eos", ctypes.c_int), ("pad", ctypes.c_int)]
 
 
 class _RunStats(ctypes.Structure):
@@ -123,6 +132,21 @@ def library() -> ctypes.CDLL:
         "gq8_decoder_set_timing": (i32, [P, i32]),
         "gq8_decoder_timing": (i32, [P, P, P]),
         "gq8_decoder_time_kernel": (i32, [P, i32, i32, ctypes.POINTER(f64), ctypes.POINTER(i32)]),
+        "gq8_safetensors_open": (i32, [ctypes.c_char_p, ctypes.POINTER(P)]),
+        "gq8_safetensors_from_bytes": (i32, [P, ctypes.c_uint64, ctypes.POINTER(P)]),
+        "gq8_safetensors_close": (None, [P]),
+        "gq8_safetensors_count": (i32, [P]),
+        "gq8_safetensors_find": (i32, [P, ctypes.c_char_p]),
+        "gq8_safetensors_info": (i32, [P, i32, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(i32),
+                                       ctypes.POINTER(i32), P, i32, ctypes.POINTER(ctypes.c_uint64)]),
+        "gq8_safetensors_read_floats": (i32, [P, i32, i64, i64, P]),
+        "gq8_safetensors_raw": (ctypes.c_void_p, [P, i32]),
+        "gq8_safetensors_metadata_count": (i32, [P]),
+        "gq8_safetensors_metadata": (i32, [P, i32, ctypes.POINTER(ctypes.c_char_p),
+                                           ctypes.POINTER(ctypes.c_char_p)]),
+        "gq8_gemma_config_parse": (i32, [ctypes.c_char_p, sz, i32, i32, ctypes.POINTER(_Shape),
+                                         ctypes.POINTER(_TokenIds)]),
+        "gq8_decoder_load_safetensors": (i32, [P, P, i32]),
         "gq8_batch_create": (i32, [P, i32, ctypes.POINTER(P)]),
         "gq8_batch_destroy": (None, [P]),
         "gq8_batch_prefill": (i32, [P, i32, P, i32]),
@@ -390,6 +414,13 @@ class Decoder:
         check(library().gq8_decoder_debug(self.handle, which, layer, _host(values), _host(q8)))
         return values, q8
 
+    def load_safetensors(self, shards) -> None:
+        """Every catalogue tensor from the checkpoint's shards, by its
+        checkpoint name, checked against the shape before any upload
+        (TensorLoader.cpp:186-347)."""
+        handles = (ctypes.c_void_p * len(shards))(*[f.handle for f in shards])
+        check(library().gq8_decoder_load_safetensors(self.handle, handles, len(shards)))
+
     def decode(self, steps: int, use_graph: bool = True) -> None:
         """Continue the greedy loop `steps` tokens (on-device token feedback)."""
         check(library().gq8_decoder_decode(self.handle, steps, int(use_graph)))
@@ -437,6 +468,100 @@ class Decoder:
                                              ctypes.byref(stats)))
         return out[:count].copy(), RunStats(stats.prefill_seconds, stats.decode_seconds,
                                             stats.step_count, stats.generated)
+
+
+class SafeTensors:
+    """SafeTensors (SafeTensors.h:78-183) over libgemma_q8: a mapped (open) or
+    copied (from_bytes) safetensors file whose header was checked whole."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    @staticmethod
+    def open(path) -> "SafeTensors":
+        handle = ctypes.c_void_p()
+        check(library().gq8_safetensors_open(os.fsencode(path), ctypes.byref(handle)))
+        return SafeTensors(handle)
+
+    @staticmethod
+    def from_bytes(data: bytes) -> "SafeTensors":
+        buf = np.frombuffer(bytes(data), dtype=np.uint8)
+        handle = ctypes.c_void_p()
+        check(library().gq8_safetensors_from_bytes(buf.ctypes.data if buf.size else None,
+                                                    buf.size, ctypes.byref(handle)))
+        return SafeTensors(handle)
+
+    def close(self) -> None:
+        if self.handle:
+            library().gq8_safetensors_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _index(self, name: str) -> int:
+        return check(library().gq8_safetensors_find(self.handle, name.encode()))
+
+    def names(self) -> list[str]:
+        return [self._info(i)[0] for i in range(check(library().gq8_safetensors_count(self.handle)))]
+
+    def _info(self, index: int):
+        name = ctypes.c_char_p()
+        dtype, rank = ctypes.c_int(), ctypes.c_int()
+        shape = np.zeros(16, dtype=np.int64)
+        nbytes = ctypes.c_uint64()
+        check(library().gq8_safetensors_info(self.handle, index, ctypes.byref(name),
+                                             ctypes.byref(dtype), ctypes.byref(rank),
+                                             shape.ctypes.data, shape.size, ctypes.byref(nbytes)))
+        return (name.value.decode(), DTYPES[dtype.value], tuple(int(d) for d in shape[:rank.value]),
+                int(nbytes.value))
+
+    def contains(self, name: str) -> bool:
+        return name in self.names()
+
+    def info(self, name: str):
+        """(dtype, shape, byte count) of a tensor; Gq8Error if there is none."""
+        return self._info(self._index(name))[1:]
+
+    def read_floats(self, name: str, first: int = 0, count: int | None = None) -> np.ndarray:
+        index = self._index(name)
+        elements = int(np.prod(self._info(index)[2], dtype=np.int64))
+        count = elements - first if count is None else count
+        out = np.empty(max(count, 0), dtype=np.float32)
+        check(library().gq8_safetensors_read_floats(self.handle, index, first, count,
+                                                    out.ctypes.data if out.size else None))
+        return out
+
+    def raw(self, name: str) -> bytes:
+        index = self._index(name)
+        nbytes = self._info(index)[3]
+        ptr = library().gq8_safetensors_raw(self.handle, index)
+        return ctypes.string_at(ptr, nbytes) if nbytes else b""
+
+    def metadata(self) -> dict:
+        out = {}
+        for i in range(check(library().gq8_safetensors_metadata_count(self.handle))):
+            k, v = ctypes.c_char_p(), ctypes.c_char_p()
+            check(library().gq8_safetensors_metadata(self.handle, i, ctypes.byref(k),
+                                                     ctypes.byref(v)))
+            out[k.value.decode()] = v.value.decode()
+        return out
+
+
+def gemma_config(text: str, max_positions: int = 0, max_step_rows: int = 0):
+    """GemmaConfig::fromJson + DecoderShape::fromConfig: (DecoderShape, (bos, eos, pad))."""
+    raw = text.encode()
+    c = _Shape()
+    ids = _TokenIds()
+    check(library().gq8_gemma_config_parse(raw, len(raw), max_positions, max_step_rows,
+                                           ctypes.byref(c), ctypes.byref(ids)))
+    shape = DecoderShape(c.width, c.heads, c.kv_heads, c.head_dim, c.layers, c.intermediate,
+                         c.vocab, c.max_positions, c.max_step_rows, c.rms_epsilon, c.rope_theta,
+                         c.embedding_scale)
+    return shape, (ids.bos, ids.eos, ids.pad)
 
 
 class Batch:

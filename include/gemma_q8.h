@@ -44,7 +44,8 @@ typedef enum gq8_status {
     GQ8_ERR_NOT_PREPARED = -7,  /* weights missing (Decoder.cpp:286-300) */
     GQ8_ERR_EMPTY = -8,         /* a step or prompt of zero tokens (Decoder.cpp:650-651) */
     GQ8_ERR_DEVICE = -9,        /* a HIP call failed */
-    GQ8_ERR_MEMORY = -10        /* device allocation failed */
+    GQ8_ERR_MEMORY = -10,       /* device allocation failed */
+    GQ8_ERR_FORMAT = -11        /* a malformed or mismatched checkpoint file (SafeTensors.h:85-101) */
 } gq8_status;
 
 const char *gq8_status_string(int status);
@@ -282,6 +283,62 @@ int gq8_decoder_timing(gq8_decoder *decoder, double *milliseconds, int *launches
  * counterpart: measurement. */
 int gq8_decoder_time_kernel(gq8_decoder *decoder, int stage, int repeats, double *milliseconds,
                             int *launches);
+
+/* ======================================================================= */
+/* Checkpoint files: safetensors (Model/SafeTensors.h:78-183) and Gemma's   */
+/* config.json (Model/GemmaConfig.h:41-92).  Host only; no GPU needed.      */
+/* ======================================================================= */
+/* dtype tags in Model/TensorType.h:12-27 order */
+enum {
+    GQ8_DTYPE_BOOL, GQ8_DTYPE_U8, GQ8_DTYPE_I8, GQ8_DTYPE_U16, GQ8_DTYPE_I16, GQ8_DTYPE_F16,
+    GQ8_DTYPE_BF16, GQ8_DTYPE_U32, GQ8_DTYPE_I32, GQ8_DTYPE_F32, GQ8_DTYPE_U64, GQ8_DTYPE_I64,
+    GQ8_DTYPE_F64
+};
+typedef struct gq8_safetensors gq8_safetensors;
+/* SafeTensors::fromFile (a read-only mapping: nothing is resident before it
+ * is read) and SafeTensors::fromBytes (a copy).  Every header rule is checked
+ * before a byte is trusted (SafeTensors.h:85-101): a malformed length, JSON,
+ * entry, dtype, byte range, shape/range mismatch or metadata value is
+ * GQ8_ERR_FORMAT. */
+int gq8_safetensors_open(const char *path, gq8_safetensors **out);
+int gq8_safetensors_from_bytes(const uint8_t *bytes, uint64_t size, gq8_safetensors **out);
+void gq8_safetensors_close(gq8_safetensors *file);
+/* SafeTensors::tensors (sorted by name) / find (GQ8_ERR_FORMAT when absent) */
+int gq8_safetensors_count(const gq8_safetensors *file);
+int gq8_safetensors_find(const gq8_safetensors *file, const char *name);
+/* TensorInfo of entry `index`; name stays valid while the file is open; up to
+ * shape_capacity dimensions are written. */
+int gq8_safetensors_info(const gq8_safetensors *file, int index, const char **name, int *dtype,
+                         int *rank, int64_t *shape, int shape_capacity, uint64_t *byte_count);
+/* widenTensorElements (SafeTensors.h:71-76): elements [first, first + count)
+ * widened to fp32 (F16 and BF16 exactly); GQ8_ERR_FORMAT for integer dtypes. */
+int gq8_safetensors_read_floats(const gq8_safetensors *file, int index, int64_t first,
+                                int64_t count, float *out);
+/* SafeTensors::rawBytes: the entry's bytes in the mapping (NULL if no such entry). */
+const uint8_t *gq8_safetensors_raw(const gq8_safetensors *file, int index);
+/* SafeTensors::metadata: the __metadata__ string pairs, sorted by key. */
+int gq8_safetensors_metadata_count(const gq8_safetensors *file);
+int gq8_safetensors_metadata(const gq8_safetensors *file, int index, const char **key,
+                             const char **value);
+
+typedef struct gq8_token_ids {
+    int bos, eos, pad;
+} gq8_token_ids;
+/* GemmaConfig::fromJson (GemmaConfig.cpp:140-205) and DecoderShape::fromConfig:
+ * every field defaults to google/gemma-2b's value; model_type must be
+ * "gemma"; token ids are a number or the first of a list.  max_positions > 0
+ * caps the window below max_position_embeddings.  An untied output projection
+ * is GQ8_ERR_SHAPE (this decoder's lm_head is the embedding). */
+int gq8_gemma_config_parse(const char *json_text, size_t length, int max_positions,
+                           int max_step_rows, gq8_shape *shape, gq8_token_ids *tokens);
+/* TensorLoader::load (TensorLoader.cpp:186-347) over the checkpoint's shards:
+ * every tensor of the catalogue is found by its checkpoint name
+ * ("model.embed_tokens.weight", "model.layers.N.self_attn.q_proj.weight", ...,
+ * "model.norm.weight"; GemmaTensors.h:29-44) and checked against the shape
+ * before anything is uploaded (GemmaTensors::checkAgainst), then widened to
+ * fp32 on the host in pieces and quantized to Int8Blocks on the device. */
+int gq8_decoder_load_safetensors(gq8_decoder *decoder, gq8_safetensors *const *shards,
+                                 int shard_count);
 
 /* ======================================================================= */
 /* Lockstep decode of up to 16 independent sequences over one decoder's     */
