@@ -9,6 +9,7 @@
  */
 #include "gemma_oracle.h"
 
+#include <float.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -461,6 +462,97 @@ int gor_argmax(const float *logits, const float *mask, int n)
     }
 
     return best < 0 ? 0 : best;
+}
+
+/* ---- Sampler.cpp:78-213: one token from one row of logits --------------
+ * Temperature 0 is the argmax.  Otherwise the unmasked tokens become
+ * candidates scored logit * (1 / temperature) in double (token order);
+ * top-k keeps the k best by (score descending, token ascending) and orders
+ * them; top-p orders the candidates, takes their softmax, and keeps the
+ * shortest prefix whose running mass reaches p (the boundary kept); the
+ * survivors' softmax is drawn from by walking them in their order until the
+ * running mass passes the uniform draw, the last one when rounding leaves the
+ * total short.  The ordered k best are what nth_element + sort leave, since
+ * the order is total; a full sort finds the same prefix. */
+typedef struct {
+    int token;
+    double score;
+} sample_candidate;
+
+static int ranks_before(const void *l, const void *r)
+{
+    const sample_candidate *a = (const sample_candidate *) l, *b = (const sample_candidate *) r;
+    if (a->score != b->score)
+        return a->score > b->score ? -1 : 1;
+    return a->token < b->token ? -1 : (a->token > b->token);
+}
+
+static void sample_softmax(const sample_candidate *c, int n, double *p)
+{
+    double largest = -DBL_MAX, total = 0.0;
+    for (int i = 0; i < n; ++i)
+        if (c[i].score > largest)
+            largest = c[i].score;
+    for (int i = 0; i < n; ++i) {
+        p[i] = exp(c[i].score - largest);
+        total += p[i];
+    }
+    for (int i = 0; i < n; ++i)
+        p[i] /= total;
+}
+
+int gor_sample(const float *logits, const float *mask, int n, float temperature, int top_k,
+               float top_p, double uniform)
+{
+    if (temperature == 0.f)
+        return gor_argmax(logits, mask, n);
+    sample_candidate *c = (sample_candidate *) malloc(sizeof(sample_candidate) * (size_t) n);
+    double *p = (double *) malloc(sizeof(double) * (size_t) n);
+    const double inverse = 1.0 / (double) temperature;
+    int count = 0;
+    for (int token = 0; token < n; ++token) {
+        if (mask && mask[token] != 0.f)
+            continue;
+        c[count].token = token;
+        c[count].score = (double) logits[token] * inverse;
+        ++count;
+    }
+    int chosen = 0;
+    if (count > 0) {
+        if (top_k > 0 && top_k < count) {
+            qsort(c, (size_t) count, sizeof(sample_candidate), ranks_before);
+            count = top_k;
+        }
+        if (top_p < 1.f) {
+            qsort(c, (size_t) count, sizeof(sample_candidate), ranks_before);
+            sample_softmax(c, count, p);
+            const double wanted = (double) top_p;
+            double mass = 0.0;
+            int kept = 0;
+            while (kept < count && mass < wanted)
+                mass += p[kept++];
+            count = kept;
+        }
+        sample_softmax(c, count, p);
+        double mass = 0.0;
+        chosen = c[count - 1].token;
+        for (int i = 0; i < count; ++i) {
+            mass += p[i];
+            if (uniform < mass) {
+                chosen = c[i].token;
+                break;
+            }
+        }
+    }
+    free(c);
+    free(p);
+    return chosen;
+}
+
+/* Sampler::uniform (Sampler.cpp:209-212): the top 53 bits of one engine draw. */
+double gor_mt64_uniform(gor_mt64 *engine)
+{
+    return (double) (gor_mt64_next(engine) >> 11) * 0x1.0p-53;
 }
 
 /* Multi-query attention of one query row over key_count cached rows

@@ -86,6 +86,11 @@ void gor_q8_matvec(const int8_t *xq, const uint16_t *xs, const uint8_t *weights,
 /* first maximum among unmasked entries, 0 when all are masked
  * (Argmax.h:14-38; Sampler.cpp:60-76). mask may be NULL. */
 int gor_argmax(const float *logits, const float *mask, int n);
+/* Sampler::uniform (Sampler.cpp:209-212). */
+double gor_mt64_uniform(gor_mt64 *engine);
+/* Sampler::sample with the draw given (Sampler.cpp:78-213). */
+int gor_sample(const float *logits, const float *mask, int n, float temperature, int top_k,
+               float top_p, double uniform);
 /* One query row (heads x head_dim) over key_count cached fp16 keys/values. */
 void gor_mqa_row_f16(const float *query, const uint16_t *keys, const uint16_t *values,
                      int heads, int kv_heads, int head_dim, int key_count, float scale,

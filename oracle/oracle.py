@@ -84,6 +84,8 @@ def lib():
         "gor_rope_row": (None, [P, i32, i32, i32, i32, P, P]),
         "gor_q8_matvec": (None, [P, P, P, i64, i64, P]),
         "gor_argmax": (i32, [P, P, i32]),
+        "gor_sample": (i32, [P, P, i32, ctypes.c_float, i32, ctypes.c_float, ctypes.c_double]),
+        "gor_mt64_uniform": (ctypes.c_double, [P]),
         "gor_mqa_row_f16": (None, [P, P, P, i32, i32, i32, i32, ctypes.c_float, P]),
         "gor_tensor_count": (i32, [P]),
         "gor_tensor_elements": (i64, [P, i32]),
@@ -200,6 +202,34 @@ def argmax(logits, mask=None):
     logits = np.ascontiguousarray(logits, dtype=np.float32)
     m = None if mask is None else np.ascontiguousarray(mask, dtype=np.float32)
     return int(lib().gor_argmax(ptr(logits), ptr(m) if m is not None else None, logits.size))
+
+
+class Sampler:
+    """Sampler (Sampler.h:52-109): options, a seeded std::mt19937_64, one draw
+    a sample (Sampler::uniform), the sample restated in C (gor_sample)."""
+
+    def __init__(self, temperature=0.0, top_k=0, top_p=1.0, seed=0):
+        self.temperature, self.top_k, self.top_p = temperature, top_k, top_p
+        self.engine = (ctypes.c_uint64 * 313)()
+        lib().gor_mt64_seed(self.engine, seed)
+
+    def uniform(self) -> float:
+        return float(lib().gor_mt64_uniform(self.engine))
+
+    def sample(self, logits, mask=None) -> int:
+        logits = np.ascontiguousarray(logits, dtype=np.float32)
+        m = None if mask is None else np.ascontiguousarray(mask, dtype=np.float32)
+        if self.temperature == 0.0:
+            return argmax(logits, m)
+        return int(lib().gor_sample(ptr(logits), ptr(m) if m is not None else None, logits.size,
+                                    self.temperature, self.top_k, self.top_p, self.uniform()))
+
+
+def uniform_draws(seed: int, count: int) -> np.ndarray:
+    """The first `count` Sampler::uniform draws of a seed."""
+    engine = (ctypes.c_uint64 * 313)()
+    lib().gor_mt64_seed(engine, seed)
+    return np.array([lib().gor_mt64_uniform(engine) for _ in range(count)], dtype=np.float64)
 
 
 # ---- the model ---------------------------------------------------------------
