@@ -159,4 +159,26 @@ hipError_t launch_q8_rows_geglu(const uint8_t *x8, int x_rows, int rows, const u
 hipError_t launch_batch_advance(const uint32_t *chosen, uint32_t *slots, int64_t slot_stride,
                                 int *positions, int rows, hipStream_t stream);
 
+// ---- sampling (Sampler::sample, Sampler.cpp:78-213) ----------------------------
+struct SampleArgs {
+    const float *logits;   // one row of fp32 [vocab]
+    const float *mask;     // nonzero: the token is never chosen (optional)
+    int vocab;
+    float temperature;     // > 0 (zero is the argmax)
+    int top_k;             // 0: no cut
+    float top_p;           // 1: no cut
+    const double *draws;   // uniform draws in [0, 1), one a sample
+    int draw_count;        // the index is clamped to the last draw
+    int *draw_index;       // the draw this sample takes; advanced by one
+    uint32_t *sequence;    // the chosen id goes to sequence[*position + offset] (optional)
+    const int *position;
+    int offset;
+    uint32_t *token_out;   // and to *token_out (optional)
+};
+
+size_t sample_workspace_bytes(int vocab);
+bool sampling_options_valid(float temperature, int top_k, float top_p);
+hipError_t launch_sample(const SampleArgs &a, void *workspace, size_t workspace_bytes,
+                         hipStream_t stream);
+
 } // namespace gq8

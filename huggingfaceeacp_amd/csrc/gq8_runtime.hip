@@ -125,6 +125,27 @@ void normal_chunk(uint64_t tensorSeed, double sigma, int64_t chunk, int64_t coun
     }
 }
 
+// Sampler::uniform (Sampler.cpp:209-212): the top 53 bits of a 64-bit
+// Mersenne Twister output, scaled into [0, 1).
+void uniform_draws(uint64_t seed, int count, double *out)
+{
+    std::mt19937_64 engine(seed);
+    for (int i = 0; i < count; ++i)
+        out[i] = (double) (engine() >> 11) * 0x1.0p-53;
+}
+
+int sampling_error(const gq8_sampling &o)
+{
+    if (!(o.temperature >= 0.f))
+        return fail(GQ8_ERR_ARGUMENT, "A sampling temperature must be zero or positive");
+    if (o.top_k < 0)
+        return fail(GQ8_ERR_ARGUMENT, "A top-k count cannot be negative");
+    if (!(o.top_p > 0.f && o.top_p <= 1.f))
+        return fail(GQ8_ERR_ARGUMENT, "A top-p mass must lie inside (0, 1]");
+    return GQ8_OK;
+}
+
+
 } // namespace
 
 // ============================================================================
@@ -373,6 +394,60 @@ extern "C" size_t gq8_argmax_workspace_bytes(int rows, int length)
     return gq8::argmax_workspace_bytes(rows, length);
 }
 
+extern "C" size_t gq8_sample_workspace_bytes(int vocab)
+{
+    // the sort's buffers, then one draw and its index
+    return vocab > 0 ? std::max(gq8::sample_workspace_bytes(vocab) + 256,
+                                gq8::argmax_workspace_bytes(1, vocab))
+                     : 0;
+}
+
+extern "C" int gq8_sample_row(const float *logits, const float *mask, int vocab,
+                              const gq8_sampling *options, double uniform, uint32_t *token,
+                              void *workspace, size_t workspace_bytes, void *stream)
+{
+    if (!logits || !options || !token || !workspace)
+        return fail(GQ8_ERR_ARGUMENT, "sample_row: null argument");
+    if (vocab <= 0)
+        return fail(GQ8_ERR_EMPTY, "Cannot sample from an empty row of logits");
+    if (int st = sampling_error(*options))
+        return st;
+    if (workspace_bytes < gq8_sample_workspace_bytes(vocab))
+        return fail(GQ8_ERR_ARGUMENT, "sample_row: workspace too small");
+    if (!(uniform >= 0.0 && uniform < 1.0))
+        return fail(GQ8_ERR_ARGUMENT, "sample_row: the draw lies outside [0, 1)");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (options->temperature == 0.f) { // Sampler.cpp:84-85
+        GQ8_LAUNCH(gq8::launch_argmax(logits, mask, 1, vocab, token, nullptr, 0, workspace,
+                                      gq8::argmax_workspace_bytes(1, vocab), st));
+        return GQ8_OK;
+    }
+    const size_t sortBytes = gq8::sample_workspace_bytes(vocab);
+    auto *tail = reinterpret_cast<uint8_t *>(workspace) + sortBytes;
+    auto *draw = reinterpret_cast<double *>(tail);
+    auto *index = reinterpret_cast<int *>(tail + sizeof(double));
+    struct {
+        double u;
+        int index;
+    } host{uniform, 0};
+    GQ8_HIP(hipMemcpyAsync(draw, &host, sizeof(host), hipMemcpyHostToDevice, st));
+    gq8::SampleArgs a{};
+    a.logits = logits;
+    a.mask = mask;
+    a.vocab = vocab;
+    a.temperature = options->temperature;
+    a.top_k = options->top_k;
+    a.top_p = options->top_p;
+    a.draws = draw;
+    a.draw_count = 1;
+    a.draw_index = index;
+    a.token_out = token;
+    GQ8_LAUNCH(gq8::launch_sample(a, workspace, sortBytes, st));
+    // the draw is read from host memory that ends with this call
+    GQ8_HIP(hipStreamSynchronize(st));
+    return GQ8_OK;
+}
+
 extern "C" int gq8_argmax_rows(const float *logits, const float *mask, int rows, int length,
                                uint32_t *indices, void *workspace, size_t workspace_bytes,
                                void *stream)
@@ -455,6 +530,14 @@ struct gq8_decoder {
     int *counters = nullptr; // attention head-group tickets
     unsigned long long *headBest = nullptr; // the lm_head argmax slots
 
+    // sampling (Gemma::setSampling, Gemma.cpp:198-202): the options, and the
+    // seed's Sampler::uniform draws, one a sampled token of a sequence
+    gq8_sampling sampling{0.f, 0, 1.f, 0};
+    double *draws = nullptr; // max_positions draws
+    int *drawIndex = nullptr;
+    void *sampleWorkspace = nullptr;
+    size_t sampleWorkspaceBytes = 0;
+
     hipGraphExec_t graph = nullptr;
     bool capturing = false;
 
@@ -470,6 +553,11 @@ struct gq8_decoder {
 };
 
 namespace {
+
+bool sampled(const gq8_decoder *d)
+{
+    return d->sampling.temperature > 0.f;
+}
 
 int64_t fused_rows_offset(const gq8_decoder *d, int role)
 {
@@ -1120,6 +1208,42 @@ extern "C" int gq8_decoder_begin_sequence(gq8_decoder *d)
     d->hostPosition = 0;
     const int zero = 0;
     GQ8_HIP(hipMemcpy(d->position, &zero, sizeof(int), hipMemcpyHostToDevice));
+    // every run draws from a freshly seeded generator (Gemma.cpp:549)
+    if (d->drawIndex)
+        GQ8_HIP(hipMemcpy(d->drawIndex, &zero, sizeof(int), hipMemcpyHostToDevice));
+    return GQ8_OK;
+}
+
+
+extern "C" int gq8_decoder_set_sampling(gq8_decoder *d, const gq8_sampling *options)
+{
+    if (!d || !options)
+        return fail(GQ8_ERR_ARGUMENT, "decoder_set_sampling: null argument");
+    if (int st = sampling_error(*options))
+        return st;
+    const int count = d->shape.max_positions;
+    if (options->temperature > 0.f && !d->draws) {
+        if (int st = alloc_as(d, &d->draws, (size_t) count * sizeof(double)))
+            return st;
+        if (int st = alloc_as(d, &d->drawIndex, sizeof(int)))
+            return st;
+        d->sampleWorkspaceBytes = gq8::sample_workspace_bytes(d->shape.vocab);
+        if (int st = device_alloc(d, &d->sampleWorkspace, d->sampleWorkspaceBytes))
+            return st;
+    }
+    GQ8_HIP(hipStreamSynchronize(d->stream));
+    if (options->temperature > 0.f) {
+        std::vector<double> draws(count);
+        uniform_draws(options->seed, count, draws.data());
+        GQ8_HIP(hipMemcpy(d->draws, draws.data(), count * sizeof(double), hipMemcpyHostToDevice));
+        const int zero = 0;
+        GQ8_HIP(hipMemcpy(d->drawIndex, &zero, sizeof(int), hipMemcpyHostToDevice));
+    }
+    d->sampling = *options;
+    if (d->graph) { // a captured step keeps the chooser it was captured with
+        (void) hipGraphExecDestroy(d->graph);
+        d->graph = nullptr;
+    }
     return GQ8_OK;
 }
 
@@ -1253,6 +1377,27 @@ struct StageTimer {
         StageTimer timer_(d, stage);              \
         GQ8_LAUNCH(expr);                         \
     } while (0)
+
+// The sample of one logits row; the id goes to slot *position + offset.
+int encode_sample(gq8_decoder *d, const float *row, int offset)
+{
+    gq8::SampleArgs a{};
+    a.logits = row;
+    a.vocab = d->shape.vocab;
+    a.temperature = d->sampling.temperature;
+    a.top_k = d->sampling.top_k;
+    a.top_p = d->sampling.top_p;
+    a.draws = d->draws;
+    a.draw_count = d->shape.max_positions;
+    a.draw_index = d->drawIndex;
+    a.sequence = d->sequence;
+    a.position = d->position;
+    a.offset = offset;
+    GQ8_STAGE(kStageArgmax, gq8::launch_sample(a, d->sampleWorkspace, d->sampleWorkspaceBytes,
+                                               d->stream));
+    return GQ8_OK;
+}
+
 
 // The one-token step as one dataflow launch (gq8_decode.hip).
 int encode_flow_token(gq8_decoder *d, float *logits, bool sample)
@@ -1534,12 +1679,16 @@ int encode_fused_token(gq8_decoder *d, float *logits, bool sample)
     h.normalised_out = d->normalisedRows;
     h.q8 = d->x8;
     h.best = d->headBest;
-    h.sequence = sample ? d->sequence : nullptr;
+    h.sequence = sample && !sampled(d) ? d->sequence : nullptr;
     h.position = d->position;
     h.advance = 1;
     GQ8_STAGE(kStageNorm, gq8::launch_final_norm(h, st));
     GQ8_STAGE(kStageLogits, gq8::launch_lmhead_argmax(h, st));
     GQ8_STAGE(kStageArgmax, gq8::launch_head_finalize(h, st));
+    // the position has advanced: the sample fills slot *position
+    if (sample && sampled(d))
+        if (int status = encode_sample(d, logits, 0))
+            return status;
     if (dbg && copy_last_q8_row(d, d->x8, 1, W, debugQ8(0, s.layers)))
         return GQ8_ERR_DEVICE;
     if (dbg) {
@@ -1561,10 +1710,12 @@ int encode_step(gq8_decoder *d, int rows, float *logits, int logitsRows, bool sa
     hipStream_t st = d->stream;
     const float attentionScale = 1.f / std::sqrt((float) s.head_dim);
     const bool dbg = d->debug;
-    if (rows == 1 && logits && logitsRows == 1 && d->usePersist && d->persistSupported
+    // the one-launch steps choose by argmax inside the launch
+    const bool oneLaunch = !(sample && sampled(d));
+    if (oneLaunch && rows == 1 && logits && logitsRows == 1 && d->usePersist && d->persistSupported
         && !(d->debug && !d->capturing))
         return encode_persist_token(d, logits, sample);
-    if (rows == 1 && logits && logitsRows == 1 && d->useFlow && d->flowSupported
+    if (oneLaunch && rows == 1 && logits && logitsRows == 1 && d->useFlow && d->flowSupported
         && !(d->debug && !d->capturing))
         return encode_flow_token(d, logits, sample);
     if (rows == 1 && logits && logitsRows == 1 && d->useFused && d->fusedSupported)
@@ -1616,10 +1767,14 @@ int encode_step(gq8_decoder *d, int rows, float *logits, int logitsRows, bool sa
     if (logits && logitsRows > 0)
         GQ8_STAGE(kStageLogits, gq8::launch_q8_product(d->x8, rows, rows - logitsRows, logitsRows,
                                           d->embedding, W, s.vocab, logits, s.vocab, 0, st));
-    if (sample)
+    if (sample && sampled(d)) {
+        if (int status = encode_sample(d, logits + (int64_t) (logitsRows - 1) * s.vocab, rows))
+            return status;
+    } else if (sample) {
         GQ8_STAGE(kStageArgmax, gq8::launch_argmax(logits + (int64_t) (logitsRows - 1) * s.vocab, nullptr, 1,
                                       s.vocab, d->sequence, d->position, rows,
                                       d->argmaxWorkspace, d->argmaxWorkspaceBytes, st));
+    }
     GQ8_LAUNCH(gq8::launch_advance(d->position, rows, st));
     return GQ8_OK;
 }

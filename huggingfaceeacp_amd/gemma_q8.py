@@ -63,6 +63,28 @@ class _TokenIds(ctypes.Structure):
     _fields_ = [("bos", ctypes.c_int), ("eos", ctypes.c_int), ("pad", ctypes.c_int)]
 
 
+class _Sampling(ctypes.Structure):
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_int),
+                ("top_p", ctypes.c_float), ("seed", ctypes.c_uint64)]
+
+
+@dataclass(frozen=True)
+class SamplingOptions:
+    """SamplingOptions (Sampling/Sampler.h:33-51): temperature 0 is the argmax,
+    top_k 0 and top_p 1 switch their cut off."""
+    temperature: float = 1.0
+    top_k: int = 0
+    top_p: float = 1.0
+    seed: int = 0
+
+    @staticmethod
+    def greedy() -> "SamplingOptions":
+        return SamplingOptions(temperature=0.0)
+
+    def as_c(self) -> _Sampling:
+        return _Sampling(self.temperature, self.top_k, self.top_p, self.seed)
+
+
 class _RunStats(ctypes.Structure):
     _fields_ = [("prefill_seconds", ctypes.c_double), ("decode_seconds", ctypes.c_double),
                 ("step_count", ctypes.c_int), ("generated", ctypes.c_int)]
@@ -155,6 +177,9 @@ def library() -> ctypes.CDLL:
         "gq8_batch_position": (i32, [P, i32]),
         "gq8_batch_tokens": (i32, [P, i32, i32, i32, P]),
         "gq8_batch_logits": (i32, [P, P]),
+        "gq8_sample_workspace_bytes": (sz, [i32]),
+        "gq8_sample_row": (i32, [P, P, i32, P, f64, P, P, sz, P]),
+        "gq8_decoder_set_sampling": (i32, [P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -233,6 +258,18 @@ def argmax_workspace_bytes(rows, length):
 def argmax_rows(logits, mask, rows, length, indices, workspace, workspace_bytes, stream=0):
     return check(library().gq8_argmax_rows(logits, mask, rows, length, indices, workspace,
                                            workspace_bytes, stream))
+
+
+def sample_workspace_bytes(vocab):
+    return int(library().gq8_sample_workspace_bytes(vocab))
+
+
+def sample_row(logits, mask, vocab, options: SamplingOptions, uniform, token, workspace,
+               workspace_bytes, stream=0):
+    """Sampler::sample of one device row of logits; the id goes to *token."""
+    c = options.as_c()
+    return check(library().gq8_sample_row(logits, mask, vocab, ctypes.byref(c), float(uniform),
+                                          token, workspace, workspace_bytes, stream))
 
 
 # ---- host format helpers ---------------------------------------------------------
@@ -398,6 +435,11 @@ class Decoder:
         """Run one-token steps as one persistent launch (one workgroup a compute
         unit); raises when the shape or device has no persistent step."""
         check(library().gq8_decoder_set_persistent(self.handle, int(enabled)))
+
+    def set_sampling(self, options: SamplingOptions) -> None:
+        """Gemma::setSampling: how generate and decode choose each id (on the device)."""
+        c = options.as_c()
+        check(library().gq8_decoder_set_sampling(self.handle, ctypes.byref(c)))
 
     def set_fused(self, enabled: bool) -> None:
         """Choose the fused one-token kernels (default) or the unfused ones."""

@@ -135,6 +135,28 @@ int gq8_mqa_prefill(const float *queries, const uint16_t *key_cache,
 int gq8_geglu(const float *fused, int rows, int intermediate, float *out, uint8_t *q8,
               void *stream);
 
+/* SamplingOptions (Sampling/Sampler.h:33-51): temperature 0 is the argmax,
+ * top_k 0 and top_p 1 switch their cut off, seed seeds std::mt19937_64. */
+typedef struct gq8_sampling {
+    float temperature;
+    int top_k;
+    float top_p;
+    uint64_t seed;
+} gq8_sampling;
+
+/* Sampler::sample (Sampler.cpp:78-213) on the device: one token from one row
+ * of vocab fp32 logits (device), the mask (device, optional, nonzero =
+ * suppressed) applied first, scores logit / temperature in double, the top-k
+ * then top-p cuts over the ranking (score descending, token ascending), the
+ * softmax over what is left and the first candidate whose running mass
+ * passes `uniform` (in [0, 1): one Sampler::uniform draw).  The id goes to
+ * *token (device).  Options are refused as SamplingError refuses them
+ * (Sampler.cpp:28-41): GQ8_ERR_ARGUMENT.  Synchronous. */
+size_t gq8_sample_workspace_bytes(int vocab);
+int gq8_sample_row(const float *logits, const float *mask, int vocab,
+                   const gq8_sampling *options, double uniform, uint32_t *token,
+                   void *workspace, size_t workspace_bytes, void *stream);
+
 /* ArgmaxPartial + ArgmaxFinal (Argmax.h:47-257): per row the first maximum
  * over unmasked entries (mask may be NULL; nonzero = suppressed), 0 if none. */
 size_t gq8_argmax_workspace_bytes(int rows, int length);
@@ -225,6 +247,16 @@ int gq8_decoder_set_flow(gq8_decoder *decoder, int enabled);
  * the per-kernel dispatch of Decoder::step (Decoder.cpp:644-706) for
  * one-token steps.  GQ8_ERR_SHAPE when the shape or device has none. */
 int gq8_decoder_set_persistent(gq8_decoder *decoder, int enabled);
+/* Gemma::setSampling (Generation/Gemma.cpp:198-202): how gq8_generate and
+ * gq8_decoder_decode choose each id.  Temperature 0 (the default) is the
+ * argmax; above it, each id is drawn on the device (gq8_sample_row's rule)
+ * and written to its sequence slot, so no logits come back to the host
+ * (Gemma::generateBySampling, Gemma.cpp:546-595, reads them back).  Every
+ * sequence draws from the seed afresh (Gemma.cpp:549), one draw a sampled
+ * token.  The one-launch steps (set_flow, set_persistent) choose by argmax
+ * only and stand aside while a temperature is set.  GQ8_ERR_ARGUMENT as
+ * SamplingError. */
+int gq8_decoder_set_sampling(gq8_decoder *decoder, const gq8_sampling *options);
 /* Decoder::hiddenStates (Decoder.h:119-121): the last step's rows after the
  * final norm, [rows, width] fp32, copied to the host. */
 int gq8_decoder_hidden(gq8_decoder *decoder, float *host_out, int rows);
