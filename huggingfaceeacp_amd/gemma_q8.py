@@ -180,6 +180,18 @@ def library() -> ctypes.CDLL:
         "gq8_sample_workspace_bytes": (sz, [i32]),
         "gq8_sample_row": (i32, [P, P, i32, P, f64, P, P, sz, P]),
         "gq8_decoder_set_sampling": (i32, [P, P]),
+        "gq8_tokenizer_from_json": (i32, [ctypes.c_char_p, sz, ctypes.POINTER(P)]),
+        "gq8_tokenizer_open": (i32, [ctypes.c_char_p, ctypes.POINTER(P)]),
+        "gq8_tokenizer_destroy": (None, [P]),
+        "gq8_tokenizer_encode": (i32, [P, ctypes.c_char_p, sz, i32, P, i32]),
+        "gq8_tokenizer_decode": (i32, [P, P, i32, i32, P, sz, ctypes.POINTER(sz)]),
+        "gq8_tokenizer_vocabulary_size": (i32, [P]),
+        "gq8_tokenizer_specials": (i32, [P, P]),
+        "gq8_tokenizer_is_special": (i32, [P, i32]),
+        "gq8_tokenizer_token_text": (i32, [P, i32, P, sz, ctypes.POINTER(sz)]),
+        "gq8_tokenizer_token_for_text": (ctypes.c_int32, [P, ctypes.c_char_p, sz]),
+        "gq8_tokenizer_metaspace": (i32, [P, P, sz, ctypes.POINTER(sz), ctypes.POINTER(i32),
+                                          ctypes.POINTER(i32)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -709,3 +721,147 @@ def algorithmic_batch_step_bytes(shape: DecoderShape, attended_lengths) -> int:
 
 def log2ceil(n: int) -> int:
     return int(math.ceil(math.log2(n))) if n > 1 else 0
+
+
+# ---- the tokenizer ----------------------------------------------------------------
+class _SpecialTokens(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_int32) for name in
+                ("pad", "eos", "bos", "unk", "start_of_turn", "end_of_turn")]
+
+
+@dataclass(frozen=True)
+class SpecialTokens:
+    """SpecialTokens (Tokenizer/SpecialTokens.h:16-24); -1 where the file has none."""
+    pad: int
+    eos: int
+    bos: int
+    unk: int
+    start_of_turn: int
+    end_of_turn: int
+
+
+@dataclass(frozen=True)
+class Metaspace:
+    replacement: str
+    prepends_dummy_prefix: bool
+    splits_before_replacement: bool
+
+
+INVALID_TOKEN = -1
+
+
+class Tokenizer:
+    """HF::Tokenizer (Tokenizer/Tokenizer.h:35-124) over libgemma_q8: Gemma's
+    SentencePiece BPE read from tokenizer.json.  Text is UTF-8 (str or bytes)."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    @staticmethod
+    def from_json_text(text) -> "Tokenizer":
+        raw = text.encode() if isinstance(text, str) else bytes(text)
+        handle = ctypes.c_void_p()
+        check(library().gq8_tokenizer_from_json(raw, len(raw), ctypes.byref(handle)))
+        return Tokenizer(handle)
+
+    @staticmethod
+    def from_file(path) -> "Tokenizer":
+        handle = ctypes.c_void_p()
+        check(library().gq8_tokenizer_open(os.fsencode(path), ctypes.byref(handle)))
+        return Tokenizer(handle)
+
+    def close(self) -> None:
+        if self.handle:
+            library().gq8_tokenizer_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _encode(self, text, with_bos) -> list[int]:
+        raw = text.encode() if isinstance(text, str) else bytes(text)
+        capacity = len(raw) + 2
+        out = (ctypes.c_int32 * capacity)()
+        count = check(library().gq8_tokenizer_encode(self.handle, raw, len(raw), int(with_bos),
+                                                     out, capacity))
+        if count > capacity:
+            out = (ctypes.c_int32 * count)()
+            check(library().gq8_tokenizer_encode(self.handle, raw, len(raw), int(with_bos), out,
+                                                 count))
+        return list(out[:count])
+
+    def encode(self, text) -> list[int]:
+        return self._encode(text, False)
+
+    def encode_with_bos(self, text) -> list[int]:
+        return self._encode(text, True)
+
+    def _decode(self, tokens, keep_special) -> bytes:
+        ids = (ctypes.c_int32 * max(1, len(tokens)))(*[int(t) for t in tokens])
+        length = ctypes.c_size_t()
+        check(library().gq8_tokenizer_decode(self.handle, ids, len(tokens), int(keep_special),
+                                             None, 0, ctypes.byref(length)))
+        out = ctypes.create_string_buffer(max(1, length.value))
+        check(library().gq8_tokenizer_decode(self.handle, ids, len(tokens), int(keep_special), out,
+                                             length.value, ctypes.byref(length)))
+        return out.raw[:length.value]
+
+    def decode_bytes(self, tokens) -> bytes:
+        return self._decode(tokens, False)
+
+    def decode(self, tokens) -> str:
+        return self._decode(tokens, False).decode("utf-8")
+
+    def decode_keeping_special_tokens(self, tokens) -> str:
+        return self._decode(tokens, True).decode("utf-8")
+
+    def vocabulary_size(self) -> int:
+        return check(library().gq8_tokenizer_vocabulary_size(self.handle))
+
+    def specials(self) -> SpecialTokens:
+        s = _SpecialTokens()
+        check(library().gq8_tokenizer_specials(self.handle, ctypes.byref(s)))
+        return SpecialTokens(s.pad, s.eos, s.bos, s.unk, s.start_of_turn, s.end_of_turn)
+
+    @property
+    def bos(self) -> int:
+        return self.specials().bos
+
+    @property
+    def eos(self) -> int:
+        return self.specials().eos
+
+    @property
+    def pad(self) -> int:
+        return self.specials().pad
+
+    @property
+    def unk(self) -> int:
+        return self.specials().unk
+
+    def is_special(self, token: int) -> bool:
+        return bool(library().gq8_tokenizer_is_special(self.handle, int(token)))
+
+    def text_for_token(self, token: int) -> str:
+        length = ctypes.c_size_t()
+        check(library().gq8_tokenizer_token_text(self.handle, int(token), None, 0,
+                                                 ctypes.byref(length)))
+        out = ctypes.create_string_buffer(max(1, length.value))
+        check(library().gq8_tokenizer_token_text(self.handle, int(token), out, length.value,
+                                                 ctypes.byref(length)))
+        return out.raw[:length.value].decode("utf-8", errors="surrogateescape")
+
+    def token_for_text(self, text) -> int:
+        raw = text.encode() if isinstance(text, str) else bytes(text)
+        return int(library().gq8_tokenizer_token_for_text(self.handle, raw, len(raw)))
+
+    def metaspace(self) -> Metaspace:
+        length, prepends, splits = ctypes.c_size_t(), ctypes.c_int(), ctypes.c_int()
+        out = ctypes.create_string_buffer(64)
+        check(library().gq8_tokenizer_metaspace(self.handle, out, 64, ctypes.byref(length),
+                                                ctypes.byref(prepends), ctypes.byref(splits)))
+        return Metaspace(out.raw[:length.value].decode("utf-8"), bool(prepends.value),
+                         bool(splits.value))

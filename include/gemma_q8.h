@@ -406,6 +406,45 @@ int gq8_batch_tokens(gq8_batch *batch, int sequence, int first, int count, int32
 /* The last lockstep step's logits, [S, vocab] fp32, copied to the host. */
 int gq8_batch_logits(gq8_batch *batch, float *host_out);
 
+/* ======================================================================= */
+/* Tokenizer: Gemma's SentencePiece BPE from tokenizer.json, on the host    */
+/* (Tokenizer/Tokenizer.h:35-124; Metaspace.h; ByteFallback.h).             */
+/* ======================================================================= */
+typedef struct gq8_tokenizer gq8_tokenizer;
+/* SpecialTokens (Tokenizer/SpecialTokens.h:16-24): -1 where the file has none. */
+typedef struct gq8_special_tokens {
+    int32_t pad, eos, bos, unk, start_of_turn, end_of_turn;
+} gq8_special_tokens;
+/* Tokenizer::fromJsonText / fromFile (Tokenizer.cpp:206-301): GQ8_ERR_FORMAT
+ * for malformed JSON, a missing model.vocab or model.merges, or a bad merge
+ * rule, with the reason in gq8_last_error. */
+int gq8_tokenizer_from_json(const char *text, size_t length, gq8_tokenizer **out);
+int gq8_tokenizer_open(const char *path, gq8_tokenizer **out);
+void gq8_tokenizer_destroy(gq8_tokenizer *tokenizer);
+/* Tokenizer::encode / encodeWithBos (Tokenizer.cpp:565-609) of `length`
+ * bytes of text: returns the number of ids (or a negative status) and writes
+ * the first min(count, capacity) of them. */
+int gq8_tokenizer_encode(const gq8_tokenizer *tokenizer, const char *text, size_t length,
+                         int with_bos, int32_t *out, int capacity);
+/* Tokenizer::decode / decodeKeepingSpecialTokens (Tokenizer.cpp:611-683):
+ * *length receives the text's byte length; the first min(length, capacity)
+ * bytes go to out (no terminator).  Ids outside the vocabulary are skipped. */
+int gq8_tokenizer_decode(const gq8_tokenizer *tokenizer, const int32_t *tokens, int count,
+                         int keep_special, char *out, size_t capacity, size_t *length);
+int gq8_tokenizer_vocabulary_size(const gq8_tokenizer *tokenizer);
+int gq8_tokenizer_specials(const gq8_tokenizer *tokenizer, gq8_special_tokens *out);
+int gq8_tokenizer_is_special(const gq8_tokenizer *tokenizer, int32_t token);
+/* Tokenizer::textForToken: the piece as the vocabulary spells it (empty
+ * outside the vocabulary); tokenForText: the id of a piece, or -1. */
+int gq8_tokenizer_token_text(const gq8_tokenizer *tokenizer, int32_t token, char *out,
+                             size_t capacity, size_t *length);
+int32_t gq8_tokenizer_token_for_text(const gq8_tokenizer *tokenizer, const char *text,
+                                     size_t length);
+/* Tokenizer::metaspace (Metaspace.h:14-45): the replacement for a space, the
+ * dummy prefix and the per-word split, as read from the file. */
+int gq8_tokenizer_metaspace(const gq8_tokenizer *tokenizer, char *replacement, size_t capacity,
+                            size_t *length, int *prepends, int *splits);
+
 #ifdef __cplusplus
 }
 #endif
