@@ -13,6 +13,8 @@ namespace gq8 {
 
 // Records a failure as the C ABI's last error and returns the status.
 int report(int status, const std::string &message);
+// SamplingError's rules (Sampling/Sampler.cpp:28-41): GQ8_OK or GQ8_ERR_ARGUMENT.
+int check_sampling(const struct gq8_sampling &options);
 
 // The safetensors dtype tags (Model/TensorType.h:12-27), in that order.
 enum Dtype {

@@ -156,6 +156,11 @@ int gq8::report(int status, const std::string &message)
     return fail(status, message);
 }
 
+int gq8::check_sampling(const gq8_sampling &options)
+{
+    return sampling_error(options);
+}
+
 extern "C" const char *gq8_status_string(int status)
 {
     switch (status) {
@@ -1917,6 +1922,15 @@ extern "C" int gq8_generate(gq8_decoder *d, const int32_t *prompt, int prompt_le
                             int max_tokens, int eos, int use_graph, int32_t *out,
                             gq8_run_stats *stats)
 {
+    return gq8_generate_streaming(d, prompt, prompt_length, max_tokens, eos, use_graph, out,
+                                  stats, nullptr, nullptr);
+}
+
+extern "C" int gq8_generate_streaming(gq8_decoder *d, const int32_t *prompt, int prompt_length,
+                                      int max_tokens, int eos, int use_graph, int32_t *out,
+                                      gq8_run_stats *stats, gq8_token_callback on_token,
+                                      void *user)
+{
     using Clock = std::chrono::steady_clock;
     if (!d || !prompt || !out)
         return fail(GQ8_ERR_ARGUMENT, "generate: null argument");
@@ -1977,8 +1991,11 @@ extern "C" int gq8_generate(gq8_decoder *d, const int32_t *prompt, int prompt_le
         std::vector<uint32_t> ids(limit);
         GQ8_HIP(hipMemcpy(ids.data(), d->sequence + prompt_length, limit * sizeof(uint32_t),
                           hipMemcpyDeviceToHost));
-        for (int i = 0; i < limit; ++i)
+        for (int i = 0; i < limit; ++i) {
             out[i] = (int32_t) ids[i];
+            if (on_token)
+                on_token(out[i], user);
+        }
         count = limit;
     } else if (limit > 0) {
         // Gemma::generateGreedily (Gemma.cpp:459-543): two steps in flight;
@@ -2022,6 +2039,8 @@ extern "C" int gq8_generate(gq8_decoder *d, const int32_t *prompt, int prompt_le
             if ((int) token == eos)
                 break;
             out[count++] = (int32_t) token;
+            if (on_token)
+                on_token((int32_t) token, user);
             if (nextStep < limit) {
                 if (int st = startStep(nextStep))
                     return finish(st);

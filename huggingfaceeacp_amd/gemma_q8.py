@@ -92,6 +92,9 @@ class _RunStats(ctypes.Structure):
 
 _lib = None
 
+# gq8_token_callback: void (*)(int32_t token, void *user)
+TOKEN_CALLBACK = ctypes.CFUNCTYPE(None, ctypes.c_int32, ctypes.c_void_p)
+
 
 def library() -> ctypes.CDLL:
     """Load libgemma_q8.so (built in-tree); raise if it is not there."""
@@ -192,6 +195,31 @@ def library() -> ctypes.CDLL:
         "gq8_tokenizer_token_for_text": (ctypes.c_int32, [P, ctypes.c_char_p, sz]),
         "gq8_tokenizer_metaspace": (i32, [P, P, sz, ctypes.POINTER(sz), ctypes.POINTER(i32),
                                           ctypes.POINTER(i32)]),
+        "gq8_generate_streaming": (i32, [P, P, i32, i32, i32, i32, P, ctypes.POINTER(_RunStats),
+                                         TOKEN_CALLBACK, P]),
+        "gq8_gemma_create": (i32, [ctypes.POINTER(P)]),
+        "gq8_gemma_destroy": (None, [P]),
+        "gq8_gemma_load": (i32, [P, ctypes.c_char_p]),
+        "gq8_gemma_directory_from_environment": (i32, [P, sz, ctypes.POINTER(sz)]),
+        "gq8_gemma_is_loaded": (i32, [P]),
+        "gq8_gemma_is_prepared": (i32, [P]),
+        "gq8_gemma_file": (i32, [P, i32, i32, P, sz, ctypes.POINTER(sz)]),
+        "gq8_gemma_shard_count": (i32, [P]),
+        "gq8_gemma_config": (i32, [P, ctypes.POINTER(_Shape), ctypes.POINTER(_TokenIds)]),
+        "gq8_gemma_set_maximum_tokens": (i32, [P, i32]),
+        "gq8_gemma_maximum_tokens": (i32, [P]),
+        "gq8_gemma_set_prompt_capacity": (i32, [P, i32]),
+        "gq8_gemma_prompt_capacity": (i32, [P]),
+        "gq8_gemma_set_sampling": (i32, [P, P]),
+        "gq8_gemma_set_on_token": (i32, [P, TOKEN_CALLBACK, P]),
+        "gq8_gemma_prepare": (i32, [P]),
+        "gq8_gemma_decoder": (P, [P]),
+        "gq8_gemma_tokenizer": (P, [P]),
+        "gq8_gemma_generate": (i32, [P, P, i32, P, i32]),
+        "gq8_gemma_generate_from_text": (i32, [P, ctypes.c_char_p, sz, P, i32]),
+        "gq8_gemma_generate_text": (i32, [P, ctypes.c_char_p, sz, P, sz, ctypes.POINTER(sz)]),
+        "gq8_gemma_text_for_tokens": (i32, [P, P, i32, P, sz, ctypes.POINTER(sz)]),
+        "gq8_gemma_last_stats": (i32, [P, ctypes.POINTER(_RunStats)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -865,3 +893,156 @@ class Tokenizer:
                                                 ctypes.byref(prepends), ctypes.byref(splits)))
         return Metaspace(out.raw[:length.value].decode("utf-8"), bool(prepends.value),
                          bool(splits.value))
+
+
+# ModelFiles' files (Model/ModelFiles.h:13-27), in the C ABI's order
+FILE_CONFIG, FILE_GENERATION_CONFIG, FILE_SHARD_INDEX, FILE_TOKENIZER_JSON, FILE_TOKENIZER_MODEL, \
+    FILE_GGUF, FILE_SHARD = range(7)
+
+
+def model_directory_from_environment() -> str:
+    """ModelFiles::directoryFromEnvironment: GEMMA_MODEL_DIR, or "" when unset."""
+    length = ctypes.c_size_t()
+    check(library().gq8_gemma_directory_from_environment(None, 0, ctypes.byref(length)))
+    out = ctypes.create_string_buffer(max(1, length.value))
+    check(library().gq8_gemma_directory_from_environment(out, length.value, ctypes.byref(length)))
+    return os.fsdecode(out.raw[:length.value])
+
+
+class Gemma:
+    """HF::Gemma (Generation/Gemma.h:65-251) over libgemma_q8: a Hugging Face
+    Gemma directory loaded on the host, prepared on the device, and generated
+    from by ids or by text.  ``on_token`` is called once per generated id."""
+
+    def __init__(self):
+        handle = ctypes.c_void_p()
+        check(library().gq8_gemma_create(ctypes.byref(handle)))
+        self.handle = handle
+        self._callback = None
+        self._on_token = None
+
+    def close(self) -> None:
+        if self.handle:
+            library().gq8_gemma_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def load(self, model_directory) -> None:
+        check(library().gq8_gemma_load(self.handle, os.fsencode(model_directory)))
+
+    def is_loaded(self) -> bool:
+        return bool(library().gq8_gemma_is_loaded(self.handle))
+
+    def is_prepared(self) -> bool:
+        return bool(library().gq8_gemma_is_prepared(self.handle))
+
+    def file(self, which: int, index: int = 0) -> str:
+        """A located file's path, "" when the directory does not hold it."""
+        length = ctypes.c_size_t()
+        check(library().gq8_gemma_file(self.handle, which, index, None, 0, ctypes.byref(length)))
+        out = ctypes.create_string_buffer(max(1, length.value))
+        check(library().gq8_gemma_file(self.handle, which, index, out, length.value,
+                                       ctypes.byref(length)))
+        return os.fsdecode(out.raw[:length.value])
+
+    def shards(self) -> list[str]:
+        count = check(library().gq8_gemma_shard_count(self.handle))
+        return [self.file(FILE_SHARD, i) for i in range(count)]
+
+    def config(self):
+        """(DecoderShape, (bos, eos, pad)) of the loaded config.json with
+        generation_config.json applied."""
+        c = _Shape()
+        ids = _TokenIds()
+        check(library().gq8_gemma_config(self.handle, ctypes.byref(c), ctypes.byref(ids)))
+        shape = DecoderShape(c.width, c.heads, c.kv_heads, c.head_dim, c.layers, c.intermediate,
+                             c.vocab, c.max_positions, c.max_step_rows, c.rms_epsilon,
+                             c.rope_theta, c.embedding_scale)
+        return shape, (ids.bos, ids.eos, ids.pad)
+
+    @property
+    def maximum_tokens(self) -> int:
+        return check(library().gq8_gemma_maximum_tokens(self.handle))
+
+    @maximum_tokens.setter
+    def maximum_tokens(self, count: int) -> None:
+        check(library().gq8_gemma_set_maximum_tokens(self.handle, int(count)))
+
+    @property
+    def prompt_capacity(self) -> int:
+        return check(library().gq8_gemma_prompt_capacity(self.handle))
+
+    @prompt_capacity.setter
+    def prompt_capacity(self, rows: int) -> None:
+        check(library().gq8_gemma_set_prompt_capacity(self.handle, int(rows)))
+
+    def set_sampling(self, options: SamplingOptions) -> None:
+        c = options.as_c()
+        check(library().gq8_gemma_set_sampling(self.handle, ctypes.byref(c)))
+
+    @property
+    def on_token(self):
+        return self._on_token
+
+    @on_token.setter
+    def on_token(self, fn) -> None:
+        self._on_token = fn
+        self._callback = TOKEN_CALLBACK(lambda token, user: fn(int(token))) if fn else None
+        check(library().gq8_gemma_set_on_token(self.handle, self._callback or TOKEN_CALLBACK(),
+                                               None))
+
+    def prepare(self) -> None:
+        check(library().gq8_gemma_prepare(self.handle))
+
+    def _window_cap(self, prompt_length: int) -> int:
+        shape, _ = self.config()
+        window = shape.max_positions - prompt_length
+        limit = self.maximum_tokens
+        return max(1, min(limit, window) if limit > 0 else window)
+
+    def generate(self, prompt) -> list[int]:
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        cap = self._window_cap(prompt.size)
+        out = np.zeros(cap, dtype=np.int32)
+        count = check(library().gq8_gemma_generate(self.handle, _host(prompt), prompt.size,
+                                                   _host(out), cap))
+        return [int(t) for t in out[:count]]
+
+    def generate_from_text(self, text) -> list[int]:
+        raw = text.encode() if isinstance(text, str) else bytes(text)
+        cap = self._window_cap(1)
+        out = np.zeros(cap, dtype=np.int32)
+        count = check(library().gq8_gemma_generate_from_text(self.handle, raw, len(raw),
+                                                             _host(out), cap))
+        return [int(t) for t in out[:min(count, cap)]]
+
+    def generate_text(self, text) -> str:
+        raw = text.encode() if isinstance(text, str) else bytes(text)
+        capacity = 1 << 16
+        out = ctypes.create_string_buffer(capacity)
+        length = ctypes.c_size_t()
+        check(library().gq8_gemma_generate_text(self.handle, raw, len(raw), out, capacity,
+                                                ctypes.byref(length)))
+        if length.value > capacity:
+            raise Gq8Error(ERR_ARGUMENT, "generate_text: text longer than the buffer")
+        return out.raw[:length.value].decode("utf-8")
+
+    def text_for_tokens(self, tokens) -> str:
+        ids = (ctypes.c_int32 * max(1, len(tokens)))(*[int(t) for t in tokens])
+        length = ctypes.c_size_t()
+        check(library().gq8_gemma_text_for_tokens(self.handle, ids, len(tokens), None, 0,
+                                                  ctypes.byref(length)))
+        out = ctypes.create_string_buffer(max(1, length.value))
+        check(library().gq8_gemma_text_for_tokens(self.handle, ids, len(tokens), out,
+                                                  length.value, ctypes.byref(length)))
+        return out.raw[:length.value].decode("utf-8")
+
+    def last_stats(self) -> RunStats:
+        st = _RunStats()
+        check(library().gq8_gemma_last_stats(self.handle, ctypes.byref(st)))
+        return RunStats(st.prefill_seconds, st.decode_seconds, st.step_count, st.generated)

@@ -288,6 +288,16 @@ typedef struct gq8_run_stats {
  * limit token ids; returns the count (>= 0) or a negative status. */
 int gq8_generate(gq8_decoder *decoder, const int32_t *prompt, int prompt_length,
                  int max_tokens, int eos, int use_graph, int32_t *out, gq8_run_stats *stats);
+/* Gemma::onToken (Generation/Gemma.h:179-183): called once a generated id is
+ * known, in order, on the thread that runs the loop (an EOS that stops the
+ * run is not passed). */
+typedef void (*gq8_token_callback)(int32_t token, void *user);
+/* gq8_generate with the callback (NULL: none).  With eos >= 0 each id is
+ * passed as it is read back, while the step after it runs; with eos < 0 the
+ * steps are enqueued back to back and the ids are passed once the run ends. */
+int gq8_generate_streaming(gq8_decoder *decoder, const int32_t *prompt, int prompt_length,
+                           int max_tokens, int eos, int use_graph, int32_t *out,
+                           gq8_run_stats *stats, gq8_token_callback on_token, void *user);
 
 /* Continue the greedy loop `steps` tokens from the current position: each
  * step embeds the id in the slot at the position, runs the decoder and writes
@@ -444,6 +454,86 @@ int32_t gq8_tokenizer_token_for_text(const gq8_tokenizer *tokenizer, const char 
  * dummy prefix and the per-word split, as read from the file. */
 int gq8_tokenizer_metaspace(const gq8_tokenizer *tokenizer, char *replacement, size_t capacity,
                             size_t *length, int *prepends, int *splits);
+
+/* ======================================================================= */
+/* Model directory runtime: HF::Gemma (Generation/Gemma.h:65-251) over a    */
+/* Hugging Face Gemma directory (Model/ModelFiles.h:11-66).                 */
+/* ======================================================================= */
+typedef struct gq8_gemma gq8_gemma;
+/* ModelFiles' files (ModelFileNames, ModelFiles.h:13-27) */
+enum {
+    GQ8_FILE_CONFIG, GQ8_FILE_GENERATION_CONFIG, GQ8_FILE_SHARD_INDEX, GQ8_FILE_TOKENIZER_JSON,
+    GQ8_FILE_TOKENIZER_MODEL, GQ8_FILE_GGUF, GQ8_FILE_SHARD
+};
+int gq8_gemma_create(gq8_gemma **out);
+void gq8_gemma_destroy(gq8_gemma *gemma);
+/* Gemma::load(modelDirectory) (Gemma.cpp:64-84): ModelFiles::fromDirectory
+ * (config.json required; model.safetensors.index.json naming its shards by
+ * plain file name, else model.safetensors, required; generation_config.json,
+ * tokenizer.json, tokenizer.model and gemma-2b.gguf recorded when present,
+ * ModelFiles.cpp:77-99), GemmaConfig::fromModelFiles (generation_config.json's
+ * bos / eos / pad over config.json's, GemmaConfig.cpp:204-223), the tokenizer
+ * (required, and no larger than the config's vocabulary, Gemma.cpp:120-139)
+ * and every shard mapped.  The maximum token count returns to 0 and a
+ * prepared decoder is dropped.  GQ8_ERR_FORMAT names the file at fault.
+ * Host only. */
+int gq8_gemma_load(gq8_gemma *gemma, const char *model_directory);
+/* ModelFiles::directoryFromEnvironment (ModelFiles.cpp:100-106): the
+ * GEMMA_MODEL_DIR variable, empty when unset.  *length gets its byte length;
+ * up to capacity bytes go to out (no terminator). */
+int gq8_gemma_directory_from_environment(char *out, size_t capacity, size_t *length);
+int gq8_gemma_is_loaded(const gq8_gemma *gemma);
+int gq8_gemma_is_prepared(const gq8_gemma *gemma);
+/* A located file's path (which = GQ8_FILE_*, index selects the shard):
+ * *length is 0 for a file the directory does not hold. */
+int gq8_gemma_file(const gq8_gemma *gemma, int which, int index, char *out, size_t capacity,
+                   size_t *length);
+int gq8_gemma_shard_count(const gq8_gemma *gemma);
+/* GemmaConfig's shape and token ids after load (config.json with
+ * generation_config.json applied). */
+int gq8_gemma_config(const gq8_gemma *gemma, gq8_shape *shape, gq8_token_ids *tokens);
+/* Gemma::setMaximumTokens / setPromptCapacity (Gemma.cpp:164-179): a
+ * negative count or a capacity below one row is GQ8_ERR_ARGUMENT.  The
+ * capacity is taken at prepare. */
+int gq8_gemma_set_maximum_tokens(gq8_gemma *gemma, int count);
+int gq8_gemma_maximum_tokens(const gq8_gemma *gemma);
+int gq8_gemma_set_prompt_capacity(gq8_gemma *gemma, int rows);
+int gq8_gemma_prompt_capacity(const gq8_gemma *gemma);
+/* Gemma::setSampling (Gemma.cpp:195-202); validated as SamplingError does. */
+int gq8_gemma_set_sampling(gq8_gemma *gemma, const gq8_sampling *options);
+/* Gemma::onToken: NULL restores the no-op. */
+int gq8_gemma_set_on_token(gq8_gemma *gemma, gq8_token_callback on_token, void *user);
+/* Gemma::prepare (Gemma.cpp:207-243): the decoder of shape
+ * DecoderShape::fromConfig with maxStepRows = min(prompt capacity, window),
+ * its weights read from the shards by checkpoint name and quantized to
+ * Int8Blocks on the device, and the sampling options.  GQ8_ERR_NOT_PREPARED
+ * before load. */
+int gq8_gemma_prepare(gq8_gemma *gemma);
+/* The prepared decoder (NULL before prepare), for the op-level calls. */
+gq8_decoder *gq8_gemma_decoder(gq8_gemma *gemma);
+/* The loaded tokenizer (NULL before load). */
+const gq8_tokenizer *gq8_gemma_tokenizer(const gq8_gemma *gemma);
+/* Gemma::generate (Gemma.cpp:402-457): the generated ids with the EOS
+ * excluded, up to min(maximum tokens or the window, max_positions - prompt
+ * length), stopping at the config's eos.  Returns the count (or a negative
+ * status); the first min(count, capacity) ids go to out.  Refusals as
+ * gq8_generate's; GQ8_ERR_NOT_PREPARED before prepare. */
+int gq8_gemma_generate(gq8_gemma *gemma, const int32_t *prompt, int prompt_length, int32_t *out,
+                       int capacity);
+/* Gemma::generateFromText (Gemma.cpp:596-603): the text encoded with the
+ * BOS in front, then generate. */
+int gq8_gemma_generate_from_text(gq8_gemma *gemma, const char *text, size_t length, int32_t *out,
+                                 int capacity);
+/* Gemma::generateText (Gemma.cpp:605-609): generateFromText decoded back
+ * with the special tokens dropped.  *length gets the text's byte length; up
+ * to capacity bytes go to out. */
+int gq8_gemma_generate_text(gq8_gemma *gemma, const char *text, size_t length, char *out,
+                            size_t capacity, size_t *out_length);
+/* Gemma::textForTokens (Gemma.cpp:611-615): after load. */
+int gq8_gemma_text_for_tokens(const gq8_gemma *gemma, const int32_t *tokens, int count, char *out,
+                              size_t capacity, size_t *length);
+/* lastPrefillSeconds / lastDecodeSeconds / lastStepCount of the last run. */
+int gq8_gemma_last_stats(const gq8_gemma *gemma, gq8_run_stats *stats);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,153 @@
+"""The model-directory runtime on the device: HF::Gemma::prepare / generate /
+generateFromText / generateText (Generation/Gemma.cpp:207-243, 402-457,
+596-615) over a small Gemma directory (two BF16 shards behind an index,
+config.json, generation_config.json, the reference's MiniTokenizer.json).
+
+The ids must be the oracle's greedy ids over the same widened weights, cut at
+generation_config's EOS (excluded) and at the token limit; onToken sees every
+returned id in order; generateText is the tokenizer's decode of the ids.
+"""
+import json
+import shutil
+
+import numpy as np
+import pytest
+
+import oracle as O
+from huggingfaceeacp_amd import gemma_q8 as G
+from test_gemma_runtime import GOLDEN_TOKENIZER, config_for
+from test_gpu_checkpoint import small_checkpoint
+from test_gpu_decoder import to_oracle_shape
+from test_gpu_persist import persist_shape
+
+pytestmark = pytest.mark.gpu
+
+WINDOW = 64
+
+
+def varied_weights(shape):
+    """N(0, sigma): embedding 0.1, norms 1.0, projections 4/sqrt(fan in).  With
+    these spreads the small model's greedy ids vary from step to step (with
+    the reference test's spreads a tied embedding this small repeats the
+    prompt's last id)."""
+    tensors = []
+    for i in range(shape.tensor_count()):
+        if i == 0:
+            sigma = 0.1
+        elif shape.tensor_is_norm(i):
+            sigma = 1.0
+        else:
+            role = (i - 1) % G.PER_LAYER
+            fan_in = {G.T_O: shape.query_width, G.T_DOWN: shape.intermediate}.get(role, shape.width)
+            sigma = 4.0 / np.sqrt(fan_in)
+        tensors.append(O.normal_fill(0x9100 + i, sigma, shape.tensor_elements(i)))
+    return tensors
+
+
+def write_directory(root, shape, eos):
+    root.mkdir(parents=True, exist_ok=True)
+    paths, widened = small_checkpoint(root, shape, varied_weights(shape))
+    weight_map = {}
+    for path in paths:
+        weight_map.update({name: path.name for name in G.SafeTensors.open(path).names()})
+    (root / "model.safetensors.index.json").write_text(json.dumps({"weight_map": weight_map}))
+    (root / "config.json").write_text(json.dumps(config_for(shape, max_position_embeddings=WINDOW)))
+    (root / "generation_config.json").write_text(json.dumps({"eos_token_id": eos}))
+    shutil.copy(GOLDEN_TOKENIZER, root / "tokenizer.json")
+    return widened
+
+
+def oracle_ids(shape, widened, prompt, count):
+    model = O.Model(to_oracle_shape(shape), O.MODE_Q8)
+    for i, values in enumerate(widened):
+        assert model.set_tensor(i, values) == 0
+    _, ids, _ = model.generate(np.asarray(prompt, dtype=np.int32), count, eos=-1)
+    return [int(t) for t in ids]
+
+
+def cut_at(ids, eos):
+    return ids[:ids.index(eos)] if eos in ids else ids
+
+
+def test_gemma_directory_generates_the_oracle_ids(torch_cuda, tmp_path):
+    shape = persist_shape(max_positions=WINDOW)
+    prompt = [2, 5, 41, 3, 17, 28, 9, 60]
+    # the oracle's run without a stop picks the EOS: its sixth id, where the
+    # five before it differ from it
+    probe_root = tmp_path / "probe"
+    widened = write_directory(probe_root, shape, eos=-1)
+    free = oracle_ids(shape, widened, prompt, WINDOW - len(prompt))
+    k = next(i for i in range(5, len(free)) if free[i] not in free[:i])
+    eos = free[k]
+
+    root = tmp_path / "model"
+    write_directory(root, shape, eos=[eos, 107])
+    gemma = G.Gemma()
+    gemma.load(root)
+    assert gemma.config()[1][1] == eos
+    seen = []
+    gemma.on_token = seen.append
+    gemma.prompt_capacity = 4  # the prompt prefills in two blocks
+    gemma.prepare()
+    assert gemma.is_prepared()
+
+    ids = gemma.generate(prompt)
+    print(f"gemma runtime: eos {eos} at step {k}, ids {ids}")
+    assert ids == free[:k]
+    assert seen == ids
+    stats = gemma.last_stats()
+    assert stats.generated == len(ids) and stats.step_count >= 2
+
+    # the token limit
+    gemma.maximum_tokens = 3
+    seen.clear()
+    assert gemma.generate(prompt) == free[:3]
+    assert seen == free[:3]
+    gemma.maximum_tokens = 0
+
+    # the window: a full prompt leaves no room, a longer one is refused
+    assert gemma.generate(list(range(3, 3 + WINDOW))) == []
+    with pytest.raises(G.Gq8Error) as e:
+        gemma.generate(list(range(3, 4 + WINDOW)))
+    assert e.value.status == G.ERR_WINDOW
+    with pytest.raises(G.Gq8Error) as e:
+        gemma.generate([2, shape.vocab])
+    assert e.value.status == G.ERR_TOKEN
+    with pytest.raises(G.Gq8Error) as e:
+        gemma.generate([])
+    assert e.value.status == G.ERR_EMPTY
+
+    # text in: the BOS in front (Tokenizer::encodeWithBos), text out: decoded
+    tokenizer = G.Tokenizer.from_file(root / "tokenizer.json")
+    text = "hello world"
+    text_prompt = tokenizer.encode_with_bos(text)
+    expected = cut_at(oracle_ids(shape, widened, text_prompt, WINDOW - len(text_prompt)), eos)
+    gemma.on_token = None
+    assert gemma.generate_from_text(text) == expected
+    assert gemma.generate_text(text) == tokenizer.decode(expected)
+    assert gemma.text_for_tokens(expected) == tokenizer.decode(expected)
+
+
+def test_gemma_directory_sampling_matches_the_decoder(torch_cuda, tmp_path):
+    shape = persist_shape(max_positions=WINDOW)
+    root = tmp_path / "model"
+    widened = write_directory(root, shape, eos=-1)
+    options = G.SamplingOptions(temperature=0.8, top_k=40, top_p=0.9, seed=1234)
+    gemma = G.Gemma()
+    gemma.load(root)
+    gemma.set_sampling(options)
+    gemma.maximum_tokens = 12
+    gemma.prepare()
+    prompt = [2, 5, 41, 3, 17]
+    first = gemma.generate(prompt)
+    again = gemma.generate(prompt)  # every run reseeds (Gemma.cpp:549)
+    assert first == again and len(first) == 12
+
+    decoder = G.Decoder(G.DecoderShape(shape.width, shape.heads, shape.kv_heads, shape.head_dim,
+                                       shape.layers, shape.intermediate, shape.vocab, WINDOW,
+                                       min(512, WINDOW)))
+    for i, values in enumerate(widened):
+        decoder.load_tensor(i, values)
+    decoder.set_sampling(options)
+    ids, _ = decoder.generate(np.asarray(prompt, dtype=np.int32), 12, eos=-1)
+    assert first == [int(t) for t in ids]
