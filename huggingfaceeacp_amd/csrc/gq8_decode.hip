@@ -182,7 +182,7 @@ __device__ void norm_q8_finish(const RowSlice<E> &r, int width, float epsilon, R
 // ---- q|k|v + RoPE + fp16 KV ---------------------------------------------------
 // A pair task is the two rows (i, i + half) of one head of q, k or v; a wave
 // owns kPairsPerWave of them.  Lane l owns block l of every row (width <= 2048).
-constexpr int kPairsPerWave = 2;
+constexpr int kPairsPerWave = 1;
 
 __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a)
 {
@@ -862,7 +862,8 @@ __global__ __launch_bounds__(64) void head_finalize_kernel(HeadArgs a)
 // arrivals, then a top count, then 16 flags that waiters spread their polls
 // over), which the finalize item waits on.
 constexpr int kFlowWaves = kFlowThreads / 64;
-constexpr int kFlowQkvPairs = kFlowWaves * kPairsPerWave;   // 16 pairs (32 rows) an item
+constexpr int kFlowPairsPerWave = 2;
+constexpr int kFlowQkvPairs = kFlowWaves * kFlowPairsPerWave;   // 16 pairs (32 rows) an item
 constexpr int kFlowORows = kFlowWaves * 2;                  // 16 rows an item
 constexpr int kFlowDownRows = kFlowWaves;                   // 8 rows an item
 constexpr int kFlowDownBlocks = 8;                          // blocks a lane (inner <= 16384)
@@ -1077,12 +1078,12 @@ __device__ __forceinline__ void flow_qkv(const FlowArgs &a, int l, int item, uin
     const int outputs = qWidth + 2 * kvWidth;
     const int pairs = (a.heads + 2 * a.kv_heads) * half;
     const int nb = a.width / kBlock;
-    const int firstPair = (item * kFlowWaves + wave) * kPairsPerWave;
+    const int firstPair = (item * kFlowWaves + wave) * kFlowPairsPerWave;
     const uint8_t *weights = a.qkv + a.qkv_stride * l;
 
-    WeightBlock lo[kPairsPerWave], hi[kPairsPerWave];
+    WeightBlock lo[kFlowPairsPerWave], hi[kFlowPairsPerWave];
 #pragma unroll
-    for (int p = 0; p < kPairsPerWave; ++p) {
+    for (int p = 0; p < kFlowPairsPerWave; ++p) {
         const int pair = firstPair + p;
         const int rowLo = (pair / half) * hd + pair % half;
         const bool valid = pair < pairs && lane < nb;
@@ -1105,10 +1106,10 @@ __device__ __forceinline__ void flow_qkv(const FlowArgs &a, int l, int item, uin
         a1 = reinterpret_cast<const int4 *>(row.q + lane * kBlock)[1];
         sa = row.scale[lane];
     }
-    constexpr int kRows = 2 * kPairsPerWave;
+    constexpr int kRows = 2 * kFlowPairsPerWave;
     double y[kRows];
 #pragma unroll
-    for (int p = 0; p < kPairsPerWave; ++p) {
+    for (int p = 0; p < kFlowPairsPerWave; ++p) {
         y[2 * p] = block_term(lo[p], a0, a1, sa);
         y[2 * p + 1] = block_term(hi[p], a0, a1, sa);
     }
