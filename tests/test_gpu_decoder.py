@@ -31,19 +31,23 @@ def to_oracle_shape(shape: G.DecoderShape):
 
 
 def small_weights(shape: G.DecoderShape):
-    """N(0, sigma) per tensor with the reference test's spreads: embedding 0.2,
-    norms 0.1, projections 1/sqrt(fan in) (Tests/Decoder/Common.h:164-237)."""
+    """N(0, sigma) per tensor, as the reference test draws them
+    (Tests/Decoder/Common.h:164-237), with wider spreads: embedding 0.1,
+    norms 0.5, projections 3/sqrt(fan in).  With the reference's spreads
+    (0.2, 0.1, 1/sqrt(fan in)) this small model's tied embedding dominates
+    and every greedy id repeats the prompt's last one; with these the ids
+    change from step to step and the smallest top-2 margin stays near 1e-2."""
     tensors = []
     for i in range(shape.tensor_count()):
         n = shape.tensor_elements(i)
         if i == 0:
-            sigma = 0.2
-        elif shape.tensor_is_norm(i):
             sigma = 0.1
+        elif shape.tensor_is_norm(i):
+            sigma = 0.5
         else:
             role = (i - 1) % G.PER_LAYER
             fan_in = {G.T_O: shape.query_width, G.T_DOWN: shape.intermediate}.get(role, shape.width)
-            sigma = 1.0 / np.sqrt(fan_in)
+            sigma = 3.0 / np.sqrt(fan_in)
         tensors.append(O.normal_fill(0x7100 + i, sigma, n))
     return tensors
 
