@@ -18,35 +18,16 @@ from huggingfaceeacp_amd import gemma_q8 as G
 from test_gemma_runtime import GOLDEN_TOKENIZER, config_for
 from test_gpu_checkpoint import small_checkpoint
 from test_gpu_decoder import to_oracle_shape
-from test_gpu_persist import persist_shape
+from test_gpu_persist import persist_shape, seeded_weights
 
 pytestmark = pytest.mark.gpu
 
 WINDOW = 64
 
 
-def varied_weights(shape):
-    """N(0, sigma): embedding 0.1, norms 1.0, projections 4/sqrt(fan in).  With
-    these spreads the small model's greedy ids vary from step to step (with
-    the reference test's spreads a tied embedding this small repeats the
-    prompt's last id)."""
-    tensors = []
-    for i in range(shape.tensor_count()):
-        if i == 0:
-            sigma = 0.1
-        elif shape.tensor_is_norm(i):
-            sigma = 1.0
-        else:
-            role = (i - 1) % G.PER_LAYER
-            fan_in = {G.T_O: shape.query_width, G.T_DOWN: shape.intermediate}.get(role, shape.width)
-            sigma = 4.0 / np.sqrt(fan_in)
-        tensors.append(O.normal_fill(0x9100 + i, sigma, shape.tensor_elements(i)))
-    return tensors
-
-
 def write_directory(root, shape, eos):
     root.mkdir(parents=True, exist_ok=True)
-    paths, widened = small_checkpoint(root, shape, varied_weights(shape))
+    paths, widened = small_checkpoint(root, shape, seeded_weights(shape))
     weight_map = {}
     for path in paths:
         weight_map.update({name: path.name for name in G.SafeTensors.open(path).names()})
