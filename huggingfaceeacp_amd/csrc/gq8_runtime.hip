@@ -18,6 +18,7 @@
 #include <cstring>
 #include <random>
 #include <string>
+#include <mutex>
 #include <thread>
 #include <vector>
 
@@ -362,6 +363,76 @@ extern "C" int gq8_mqa_decode(const float *query, const uint16_t *key_cache,
     GQ8_LAUNCH(gq8::launch_mqa(query, heads * head_dim, key_cache, value_cache, heads, kv_heads,
                                head_dim, 1, nullptr, key_count - 1, key_count, scale, out, nullptr,
                                workspace, workspace_bytes, as_stream(stream)));
+    return GQ8_OK;
+}
+
+// ---- mqa_decode without an allocation ------------------------------------
+// The split partials of gq8_mqa_decode_noalloc live in this file-scope device
+// array: rows 1, at most kMaxHeads heads and a 2048-wide query row, i.e.
+// kAttentionSplits x (2048 + 2 x 16) doubles = 1 064 960 bytes per GPU, held
+// until the process ends.  The kernels take its device address, which
+// hipGetSymbolAddress gives once per device (the array's name is a host-side
+// stand-in, not a device address).  The merge reads only the splits the
+// partial kernel wrote in the same call, so nothing needs clearing; calls that
+// overlap on one GPU share the array and race.
+namespace {
+constexpr size_t kNoAllocScratchBytes =
+    (size_t) gq8::kAttentionSplits * (2048 + 2 * gq8::kMaxHeads) * sizeof(double);
+constexpr int kNoAllocMaxDevices = 64;
+}
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+std::mutex g_scratchMutex;
+void *g_scratchAddress[kNoAllocMaxDevices] = {};
+
+// The calling thread's current device's address of `scratch`, resolved once.
+int scratch_address(void **out)
+{
+    int device = 0;
+    GQ8_HIP(hipGetDevice(&device));
+    if (device < 0 || device >= kNoAllocMaxDevices)
+        return fail(GQ8_ERR_DEVICE, "mqa_decode_noalloc: device ordinal past the table");
+    std::lock_guard<std::mutex> lock(g_scratchMutex);
+    if (!g_scratchAddress[device]) {
+        void *address = nullptr;
+        GQ8_HIP(hipGetSymbolAddress(&address, HIP_SYMBOL(scratch)));
+        if (!address)
+            return fail(GQ8_ERR_DEVICE, "mqa_decode_noalloc: no device address for the scratch array");
+        g_scratchAddress[device] = address;
+    }
+    *out = g_scratchAddress[device];
+    return GQ8_OK;
+}
+} // namespace
+
+extern "C" size_t gq8_mqa_decode_noalloc_limit_bytes(void)
+{
+    return kNoAllocScratchBytes;
+}
+
+extern "C" int gq8_mqa_decode_noalloc(const float *query, const uint16_t *key_cache,
+                                      const uint16_t *value_cache, int heads, int kv_heads,
+                                      int head_dim, int key_count, float scale, float *out,
+                                      void *stream)
+{
+    if (int s = check_attention_shape(heads, kv_heads, head_dim))
+        return s;
+    if (!query || !key_cache || !value_cache || !out || key_count < 1)
+        return fail(GQ8_ERR_ARGUMENT, "mqa_decode_noalloc: bad arguments");
+    const size_t needed = gq8::mqa_workspace_bytes(1, heads, head_dim, key_count);
+    if (needed > kNoAllocScratchBytes)
+        return fail(GQ8_ERR_ARGUMENT, "mqa_decode_noalloc: the split partials need "
+                                          + std::to_string(needed) + " bytes, past the "
+                                          + std::to_string(kNoAllocScratchBytes)
+                                          + "-byte static scratch");
+    void *workspace = nullptr;
+    if (int s = scratch_address(&workspace))
+        return s;
+    GQ8_LAUNCH(gq8::launch_mqa(query, heads * head_dim, key_cache, value_cache, heads, kv_heads,
+                               head_dim, 1, nullptr, key_count - 1, key_count, scale, out, nullptr,
+                               workspace, kNoAllocScratchBytes, as_stream(stream)));
     return GQ8_OK;
 }
 

@@ -125,6 +125,8 @@ def library() -> ctypes.CDLL:
         "gq8_kv_store_f16": (i32, [P, P, i32, i32, i32, P, P, i32, P]),
         "gq8_mqa_workspace_bytes": (sz, [i32, i32, i32, i32]),
         "gq8_mqa_decode": (i32, [P, P, P, i32, i32, i32, i32, f32, P, P, sz, P]),
+        "gq8_mqa_decode_noalloc_limit_bytes": (sz, []),
+        "gq8_mqa_decode_noalloc": (i32, [P, P, P, i32, i32, i32, i32, f32, P, P]),
         "gq8_mqa_prefill": (i32, [P, P, P, i32, i32, i32, i32, i32, f32, P, P, sz, P]),
         "gq8_geglu": (i32, [P, i32, i32, P, P, P]),
         "gq8_argmax_workspace_bytes": (sz, [i32, i32]),
@@ -278,6 +280,18 @@ def mqa_decode(query, keys, values, heads, kv_heads, head_dim, key_count, scale,
     return check(library().gq8_mqa_decode(query, keys, values, heads, kv_heads, head_dim,
                                           key_count, scale, out, workspace, workspace_bytes,
                                           stream))
+
+
+def mqa_decode_noalloc_limit_bytes():
+    return int(library().gq8_mqa_decode_noalloc_limit_bytes())
+
+
+def mqa_decode_noalloc(query, keys, values, heads, kv_heads, head_dim, key_count, scale, out,
+                       stream=0):
+    """mqa_decode with its split partials in the library's static device
+    array: no workspace argument, no allocation."""
+    return check(library().gq8_mqa_decode_noalloc(query, keys, values, heads, kv_heads,
+                                                  head_dim, key_count, scale, out, stream))
 
 
 def mqa_prefill(queries, keys, values, heads, kv_heads, head_dim, rows, position_offset, scale,

@@ -123,6 +123,20 @@ int gq8_mqa_decode(const float *query, const uint16_t *key_cache, const uint16_t
                    int heads, int kv_heads, int head_dim, int key_count, float scale, float *out,
                    void *workspace, size_t workspace_bytes, void *stream);
 
+/* gq8_mqa_decode without a workspace argument and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The split partials live in a static device array of
+ * gq8_mqa_decode_noalloc_limit_bytes() bytes per GPU (1 064 960: one query
+ * row of at most 16 heads and 2048 channels), held until the process ends;
+ * a shape needing more is refused with GQ8_ERR_ARGUMENT.  Every call on one
+ * GPU shares that array, so calls that overlap on one GPU (two streams, two
+ * threads) race. */
+size_t gq8_mqa_decode_noalloc_limit_bytes(void);
+int gq8_mqa_decode_noalloc(const float *query, const uint16_t *key_cache,
+                           const uint16_t *value_cache, int heads, int kv_heads, int head_dim,
+                           int key_count, float scale, float *out, void *stream);
+
 /* MultiQueryPrefillAttention (MultiQueryAttention.h:275-308): rows query rows
  * at positions position_offset + r, row r over keys [0, position_offset + r]. */
 int gq8_mqa_prefill(const float *queries, const uint16_t *key_cache,
