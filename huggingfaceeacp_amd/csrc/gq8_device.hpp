@@ -177,9 +177,11 @@ __device__ inline double block_term(const WeightBlock &b, const int4 &a0, const 
 
 // Larger floats give larger keys; NaN gives 0, below every ordered value, so
 // it is never chosen (a NaN logit never compares greater in the scan either).
+// -0 is folded into +0 first: the two compare equal, so the lower index must
+// win between them as between any equal values (Sampler.cpp:60-76).
 __device__ inline unsigned long long candidate_key(float value, uint32_t index)
 {
-    const uint32_t bits = __float_as_uint(value);
+    const uint32_t bits = value == 0.f ? 0u : __float_as_uint(value);
     uint32_t key = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
     if (value != value)
         key = 0;

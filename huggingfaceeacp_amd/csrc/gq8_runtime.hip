@@ -1582,6 +1582,20 @@ int encode_persist_token(gq8_decoder *d, float *logits, bool sample)
     return GQ8_OK;
 }
 
+// After a one-launch step gave up, the steps enqueued behind it gave up too
+// and none of them advanced the device position: the host's count of enqueued
+// steps is set back to the device's, so the next step writes its slot at the
+// position the device actually holds.
+int resync_position(gq8_decoder *d)
+{
+    int position = 0;
+    GQ8_HIP(hipMemcpy(&position, d->position, sizeof(int), hipMemcpyDeviceToHost));
+    if (position < 0 || position > d->shape.max_positions)
+        return fail(GQ8_ERR_DEVICE, "one-launch step: the device position is out of range");
+    d->hostPosition = position;
+    return GQ8_OK;
+}
+
 // Reads and clears the persistent step's error word, as check_flow_error does
 // for the dataflow step.
 int check_persist_error(gq8_decoder *d)
@@ -1601,6 +1615,8 @@ int check_persist_error(gq8_decoder *d)
     GQ8_HIP(hipMemcpy(d->persistEpoch, &epoch, sizeof(epoch), hipMemcpyHostToDevice));
     GQ8_HIP(hipMemset(d->persistTagged, 0, d->persistTaggedBytes));
     GQ8_HIP(hipMemset(d->persistError, 0, sizeof(int)));
+    if (int s = resync_position(d))
+        return s;
     return fail(GQ8_ERR_DEVICE, "persistent step: a wait gave up (the step's results are invalid)");
 }
 
@@ -1640,6 +1656,8 @@ int check_flow_error(gq8_decoder *d)
     GQ8_HIP(hipMemset(d->flowError, 0, sizeof(int)));
     GQ8_HIP(hipMemset(d->counters, 0, gq8::kDecodeCounters * sizeof(int)));
     GQ8_HIP(hipMemset(d->headBest, 0, gq8::kHeadSlots * gq8::kHeadSlotStride * sizeof(unsigned long long)));
+    if (int s = resync_position(d))
+        return s;
     return fail(GQ8_ERR_DEVICE, "dataflow step: a wait gave up (the step's results are invalid)");
 }
 
