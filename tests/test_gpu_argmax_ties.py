@@ -1,0 +1,86 @@
+"""The first-maximum rule of the fused lm_head argmax (Argmax.h:10-45,
+ArgmaxTests.cpp:207-245; Sampler.cpp:60-76): among equal logits the lowest
+id wins.
+
+A tie is planted through the tied embedding: row w, the greedy winner at some
+step, is copied into a row u < w that neither the prompt nor the run uses.
+Int8Blocks quantizes a row's 32-element blocks on their own, so the two rows
+hold the same bytes and every step gives u and w the same logit.  Feeding u
+instead of w embeds the same row, so the expected run is the untouched run
+with every w replaced by u; the oracle (whose argmax keeps the first maximum)
+must agree.  u is taken in the same wave's eight rows as w, or in another
+workgroup (another of the 64 argmax slots), and the run goes through every
+decode path that chooses ids: the fused kernels (plain and graph replay),
+the dataflow and persistent one-launch steps, and a one-sequence lockstep
+batch."""
+import numpy as np
+import pytest
+
+import oracle as O
+from huggingfaceeacp_amd import gemma_q8 as G
+from test_gpu_configs import VARIED_SEED, varied_sigma
+
+pytestmark = pytest.mark.gpu
+
+LAYERS, POSITIONS, STEPS = 2, 96, 12
+
+
+def tied_pair(winners, used, placement):
+    """(step, w, u): the first step whose winner w has an unused lower row u in
+    the same eight-row wave group (placement "wave") or in the previous
+    32-row workgroup (placement "slot")."""
+    for step, w in enumerate(winners):
+        if placement == "wave":
+            candidates = range(w & ~7, w)
+        else:
+            candidates = [w - 32] if w >= 32 else []
+        for u in candidates:
+            if u not in used:
+                return step, int(w), int(u)
+    return None
+
+
+@pytest.mark.parametrize("placement", ["wave", "slot"])
+def test_lm_head_ties_go_to_the_lower_id(torch_cuda, placement):
+    shape = G.DecoderShape.gemma_2b(layers=LAYERS, max_positions=POSITIONS, max_step_rows=64)
+    oshape = O.gemma_2b_shape(layers=LAYERS, max_positions=POSITIONS)
+    tensors = [G.normal_fill_host(VARIED_SEED + i, varied_sigma(shape, i), shape.tensor_elements(i))
+               for i in range(shape.tensor_count())]
+    prompt = O.prompt_ids(0xC0FFEE + 9, shape.vocab, 20)
+    model = O.Model(oshape, O.MODE_Q8)
+    for i, values in enumerate(tensors):
+        assert model.set_tensor(i, values) == 0
+    _, plain_ids, _ = model.generate(prompt, STEPS, eos=-1)
+    used = set(int(t) for t in prompt) | set(int(t) for t in plain_ids)
+    found = tied_pair([int(t) for t in plain_ids], used, placement)
+    assert found is not None, "no winner with a free lower row"
+    step, w, u = found
+    width = shape.width
+    embedding = tensors[0]
+    embedding[u * width:(u + 1) * width] = embedding[w * width:(w + 1) * width]
+    expected = [u if int(t) == w else int(t) for t in plain_ids]
+    print(f"{placement}: winner {w} copied to {u} (first at step {step}); expected {expected}",
+          flush=True)
+    assert model.set_tensor(0, embedding) == 0
+    _, tied_ids, margins = model.generate(prompt, STEPS, eos=-1)
+    assert list(tied_ids) == expected
+    assert float(margins[step]) == 0.0  # the planted tie is exact in the oracle too
+
+    decoder = G.Decoder(shape)
+    for i, values in enumerate(tensors):
+        decoder.load_tensor(i, values)
+    for label, graph, flow, persistent in (("plain", False, False, False),
+                                           ("graph", True, False, False),
+                                           ("flow", True, True, False),
+                                           ("persistent", True, False, True)):
+        decoder.set_flow(flow)
+        decoder.set_persistent(persistent)
+        tokens, _ = decoder.generate(prompt, STEPS, eos=-1, use_graph=graph)
+        assert list(tokens) == expected, label
+    decoder.set_flow(False)
+    decoder.set_persistent(False)
+    batch = G.Batch(decoder, 1)
+    batch.prefill(0, prompt)
+    batch.decode(STEPS - 1, use_graph=True)
+    assert list(batch.tokens(0, prompt.size, STEPS)) == expected, "lockstep"
+    batch.close()
