@@ -6,6 +6,7 @@ travels with the source tree.
 """
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import shutil
 import subprocess
@@ -38,23 +39,42 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the gfx950 library cannot be built")
 
 
-def build(verbose: bool = False) -> str:
-    objects = []
-    tmp = LIBRARY + ".tmp"
-    cmd = [hipcc(), *HIP_FLAGS, "-I", INCLUDE, "-I", CSRC,
-           *[os.path.join(CSRC, s) for s in SOURCES], "-o", tmp, "-lpthread"]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     result = subprocess.run(cmd, capture_output=True, text=True)
     noise = [line for line in (result.stderr or "").splitlines()
              if "packed-fp32-ops' is not a recognized feature" not in line]
-    if result.returncode != 0:
-        sys.stderr.write("\n".join(noise) + "\n")
+    return result.returncode, noise
+
+
+def build(verbose: bool = False, jobs: int = 0) -> str:
+    """Compiles every source to an object (in parallel: each translation unit
+    holds its own kernels), then links the shared library."""
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    base = [hipcc(), *HIP_FLAGS, "-I", INCLUDE, "-I", CSRC]
+    compiles = []
+    for source in SOURCES:
+        obj = os.path.join(objdir, os.path.splitext(source)[0] + ".o")
+        cmd = [*[a for a in base if a != "-shared"], "-c", os.path.join(CSRC, source), "-o", obj]
+        compiles.append((source, obj, cmd))
+    workers = jobs if jobs > 0 else min(len(compiles), os.cpu_count() or 1, 16)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
+        results = list(pool.map(lambda c: _run(c[2], verbose), compiles))
+    failed = False
+    for (source, _, _), (code, noise) in zip(compiles, results):
+        if code != 0 or (verbose and noise):
+            sys.stderr.write(f"--- {source}\n" + "\n".join(noise) + "\n")
+        failed |= code != 0
+    if failed:
         raise RuntimeError("hipcc failed building libgemma_q8.so")
-    if verbose and noise:
+    tmp = LIBRARY + ".tmp"
+    code, noise = _run([*base, *[o for _, o, _ in compiles], "-o", tmp, "-lpthread"], verbose)
+    if code != 0:
         sys.stderr.write("\n".join(noise) + "\n")
+        raise RuntimeError("linking libgemma_q8.so failed")
     os.replace(tmp, LIBRARY)
-    del objects
     return LIBRARY
 
 
