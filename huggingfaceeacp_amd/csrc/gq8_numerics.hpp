@@ -15,6 +15,8 @@
 
 #define GQ8_HD __host__ __device__ inline
 
+#include "gq8_tanh.hpp"
+
 namespace gq8 {
 
 constexpr int kBlock = 32;          // Int8Blocks.h:56
@@ -71,14 +73,25 @@ GQ8_HD int quantize_value(float x, float scale, float inverse)
     return (int) k;
 }
 
+// The candidate hint of quantize_value on the device: a reciprocal of the
+// fp16 scale good to an ulp (v_rcp_f32).  The exact boundary compares above
+// make the quantized value independent of the hint as long as the candidate
+// lands within one of the exact quotient, which an ulp of error at
+// |x / s| <= 256 keeps.
+__device__ inline float quantize_hint(float scale)
+{
+    return __builtin_amdgcn_rcpf(scale);
+}
+
 // tanh GELU (Lib/HuggingFaceEACP/Kernels/Gelu.h:27-46, double constants of
-// Tests/Kernels/Common.h:170-175), the tanh argument saturating at |z| >= 10.
+// Tests/Kernels/Common.h:170-175), the tanh argument saturating at |z| >= 10;
+// tanh from the exponential (gq8_tanh.hpp), within a few ulps of libm's.
 GQ8_HD double tanh_gelu(double x)
 {
 #pragma clang fp contract(off)
     const double rootTwoOverPi = 0.7978845608028654;
     const double inner = rootTwoOverPi * (x + 0.044715 * x * x * x);
-    const double t = inner >= 10.0 ? 1.0 : (inner <= -10.0 ? -1.0 : tanh(inner));
+    const double t = inner >= 10.0 ? 1.0 : (inner <= -10.0 ? -1.0 : tanh_from_exp(inner));
     return 0.5 * x * (1.0 + t);
 }
 
@@ -104,10 +117,14 @@ GQ8_HD float norm_value(float x, double scale, float weight)
     return (float) (((double) x * scale) * (1.0 + (double) weight));
 }
 
+// A width that is a power of two divides by an exact scaling (the same
+// double as the division, without its iteration).
 GQ8_HD double norm_scale(double squares, int n, float epsilon)
 {
 #pragma clang fp contract(off)
-    return 1.0 / sqrt(squares / (double) n + (double) epsilon);
+    const double mean = (n & (n - 1)) == 0 ? ldexp(squares, -__builtin_ctz((unsigned) n))
+                                           : squares / (double) n;
+    return 1.0 / sqrt(mean + (double) epsilon);
 }
 
 } // namespace gq8
