@@ -42,11 +42,19 @@ constexpr int kStageScales = kStageRows * kChunk;                           // 1
 
 constexpr int kScalePieces = (kStageScales + kGemmThreads - 1) / kGemmThreads; // 3 a thread
 
+// kGeglu: the gate|up product of a fused [2 F, inner] weight (gate rows
+// first) with GeGLU and its Q8 folded in.  Tile column block bx stages gate
+// rows [32 bx, 32 bx + 32) as B rows 0..31 and the matching up rows as B rows
+// 32..63, so a tile holds both halves of 32 GeGLU outputs of 128 rows: the
+// epilogue rounds both to fp32 (the stores the unfused product makes), takes
+// the GeGLU of each pair and quantizes each row's 32 outputs as one block into
+// q8_out ([rows, F] Q8 row buffer), with the fp32 outputs to debug_out if set.
+template <bool kGeglu>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void q8_gemm_kernel(
     const uint8_t *__restrict__ x8, int64_t xElements, int xRow0, int rows,
     const uint8_t *__restrict__ w8, int inner, int outputs, float *__restrict__ y, int yStride,
-    int residual)
+    int residual, uint8_t *__restrict__ q8_out, float *__restrict__ debug_out)
 {
     // rows [0, 128) of a buffer are A (activation rows), [128, 192) B (weight rows)
     __shared__ __attribute__((aligned(16))) uint8_t sOps[1][kStageRows * kRowBytes];
@@ -66,13 +74,21 @@ void q8_gemm_kernel(
     // 4 x 512), the rest B rows
     const uint8_t *aBase = x8 + (int64_t) xRow0 * inner;
     const uint16_t *aScales = xScales + (int64_t) xRow0 * nb;
+    // the weight row of B stage row j (0..63) of this tile
+    const int F = outputs / 2;
+    auto weight_row = [&](int j) {
+        if constexpr (kGeglu)
+            return (j < 32 ? 0 : F) + min((int) blockIdx.x * 32 + (j & 31), F - 1);
+        else
+            return min(n0 + j, outputs - 1);
+    };
     uint32_t srcOff[kStageVectors];
 #pragma unroll
     for (int i = 0; i < kStageVectors; ++i) {
         const int piece = t + i * kGemmThreads;     // 16-byte pieces, 16 a row
         const int r = piece >> 4, col = (piece & 15) * 16;
         srcOff[i] = r < kTileM ? (uint32_t) min(m0 + r, rows - 1) * (uint32_t) inner + col
-                               : (uint32_t) min(n0 + r - kTileM, outputs - 1) * (uint32_t) inner + col;
+                               : (uint32_t) weight_row(r - kTileM) * (uint32_t) inner + col;
     }
     uint32_t scaleOff[kScalePieces];
 #pragma unroll
@@ -80,7 +96,7 @@ void q8_gemm_kernel(
         const int e = t + i * kGemmThreads;
         const int r = e / kChunk, b = e % kChunk;
         scaleOff[i] = (r < kTileM ? (uint32_t) min(m0 + r, rows - 1)
-                                  : (uint32_t) min(n0 + r - kTileM, outputs - 1)) * (uint32_t) nb + b;
+                                  : (uint32_t) weight_row(r - kTileM)) * (uint32_t) nb + b;
     }
     static_assert(kTileM * 16 == 4 * kGemmThreads && kStageVectors == 6, "piece split");
     static_assert(kTileM * kChunk == 2 * kGemmThreads && kScalePieces == 3, "scale split");
@@ -158,21 +174,68 @@ void q8_gemm_kernel(
         }
     }
 
+    if constexpr (!kGeglu) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int n = n0 + wn + j * 16 + (lane & 15);
+            for (int j = 0; j < 2; ++j) {
+                const int n = n0 + wn + j * 16 + (lane & 15);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = m0 + wm + i * 16 + (lane >> 4) * 4 + r;
-                if (m < rows && n < outputs) {
-                    float *out = y + (int64_t) m * yStride + n;
-                    const double old = residual ? (double) *out : 0.0;
-                    *out = (float) (acc[i][j][r] + old);
+                for (int r = 0; r < 4; ++r) {
+                    const int m = m0 + wm + i * 16 + (lane >> 4) * 4 + r;
+                    if (m < rows && n < outputs) {
+                        float *out = y + (int64_t) m * yStride + n;
+                        const double old = residual ? (double) *out : 0.0;
+                        *out = (float) (acc[i][j][r] + old);
+                    }
                 }
             }
+    } else {
+        // the fp32 gate (columns 0..31) and up (32..63) values of the tile in
+        // LDS, over the staging buffer (every wave is past its last read)
+        __syncthreads();
+        float *sOut = reinterpret_cast<float *>(sOps[0]); // [128][65]
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int c = wn + j * 16 + (lane & 15);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    sOut[(wm + i * 16 + (lane >> 4) * 4 + r) * 65 + c] = (float) acc[i][j][r];
+            }
+        __syncthreads();
+        // thread t: row t / 4, outputs 8 (t % 4) .. + 8 (four lanes a 32-block)
+        const int row = t >> 2, c0 = (t & 3) * 8;
+        const int m = m0 + row;
+        float v[8];
+        float amax = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            v[k] = geglu(sOut[row * 65 + c0 + k], sOut[row * 65 + 32 + c0 + k]);
+            amax = fmaxf(amax, fabsf(v[k]));
         }
+        amax = fmaxf(amax, __shfl_xor(amax, 1));
+        amax = fmaxf(amax, __shfl_xor(amax, 2));
+        const int o0 = blockIdx.x * 32 + c0;
+        if (m < rows && o0 < F) {
+            const uint16_t bits = scale_bits_from_amax(amax);
+            const float sc = half_value(bits);
+            const float inv = bits ? quantize_hint(sc) : 0.f;
+            uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                packed[k / 4] |= (uint32_t) (uint8_t) (int8_t) (bits ? quantize_value(v[k], sc, inv) : 0)
+                                 << (8 * (k % 4));
+            *reinterpret_cast<uint2 *>(q8_out + (int64_t) m * F + o0) = make_uint2(packed[0], packed[1]);
+            if ((t & 3) == 0)
+                reinterpret_cast<uint16_t *>(q8_out + (int64_t) rows * F)[(int64_t) m * (F / kBlock) + blockIdx.x] = bits;
+            if (debug_out)
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    debug_out[(int64_t) m * F + o0 + k] = v[k];
+        }
+    }
 }
 
 } // namespace
@@ -189,8 +252,25 @@ hipError_t launch_q8_gemm(const uint8_t *x8, int64_t x_elements, int x_row0, int
     if (rows <= 0 || outputs <= 0 || inner <= 0 || inner % kChunkBytes != 0 || y_stride < outputs)
         return hipErrorInvalidValue;
     const dim3 grid((outputs + kTileN - 1) / kTileN, (rows + kTileM - 1) / kTileM);
-    hipLaunchKernelGGL(q8_gemm_kernel, grid, dim3(kGemmThreads), 0, stream, x8, x_elements, x_row0,
-                       rows, w8, inner, outputs, y, y_stride, residual);
+    hipLaunchKernelGGL(q8_gemm_kernel<false>, grid, dim3(kGemmThreads), 0, stream, x8, x_elements,
+                       x_row0, rows, w8, inner, outputs, y, y_stride, residual, nullptr, nullptr);
+    return hipGetLastError();
+}
+
+bool q8_gemm_geglu_supported(int rows, int inner, int intermediate)
+{
+    return q8_gemm_supported(rows, inner, 2 * intermediate) && intermediate % kBlock == 0;
+}
+
+hipError_t launch_q8_gemm_geglu(const uint8_t *x8, int64_t x_elements, int x_row0, int rows,
+                                const uint8_t *w8, int inner, int intermediate, uint8_t *q8_out,
+                                float *debug_out, hipStream_t stream)
+{
+    if (rows <= 0 || !q8_gemm_geglu_supported(rows, inner, intermediate) || !q8_out)
+        return hipErrorInvalidValue;
+    const dim3 grid(intermediate / kBlock, (rows + kTileM - 1) / kTileM);
+    hipLaunchKernelGGL(q8_gemm_kernel<true>, grid, dim3(kGemmThreads), 0, stream, x8, x_elements,
+                       x_row0, rows, w8, inner, 2 * intermediate, nullptr, 0, 0, q8_out, debug_out);
     return hipGetLastError();
 }
 

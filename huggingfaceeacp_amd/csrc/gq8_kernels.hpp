@@ -51,6 +51,13 @@ hipError_t launch_kv_store(const float *k, const float *v, int src_stride, int r
 // 256-byte chunks run on the int8 MFMA GEMM (gq8_gemm.hip).
 constexpr int kGemmMinRows = 32;
 bool q8_gemm_supported(int rows, int inner, int outputs);
+// The gate|up product of a fused [2 F, inner] weight with GeGLU and its Q8
+// folded into the GEMM's epilogue: q8_out receives the [rows, F] Q8 row
+// buffer of the activations, debug_out (optional) their fp32 values.
+bool q8_gemm_geglu_supported(int rows, int inner, int intermediate);
+hipError_t launch_q8_gemm_geglu(const uint8_t *x8, int64_t x_elements, int x_row0, int rows,
+                                const uint8_t *w8, int inner, int intermediate, uint8_t *q8_out,
+                                float *debug_out, hipStream_t stream);
 hipError_t launch_q8_gemm(const uint8_t *x8, int64_t x_elements, int x_row0, int rows,
                           const uint8_t *w8, int inner, int outputs, float *y, int y_stride,
                           int residual, hipStream_t stream);

@@ -1842,14 +1842,27 @@ int encode_step(gq8_decoder *d, int rows, float *logits, int logitsRows, bool sa
                                           d->hidden, W, 1, st));
         GQ8_STAGE(kStageNorm, gq8::launch_rmsnorm(d->hidden, d->postNorm[l], rows, W, s.rms_epsilon,
                                        nullptr, d->x8, st));
-        GQ8_STAGE(kStageGateUp, gq8::launch_q8_product(d->x8, rows, 0, rows, d->gateUp[l], W, 2 * F, d->fused,
-                                          2 * F, 0, st));
-        GQ8_STAGE(kStageGeglu, gq8::launch_geglu(d->fused, rows, F, dbg ? d->debugActivated : nullptr, d->x8,
-                                     st));
-        if (dbg && capture_debug(d, 2, l, d->debugActivated, rows, F, d->x8))
-            return GQ8_ERR_DEVICE;
-        GQ8_STAGE(kStageDown, gq8::launch_q8_product(d->x8, rows, 0, rows, d->down[l], F, W, d->hidden, W,
-                                          1, st));
+        if (gq8::q8_gemm_geglu_supported(rows, W, F)) {
+            // gate|up, GeGLU and its Q8 in one GEMM; the activation rows go
+            // to the fused buffer (the GEMM still reads x8)
+            uint8_t *act8 = reinterpret_cast<uint8_t *>(d->fused);
+            GQ8_STAGE(kStageGateUp, gq8::launch_q8_gemm_geglu(d->x8, (int64_t) rows * W, 0, rows,
+                                                              d->gateUp[l], W, F, act8,
+                                                              dbg ? d->debugActivated : nullptr, st));
+            if (dbg && capture_debug(d, 2, l, d->debugActivated, rows, F, act8))
+                return GQ8_ERR_DEVICE;
+            GQ8_STAGE(kStageDown, gq8::launch_q8_product(act8, rows, 0, rows, d->down[l], F, W,
+                                                         d->hidden, W, 1, st));
+        } else {
+            GQ8_STAGE(kStageGateUp, gq8::launch_q8_product(d->x8, rows, 0, rows, d->gateUp[l], W,
+                                                           2 * F, d->fused, 2 * F, 0, st));
+            GQ8_STAGE(kStageGeglu, gq8::launch_geglu(d->fused, rows, F,
+                                                     dbg ? d->debugActivated : nullptr, d->x8, st));
+            if (dbg && capture_debug(d, 2, l, d->debugActivated, rows, F, d->x8))
+                return GQ8_ERR_DEVICE;
+            GQ8_STAGE(kStageDown, gq8::launch_q8_product(d->x8, rows, 0, rows, d->down[l], F, W,
+                                                         d->hidden, W, 1, st));
+        }
         if (dbg && capture_debug(d, 3, l, d->hidden, rows, W, nullptr))
             return GQ8_ERR_DEVICE;
     }
