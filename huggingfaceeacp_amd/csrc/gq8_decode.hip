@@ -152,7 +152,7 @@ __device__ void norm_q8_finish(const RowSlice<E> &r, int width, float epsilon, R
     amax = max_lanes<kBlock / E / 2>(amax);
     const uint16_t bits = scale_bits_from_amax(amax);
     const float s = half_value(bits);
-    const float inverse = bits ? 1.0f / s : 0.f;
+    const float inverse = bits ? quantize_hint(s) : 0.f;
     int packed[E / 4] = {};
 #pragma unroll
     for (int k = 0; k < E; ++k) {
@@ -213,6 +213,18 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a)
     }
     __builtin_amdgcn_sched_barrier(0); // every load issued before the norm's first wait
 
+    // the rotation of this wave's pairs, fetched while the weights stream in
+    // (the pair index is the same in every lane: scalar loads)
+    const int position = *a.position;
+    float cosine[kPairsPerWave], sine[kPairsPerWave];
+#pragma unroll
+    for (int p = 0; p < kPairsPerWave; ++p) {
+        const int pair = __builtin_amdgcn_readfirstlane(firstPair + p);
+        const int64_t angle = (int64_t) position * half + (pair < pairs ? pair % half : 0);
+        cosine[p] = a.cosines[angle];
+        sine[p] = a.sines[angle];
+    }
+
     norm_q8_finish(slice, a.width, a.epsilon, row, sPartial, a.debug_normalised, a.debug_q8);
 
     int4 a0 = make_int4(0, 0, 0, 0), a1 = a0;
@@ -222,7 +234,6 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a)
         a1 = reinterpret_cast<const int4 *>(row.q + lane * kBlock)[1];
         sa = row.scale[lane];
     }
-    const int position = *a.position;
     constexpr int kRows = 2 * kPairsPerWave;
     double y[kRows];
 #pragma unroll
@@ -241,17 +252,16 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a)
         const int pair = firstPair + p;
         if (lane != 0 || pair >= pairs)
             continue;
-        const int r = rowLo[p], i = pair % half;
+        const int r = rowLo[p];
         const float fLo = (float) yLo, fHi = (float) yHi; // the product's fp32 outputs
-        const int64_t angle = (int64_t) position * half + i;
         if (r < qWidth) {
             float outLo, outHi;
-            rotate_pair(fLo, fHi, a.cosines[angle], a.sines[angle], &outLo, &outHi);
+            rotate_pair(fLo, fHi, cosine[p], sine[p], &outLo, &outHi);
             a.query[r] = outLo;
             a.query[r + half] = outHi;
         } else if (r < qWidth + kvWidth) {
             float outLo, outHi;
-            rotate_pair(fLo, fHi, a.cosines[angle], a.sines[angle], &outLo, &outHi);
+            rotate_pair(fLo, fHi, cosine[p], sine[p], &outLo, &outHi);
             uint16_t *keys = a.key_cache + (int64_t) position * kvWidth + (r - qWidth);
             keys[0] = half_bits(outLo);
             keys[half] = half_bits(outHi);
@@ -547,7 +557,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
     if (t < groupWidth) { // whole 32-blocks: groupWidth is a multiple of 32
         const uint16_t bits = scale_bits_from_amax(amax);
         const float sc = half_value(bits);
-        a.q8[idx] = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);
+        a.q8[idx] = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, quantize_hint(sc)) : 0);
         if ((t & 31) == 0)
             reinterpret_cast<uint16_t *>(a.q8 + qWidth)[idx / kBlock] = bits;
     }
@@ -567,9 +577,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
 // dependent round of stores.
 constexpr int kOMergeThreads = 512;
 constexpr int kOMergeRows = 16;
-constexpr int kOMergeBatch = 8; // splits a thread loads at once
+constexpr int kOMergeBatch = 8; // splits a thread loads at once; two batches in flight
 
-__global__ __launch_bounds__(kOMergeThreads) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ __launch_bounds__(kOMergeThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void o_merge_kernel(OMergeArgs a)
 {
     __shared__ RowQ8 row;
@@ -588,8 +598,9 @@ void o_merge_kernel(OMergeArgs a)
     const bool live = t * 4 < qWidth;
     const int e0 = live ? t * 4 : 0;
     const int h = e0 / hd;
-    double2 part[kOMergeBatch][2]; // the partials were stored by the previous launch
-    auto load_batch = [&](int s0, int last) {
+    // two batches of partials (the partials were stored by the previous launch)
+    double2 partA[kOMergeBatch][2], partB[kOMergeBatch][2];
+    auto load_batch = [&](double2 (&part)[kOMergeBatch][2], int s0, int last) {
 #pragma unroll
         for (int u = 0; u < kOMergeBatch; ++u) {
             const int sp = min(s0 + u, last);
@@ -606,7 +617,7 @@ void o_merge_kernel(OMergeArgs a)
         const int hh = min(wave + k * (kOMergeThreads / 64), heads - 1);
         ml[k] = *reinterpret_cast<const double2 *>(a.ws_ml + (lane * heads + hh) * 2);
     }
-    load_batch(0, kDecodeSplits - 1);
+    load_batch(partA, 0, kDecodeSplits - 1);
     WeightBlock w[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k)
@@ -629,11 +640,12 @@ void o_merge_kernel(OMergeArgs a)
     }
     __syncthreads();
 
-    // the merged elements, then their Q8
+    // the merged elements, in split order, then their Q8; past the first batch
+    // the next one is in flight while one is folded
+    if (splits > kOMergeBatch)
+        load_batch(partB, kOMergeBatch, splits - 1);
     double weighted[4] = {0.0, 0.0, 0.0, 0.0};
-    for (int s0 = 0; s0 < splits; s0 += kOMergeBatch) {
-        if (s0 > 0)
-            load_batch(s0, splits - 1);
+    auto fold = [&](const double2 (&part)[kOMergeBatch][2], int s0) {
 #pragma unroll
         for (int u = 0; u < kOMergeBatch; ++u)
             if (s0 + u < splits) {
@@ -643,6 +655,14 @@ void o_merge_kernel(OMergeArgs a)
                 weighted[2] += part[u][1].x * f;
                 weighted[3] += part[u][1].y * f;
             }
+    };
+    for (int s0 = 0; s0 < splits; s0 += 2 * kOMergeBatch) {
+        fold(partA, s0);
+        if (s0 + 2 * kOMergeBatch < splits)
+            load_batch(partA, s0 + 2 * kOMergeBatch, splits - 1);
+        fold(partB, s0 + kOMergeBatch);
+        if (s0 + 3 * kOMergeBatch < splits)
+            load_batch(partB, s0 + 3 * kOMergeBatch, splits - 1);
     }
     float v[4];
     float amax = 0.f;
@@ -654,7 +674,7 @@ void o_merge_kernel(OMergeArgs a)
     amax = max_lanes<kBlock / 4 / 2>(amax);
     const uint16_t bits = scale_bits_from_amax(amax);
     const float sc = half_value(bits);
-    const float inverse = bits ? 1.0f / sc : 0.f;
+    const float inverse = bits ? quantize_hint(sc) : 0.f;
     if (live) {
         int packed = 0;
 #pragma unroll
@@ -744,7 +764,7 @@ void gateup_geglu_kernel(GateUpArgs a)
         amax = max_lanes<16>(amax);
         const uint16_t bits = scale_bits_from_amax(amax);
         const float sc = half_value(bits);
-        a.q8[o] = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);
+        a.q8[o] = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, quantize_hint(sc)) : 0);
         if (threadIdx.x == 0)
             reinterpret_cast<uint16_t *>(a.q8 + F)[blockIdx.x] = bits;
     }
@@ -1437,7 +1457,7 @@ __device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int ite
     amax = max_lanes<16>(amax);
     const uint16_t bits = scale_bits_from_amax(amax);
     const float sc = half_value(bits);
-    const uint8_t byte = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);
+    const uint8_t byte = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, quantize_hint(sc)) : 0);
     flow_put_q8(a.attn_ll, qWidth, idx, byte, bits, live, tag);
 }
 
@@ -1524,7 +1544,7 @@ __device__ __forceinline__ void flow_gateup(const FlowArgs &a, int l, int item, 
         amax = max_lanes<16>(amax);
         const uint16_t bits = scale_bits_from_amax(amax);
         const float sc = half_value(bits);
-        const uint8_t byte = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, 1.0f / sc) : 0);
+        const uint8_t byte = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, quantize_hint(sc)) : 0);
         flow_put_q8(a.act_ll, F, o, byte, bits, live, word_tag(epoch, l));
     }
 }

@@ -38,7 +38,7 @@ __device__ inline void quantize_in_group(float value, int lane32, uint8_t *byte,
     int q = 0;
     if (bits != 0) {
         const float scale = half_value(bits);
-        q = quantize_value(value, scale, 1.0f / scale);
+        q = quantize_value(value, scale, quantize_hint(scale));
     }
     *byte = (uint8_t) (int8_t) q;
     if (lane32 == 0)
@@ -406,6 +406,12 @@ __global__ __launch_bounds__(kThreads) void q8_matvec_kernel(
         a1[j] = p[1];
         saBits[j] = xScales[(int64_t) x_row * nb + c] & (valid ? 0xFFFFu : 0u);
     }
+    // the residual of the wave's rows, issued last: it arrives behind the
+    // weights, so the store at the end does not wait for a fresh round trip
+    float old[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        old[u] = y[min(row0 + u, outputs - 1)];
     __builtin_amdgcn_sched_barrier(0);
     double sa[S];
 #pragma unroll
@@ -458,10 +464,8 @@ __global__ __launch_bounds__(kThreads) void q8_matvec_kernel(
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int o = row0 + u;
-            if (o < outputs) {
-                const double old = residual ? (double) y[o] : 0.0;
-                y[o] = (float) (acc[u] + old);
-            }
+            if (o < outputs)
+                y[o] = (float) (acc[u] + (residual ? (double) old[u] : 0.0));
         }
     }
 }

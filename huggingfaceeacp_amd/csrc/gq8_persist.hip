@@ -385,7 +385,7 @@ __device__ __forceinline__ void quarter_q8(const float *row, const NormQuarter &
     amax = max_lanes<2>(amax); // the four lanes of the block
     const uint16_t bits = scale_bits_from_amax(amax);
     const float s = half_value(bits);
-    const float inverse = bits ? 1.0f / s : 0.f;
+    const float inverse = bits ? quantize_hint(s) : 0.f;
     uint32_t packed[2] = {0u, 0u};
 #pragma unroll
     for (int k = 0; k < 8; ++k)
@@ -1034,7 +1034,7 @@ __device__ __forceinline__ bool merge_task(const PersistArgs &a, int l, int h, i
     amax = max_lanes<16>(amax);
     const uint16_t bits = scale_bits_from_amax(amax);
     const float sc = half_value(bits);
-    const int byte = bits ? quantize_value(v, sc, 1.0f / sc) : 0;
+    const int byte = bits ? quantize_value(v, sc, quantize_hint(sc)) : 0;
     put_q8(a.attn_ll, qWidth, ch, byte, bits, lane < kBlock, tag);
     return true;
 }
@@ -1149,7 +1149,7 @@ __device__ __forceinline__ bool phase_gateup(const PersistArgs &a, const Plan &p
             amax = max_lanes<16>(amax);
             const uint16_t bits = scale_bits_from_amax(amax);
             const float sc = half_value(bits);
-            const int byte = bits ? quantize_value(v, sc, 1.0f / sc) : 0;
+            const int byte = bits ? quantize_value(v, sc, quantize_hint(sc)) : 0;
             put_q8(a.act_ll, F, o, byte, bits, lane < kBlock, tag);
         }
     }

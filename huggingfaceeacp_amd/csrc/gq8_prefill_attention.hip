@@ -226,7 +226,7 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillAr
             if (a.q8 && live) {
                 const uint16_t bits = scale_bits_from_amax(amax);
                 const float sc = half_value(bits);
-                const float inv = bits ? 1.0f / sc : 0.f;
+                const float inv = bits ? quantize_hint(sc) : 0.f;
                 a.q8[rowBase + 32 * b + j] = (uint8_t) (int8_t) (bits ? quantize_value(v0, sc, inv) : 0);
                 a.q8[rowBase + 32 * b + 16 + j] =
                     (uint8_t) (int8_t) (bits ? quantize_value(v1, sc, inv) : 0);
