@@ -396,6 +396,9 @@ void gor_rope_row(float *x, int row_stride, int heads, int head_dim, int positio
  * r at half index rows * inner / 2 + r * inner / 32 + b).  This is the product
  * of SplitLinearProgram<Int8Blocks> (Lib/HuggingFaceEACP/Kernels/Linear.h:
  * 128-357) with the activation row taken through Int8Blocks as well. */
+/* Built for three instruction sets, picked at load time by the CPU (the
+ * integer dots vectorize; the double sum stays in block order on each). */
+__attribute__((target_clones("avx512f", "avx2", "default")))
 static double q8_row_dot(const int8_t *xq, const double *xs, const uint8_t *weights,
                          int64_t rows, int64_t inner, int64_t row)
 {
@@ -1081,6 +1084,206 @@ static void q8_token(gor_model *model, int32_t token, float *logits, float *hidd
 
     free(h); free(n); free(q); free(k); free(v); free(att);
     free(gate); free(up); free(act); free(xq); free(xs); free(y);
+}
+
+/* ---- Q8 path: a block of tokens ------------------------------------------
+ * The same arithmetic as q8_token for each row of the block, with the
+ * products taken over all rows at once so each weight row is read once a
+ * block (a prefill of hundreds of rows then costs a few token steps).  Every
+ * element is computed by the same expressions in the same order as in
+ * q8_token; only the order in which rows and outputs are visited differs, so
+ * the results are bit-identical (tests/test_oracle_decoder.py holds them to
+ * that).  The debug views keep the block's last row. */
+static void q8_products(const int8_t *xq, const uint16_t *xs, int n, int64_t inner,
+                        const uint8_t *weights, int64_t rows, double *out)
+{
+    ensure_half_table();
+    const int64_t nb = inner / GOR_BLOCK;
+    double *activationScales = (double *) malloc(sizeof(double) * (size_t) (n * nb));
+    for (int64_t i = 0; i < (int64_t) n * nb; ++i)
+        activationScales[i] = (double) g_half_table[xs[i]];
+#pragma omp parallel for schedule(static)
+    for (int64_t row = 0; row < rows; ++row)
+        for (int t = 0; t < n; ++t)
+            out[(int64_t) t * rows + row] =
+                q8_row_dot(xq + (int64_t) t * inner, activationScales + (int64_t) t * nb, weights,
+                           rows, inner, row);
+    free(activationScales);
+}
+
+static void q8_block(gor_model *model, const int32_t *tokens, int n, float *logits,
+                     int logitsRows, float *hiddenOut)
+{
+    const gor_shape *s = &model->shape;
+    const int width = s->width;
+    const int qw = s->heads * s->head_dim;
+    const int kvw = s->kv_heads * s->head_dim;
+    const int inter = s->intermediate;
+    const int position = model->position;
+    const int64_t embedElements = (int64_t) s->vocab * width;
+    const int64_t maxCacheRow = (int64_t) s->max_positions * kvw;
+    int maxInner = inter > qw ? inter : qw;
+    if (width > maxInner)
+        maxInner = width;
+    int64_t maxOut = inter > qw ? inter : qw;
+    if (width > maxOut)
+        maxOut = width;
+
+    float *h = (float *) malloc(sizeof(float) * (size_t) n * width);
+    float *nrm = (float *) malloc(sizeof(float) * (size_t) n * width);
+    float *q = (float *) malloc(sizeof(float) * (size_t) n * qw);
+    float *k = (float *) malloc(sizeof(float) * (size_t) n * kvw);
+    float *v = (float *) malloc(sizeof(float) * (size_t) n * kvw);
+    float *att = (float *) malloc(sizeof(float) * (size_t) n * qw);
+    float *gate = (float *) malloc(sizeof(float) * (size_t) n * inter);
+    float *up = (float *) malloc(sizeof(float) * (size_t) n * inter);
+    float *act = (float *) malloc(sizeof(float) * (size_t) n * inter);
+    int8_t *xq = (int8_t *) malloc((size_t) n * maxInner);
+    uint16_t *xs = (uint16_t *) malloc(sizeof(uint16_t) * (size_t) n * (maxInner / GOR_BLOCK + 1));
+    double *y = (double *) malloc(sizeof(double) * (size_t) n * maxOut);
+
+    ensure_half_table();
+    for (int t = 0; t < n; ++t) {
+        const uint8_t *table = model->bytes[0];
+        for (int c = 0; c < width; ++c) {
+            const int64_t e = (int64_t) tokens[t] * width + c;
+            const int64_t at = embedElements + 2 * (e / GOR_BLOCK);
+            const uint16_t bits = (uint16_t) (table[at] | ((uint32_t) table[at + 1] << 8));
+            const float gathered = g_half_table[bits] * (float) (int8_t) table[e];
+            h[(int64_t) t * width + c] = (float) ((double) s->embedding_scale * (double) gathered);
+        }
+    }
+
+    /* the row's norm and its Q8 input, row by row */
+#define ORACLE_NORM_ROWS(src, weight, len)                                                   \
+    for (int t = 0; t < n; ++t) {                                                            \
+        gor_rmsnorm_row((src) + (int64_t) t * width, (weight), width, s->rms_epsilon,       \
+                        nrm + (int64_t) t * width);                                          \
+        gor_quantize_row(nrm + (int64_t) t * width, width, xq + (int64_t) t * width,        \
+                         xs + (int64_t) t * (width / GOR_BLOCK));                            \
+    }
+
+    for (int layer = 0; layer < s->layers; ++layer) {
+        gor_layer_debug *dbg = &model->debug[layer];
+        ORACLE_NORM_ROWS(h, layer_norm(model, layer, GOR_T_INPUT_NORM), width)
+        memcpy(dbg->normalised, nrm + (int64_t) (n - 1) * width, sizeof(float) * (size_t) width);
+        memcpy(dbg->normalisedQ, xq + (int64_t) (n - 1) * width, (size_t) width);
+        memcpy(dbg->normalisedS, xs + (int64_t) (n - 1) * (width / GOR_BLOCK),
+               sizeof(uint16_t) * (size_t) (width / GOR_BLOCK));
+
+        q8_products(xq, xs, n, width, layer_bytes(model, layer, GOR_T_Q), qw, y);
+        for (int64_t i = 0; i < (int64_t) n * qw; ++i) q[i] = (float) y[i];
+        q8_products(xq, xs, n, width, layer_bytes(model, layer, GOR_T_K), kvw, y);
+        for (int64_t i = 0; i < (int64_t) n * kvw; ++i) k[i] = (float) y[i];
+        q8_products(xq, xs, n, width, layer_bytes(model, layer, GOR_T_V), kvw, y);
+        for (int64_t i = 0; i < (int64_t) n * kvw; ++i) v[i] = (float) y[i];
+
+        uint16_t *keyRows = model->keyCache + (int64_t) layer * maxCacheRow;
+        uint16_t *valueRows = model->valueCache + (int64_t) layer * maxCacheRow;
+        for (int t = 0; t < n; ++t) {
+            gor_rope_row(q + (int64_t) t * qw, qw, s->heads, s->head_dim, position + t,
+                         model->cosines, model->sines);
+            gor_rope_row(k + (int64_t) t * kvw, kvw, s->kv_heads, s->head_dim, position + t,
+                         model->cosines, model->sines);
+            for (int i = 0; i < kvw; ++i) {
+                keyRows[(int64_t) (position + t) * kvw + i] = gor_half_from_float(k[(int64_t) t * kvw + i]);
+                valueRows[(int64_t) (position + t) * kvw + i] = gor_half_from_float(v[(int64_t) t * kvw + i]);
+            }
+        }
+        const float scale = 1.f / sqrtf((float) s->head_dim);
+#pragma omp parallel for schedule(dynamic, 1)
+        for (int t = 0; t < n; ++t)
+            mqa_row(q + (int64_t) t * qw, keyRows, valueRows, read_half_cache, s->heads,
+                    s->kv_heads, s->head_dim, position + t + 1, scale, att + (int64_t) t * qw);
+        for (int t = 0; t < n; ++t)
+            gor_quantize_row(att + (int64_t) t * qw, qw, xq + (int64_t) t * qw,
+                             xs + (int64_t) t * (qw / GOR_BLOCK));
+        memcpy(dbg->attended, att + (int64_t) (n - 1) * qw, sizeof(float) * (size_t) qw);
+        memcpy(dbg->attendedQ, xq + (int64_t) (n - 1) * qw, (size_t) qw);
+        memcpy(dbg->attendedS, xs + (int64_t) (n - 1) * (qw / GOR_BLOCK),
+               sizeof(uint16_t) * (size_t) (qw / GOR_BLOCK));
+
+        q8_products(xq, xs, n, qw, layer_bytes(model, layer, GOR_T_O), width, y);
+        for (int64_t i = 0; i < (int64_t) n * width; ++i)
+            h[i] = (float) ((double) h[i] + y[i]);
+
+        ORACLE_NORM_ROWS(h, layer_norm(model, layer, GOR_T_POST_NORM), width)
+        q8_products(xq, xs, n, width, layer_bytes(model, layer, GOR_T_GATE), inter, y);
+        for (int64_t i = 0; i < (int64_t) n * inter; ++i) gate[i] = (float) y[i];
+        q8_products(xq, xs, n, width, layer_bytes(model, layer, GOR_T_UP), inter, y);
+        for (int64_t i = 0; i < (int64_t) n * inter; ++i) up[i] = (float) y[i];
+        for (int64_t i = 0; i < (int64_t) n * inter; ++i)
+            act[i] = gor_geglu(gate[i], up[i]);
+        for (int t = 0; t < n; ++t)
+            gor_quantize_row(act + (int64_t) t * inter, inter, xq + (int64_t) t * inter,
+                             xs + (int64_t) t * (inter / GOR_BLOCK));
+        memcpy(dbg->activated, act + (int64_t) (n - 1) * inter, sizeof(float) * (size_t) inter);
+        memcpy(dbg->activatedQ, xq + (int64_t) (n - 1) * inter, (size_t) inter);
+        memcpy(dbg->activatedS, xs + (int64_t) (n - 1) * (inter / GOR_BLOCK),
+               sizeof(uint16_t) * (size_t) (inter / GOR_BLOCK));
+
+        q8_products(xq, xs, n, inter, layer_bytes(model, layer, GOR_T_DOWN), width, y);
+        for (int64_t i = 0; i < (int64_t) n * width; ++i)
+            h[i] = (float) ((double) h[i] + y[i]);
+        memcpy(dbg->hidden, h + (int64_t) (n - 1) * width, sizeof(float) * (size_t) width);
+    }
+
+    {
+        gor_layer_debug *dbg = &model->debug[s->layers];
+        ORACLE_NORM_ROWS(h, model->norms[1 + GOR_T_PER_LAYER * s->layers], width)
+        memcpy(dbg->normalised, nrm + (int64_t) (n - 1) * width, sizeof(float) * (size_t) width);
+        memcpy(dbg->normalisedQ, xq + (int64_t) (n - 1) * width, (size_t) width);
+        memcpy(dbg->normalisedS, xs + (int64_t) (n - 1) * (width / GOR_BLOCK),
+               sizeof(uint16_t) * (size_t) (width / GOR_BLOCK));
+        if (hiddenOut)
+            memcpy(hiddenOut, nrm, sizeof(float) * (size_t) n * width);
+        if (logits && logitsRows > 0) {
+            const int first = n - logitsRows;
+            double *row = (double *) malloc(sizeof(double) * (size_t) s->vocab);
+            for (int t = first; t < n; ++t) {
+                q8_matvec_double(xq + (int64_t) t * width, xs + (int64_t) t * (width / GOR_BLOCK),
+                                 model->bytes[0], s->vocab, width, row);
+                for (int64_t i = 0; i < s->vocab; ++i)
+                    logits[(int64_t) (t - first) * s->vocab + i] = (float) row[i];
+            }
+            free(row);
+        }
+    }
+#undef ORACLE_NORM_ROWS
+    model->position = position + n;
+
+    free(h); free(nrm); free(q); free(k); free(v); free(att);
+    free(gate); free(up); free(act); free(xq); free(xs); free(y);
+}
+
+/* The block step of the Q8 path (q8_block) in blocks of at most 256 rows:
+ * logits for the last logitsRows rows (0: none). */
+int gor_model_step_block(gor_model *model, const int32_t *tokens, int n, float *logits,
+                         int logitsRows)
+{
+    for (int i = 0; i < model->tensorCount; ++i)
+        if (!model->present[i])
+            return -4;
+    if (n <= 0 || logitsRows < 0 || logitsRows > n)
+        return -1;
+    if (model->position + n > model->shape.max_positions)
+        return -2;
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= model->shape.vocab)
+            return -3;
+    if (model->mode != GOR_MODE_Q8)
+        return -1;
+    const int chunk = 256;
+    for (int start = 0; start < n; start += chunk) {
+        const int rows = n - start < chunk ? n - start : chunk;
+        /* the logits rows that fall in this chunk */
+        const int firstLogit = n - logitsRows;
+        const int from = firstLogit > start ? firstLogit : start;
+        const int want = start + rows > from ? start + rows - from : 0;
+        q8_block(model, tokens + start, rows, want ? logits + (int64_t) (from - firstLogit) * model->shape.vocab : NULL,
+                 want, NULL);
+    }
+    return 0;
 }
 
 /* ---- reference path: one token, ReferenceDecoder.h:294-375 in double, ---- */

@@ -141,6 +141,12 @@ int gor_model_position(const gor_model *model);
 /* One decoder step over n tokens at positions position..position+n-1.
  * logits: n x vocab (or NULL); hidden: n x width after the final norm (or
  * NULL); returns 0 or a negative refusal code (see gemma_oracle.c). */
+/* The Q8 path's step over a block of n tokens with the products taken over
+ * all rows at once (the same arithmetic as n single steps, bit for bit);
+ * logits receives the last logits_rows rows (0: none).  -1 outside the Q8
+ * mode. */
+int gor_model_step_block(gor_model *model, const int32_t *tokens, int n, float *logits,
+                         int logits_rows);
 int gor_model_step(gor_model *model, const int32_t *tokens, int n, float *logits,
                    float *hidden);
 /* Intermediates of the last token of the last step, for bisecting. */

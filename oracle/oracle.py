@@ -100,6 +100,7 @@ def lib():
         "gor_model_begin": (None, [P]),
         "gor_model_position": (i32, [P]),
         "gor_model_step": (i32, [P, P, i32, P, P]),
+        "gor_model_step_block": (i32, [P, P, i32, P, i32]),
         "gor_model_debug": (P, [P, i32, i32]),
         "gor_model_debug_q": (P, [P, i32, i32]),
         "gor_model_debug_s": (P, [P, i32, i32]),
@@ -291,6 +292,18 @@ class Model:
                                           ptr(logits) if logits is not None else None,
                                           ptr(hidden) if hidden is not None else None))
         return status, logits, hidden
+
+    def step_block(self, tokens, logits_rows=1):
+        """The Q8 path's step over a block of tokens with the products taken
+        over all rows at once: bit-identical to step(), much faster for long
+        prompts; (status, logits of the last logits_rows rows or None)."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        logits = (np.empty((logits_rows, self.shape.vocab), dtype=np.float32)
+                  if logits_rows > 0 else None)
+        status = int(lib().gor_model_step_block(self.handle, ptr(tokens), tokens.size,
+                                                ptr(logits) if logits is not None else None,
+                                                logits_rows))
+        return status, logits
 
     def debug(self, which: int, layer: int) -> np.ndarray:
         sizes = {DBG_NORMALISED: self.shape.width,

@@ -159,8 +159,8 @@ def greedy(model, prompt, steps, digest_steps=()):
     prompt step with its last row's logits, then a step a token; each step's
     top-8 ids and logits and top-2 margin, and the Q8 digests of the last
     prompt row (index 0 of `digests`) and of the steps in digest_steps."""
-    if len(prompt) > 1:
-        assert model.step(prompt[:-1], want_logits=False)[0] == 0
+    if len(prompt) > 1:  # the blocked step: the single steps' bits, far faster
+        assert model.step_block(prompt[:-1], 0)[0] == 0
     status, logits, _ = model.step(prompt[-1:])
     assert status == 0
     digests = [q8_digests(model)]
@@ -207,9 +207,9 @@ def gemma_prefill2048():
     digests = []
     assert model.step(prompt[:1], want_logits=False)[0] == 0
     digests.append(q8_digests(model))
-    assert model.step(prompt[1:1024], want_logits=False)[0] == 0
+    assert model.step_block(prompt[1:1024], 0)[0] == 0
     digests.append(q8_digests(model))
-    assert model.step(prompt[1024:2047], want_logits=False)[0] == 0
+    assert model.step_block(prompt[1024:2047], 0)[0] == 0
     status, logits, _ = model.step(prompt[2047:])
     assert status == 0
     digests.append(q8_digests(model))

@@ -156,3 +156,33 @@ def test_q8_path_is_within_one_percent_of_the_reference_at_the_gemma_shape():
         scale = float(np.max(np.abs(want[row])))
         assert float(np.max(np.abs(got[row] - want[row]))) <= 1e-2 * scale
         assert int(np.argmax(got[row])) == int(np.argmax(want[row]))
+
+
+@pytest.mark.parametrize("gemma", [False, True])
+def test_block_step_is_bit_identical_to_single_steps(small, gemma):
+    """The oracle's blocked prefill (products over all rows of a block at
+    once) against token-at-a-time steps: the same logits and Q8 activation
+    bytes, bit for bit, including across the block boundary of 256 rows."""
+    if gemma:
+        shape = O.gemma_2b_shape(layers=1, max_positions=320)
+        prompt = O.prompt_ids(0xC0FFEE + 11, shape.vocab, 300)
+        one, block = O.Model(shape, O.MODE_Q8), O.Model(shape, O.MODE_Q8)
+        assert one.fill_synthetic() == 0 and block.fill_synthetic() == 0
+    else:
+        shape, values = small
+        prompt = np.array(PROMPT * 2, dtype=np.int32)
+        one, block = build(shape, O.MODE_Q8, values), build(shape, O.MODE_Q8, values)
+    assert one.step(prompt[:-1], want_logits=False)[0] == 0
+    status, want, _ = one.step(prompt[-1:])
+    assert status == 0
+    status, got = block.step_block(prompt, logits_rows=1)
+    assert status == 0
+    assert np.array_equal(got[0].view(np.uint32), want[0].view(np.uint32))
+    assert block.position == one.position == prompt.size
+    for layer in range(shape.layers):
+        for which in (O.DBG_NORMALISED, O.DBG_ATTENDED, O.DBG_ACTIVATED):
+            for a, b in zip(block.debug_q(which, layer), one.debug_q(which, layer)):
+                assert np.array_equal(a, b), (layer, which)
+    # and the next single step continues from the block's cache exactly
+    token = np.array([int(np.argmax(want[0]))], dtype=np.int32)
+    assert np.array_equal(block.step(token)[1][0].view(np.uint32), one.step(token)[1][0].view(np.uint32))
