@@ -977,7 +977,8 @@ hipError_t launch_mqa(const float *queries, int q_stride, const uint16_t *key_ca
         return hipErrorInvalidValue;
     if (q8 && (heads * head_dim) % kBlock != 0)
         return hipErrorInvalidValue;
-    if (rows >= kPrefillAttentionMinRows && prefill_attention_supported(head_dim))
+    if (rows >= kPrefillAttentionMinRows
+        && prefill_attention_supported(head_dim, queries, q_stride, key_cache, value_cache, out, q8))
         return launch_prefill_attention(queries, q_stride, key_cache, value_cache, heads, kv_heads,
                                         head_dim, rows, pos_ptr, pos_value, scale, out, q8, stream);
     double *wsO = reinterpret_cast<double *>(workspace);

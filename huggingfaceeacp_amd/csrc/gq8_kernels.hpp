@@ -72,10 +72,13 @@ constexpr int kMaxHeadDim = 256;
 size_t mqa_workspace_bytes(int rows, int heads, int head_dim, int max_keys);
 
 // Blocks of kPrefillAttentionMinRows rows or more with a head width of 64, 128
-// or 256 take the fp64-MFMA prefill kernel (gq8_prefill_attention.hip); no
-// workspace.
+// or 256 take the fp64-MFMA prefill kernel (gq8_prefill_attention.hip; no
+// workspace) when its 16-byte loads and stores fit the buffers: queries, caches,
+// out and q8 16-byte aligned, q_stride a multiple of 4.
 constexpr int kPrefillAttentionMinRows = 16;
-bool prefill_attention_supported(int head_dim);
+bool prefill_attention_supported(int head_dim, const float *queries, int q_stride,
+                                 const uint16_t *key_cache, const uint16_t *value_cache,
+                                 const float *out, const uint8_t *q8);
 hipError_t launch_prefill_attention(const float *queries, int q_stride, const uint16_t *key_cache,
                                     const uint16_t *value_cache, int heads, int kv_heads,
                                     int head_dim, int rows, const int *pos_ptr, int pos_value,

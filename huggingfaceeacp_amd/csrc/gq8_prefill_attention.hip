@@ -8,18 +8,32 @@
 // the o product.
 //
 // Work split: a workgroup owns 16 consecutive rows of one head; its four
-// waves take the key tiles (16 keys) round robin and each keeps an online
-// softmax state (row maximum, sum and the 16 x head_dim sums); the states are
-// merged in LDS at the end.  Per tile a wave computes S = Q K^T with
-// v_mfma_f64_16x16x4f64 (the query in registers as fp32, the keys straight
-// from the fp16 cache), rescales, and adds P V with the same instruction.
+// waves take the key tiles (16 keys) round robin, each keeping an online
+// softmax state (row maximum, sum and the 16 x head_dim sums), and the states
+// are merged in LDS at the end.  The grid starts the longest row blocks
+// first, so the short ones fill in behind them.  A wave loads its next tile's
+// keys and values (16-byte loads) before it works on the current one.
+//
+// Per tile a wave computes S^T = K Q^T with v_mfma_f64_16x16x4f64, so the
+// result holds row j of the block on lanes j, j + 16, j + 32, j + 48 and is
+// already the P operand of O += P V (no transpose through LDS).  The online
+// softmax is lazy: a row's reference maximum moves (and its sums are
+// rescaled) only when a tile's maximum exceeds it by more than kLazyMargin,
+// so most tiles need no rescaling; the weights exp(s - m) stay below
+// e^kLazyMargin and every sum stays double.
 //
 // fp64 MFMA operand layout (checked on gfx950): A 16 x 4 with lane l holding
 // A[l % 16][l / 16]; B 4 x 16 with lane l holding B[l / 16][l % 16]; D 16 x 16
-// with lane l holding D[l / 16 + 4 r][l % 16], r = 0..3.  For S the reduction
-// index is the channel, mapped so that lane group g = l / 16 supplies the
-// channels [g E, g E + E) (E = head_dim / 4) over the steps: a lane reads its
-// E channels of a query row and of a key row contiguously.
+// with lane l holding D[l / 16 + 4 r][l % 16], r = 0..3.  With g = l / 16 and
+// j = l % 16:
+//  - S^T (keys x rows, reduced over channels): lane (g, j) supplies key j's
+//    and query row j's channels [g E, g E + E) (E = head_dim / 4), read
+//    contiguously, and receives the scores of row j against keys g + 4 r.
+//  - O (rows x channels, reduced over 4 keys a step): step st takes keys
+//    g + 4 st, so lane (g, j) supplies its own weight p[st]; output tile n
+//    holds channels j T + n (T = head_dim / 16), so a lane's value operands
+//    are T contiguous channels of one key row and its outputs T contiguous
+//    channels of rows g + 4 r.
 #include "gq8_kernels.hpp"
 #include "gq8_numerics.hpp"
 
@@ -32,6 +46,7 @@ constexpr int kPaRows = 16;   // query rows a workgroup
 constexpr int kPaWaves = 4;
 constexpr int kPaThreads = kPaWaves * 64;
 constexpr int kPaKeys = 16;   // keys a tile
+constexpr double kLazyMargin = 8.0;
 
 struct PrefillArgs {
     const float *queries;
@@ -51,9 +66,27 @@ __device__ inline v4d mfma(double a, double b, v4d c)
     return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
 }
 
-__device__ inline double shfl_xor_d(double v, int mask)
+// N consecutive fp16 values (N a multiple of 4), as N / 2 words
+template <int N>
+__device__ inline void load_halves(const uint16_t *p, uint32_t (&w)[N / 2])
 {
-    return __shfl_xor(v, mask);
+    if constexpr (N % 8 == 0) {
+#pragma unroll
+        for (int i = 0; i < N / 8; ++i) {
+            const uint4 v = reinterpret_cast<const uint4 *>(p)[i];
+            w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+        }
+    } else {
+        static_assert(N == 4, "4, 8, 16, ... halves");
+        const uint2 v = *reinterpret_cast<const uint2 *>(p);
+        w[0] = v.x; w[1] = v.y;
+    }
+}
+
+template <int N>
+__device__ inline double half_at(const uint32_t (&w)[N], int i)
+{
+    return (double) half_value((uint16_t) (w[i >> 1] >> (16 * (i & 1))));
 }
 
 // E channels a lane group, T = head_dim / 16 output column tiles.
@@ -61,125 +94,151 @@ template <int E>
 __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillArgs a)
 {
     constexpr int HD = 4 * E, T = HD / 16;
-    // the P tile of each wave (its rows on l % 16 for the P V product), and
-    // one wave's state at a time for the merge
-    __shared__ double sP[kPaWaves][kPaRows][kPaKeys + 1];
+    constexpr int KW = E / 2, VW = T / 2; // words of a lane's key channels / value channels
+    constexpr int kBlockLanes = kBlock / T;  // lanes holding one 32-channel block of an output row
+    // one wave's state at a time for the merge: o (T x 4), then m and l of the rows g + 4 r
     __shared__ double sState[64][T * 4 + 8 + 1];
+    __shared__ __align__(16) float sQ[kPaRows][HD + 4]; // padded: a 16-lane group's rows on distinct banks
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int g = lane >> 4, j = lane & 15;
-    const int r0 = blockIdx.x * kPaRows, h = blockIdx.y;
+    const int blocks = (a.rows + kPaRows - 1) / kPaRows;
+    const int rb = blocks - 1 - (int) blockIdx.x / a.heads; // the longest row blocks first
+    const int h = (int) blockIdx.x % a.heads;
+    const int r0 = rb * kPaRows;
     const int qWidth = a.heads * HD, kvWidth = a.kv_heads * HD;
     const int kvh = h / (a.heads / a.kv_heads);
     const int base = (a.pos_ptr ? *a.pos_ptr : 0) + a.pos_value;
     const int rowsHere = min(kPaRows, a.rows - r0);
     const int lastKey = base + r0 + rowsHere - 1;  // the block's last row attends [0, lastKey]
     const int tiles = lastKey / kPaKeys + 1;
+    const int myRow = min(j, rowsHere - 1);        // rows past the block repeat its last row
+    const int rowPos = base + r0 + myRow;
 
-    // this lane's query channels: row r0 + j (clamped), channels [g E, g E + E)
-    float q[E];
-    {
-        const float *src = a.queries + (int64_t) (r0 + min(j, rowsHere - 1)) * a.q_stride + h * HD + g * E;
+    // the block's query rows in LDS (rows past the block repeat its last row);
+    // lane (g, j) reads row j's channels [g E, g E + E), the B operand of S^T
 #pragma unroll
-        for (int c = 0; c < E; c += 4) {
-            const float4 v = *reinterpret_cast<const float4 *>(src + c);
-            q[c] = v.x; q[c + 1] = v.y; q[c + 2] = v.z; q[c + 3] = v.w;
-        }
+    for (int i = t; i < kPaRows * HD / 4; i += kPaThreads) {
+        const int row = i / (HD / 4), c = (i % (HD / 4)) * 4;
+        const float *src = a.queries + (int64_t) (r0 + min(row, rowsHere - 1)) * a.q_stride + h * HD + c;
+        *reinterpret_cast<float4 *>(&sQ[row][c]) = *reinterpret_cast<const float4 *>(src);
     }
-    // the rows this lane holds in S and O layouts: g + 4 r, at positions
-    int rowPos[4];
+    __syncthreads();
+    const int qAt = j * (HD + 4) + g * E; // lane (g, j)'s first query channel in sQ
+    const uint16_t *keys = a.key_cache + kvh * HD + g * E;
+    const uint16_t *values = a.value_cache + kvh * HD + j * T;
+    // a tile's operands: key k0 + j's channels, and keys k0 + g + 4 st's value channels
+    // (keys past the block's last are clamped to it and masked)
+    auto load_tile = [&](int tile, uint32_t (&kw)[KW], uint32_t (&vw)[4][VW]) {
+        const int k0 = tile * kPaKeys;
+        load_halves<E>(keys + (int64_t) min(k0 + j, lastKey) * kvWidth, kw);
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-        rowPos[r] = base + r0 + g + 4 * r;
+        for (int st = 0; st < 4; ++st)
+            load_halves<T>(values + (int64_t) min(k0 + g + 4 * st, lastKey) * kvWidth, vw[st]);
+    };
 
-    double m[4], l[4];
+    double m = -INFINITY, l = 0.0; // row j's reference maximum and sum (alike on its 4 lanes)
     v4d o[T];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        m[r] = -INFINITY;
-        l[r] = 0.0;
-    }
 #pragma unroll
     for (int n = 0; n < T; ++n)
         o[n] = v4d{0.0, 0.0, 0.0, 0.0};
 
-    const uint16_t *keys = a.key_cache + kvh * HD;
-    const uint16_t *values = a.value_cache + kvh * HD;
+    uint32_t kw[KW], vw[4][VW];
+    if (wave < tiles)
+        load_tile(wave, kw, vw);
     for (int tile = wave; tile < tiles; tile += kPaWaves) {
+        uint32_t kn[KW], vn[4][VW];
+        load_tile(min(tile + kPaWaves, tiles - 1), kn, vn);
         const int k0 = tile * kPaKeys;
-        // S = Q K^T: lane (g, j) supplies K[k0 + j][g E + c] (a B element)
-        uint16_t kh[E];
-        {
-            const int key = min(k0 + j, lastKey);
-            const uint16_t *src = keys + (int64_t) key * kvWidth + g * E;
-#pragma unroll
-            for (int c = 0; c < E; c += 8) {
-                const uint4 v = *reinterpret_cast<const uint4 *>(src + c);
-                kh[c] = (uint16_t) (v.x & 0xFFFFu); kh[c + 1] = (uint16_t) (v.x >> 16);
-                kh[c + 2] = (uint16_t) (v.y & 0xFFFFu); kh[c + 3] = (uint16_t) (v.y >> 16);
-                kh[c + 4] = (uint16_t) (v.z & 0xFFFFu); kh[c + 5] = (uint16_t) (v.z >> 16);
-                kh[c + 6] = (uint16_t) (v.w & 0xFFFFu); kh[c + 7] = (uint16_t) (v.w >> 16);
-            }
-        }
+
+        // the query is read from LDS every tile: an opaque offset keeps the
+        // compiler from holding all E channels as doubles across the loop
+        int qOff = qAt;
+        asm volatile("" : "+v"(qOff));
+        const float *qRow = &sQ[0][0] + qOff;
         v4d s = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-        for (int c = 0; c < E; ++c)
-            s = mfma((double) q[c], (double) half_value(kh[c]), s);
+        for (int c = 0; c < E; c += 4) {
+            const float4 qv = *reinterpret_cast<const float4 *>(qRow + c);
+            s = mfma(half_at(kw, c), (double) qv.x, s);
+            s = mfma(half_at(kw, c + 1), (double) qv.y, s);
+            s = mfma(half_at(kw, c + 2), (double) qv.z, s);
+            s = mfma(half_at(kw, c + 3), (double) qv.w, s);
+        }
 
-        // online softmax over this tile: row g + 4 r, key k0 + j
-        double p[4], alpha[4];
+        // row j against keys k0 + g + 4 r
+        double sv[4];
+        bool live[4];
+        double tileMax = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const bool live = k0 + j <= rowPos[r];
-            const double score = live ? (double) a.scale * s[r] : -INFINITY;
-            double tileMax = score;
-            for (int mask = 1; mask < 16; mask <<= 1)
-                tileMax = fmax(tileMax, shfl_xor_d(tileMax, mask));
-            const double newMax = fmax(m[r], tileMax);
-            alpha[r] = newMax == -INFINITY ? 1.0 : exp(m[r] - newMax);
-            p[r] = live ? exp(score - newMax) : 0.0;
-            double sum = p[r];
-            for (int mask = 1; mask < 16; mask <<= 1)
-                sum += shfl_xor_d(sum, mask);
-            l[r] = l[r] * alpha[r] + sum;
-            m[r] = newMax;
+            live[r] = k0 + g + 4 * r <= rowPos;
+            sv[r] = live[r] ? (double) a.scale * s[r] : -INFINITY;
+            tileMax = fmax(tileMax, sv[r]);
         }
-#pragma unroll
-        for (int n = 0; n < T; ++n)
+        tileMax = fmax(tileMax, __shfl_xor(tileMax, 16));
+        tileMax = fmax(tileMax, __shfl_xor(tileMax, 32));
+        const bool raise = tileMax > m + kLazyMargin; // false while the tile is all masked
+        const bool rescale = raise && m != -INFINITY;
+        if (__any(rescale)) {
+            const double alpha = rescale ? exp(m - tileMax) : 1.0;
+            double alphaO[4]; // the factors of output rows g + 4 r
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                o[n][r] *= alpha[r];
-        // P to LDS with its rows on l % 16 for the A operand
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            sP[wave][g + 4 * r][j] = p[r];
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        double pa[4];
-#pragma unroll
-        for (int st = 0; st < 4; ++st)
-            pa[st] = sP[wave][j][4 * st + g]; // A[row j][key 4 st + g]
-        // O += P V: lane (g, j) supplies V[k0 + 4 st + g][16 n + j]
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            const int key = min(k0 + 4 * st + g, lastKey);
-            const uint16_t *vrow = values + (int64_t) key * kvWidth + j;
+                alphaO[r] = __shfl(alpha, g + 4 * r);
 #pragma unroll
             for (int n = 0; n < T; ++n)
-                o[n] = mfma(pa[st], (double) half_value(vrow[16 * n]), o[n]);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    o[n][r] *= alphaO[r];
+            l *= alpha;
         }
-        __builtin_amdgcn_wave_barrier(); // sP is rewritten by the next tile
+        if (raise)
+            m = tileMax;
+        double p[4], sum = 0.0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            p[r] = live[r] ? exp(sv[r] - m) : 0.0;
+            sum += p[r];
+        }
+        sum += __shfl_xor(sum, 16);
+        sum += __shfl_xor(sum, 32);
+        l += sum;
+
+        // O += P V, four keys a step
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int n = 0; n < T; ++n)
+                o[n] = mfma(p[st], half_at(vw[st], n), o[n]);
+
+#pragma unroll
+        for (int i = 0; i < KW; ++i)
+            kw[i] = kn[i];
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int i = 0; i < VW; ++i)
+                vw[st][i] = vn[st][i];
     }
 
-    // merge the waves' states into wave 0, one wave at a time
+    // the maximum and sum of output rows g + 4 r
+    double mO[4], lO[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        mO[r] = __shfl(m, g + 4 * r);
+        lO[r] = __shfl(l, g + 4 * r);
+    }
+
+    // merge the waves' states into wave 0, one wave at a time (wave 0 holds
+    // tile 0, which every row attends, so its maxima are finite)
     for (int w = 1; w < kPaWaves; ++w) {
         __syncthreads();
         if (wave == w) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                sState[lane][T * 4 + r] = m[r];
-                sState[lane][T * 4 + 4 + r] = l[r];
+                sState[lane][T * 4 + r] = mO[r];
+                sState[lane][T * 4 + 4 + r] = lO[r];
             }
 #pragma unroll
             for (int n = 0; n < T; ++n)
@@ -192,11 +251,11 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillAr
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const double om = sState[lane][T * 4 + r], ol = sState[lane][T * 4 + 4 + r];
-                const double newMax = fmax(m[r], om);
-                const double fa = newMax == -INFINITY ? 0.0 : exp(m[r] - newMax);
-                const double fb = newMax == -INFINITY ? 0.0 : exp(om - newMax);
-                l[r] = l[r] * fa + ol * fb;
-                m[r] = newMax;
+                const double newMax = fmax(mO[r], om);
+                const double fa = newMax == -INFINITY ? 0.0 : exp(mO[r] - newMax);
+                const double fb = om == -INFINITY ? 0.0 : exp(om - newMax);
+                lO[r] = lO[r] * fa + ol * fb;
+                mO[r] = newMax;
 #pragma unroll
                 for (int n = 0; n < T; ++n)
                     o[n][r] = o[n][r] * fa + sState[lane][n * 4 + r] * fb;
@@ -206,32 +265,52 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillAr
     if (wave != 0)
         return;
 
-    // rows g + 4 r, channels 16 n + j: fp32, then Q8 per 32-block (tiles 2b, 2b + 1)
+    // rows g + 4 r, channels [j T, j T + T): fp32, then Q8 per 32-block
+    // (kBlockLanes neighbouring lanes a block)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int row = g + 4 * r;
         const bool live = row < rowsHere;
-        const int64_t rowBase = (int64_t) (r0 + min(row, rowsHere - 1)) * qWidth + h * HD;
+        const int64_t at = (int64_t) (r0 + min(row, rowsHere - 1)) * qWidth + h * HD + j * T;
+        float v[T];
+        float amax = 0.f;
 #pragma unroll
-        for (int b = 0; b < T / 2; ++b) {
-            const float v0 = (float) (o[2 * b][r] / l[r]);
-            const float v1 = (float) (o[2 * b + 1][r] / l[r]);
-            if (a.out && live) {
-                a.out[rowBase + 32 * b + j] = v0;
-                a.out[rowBase + 32 * b + 16 + j] = v1;
-            }
-            float amax = fmaxf(fabsf(v0), fabsf(v1));
-            for (int mask = 1; mask < 16; mask <<= 1)
+        for (int n = 0; n < T; ++n) {
+            v[n] = (float) (o[n][r] / lO[r]);
+            amax = fmaxf(amax, fabsf(v[n]));
+        }
+        if (a.out && live) {
+#pragma unroll
+            for (int n = 0; n < T; n += 4)
+                *reinterpret_cast<float4 *>(a.out + at + n) = float4{v[n], v[n + 1], v[n + 2], v[n + 3]};
+        }
+        if (a.q8) {
+#pragma unroll
+            for (int mask = 1; mask < kBlockLanes; mask <<= 1)
                 amax = fmaxf(amax, __shfl_xor(amax, mask));
-            if (a.q8 && live) {
-                const uint16_t bits = scale_bits_from_amax(amax);
-                const float sc = half_value(bits);
-                const float inv = bits ? quantize_hint(sc) : 0.f;
-                a.q8[rowBase + 32 * b + j] = (uint8_t) (int8_t) (bits ? quantize_value(v0, sc, inv) : 0);
-                a.q8[rowBase + 32 * b + 16 + j] =
-                    (uint8_t) (int8_t) (bits ? quantize_value(v1, sc, inv) : 0);
-                if (j == 0)
-                    reinterpret_cast<uint16_t *>(a.q8 + (int64_t) a.rows * qWidth)[(rowBase + 32 * b) / kBlock] = bits;
+            const uint16_t bits = scale_bits_from_amax(amax);
+            const float sc = half_value(bits);
+            const float inv = bits ? quantize_hint(sc) : 0.f;
+            uint32_t packed[T / 4];
+#pragma unroll
+            for (int i = 0; i < T / 4; ++i) {
+                uint32_t word = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const int qv = bits ? quantize_value(v[4 * i + b], sc, inv) : 0;
+                    word |= (uint32_t) (uint8_t) (int8_t) qv << (8 * b);
+                }
+                packed[i] = word;
+            }
+            if (live) {
+                if constexpr (T == 16)
+                    *reinterpret_cast<uint4 *>(a.q8 + at) = uint4{packed[0], packed[1], packed[2], packed[3]};
+                else if constexpr (T == 8)
+                    *reinterpret_cast<uint2 *>(a.q8 + at) = uint2{packed[0], packed[1]};
+                else
+                    *reinterpret_cast<uint32_t *>(a.q8 + at) = packed[0];
+                if (j % kBlockLanes == 0)
+                    reinterpret_cast<uint16_t *>(a.q8 + (int64_t) a.rows * qWidth)[at / kBlock] = bits;
             }
         }
     }
@@ -239,9 +318,14 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillAr
 
 } // namespace
 
-bool prefill_attention_supported(int head_dim)
+bool prefill_attention_supported(int head_dim, const float *queries, int q_stride,
+                                 const uint16_t *key_cache, const uint16_t *value_cache,
+                                 const float *out, const uint8_t *q8)
 {
-    return head_dim == 64 || head_dim == 128 || head_dim == 256;
+    auto aligned = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && q_stride % 4 == 0
+           && aligned(queries) && aligned(key_cache) && aligned(value_cache) && aligned(out)
+           && aligned(q8);
 }
 
 hipError_t launch_prefill_attention(const float *queries, int q_stride, const uint16_t *key_cache,
@@ -250,11 +334,12 @@ hipError_t launch_prefill_attention(const float *queries, int q_stride, const ui
                                     float scale, float *out, uint8_t *q8, hipStream_t stream)
 {
     if (rows <= 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0
-        || !prefill_attention_supported(head_dim) || q_stride < heads * head_dim)
+        || !prefill_attention_supported(head_dim, queries, q_stride, key_cache, value_cache, out, q8)
+        || q_stride < heads * head_dim)
         return hipErrorInvalidValue;
     PrefillArgs a{queries, q_stride, key_cache, value_cache, heads, kv_heads, head_dim, rows,
                   pos_ptr, pos_value, scale, out, q8};
-    const dim3 grid((rows + kPaRows - 1) / kPaRows, heads);
+    const dim3 grid((unsigned) ((rows + kPaRows - 1) / kPaRows * heads));
     switch (head_dim) {
     case 256:
         hipLaunchKernelGGL(prefill_attention_kernel<64>, grid, dim3(kPaThreads), 0, stream, a);
