@@ -119,22 +119,25 @@ void q8_gemm_kernel(
     }
 
     const int chunks = nb / kChunk;
+    // a chunk's pieces go global -> registers one chunk ahead, so their loads
+    // are in flight while the previous chunk is computed
+    // (native vectors in plain unrolled loops: HIP's int4 carried across the
+    // loop, or arrays captured by a lambda, are left in scratch memory)
+    v4i v[kStageVectors];
+    uint16_t sc[kScalePieces];
+#pragma unroll
+    for (int i = 0; i < kStageVectors; ++i)
+        v[i] = *reinterpret_cast<const v4i *>((i < 4 ? aBase : w8) + srcOff[i]);
+#pragma unroll
+    for (int i = 0; i < kScalePieces; ++i)
+        sc[i] = (i < 2 ? aScales : wScales)[scaleOff[i]];
     for (int c = 0; c < chunks; ++c) {
         __syncthreads(); // the previous chunk has been read
         {
-            const int64_t c0 = (int64_t) c * kChunk;
-            int4 v[kStageVectors];
-            uint16_t sc[kScalePieces];
-#pragma unroll
-            for (int i = 0; i < kStageVectors; ++i)
-                v[i] = *reinterpret_cast<const int4 *>((i < 4 ? aBase : w8) + srcOff[i] + c0 * kBlock);
-#pragma unroll
-            for (int i = 0; i < kScalePieces; ++i)
-                sc[i] = (i < 2 ? aScales : wScales)[scaleOff[i] + c0];
 #pragma unroll
             for (int i = 0; i < kStageVectors; ++i) {
                 const int piece = t + i * kGemmThreads;
-                *reinterpret_cast<int4 *>(&sOps[0][(piece >> 4) * kRowBytes + (piece & 15) * 16]) = v[i];
+                *reinterpret_cast<v4i *>(&sOps[0][(piece >> 4) * kRowBytes + (piece & 15) * 16]) = v[i];
             }
 #pragma unroll
             for (int i = 0; i < kScalePieces; ++i) {
@@ -143,6 +146,15 @@ void q8_gemm_kernel(
             }
         }
         __syncthreads();
+        {
+            const int64_t c0 = (int64_t) min(c + 1, chunks - 1) * kChunk; // the last is a repeat, never stored
+#pragma unroll
+            for (int i = 0; i < kStageVectors; ++i)
+                v[i] = *reinterpret_cast<const v4i *>((i < 4 ? aBase : w8) + srcOff[i] + c0 * kBlock);
+#pragma unroll
+            for (int i = 0; i < kScalePieces; ++i)
+                sc[i] = (i < 2 ? aScales : wScales)[scaleOff[i] + c0];
+        }
         const uint8_t *ops = sOps[0];
 #pragma unroll 1
         for (int kb = 0; kb < kChunk; ++kb) {
