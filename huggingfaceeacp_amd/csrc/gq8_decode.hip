@@ -332,6 +332,28 @@ __device__ inline void load_halves(const uint16_t *p, uint16_t (&h)[C])
     }
 }
 
+// The same C halves kept as loaded, (C + 1) / 2 words (half the registers of
+// one a half), and half i of them.
+template <int C>
+__device__ inline void load_words(const uint16_t *p, uint32_t (&w)[(C + 1) / 2])
+{
+    if constexpr (C == 4) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(p);
+        w[0] = v.x;
+        w[1] = v.y;
+    } else if constexpr (C == 2) {
+        w[0] = *reinterpret_cast<const uint32_t *>(p);
+    } else {
+        w[0] = *p;
+    }
+}
+
+template <int C>
+__device__ inline double word_half(const uint32_t (&w)[(C + 1) / 2], int i)
+{
+    return (double) half_value((uint16_t) (w[i >> 1] >> (16 * (i & 1))));
+}
+
 __device__ inline void store_agent(double *p, double v)
 {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -382,14 +404,15 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
     // one round [64 s, 64 s + 64): its rows are loaded before the position
     // arrives (rows past the position are read, inside the cache, and never
     // used), so the two loads do not wait on each other.
-    uint16_t kh[kScoreBatch][G][C], vh[kScoreBatch][G][C];
+    constexpr int CW = (C + 1) / 2; // words of a lane's channels of one row
+    uint32_t kh[kScoreBatch][G][CW], vh[kScoreBatch][G][CW];
 #pragma unroll
     for (int b = 0; b < kScoreBatch; ++b) {
         const int j = min(split * kRoundKeys + wave + b * kAttnWaves, a.max_positions - 1);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            load_halves<C>(a.key_cache + (int64_t) j * kvWidth + kvOffset[g], kh[b][g]);
-            load_halves<C>(a.value_cache + (int64_t) j * kvWidth + kvOffset[g], vh[b][g]);
+            load_words<C>(a.key_cache + (int64_t) j * kvWidth + kvOffset[g], kh[b][g]);
+            load_words<C>(a.value_cache + (int64_t) j * kvWidth + kvOffset[g], vh[b][g]);
         }
     }
     // keeps the loads above the position-dependent exit: the compiler would
@@ -407,23 +430,29 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
 
     // a round's rows for this wave: keys r0 + wave + 8 b, clamped into range
     // (the clamped duplicates are masked where they are used)
-    auto load_round = [&](const uint16_t *base, int r0, uint16_t (&dst)[kScoreBatch][G][C]) {
+    auto load_round = [&](const uint16_t *base, int r0, uint32_t (&dst)[kScoreBatch][G][CW]) {
 #pragma unroll
         for (int b = 0; b < kScoreBatch; ++b) {
             const int j = min(r0 + wave + b * kAttnWaves, n - 1);
 #pragma unroll
             for (int g = 0; g < G; ++g)
-                load_halves<C>(base + (int64_t) j * kvWidth + kvOffset[g], dst[b][g]);
+                load_words<C>(base + (int64_t) j * kvWidth + kvOffset[g], dst[b][g]);
         }
     };
     if (plan.perSplit != kRoundKeys) { // longer splits: the first round again, from k0
         load_round(keys, 0, kh);
         load_round(values, 0, vh);
     }
+    // a two-round split (a window of 4097 .. 8192 keys) has its second round's
+    // rows in flight with the first's
+    const bool twoRounds = plan.perSplit == 2 * kRoundKeys;
+    uint32_t kh2[kScoreBatch][G][CW], vh2[kScoreBatch][G][CW];
+    if (twoRounds) {
+        load_round(keys, kRoundKeys, kh2);
+        load_round(values, kRoundKeys, vh2);
+    }
 
-    for (int r0 = 0; r0 < n; r0 += kRoundKeys) {
-        if (r0 > 0)
-            load_round(keys, r0, kh);
+    auto score_round = [&](const uint32_t (&k)[kScoreBatch][G][CW], int r0) {
         double y[kRows];
 #pragma unroll
         for (int b = 0; b < kScoreBatch; ++b)
@@ -432,7 +461,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
                 double p = 0.0;
 #pragma unroll
                 for (int i = 0; i < C; ++i)
-                    p += q[g][i] * (double) half_value(kh[b][g][i]);
+                    p += q[g][i] * word_half<C>(k[b][g], i);
                 y[b * G + g] = p;
             }
         const double total = reduce_rows<kRows>(y, lane);
@@ -441,6 +470,15 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
             const int j = r0 + wave + (r / G) * kAttnWaves;
             if (j < n)
                 sScore[r % G][j] = (double) a.scale * total;
+        }
+    };
+    score_round(kh, 0);
+    if (twoRounds) {
+        score_round(kh2, kRoundKeys);
+    } else {
+        for (int r0 = kRoundKeys; r0 < n; r0 += kRoundKeys) {
+            load_round(keys, r0, kh);
+            score_round(kh, r0);
         }
     }
     __syncthreads();
@@ -471,9 +509,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
 #pragma unroll
         for (int i = 0; i < C; ++i)
             acc[g][i] = 0.0;
-    for (int r0 = 0; r0 < n; r0 += kRoundKeys) {
-        if (r0 > 0)
-            load_round(values, r0, vh);
+    auto value_round = [&](const uint32_t (&v)[kScoreBatch][G][CW], int r0) {
 #pragma unroll
         for (int b = 0; b < kScoreBatch; ++b) {
             const int j = r0 + wave + b * kAttnWaves;
@@ -484,8 +520,17 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
                 const double w = sScore[g][j];
 #pragma unroll
                 for (int i = 0; i < C; ++i)
-                    acc[g][i] += w * (double) half_value(vh[b][g][i]);
+                    acc[g][i] += w * word_half<C>(v[b][g], i);
             }
+        }
+    };
+    value_round(vh, 0);
+    if (twoRounds) {
+        value_round(vh2, kRoundKeys);
+    } else {
+        for (int r0 = kRoundKeys; r0 < n; r0 += kRoundKeys) {
+            load_round(values, r0, vh);
+            value_round(vh, r0);
         }
     }
     if (active)
@@ -507,7 +552,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
         store_agent(a.ws_ml + (split * heads + h0 + t) * 2, sMax[t]);
         store_agent(a.ws_ml + (split * heads + h0 + t) * 2 + 1, sSum[t]);
     }
-    if (a.partials_only)
+    if (a.partials_only && plan.splits <= kAttnMergeSplits)
         return; // o_merge_kernel merges them after this launch
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // the stores have completed
     __syncthreads();
@@ -627,6 +672,28 @@ void o_merge_kernel(OMergeArgs a)
     const float old = a.hidden[stores ? r : 0]; // the residual, read with the rest
     __builtin_amdgcn_sched_barrier(0);
     const int splits = plan_splits(*a.position + 1).splits;
+    // this lane's 32-block of the attention row and the product of its rows
+    auto product = [&](const int4 &x0, const int4 &x1, double sx) {
+        double y[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+            y[k] = block_term(w[k], x0, x1, sx);
+        const double total = reduce_rows<2>(y, lane);
+        if (stores)
+            a.hidden[r] = (float) (total + (double) old);
+    };
+    if (splits > kAttnMergeSplits) {
+        // the attention kernel has merged the splits: its Q8 row (every wave alike)
+        int4 x0 = make_int4(0, 0, 0, 0), x1 = x0;
+        double sx = 0.0;
+        if (valid) {
+            x0 = reinterpret_cast<const int4 *>(a.q8_row + lane * kBlock)[0];
+            x1 = reinterpret_cast<const int4 *>(a.q8_row + lane * kBlock)[1];
+            sx = (double) half_value(reinterpret_cast<const uint16_t *>(a.q8_row + qWidth)[lane]);
+        }
+        product(x0, x1, sx);
+        return;
+    }
 #pragma unroll
     for (int k = 0; k < kHeadsPerWave; ++k) {
         const int hh = wave + k * (kOMergeThreads / 64);
@@ -693,13 +760,7 @@ void o_merge_kernel(OMergeArgs a)
         a1 = reinterpret_cast<const int4 *>(row.q + lane * kBlock)[1];
         sa = row.scale[lane];
     }
-    double y[2];
-#pragma unroll
-    for (int k = 0; k < 2; ++k)
-        y[k] = block_term(w[k], a0, a1, sa);
-    const double total = reduce_rows<2>(y, lane);
-    if (stores)
-        a.hidden[r] = (float) (total + (double) old);
+    product(a0, a1, sa);
 }
 
 // ---- gate|up + GeGLU + Q8 -----------------------------------------------------------
@@ -1826,7 +1887,8 @@ hipError_t launch_qkv_rope(const QkvArgs &a, hipStream_t stream)
 hipError_t launch_attention(const AttentionArgs &a, hipStream_t stream)
 {
     int channels = 0, group = 0;
-    if (!attention_layout(a.head_dim, &channels, &group) || a.heads % group != 0)
+    if (!attention_layout(a.head_dim, &channels, &group) || a.heads % group != 0 || !a.q8
+        || !a.counter)
         return hipErrorInvalidValue;
     const dim3 grid(kDecodeSplits, a.heads / group);
     if (channels == 4)
@@ -1849,7 +1911,7 @@ bool o_merge_supported(int heads, int head_dim)
 
 hipError_t launch_o_merge(const OMergeArgs &a, hipStream_t stream)
 {
-    if (!o_merge_supported(a.heads, a.head_dim) || a.width <= 0)
+    if (!o_merge_supported(a.heads, a.head_dim) || a.width <= 0 || !a.q8_row)
         return hipErrorInvalidValue;
     const int grid = (a.width + kOMergeRows - 1) / kOMergeRows;
     hipLaunchKernelGGL(o_merge_kernel, dim3(grid), dim3(kOMergeThreads), 0, stream, a);

@@ -47,8 +47,15 @@ struct AttentionArgs {
     int *counter;             // one a head group (kDecodeCounters), zero between launches
     float *out;               // optional fp32 row
     uint8_t *q8;              // Q8 row for o_proj
-    int partials_only;        // nonzero: store the split partials and stop (o_merge merges them)
+    int partials_only;        // nonzero: up to kAttnMergeSplits splits, store the partials and
+                              // stop (o_merge merges them); more, merge here as without it
 };
+
+// Rows with more splits than this are merged once by the attention kernel
+// (its last workgroup of a head group), and o_merge reads the merged Q8 row:
+// past it, the merge each o workgroup would repeat costs more than the
+// attention kernel's ticket.  Both kernels decide from the device position.
+constexpr int kAttnMergeSplits = 16;
 
 // o_proj fed by the attention partials: every workgroup merges the splits
 // itself (the same arithmetic as the attention kernel's merge), quantizes the
@@ -61,6 +68,7 @@ struct OMergeArgs {
     const uint8_t *weights;      // o, Int8Blocks [width, heads * head_dim]
     int width;
     float *hidden;               // residual row, updated in place
+    const uint8_t *q8_row;       // the attention kernel's merged Q8 row (past kAttnMergeSplits)
 };
 
 struct GateUpArgs {

@@ -1737,6 +1737,7 @@ int encode_fused_token(gq8_decoder *d, float *logits, bool sample)
             om.weights = d->out[l];
             om.width = W;
             om.hidden = d->hidden;
+            om.q8_row = d->x8;
             GQ8_STAGE(kStageO, gq8::launch_o_merge(om, st));
         } else {
             GQ8_STAGE(kStageO, gq8::launch_q8_product(d->x8, 1, 0, 1, d->out[l], d->qWidth, W,

@@ -70,3 +70,40 @@ def test_long_context_window(torch_cuda):
     print(f"  position 8191 logits, one-token vs multi-row: worst {err:.3g}, exact {exact:.4f}")
     assert err <= 1e-6
     assert exact >= 0.99
+
+
+def test_split_merge_moves_into_attention(torch_cuda):
+    """Up to 16 key splits the o product merges the attention splits itself;
+    past that the attention kernel merges them once and the o product reads
+    its Q8 row.  One-token steps across the change (keys 1017 .. 1040, 16 then
+    17 .. 17 splits of 64 keys) give the oracle's logits and greedy ids at
+    Gemma-2B dims (2 layers), and the graph replay of a captured step switches
+    with the device position."""
+    torch = torch_cuda
+    shape, decoder, model = gemma_pair(2, 1152, max_step_rows=256)
+    prompt = O.prompt_ids(0xC0FFEE + 7, shape.vocab, 1016)
+    capacity = shape.step_capacity()
+    for start in range(0, len(prompt), capacity):
+        last = gpu_step(torch, decoder, prompt[start:start + capacity], 1)[0]
+    status, ref = model.step_block(prompt, 1)
+    assert status == 0
+    worst, exact = worst_error(last, ref[0]), [exact_fraction(last, ref[0])]
+    token = int(np.argmax(ref[0]))
+    ids = []
+    for i in range(24):
+        got = gpu_step(torch, decoder, [token])[0]
+        status, ref, _ = model.step(np.array([token]))
+        assert status == 0
+        worst = max(worst, worst_error(got, ref[0]))
+        exact.append(exact_fraction(got, ref[0]))
+        assert int(np.argmax(got)) == int(np.argmax(ref[0])), f"step {i}"
+        token = int(np.argmax(ref[0]))
+        ids.append(token)
+    print(f"  keys 1017..1040: worst {worst:.3g}, bit-identical {np.mean(exact):.4f}")
+    assert worst <= 1e-2
+    # the captured step replays across the change: greedy ids from the same prefix
+    decoder.begin_sequence()
+    graph, _ = decoder.generate(prompt, 24, eos=-1, use_graph=True)
+    decoder.begin_sequence()
+    plain, _ = decoder.generate(prompt, 24, eos=-1, use_graph=False)
+    assert list(graph) == list(plain)
