@@ -184,6 +184,10 @@ __device__ void norm_q8_finish(const RowSlice<E> &r, int width, float epsilon, R
 // owns kPairsPerWave of them.  Lane l owns block l of every row (width <= 2048).
 constexpr int kPairsPerWave = 1;
 
+// Embed: the first layer, which gathers its row from the embedding table at
+// the id in the position's sequence slot (the position is then needed before
+// the row loads); the other layers load the residual row.
+template <bool Embed>
 __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a)
 {
     __shared__ RowQ8 row;
@@ -196,10 +200,22 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a)
     const int nb = a.width / kBlock;
     const int firstPair = (blockIdx.x * kWaves + wave) * kPairsPerWave;
 
-    const uint32_t *token = a.embedding ? a.sequence + *a.position : nullptr;
-    const RowSlice<8> slice = load_row_slice<8>(a.hidden, token, a.embedding, a.vocab,
-                                                a.embed_scale, a.hidden_out, a.norm_weight,
-                                                a.width);
+    // The position is requested first, with a vector load: the rotation's
+    // table rows depend on it, and a scalar load still in flight would hold
+    // up the norm's LDS waits (LDS and scalar memory share one wait counter).
+    // Past the first layer it is not waited for until the row and weight
+    // loads are issued.
+    const int positionLoaded = ld_agent_i(a.position);
+    int position = 0;
+    RowSlice<8> slice;
+    if constexpr (Embed) {
+        position = __builtin_amdgcn_readfirstlane(positionLoaded);
+        slice = load_row_slice<8>(nullptr, a.sequence + position, a.embedding, a.vocab,
+                                  a.embed_scale, a.hidden_out, a.norm_weight, a.width);
+    } else {
+        slice = load_row_slice<8>(a.hidden, nullptr, nullptr, 0, 0.f, nullptr, a.norm_weight,
+                                  a.width);
+    }
     WeightBlock lo[kPairsPerWave], hi[kPairsPerWave];
     int rowLo[kPairsPerWave];
 #pragma unroll
@@ -212,17 +228,19 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a)
         hi[p] = load_block(a.weights, outputs, a.width, rowLo[p] + half, lane, valid);
     }
     __builtin_amdgcn_sched_barrier(0); // every load issued before the norm's first wait
+    if constexpr (!Embed)
+        position = __builtin_amdgcn_readfirstlane(positionLoaded);
 
-    // the rotation of this wave's pairs, fetched while the weights stream in
-    // (the pair index is the same in every lane: scalar loads)
-    const int position = *a.position;
+    // the rotation of this wave's pairs, fetched while the weights stream in,
+    // with vector loads (every lane the same address), so that the norm's
+    // LDS waits below do not wait for them
     float cosine[kPairsPerWave], sine[kPairsPerWave];
 #pragma unroll
     for (int p = 0; p < kPairsPerWave; ++p) {
-        const int pair = __builtin_amdgcn_readfirstlane(firstPair + p);
+        const int pair = firstPair + p;
         const int64_t angle = (int64_t) position * half + (pair < pairs ? pair % half : 0);
-        cosine[p] = a.cosines[angle];
-        sine[p] = a.sines[angle];
+        cosine[p] = __builtin_nontemporal_load(a.cosines + angle);
+        sine[p] = __builtin_nontemporal_load(a.sines + angle);
     }
 
     norm_q8_finish(slice, a.width, a.epsilon, row, sPartial, a.debug_normalised, a.debug_q8);
@@ -307,11 +325,11 @@ struct SplitPlan {
     int splits, perSplit;
 };
 
-// Whole rounds a split, as few as kDecodeSplits splits allow.
-__device__ inline SplitPlan plan_splits(int keyCount)
+// Whole rounds a split, as few as the launch's gridSplits splits allow.
+__device__ inline SplitPlan plan_splits(int keyCount, int gridSplits)
 {
     const int roundsPerSplit =
-        (keyCount + kRoundKeys * kDecodeSplits - 1) / (kRoundKeys * kDecodeSplits);
+        (keyCount + kRoundKeys * gridSplits - 1) / (kRoundKeys * gridSplits);
     const int perSplit = roundsPerSplit * kRoundKeys;
     return {(keyCount + perSplit - 1) / perSplit, perSplit};
 }
@@ -400,7 +418,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
     for (int g = 0; g < G; ++g)
         kvOffset[g] = ((h0 + g) / perKv) * hd + c0;
 
-    // While at most kDecodeSplits rounds of keys are attended, split s is the
+    // While at most grid_splits rounds of keys are attended, split s is the
     // one round [64 s, 64 s + 64): its rows are loaded before the position
     // arrives (rows past the position are read, inside the cache, and never
     // used), so the two loads do not wait on each other.
@@ -420,8 +438,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
     asm volatile("" ::: "memory");
 
     const int keyCount = *a.position + 1;
-    const SplitPlan plan = plan_splits(keyCount);
-    if (split >= plan.splits)
+    const SplitPlan plan = plan_splits(keyCount, a.grid_splits);
+    // a launch too small for its step's keys (the host sizes it to the range:
+    // attention_grid_splits) would overrun sScore; it does nothing instead
+    if (split >= plan.splits || plan.perSplit > kMaxSplitKeys)
         return;
     const int k0 = split * plan.perSplit;
     const int n = min(plan.perSplit, keyCount - k0);
@@ -552,8 +572,6 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
         store_agent(a.ws_ml + (split * heads + h0 + t) * 2, sMax[t]);
         store_agent(a.ws_ml + (split * heads + h0 + t) * 2 + 1, sSum[t]);
     }
-    if (a.partials_only && plan.splits <= kAttnMergeSplits)
-        return; // o_merge_kernel merges them after this launch
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // the stores have completed
     __syncthreads();
     if (t == 0)
@@ -563,8 +581,17 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
     if (!sLast)
         return;
 
-    // the merge of the group's splits: wave g takes head h0 + g
+    // the merge of the group's splits: wave g takes head h0 + g.  The first
+    // batch of partials is requested together with the (max, sum) pairs, so
+    // the merge waits on one round trip.
     const int splits = plan.splits;
+    const bool merging = t < ((groupWidth + 63) / 64) * 64; // whole waves, for the block reductions
+    double part[kMergeBatch];
+    if (merging)
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u)
+            part[u] = (u < splits && t < groupWidth)
+                          ? load_agent(a.ws_o + (int64_t) u * qWidth + h0 * hd + t) : 0.0;
     if (wave < G) {
         const bool liveSplit = lane < splits;
         const int sp = liveSplit ? lane : 0;
@@ -578,16 +605,16 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
             sSum[wave] = total;
     }
     __syncthreads();
-    if (t >= ((groupWidth + 63) / 64) * 64)
-        return; // whole waves remain for the block reductions
+    if (!merging)
+        return;
     const int g = min(t / hd, G - 1);
     double weighted = 0.0;
     for (int s0 = 0; s0 < splits; s0 += kMergeBatch) {
-        double part[kMergeBatch];
+        if (s0 > 0)
 #pragma unroll
-        for (int u = 0; u < kMergeBatch; ++u)
-            part[u] = (s0 + u < splits && t < groupWidth)
-                          ? load_agent(a.ws_o + (int64_t) (s0 + u) * qWidth + h0 * hd + t) : 0.0;
+            for (int u = 0; u < kMergeBatch; ++u)
+                part[u] = (s0 + u < splits && t < groupWidth)
+                              ? load_agent(a.ws_o + (int64_t) (s0 + u) * qWidth + h0 * hd + t) : 0.0;
 #pragma unroll
         for (int u = 0; u < kMergeBatch; ++u)
             if (s0 + u < splits)
@@ -610,159 +637,6 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
         __hip_atomic_store(a.counter + group, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// ---- o_proj with the attention merge ---------------------------------------------
-// A workgroup of eight waves owns 16 rows of o (two a wave).  It issues its
-// weight loads, then merges the attention splits of every head exactly as the
-// attention kernel's last workgroup would (MultiQueryAttention.h:43-49: the
-// splits rescaled to the row maximum, in split order, the sums divided by the
-// total), quantizes the attention row into LDS (thread t owns elements
-// 4 t .. 4 t + 3, eight threads a 32-block) and takes its rows of the product
-// (Linear.h:284-298, + residual).  Every workgroup repeats the merge; it
-// saves the attention kernel's ticket, its last workgroup's reads and a
-// dependent round of stores.
-constexpr int kOMergeThreads = 512;
-constexpr int kOMergeRows = 16;
-constexpr int kOMergeBatch = 8; // splits a thread loads at once; two batches in flight
-
-__global__ __launch_bounds__(kOMergeThreads) __attribute__((amdgpu_waves_per_eu(2)))
-void o_merge_kernel(OMergeArgs a)
-{
-    __shared__ RowQ8 row;
-    __shared__ double sFactor[kOMergeMaxHeads][kDecodeSplits];
-    __shared__ double sTotal[kOMergeMaxHeads];
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int hd = a.head_dim, heads = a.heads, qWidth = heads * hd, nb = qWidth / kBlock;
-    const int W = a.width;
-    const int r0 = blockIdx.x * kOMergeRows + wave * 2;
-    const bool valid = lane < nb;
-    // loads in the order they are consumed (a wave's loads complete in
-    // order): the (max, sum) pairs, the partials, the o rows, the residual.
-    // Thread t's four elements of the attention row: the partials of the first
-    // kOMergeBatch splits, and every split's (max, sum), are loaded before the
-    // position (so the split count) arrives; unused ones are never read
-    const bool live = t * 4 < qWidth;
-    const int e0 = live ? t * 4 : 0;
-    const int h = e0 / hd;
-    // two batches of partials (the partials were stored by the previous launch)
-    double2 partA[kOMergeBatch][2], partB[kOMergeBatch][2];
-    auto load_batch = [&](double2 (&part)[kOMergeBatch][2], int s0, int last) {
-#pragma unroll
-        for (int u = 0; u < kOMergeBatch; ++u) {
-            const int sp = min(s0 + u, last);
-            const double2 *src = reinterpret_cast<const double2 *>(a.ws_o + (int64_t) sp * qWidth + e0);
-            part[u][0] = src[0];
-            part[u][1] = src[1];
-        }
-    };
-    // wave w takes heads w, w + 8, ...: lane sp holds split sp's (max, sum)
-    constexpr int kHeadsPerWave = kOMergeMaxHeads / (kOMergeThreads / 64);
-    double2 ml[kHeadsPerWave];
-#pragma unroll
-    for (int k = 0; k < kHeadsPerWave; ++k) {
-        const int hh = min(wave + k * (kOMergeThreads / 64), heads - 1);
-        ml[k] = *reinterpret_cast<const double2 *>(a.ws_ml + (lane * heads + hh) * 2);
-    }
-    load_batch(partA, 0, kDecodeSplits - 1);
-    WeightBlock w[2];
-#pragma unroll
-    for (int k = 0; k < 2; ++k)
-        w[k] = load_block(a.weights, W, qWidth, r0 + k, lane, valid && r0 + k < W);
-    const int r = r0 + row_of_lane<2>(lane);
-    const bool stores = stores_row<2>(lane) && r < W;
-    const float old = a.hidden[stores ? r : 0]; // the residual, read with the rest
-    __builtin_amdgcn_sched_barrier(0);
-    const int splits = plan_splits(*a.position + 1).splits;
-    // this lane's 32-block of the attention row and the product of its rows
-    auto product = [&](const int4 &x0, const int4 &x1, double sx) {
-        double y[2];
-#pragma unroll
-        for (int k = 0; k < 2; ++k)
-            y[k] = block_term(w[k], x0, x1, sx);
-        const double total = reduce_rows<2>(y, lane);
-        if (stores)
-            a.hidden[r] = (float) (total + (double) old);
-    };
-    if (splits > kAttnMergeSplits) {
-        // the attention kernel has merged the splits: its Q8 row (every wave alike)
-        int4 x0 = make_int4(0, 0, 0, 0), x1 = x0;
-        double sx = 0.0;
-        if (valid) {
-            x0 = reinterpret_cast<const int4 *>(a.q8_row + lane * kBlock)[0];
-            x1 = reinterpret_cast<const int4 *>(a.q8_row + lane * kBlock)[1];
-            sx = (double) half_value(reinterpret_cast<const uint16_t *>(a.q8_row + qWidth)[lane]);
-        }
-        product(x0, x1, sx);
-        return;
-    }
-#pragma unroll
-    for (int k = 0; k < kHeadsPerWave; ++k) {
-        const int hh = wave + k * (kOMergeThreads / 64);
-        if (hh < heads) {
-            double total;
-            const double f = merge_factor(ml[k].x, ml[k].y, lane < splits, total);
-            sFactor[hh][lane] = f;
-            if (lane == 0)
-                sTotal[hh] = total;
-        }
-    }
-    __syncthreads();
-
-    // the merged elements, in split order, then their Q8; past the first batch
-    // the next one is in flight while one is folded
-    if (splits > kOMergeBatch)
-        load_batch(partB, kOMergeBatch, splits - 1);
-    double weighted[4] = {0.0, 0.0, 0.0, 0.0};
-    auto fold = [&](const double2 (&part)[kOMergeBatch][2], int s0) {
-#pragma unroll
-        for (int u = 0; u < kOMergeBatch; ++u)
-            if (s0 + u < splits) {
-                const double f = sFactor[h][s0 + u];
-                weighted[0] += part[u][0].x * f;
-                weighted[1] += part[u][0].y * f;
-                weighted[2] += part[u][1].x * f;
-                weighted[3] += part[u][1].y * f;
-            }
-    };
-    for (int s0 = 0; s0 < splits; s0 += 2 * kOMergeBatch) {
-        fold(partA, s0);
-        if (s0 + 2 * kOMergeBatch < splits)
-            load_batch(partA, s0 + 2 * kOMergeBatch, splits - 1);
-        fold(partB, s0 + kOMergeBatch);
-        if (s0 + 3 * kOMergeBatch < splits)
-            load_batch(partB, s0 + 3 * kOMergeBatch, splits - 1);
-    }
-    float v[4];
-    float amax = 0.f;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        v[k] = live ? (float) (weighted[k] / sTotal[h]) : 0.f;
-        amax = fmaxf(amax, fabsf(v[k]));
-    }
-    amax = max_lanes<kBlock / 4 / 2>(amax);
-    const uint16_t bits = scale_bits_from_amax(amax);
-    const float sc = half_value(bits);
-    const float inverse = bits ? quantize_hint(sc) : 0.f;
-    if (live) {
-        int packed = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            packed |= ((bits ? quantize_value(v[k], sc, inverse) : 0) & 0xFF) << (8 * k);
-        __builtin_memcpy(row.q + e0, &packed, 4);
-        if ((t & 7) == 0)
-            row.scale[e0 / kBlock] = (double) sc;
-    }
-    __syncthreads();
-
-    int4 a0 = make_int4(0, 0, 0, 0), a1 = a0;
-    double sa = 0.0;
-    if (valid) {
-        a0 = reinterpret_cast<const int4 *>(row.q + lane * kBlock)[0];
-        a1 = reinterpret_cast<const int4 *>(row.q + lane * kBlock)[1];
-        sa = row.scale[lane];
-    }
-    product(a0, a1, sa);
-}
-
 // ---- gate|up + GeGLU + Q8 -----------------------------------------------------------
 // A workgroup of eight waves owns one 32-element block of the GeGLU output:
 // gate rows [32 b, 32 b + 32) and the matching up rows; a wave owns four of
@@ -771,30 +645,39 @@ constexpr int kGluThreads = 512;
 constexpr int kGluWaves = kGluThreads / 64;
 constexpr int kGluPerWave = kBlock / kGluWaves; // 4
 
-__global__ __launch_bounds__(kGluThreads) __attribute__((amdgpu_waves_per_eu(4)))
-void gateup_geglu_kernel(GateUpArgs a)
+// Element t of one activation block (thread t < 32): the GeGLU value and its
+// Int8Blocks byte and block scale.
+struct ActElement {
+    float v;
+    int q;
+    uint16_t bits;
+};
+
+// The body both gate|up launches share: the post-attention norm of the
+// residual row and its Q8 in LDS (issued before the weight loads), the gate
+// rows [32 b, 32 b + 32) and the matching up rows of block b = blockIdx.x,
+// GeGLU and the block's Q8.  Thread t < 32 gets element t.
+__device__ __attribute__((always_inline)) inline ActElement
+gateup_geglu_block(const float *hidden, const float *normWeight, int width, float epsilon,
+                   const uint8_t *weights, int F, RowQ8 &row, double *sPartial, float *sGate,
+                   float *sUp)
 {
-    __shared__ RowQ8 row;
-    __shared__ double sPartial[kGluWaves];
-    __shared__ float sGate[kBlock], sUp[kBlock];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int nb = a.width / kBlock;
-    const int F = a.intermediate;
+    const int nb = width / kBlock;
     const int o0 = blockIdx.x * kBlock + wave * kGluPerWave;
     const bool valid = lane < nb;
 
-    const RowSlice<4> slice = load_row_slice<4>(a.hidden, nullptr, nullptr, 0, 0.f, nullptr,
-                                                a.norm_weight, a.width);
+    const RowSlice<4> slice = load_row_slice<4>(hidden, nullptr, nullptr, 0, 0.f, nullptr,
+                                                normWeight, width);
     // rows 0..3 gate, 4..7 up
     WeightBlock w[2 * kGluPerWave];
 #pragma unroll
     for (int k = 0; k < kGluPerWave; ++k) {
-        w[k] = load_block(a.weights, 2 * (int64_t) F, a.width, o0 + k, lane, valid);
-        w[kGluPerWave + k] =
-            load_block(a.weights, 2 * (int64_t) F, a.width, (int64_t) F + o0 + k, lane, valid);
+        w[k] = load_block(weights, 2 * (int64_t) F, width, o0 + k, lane, valid);
+        w[kGluPerWave + k] = load_block(weights, 2 * (int64_t) F, width, (int64_t) F + o0 + k, lane, valid);
     }
     __builtin_amdgcn_sched_barrier(0); // every load issued before the norm's first wait
-    norm_q8_finish(slice, a.width, a.epsilon, row, sPartial, nullptr, nullptr);
+    norm_q8_finish(slice, width, epsilon, row, sPartial, nullptr, nullptr);
     int4 a0 = make_int4(0, 0, 0, 0), a1 = a0;
     double sa = 0.0;
     if (valid) {
@@ -816,18 +699,33 @@ void gateup_geglu_kernel(GateUpArgs a)
             sUp[o] = (float) total;
     }
     __syncthreads();
+    ActElement e{0.f, 0, 0};
+    if (threadIdx.x < kBlock) {
+        e.v = geglu(sGate[threadIdx.x], sUp[threadIdx.x]);
+        float amax = fabsf(e.v);
+        amax = max_lanes<16>(amax);
+        e.bits = scale_bits_from_amax(amax);
+        const float sc = half_value(e.bits);
+        e.q = e.bits ? quantize_value(e.v, sc, quantize_hint(sc)) : 0;
+    }
+    return e;
+}
+
+__global__ __launch_bounds__(kGluThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void gateup_geglu_kernel(GateUpArgs a)
+{
+    __shared__ RowQ8 row;
+    __shared__ double sPartial[kGluWaves];
+    __shared__ float sGate[kBlock], sUp[kBlock];
+    const ActElement e = gateup_geglu_block(a.hidden, a.norm_weight, a.width, a.epsilon, a.weights,
+                                            a.intermediate, row, sPartial, sGate, sUp);
     if (threadIdx.x < kBlock) {
         const int o = blockIdx.x * kBlock + threadIdx.x;
-        const float v = geglu(sGate[threadIdx.x], sUp[threadIdx.x]);
         if (a.debug_activated)
-            a.debug_activated[o] = v;
-        float amax = fabsf(v);
-        amax = max_lanes<16>(amax);
-        const uint16_t bits = scale_bits_from_amax(amax);
-        const float sc = half_value(bits);
-        a.q8[o] = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, quantize_hint(sc)) : 0);
+            a.debug_activated[o] = e.v;
+        a.q8[o] = (uint8_t) (int8_t) e.q;
         if (threadIdx.x == 0)
-            reinterpret_cast<uint16_t *>(a.q8 + F)[blockIdx.x] = bits;
+            reinterpret_cast<uint16_t *>(a.q8 + a.intermediate)[blockIdx.x] = e.bits;
     }
 }
 
@@ -1879,9 +1777,26 @@ hipError_t launch_qkv_rope(const QkvArgs &a, hipStream_t stream)
 {
     const int pairs = (a.heads + 2 * a.kv_heads) * (a.head_dim / 2);
     const int perGroup = kWaves * kPairsPerWave;
-    hipLaunchKernelGGL(qkv_rope_kernel, dim3((pairs + perGroup - 1) / perGroup), dim3(kThreads), 0,
-                       stream, a);
+    const dim3 grid((pairs + perGroup - 1) / perGroup);
+    if (a.embedding)
+        hipLaunchKernelGGL(qkv_rope_kernel<true>, grid, dim3(kThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL(qkv_rope_kernel<false>, grid, dim3(kThreads), 0, stream, a);
     return hipGetLastError();
+}
+
+int attention_grid_splits(int keyCount)
+{
+    for (int splits = 16; splits < kDecodeSplits; splits *= 2)
+        if (keyCount <= splits * kRoundKeys)
+            return splits;
+    return kDecodeSplits;
+}
+
+int attention_key_range(int keyCount, int maxPositions)
+{
+    const int splits = attention_grid_splits(keyCount);
+    return splits < kDecodeSplits ? splits * kRoundKeys : maxPositions;
 }
 
 hipError_t launch_attention(const AttentionArgs &a, hipStream_t stream)
@@ -1890,7 +1805,9 @@ hipError_t launch_attention(const AttentionArgs &a, hipStream_t stream)
     if (!attention_layout(a.head_dim, &channels, &group) || a.heads % group != 0 || !a.q8
         || !a.counter)
         return hipErrorInvalidValue;
-    const dim3 grid(kDecodeSplits, a.heads / group);
+    if (a.grid_splits < 1 || a.grid_splits > kDecodeSplits)
+        return hipErrorInvalidValue;
+    const dim3 grid(a.grid_splits, a.heads / group);
     if (channels == 4)
         hipLaunchKernelGGL((attention_kernel<4, 1>), grid, dim3(kAttnThreads), 0, stream, a);
     else if (channels == 2)
@@ -1899,22 +1816,6 @@ hipError_t launch_attention(const AttentionArgs &a, hipStream_t stream)
         hipLaunchKernelGGL((attention_kernel<1, 1>), grid, dim3(kAttnThreads), 0, stream, a);
     else
         hipLaunchKernelGGL((attention_kernel<1, 2>), grid, dim3(kAttnThreads), 0, stream, a);
-    return hipGetLastError();
-}
-
-bool o_merge_supported(int heads, int head_dim)
-{
-    const int qWidth = heads * head_dim;
-    return heads <= kOMergeMaxHeads && qWidth % kBlock == 0 && qWidth <= kFusedMaxWidth
-           && qWidth <= 4 * kOMergeThreads && head_dim % 4 == 0;
-}
-
-hipError_t launch_o_merge(const OMergeArgs &a, hipStream_t stream)
-{
-    if (!o_merge_supported(a.heads, a.head_dim) || a.width <= 0 || !a.q8_row)
-        return hipErrorInvalidValue;
-    const int grid = (a.width + kOMergeRows - 1) / kOMergeRows;
-    hipLaunchKernelGGL(o_merge_kernel, dim3(grid), dim3(kOMergeThreads), 0, stream, a);
     return hipGetLastError();
 }
 

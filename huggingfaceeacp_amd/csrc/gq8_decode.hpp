@@ -47,29 +47,19 @@ struct AttentionArgs {
     int *counter;             // one a head group (kDecodeCounters), zero between launches
     float *out;               // optional fp32 row
     uint8_t *q8;              // Q8 row for o_proj
-    int partials_only;        // nonzero: up to kAttnMergeSplits splits, store the partials and
-                              // stop (o_merge merges them); more, merge here as without it
+    int grid_splits;          // the launch's key splits (attention_grid_splits of the step's
+                              // key-count range)
 };
 
-// Rows with more splits than this are merged once by the attention kernel
-// (its last workgroup of a head group), and o_merge reads the merged Q8 row:
-// past it, the merge each o workgroup would repeat costs more than the
-// attention kernel's ticket.  Both kernels decide from the device position.
-constexpr int kAttnMergeSplits = 16;
-
-// o_proj fed by the attention partials: every workgroup merges the splits
-// itself (the same arithmetic as the attention kernel's merge), quantizes the
-// attention row into LDS and takes its rows of the product (+ residual).
-constexpr int kOMergeMaxHeads = 16;
-struct OMergeArgs {
-    const double *ws_o, *ws_ml;  // the attention kernel's partials
-    const int *position;
-    int heads, head_dim;
-    const uint8_t *weights;      // o, Int8Blocks [width, heads * head_dim]
-    int width;
-    float *hidden;               // residual row, updated in place
-    const uint8_t *q8_row;       // the attention kernel's merged Q8 row (past kAttnMergeSplits)
-};
+// Key splits of the one-token attention launch for steps of at most
+// `keyCount` keys: the fewest of 16, 32 and kDecodeSplits that give every
+// split at most one 64-key round (64 past 4096 keys).  Splits past the
+// step's keys exit after their speculative first-round loads, so a launch
+// sized to the range keeps those loads few.  A captured step replays within
+// the range it was captured for (attention_key_range).
+int attention_grid_splits(int keyCount);
+// The largest key count of the range that `keyCount` falls in.
+int attention_key_range(int keyCount, int maxPositions);
 
 struct GateUpArgs {
     const float *hidden;
@@ -218,8 +208,6 @@ size_t decode_workspace_bytes(int heads, int head_dim);
 
 hipError_t launch_qkv_rope(const QkvArgs &a, hipStream_t stream);
 hipError_t launch_attention(const AttentionArgs &a, hipStream_t stream);
-bool o_merge_supported(int heads, int head_dim);
-hipError_t launch_o_merge(const OMergeArgs &a, hipStream_t stream);
 hipError_t launch_gateup_geglu(const GateUpArgs &a, hipStream_t stream);
 hipError_t launch_final_norm(const HeadArgs &a, hipStream_t stream);    // one workgroup
 hipError_t launch_lmhead_argmax(const HeadArgs &a, hipStream_t stream); // logits + packed maximum

@@ -614,8 +614,12 @@ struct gq8_decoder {
     void *sampleWorkspace = nullptr;
     size_t sampleWorkspaceBytes = 0;
 
-    hipGraphExec_t graph = nullptr;
+    // the captured one-token step, one a key-count range (the attention
+    // launch is sized to its range: gq8::attention_grid_splits)
+    static constexpr int kGraphRanges = 3;
+    hipGraphExec_t graphs[kGraphRanges] = {};
     bool capturing = false;
+    int captureKeys = 0; // while capturing: the largest key count of the range
 
     unsigned timing = 0; // bit s: bracket stage s with events
     struct Mark {
@@ -629,6 +633,15 @@ struct gq8_decoder {
 };
 
 namespace {
+
+void drop_graphs(gq8_decoder *d)
+{
+    for (hipGraphExec_t &g : d->graphs)
+        if (g) {
+            (void) hipGraphExecDestroy(g);
+            g = nullptr;
+        }
+}
 
 bool sampled(const gq8_decoder *d)
 {
@@ -771,8 +784,7 @@ extern "C" void gq8_decoder_destroy(gq8_decoder *d)
 {
     if (!d)
         return;
-    if (d->graph)
-        (void) hipGraphExecDestroy(d->graph);
+    drop_graphs(d);
     if (d->stream)
         (void) hipStreamSynchronize(d->stream);
     for (auto &m : d->marks) {
@@ -1316,10 +1328,7 @@ extern "C" int gq8_decoder_set_sampling(gq8_decoder *d, const gq8_sampling *opti
         GQ8_HIP(hipMemcpy(d->drawIndex, &zero, sizeof(int), hipMemcpyHostToDevice));
     }
     d->sampling = *options;
-    if (d->graph) { // a captured step keeps the chooser it was captured with
-        (void) hipGraphExecDestroy(d->graph);
-        d->graph = nullptr;
-    }
+    drop_graphs(d); // a captured step keeps the chooser it was captured with
     return GQ8_OK;
 }
 
@@ -1335,10 +1344,7 @@ extern "C" int gq8_decoder_set_flow(gq8_decoder *d, int enabled)
     if (enabled && !d->flowSupported)
         return fail(GQ8_ERR_SHAPE, "decoder_set_flow: the shape has no dataflow step");
     d->useFlow = enabled != 0;
-    if (d->graph) { // a captured step follows the path it was captured with
-        (void) hipGraphExecDestroy(d->graph);
-        d->graph = nullptr;
-    }
+    drop_graphs(d); // a captured step follows the path it was captured with
     return GQ8_OK;
 }
 
@@ -1349,10 +1355,7 @@ extern "C" int gq8_decoder_set_persistent(gq8_decoder *d, int enabled)
     if (enabled && !d->persistSupported)
         return fail(GQ8_ERR_SHAPE, "decoder_set_persistent: the shape or device has no persistent step");
     d->usePersist = enabled != 0;
-    if (d->graph) { // a captured step follows the path it was captured with
-        (void) hipGraphExecDestroy(d->graph);
-        d->graph = nullptr;
-    }
+    drop_graphs(d); // a captured step follows the path it was captured with
     return GQ8_OK;
 }
 
@@ -1361,10 +1364,7 @@ extern "C" int gq8_decoder_set_fused(gq8_decoder *d, int enabled)
     if (!d)
         return fail(GQ8_ERR_ARGUMENT, "null decoder");
     d->useFused = enabled != 0;
-    if (d->graph) { // a captured step follows the path it was captured with
-        (void) hipGraphExecDestroy(d->graph);
-        d->graph = nullptr;
-    }
+    drop_graphs(d); // a captured step follows the path it was captured with
     return GQ8_OK;
 }
 
@@ -1719,30 +1719,14 @@ int encode_fused_token(gq8_decoder *d, float *logits, bool sample)
         at.counter = d->counters;
         at.out = debugValues(1, l);
         at.q8 = d->x8;
-        // the o product merges the attention splits itself, except for the
-        // debug views, which need the merged row
-        const bool merged = !dbg && gq8::o_merge_supported(s.heads, s.head_dim);
-        at.partials_only = merged ? 1 : 0;
+        at.grid_splits = gq8::attention_grid_splits(d->capturing ? d->captureKeys
+                                                                  : d->hostPosition + 1);
         GQ8_STAGE(kStageAttention, gq8::launch_attention(at, st));
         if (dbg && copy_last_q8_row(d, d->x8, 1, d->qWidth, debugQ8(1, l)))
             return GQ8_ERR_DEVICE;
 
-        if (merged) {
-            gq8::OMergeArgs om{};
-            om.ws_o = d->decodeO;
-            om.ws_ml = d->decodeMl;
-            om.position = d->position;
-            om.heads = s.heads;
-            om.head_dim = s.head_dim;
-            om.weights = d->out[l];
-            om.width = W;
-            om.hidden = d->hidden;
-            om.q8_row = d->x8;
-            GQ8_STAGE(kStageO, gq8::launch_o_merge(om, st));
-        } else {
-            GQ8_STAGE(kStageO, gq8::launch_q8_product(d->x8, 1, 0, 1, d->out[l], d->qWidth, W,
-                                                      d->hidden, W, 1, st));
-        }
+        GQ8_STAGE(kStageO, gq8::launch_q8_product(d->x8, 1, 0, 1, d->out[l], d->qWidth, W,
+                                                  d->hidden, W, 1, st));
 
         gq8::GateUpArgs g{};
         g.hidden = d->hidden;
@@ -1966,17 +1950,32 @@ extern "C" int gq8_decoder_debug(gq8_decoder *d, int which, int layer, float *ho
 // ============================================================================
 namespace {
 
-int ensure_graph(gq8_decoder *d)
+// The captured step for steps of `keyCount` keys: one graph a key-count
+// range, captured on first use.
+int graph_range(const gq8_decoder *d, int keyCount)
 {
-    if (d->graph)
+    const int splits = gq8::attention_grid_splits(keyCount);
+    int range = 0;
+    for (int s = 16; s < splits && range + 1 < gq8_decoder::kGraphRanges; s *= 2)
+        ++range;
+    (void) d;
+    return range;
+}
+
+int ensure_graph(gq8_decoder *d, int keyCount)
+{
+    const int range = graph_range(d, keyCount);
+    if (d->graphs[range])
         return GQ8_OK;
     // One decode step reads its token and position from device memory and
-    // advances the position itself, so the same graph replays at every step.
+    // advances the position itself, so the same graph replays at every step
+    // of its key-count range.
     hipGraph_t graph = nullptr;
     GQ8_HIP(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
     const bool debug = d->debug;
     d->debug = false;
     d->capturing = true;
+    d->captureKeys = gq8::attention_key_range(keyCount, d->shape.max_positions);
     const int status = encode_step(d, 1, d->logits, 1, true);
     d->capturing = false;
     d->debug = debug;
@@ -1988,11 +1987,24 @@ int ensure_graph(gq8_decoder *d)
     }
     if (end != hipSuccess)
         return fail(GQ8_ERR_DEVICE, std::string("hipStreamEndCapture: ") + hipGetErrorString(end));
-    hipError_t inst = hipGraphInstantiate(&d->graph, graph, nullptr, nullptr, 0);
+    hipError_t inst = hipGraphInstantiate(&d->graphs[range], graph, nullptr, nullptr, 0);
     (void) hipGraphDestroy(graph);
     if (inst != hipSuccess) {
-        d->graph = nullptr;
+        d->graphs[range] = nullptr;
         return fail(GQ8_ERR_DEVICE, std::string("hipGraphInstantiate: ") + hipGetErrorString(inst));
+    }
+    return GQ8_OK;
+}
+
+// Captures, before a run, the graphs of every key-count range its decode
+// steps [firstKeys, lastKeys] touch, so no capture falls inside the run.
+int ensure_graphs(gq8_decoder *d, int firstKeys, int lastKeys)
+{
+    lastKeys = std::min(lastKeys, d->shape.max_positions);
+    for (int keys = std::max(firstKeys, 1); keys <= lastKeys;) {
+        if (int st = ensure_graph(d, keys))
+            return st;
+        keys = gq8::attention_key_range(keys, d->shape.max_positions) + 1;
     }
     return GQ8_OK;
 }
@@ -2002,7 +2014,9 @@ int decode_one(gq8_decoder *d, bool useGraph)
     if (int s = check_step(d, 1))
         return s;
     if (useGraph) {
-        GQ8_HIP(hipGraphLaunch(d->graph, d->stream));
+        if (int s = ensure_graph(d, d->hostPosition + 1))
+            return s;
+        GQ8_HIP(hipGraphLaunch(d->graphs[graph_range(d, d->hostPosition + 1)], d->stream));
     } else if (int s = encode_step(d, 1, d->logits, 1, true)) {
         return s;
     }
@@ -2054,12 +2068,11 @@ extern "C" int gq8_generate_streaming(gq8_decoder *d, const int32_t *prompt, int
     if (int st = gq8_decoder_begin_sequence(d))
         return st;
     GQ8_HIP(hipMemcpy(d->sequence, prompt, prompt_length * sizeof(uint32_t), hipMemcpyHostToDevice));
-    if (use_graph)
-        if (int st = ensure_graph(d))
-            return st;
-
     const int window = s.max_positions - prompt_length;
     const int limit = max_tokens > 0 ? std::min(max_tokens, window) : window;
+    if (use_graph) // the decode steps attend prompt_length + 1 .. prompt_length + limit keys
+        if (int st = ensure_graphs(d, prompt_length + 1, prompt_length + limit))
+            return st;
     gq8_run_stats local{};
     int steps = 0;
 
@@ -2169,7 +2182,7 @@ extern "C" int gq8_decoder_decode(gq8_decoder *d, int steps, int use_graph)
     if (d->hostPosition + steps > d->shape.max_positions)
         return fail(GQ8_ERR_WINDOW, "decoder_decode: the steps would pass the window");
     if (use_graph)
-        if (int st = ensure_graph(d))
+        if (int st = ensure_graphs(d, d->hostPosition + 1, d->hostPosition + steps))
             return st;
     for (int i = 0; i < steps; ++i)
         if (int st = decode_one(d, use_graph != 0))
