@@ -314,7 +314,7 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
             const float sc = half_value(bits);
             const int j = blockIdx.x * 2 * kRowsTile + jj;
             if (m < a.rows) {
-                a.geglu8[(int64_t) m * F + j] = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, quantize_hint(sc)) : 0);
+                a.geglu8[(int64_t) m * F + j] = (uint8_t) (int8_t) quantize_in_block(v, bits, sc, quantize_hint(sc));
                 if (jj == 0)
                     scales[(int64_t) m * (F / kBlock) + j / kBlock] = bits;
             }
@@ -673,7 +673,7 @@ __global__ __launch_bounds__(kRowsThreads) void attention_merge_rows_kernel(Rows
     const float amax = max_lanes<16>(fabsf(v)); // a 32-block is 32 consecutive lanes
     const uint16_t bits = scale_bits_from_amax(amax);
     const float sc = half_value(bits);
-    a.q8[(int64_t) seq * qW + o] = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, quantize_hint(sc)) : 0);
+    a.q8[(int64_t) seq * qW + o] = (uint8_t) (int8_t) quantize_in_block(v, bits, sc, quantize_hint(sc));
     if ((t & 31) == 0)
         reinterpret_cast<uint16_t *>(a.q8 + (int64_t) a.q8_rows * qW)[(int64_t) seq * (qW / kBlock)
                                                                       + o / kBlock] = bits;

@@ -156,7 +156,7 @@ __device__ void norm_q8_finish(const RowSlice<E> &r, int width, float epsilon, R
     int packed[E / 4] = {};
 #pragma unroll
     for (int k = 0; k < E; ++k) {
-        const int q = bits ? quantize_value(n[k], s, inverse) : 0;
+        const int q = quantize_in_block(n[k], bits, s, inverse);
         packed[k / 4] |= (q & 0xFF) << (8 * (k % 4));
     }
     const bool first = (t % (kBlock / E)) == 0; // the block's first thread
@@ -629,7 +629,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
     if (t < groupWidth) { // whole 32-blocks: groupWidth is a multiple of 32
         const uint16_t bits = scale_bits_from_amax(amax);
         const float sc = half_value(bits);
-        a.q8[idx] = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, quantize_hint(sc)) : 0);
+        a.q8[idx] = (uint8_t) (int8_t) quantize_in_block(v, bits, sc, quantize_hint(sc));
         if ((t & 31) == 0)
             reinterpret_cast<uint16_t *>(a.q8 + qWidth)[idx / kBlock] = bits;
     }
@@ -706,7 +706,7 @@ gateup_geglu_block(const float *hidden, const float *normWeight, int width, floa
         amax = max_lanes<16>(amax);
         e.bits = scale_bits_from_amax(amax);
         const float sc = half_value(e.bits);
-        e.q = e.bits ? quantize_value(e.v, sc, quantize_hint(sc)) : 0;
+        e.q = quantize_in_block(e.v, e.bits, sc, quantize_hint(sc));
     }
     return e;
 }
@@ -1416,7 +1416,7 @@ __device__ __forceinline__ void flow_attention(const FlowArgs &a, int l, int ite
     amax = max_lanes<16>(amax);
     const uint16_t bits = scale_bits_from_amax(amax);
     const float sc = half_value(bits);
-    const uint8_t byte = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, quantize_hint(sc)) : 0);
+    const uint8_t byte = (uint8_t) (int8_t) quantize_in_block(v, bits, sc, quantize_hint(sc));
     flow_put_q8(a.attn_ll, qWidth, idx, byte, bits, live, tag);
 }
 
@@ -1503,7 +1503,7 @@ __device__ __forceinline__ void flow_gateup(const FlowArgs &a, int l, int item, 
         amax = max_lanes<16>(amax);
         const uint16_t bits = scale_bits_from_amax(amax);
         const float sc = half_value(bits);
-        const uint8_t byte = (uint8_t) (int8_t) (bits ? quantize_value(v, sc, quantize_hint(sc)) : 0);
+        const uint8_t byte = (uint8_t) (int8_t) quantize_in_block(v, bits, sc, quantize_hint(sc));
         flow_put_q8(a.act_ll, F, o, byte, bits, live, word_tag(epoch, l));
     }
 }

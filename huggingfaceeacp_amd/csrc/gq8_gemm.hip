@@ -237,7 +237,7 @@ void q8_gemm_kernel(
             uint32_t packed[2] = {0u, 0u};
 #pragma unroll
             for (int k = 0; k < 8; ++k)
-                packed[k / 4] |= (uint32_t) (uint8_t) (int8_t) (bits ? quantize_value(v[k], sc, inv) : 0)
+                packed[k / 4] |= (uint32_t) (uint8_t) (int8_t) quantize_in_block(v[k], bits, sc, inv)
                                  << (8 * (k % 4));
             *reinterpret_cast<uint2 *>(q8_out + (int64_t) m * F + o0) = make_uint2(packed[0], packed[1]);
             if ((t & 3) == 0)

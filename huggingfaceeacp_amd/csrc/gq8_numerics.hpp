@@ -54,23 +54,30 @@ GQ8_HD uint16_t scale_bits_from_amax(float amax)
 // quotient; it is found here without a division: a candidate from the fp32
 // product x * (1 / s) is within one of it, and the exact fp32 products
 // (k +- 0.5) * s (at most 10 + 11 significant bits) say which side of each
-// boundary x lies on.  A NaN element is stored as zero.
+// boundary x lies on.  A NaN element is stored as zero.  Written without
+// branches: the two corrections exclude each other (hi > lo), and a kernel
+// quantizing several elements a thread then interleaves them instead of
+// running each element's branches in turn.
 GQ8_HD int quantize_value(float x, float scale, float inverse)
 {
 #pragma clang fp contract(off)
-    if (!(x == x))
-        return 0;
-    float k = rintf(x * inverse);
-    k = fminf(fmaxf(k, -256.f), 256.f);
+    const float k = fminf(fmaxf(rintf(x * inverse), -256.f), 256.f); // NaN x: -256, discarded
     const float hi = (k + 0.5f) * scale;
     const float lo = (k - 0.5f) * scale;
     const bool kOdd = ((int) k & 1) != 0;
-    if (x > hi || (x == hi && kOdd))
-        k += 1.f;
-    else if (x < lo || (x == lo && kOdd))
-        k -= 1.f;
-    k = fminf(fmaxf(k, -127.f), 127.f);
-    return (int) k;
+    const float up = (x > hi || (x == hi && kOdd)) ? 1.f : 0.f;
+    const float down = (x < lo || (x == lo && kOdd)) ? 1.f : 0.f;
+    const int q = (int) fminf(fmaxf(k + up - down, -127.f), 127.f);
+    return x == x ? q : 0;
+}
+
+// quantize_value of an element of a block whose fp16 scale bits are `bits`:
+// a block stored with a zero scale holds zero bytes.  The scale's test masks
+// the result rather than guarding the arithmetic, so the compiler does not
+// turn it into a branch around each element.
+GQ8_HD int quantize_in_block(float x, uint16_t bits, float scale, float inverse)
+{
+    return quantize_value(x, scale, inverse) & (bits ? -1 : 0);
 }
 
 // The candidate hint of quantize_value on the device: a reciprocal of the

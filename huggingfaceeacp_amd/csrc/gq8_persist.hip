@@ -389,7 +389,7 @@ __device__ __forceinline__ void quarter_q8(const float *row, const NormQuarter &
     uint32_t packed[2] = {0u, 0u};
 #pragma unroll
     for (int k = 0; k < 8; ++k)
-        packed[k / 4] |= (uint32_t) ((bits ? quantize_value(n[k], s, inverse) : 0) & 0xFF) << (8 * (k % 4));
+        packed[k / 4] |= (uint32_t) (quantize_in_block(n[k], bits, s, inverse) & 0xFF) << (8 * (k % 4));
     if (q.live) {
         *reinterpret_cast<uint2 *>(qBytes + e0) = make_uint2(packed[0], packed[1]);
         if (q.part == 0)
@@ -1034,7 +1034,7 @@ __device__ __forceinline__ bool merge_task(const PersistArgs &a, int l, int h, i
     amax = max_lanes<16>(amax);
     const uint16_t bits = scale_bits_from_amax(amax);
     const float sc = half_value(bits);
-    const int byte = bits ? quantize_value(v, sc, quantize_hint(sc)) : 0;
+    const int byte = quantize_in_block(v, bits, sc, quantize_hint(sc));
     put_q8(a.attn_ll, qWidth, ch, byte, bits, lane < kBlock, tag);
     return true;
 }
@@ -1149,7 +1149,7 @@ __device__ __forceinline__ bool phase_gateup(const PersistArgs &a, const Plan &p
             amax = max_lanes<16>(amax);
             const uint16_t bits = scale_bits_from_amax(amax);
             const float sc = half_value(bits);
-            const int byte = bits ? quantize_value(v, sc, quantize_hint(sc)) : 0;
+            const int byte = quantize_in_block(v, bits, sc, quantize_hint(sc));
             put_q8(a.act_ll, F, o, byte, bits, lane < kBlock, tag);
         }
     }

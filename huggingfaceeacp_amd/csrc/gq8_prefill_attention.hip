@@ -297,7 +297,7 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillAr
                 uint32_t word = 0;
 #pragma unroll
                 for (int b = 0; b < 4; ++b) {
-                    const int qv = bits ? quantize_value(v[4 * i + b], sc, inv) : 0;
+                    const int qv = quantize_in_block(v[4 * i + b], bits, sc, inv);
                     word |= (uint32_t) (uint8_t) (int8_t) qv << (8 * b);
                 }
                 packed[i] = word;
