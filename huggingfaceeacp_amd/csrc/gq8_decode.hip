@@ -123,7 +123,10 @@ __device__ void norm_q8_finish(const RowSlice<E> &r, int width, float epsilon, R
                                double *sPartial, float *normalised_out, uint8_t *q8_out)
 {
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int waves = blockDim.x / 64;
+    // a workgroup covers the widest row with E elements a thread; a compile-
+    // time count (reading blockDim would be a scalar load from the kernel's
+    // implicit arguments, waited for at the first barrier)
+    constexpr int waves = kFusedMaxWidth / E / 64;
     const int i0 = t * E;
     float v[E];
 #pragma unroll
@@ -385,6 +388,8 @@ __device__ inline double load_agent(const double *p)
 template <int C, int G>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a)
 {
+    GQ8_ARGS_EARLY("s"(a.grid_splits), "s"(a.scale), "s"(a.ws_o), "s"(a.ws_ml), "s"(a.counter),
+                   "s"(a.out), "s"(a.q8));
     constexpr int kRows = kScoreBatch * G; // reduce_rows width: (key, head) pairs
     __shared__ double sScore[G][kMaxSplitKeys];
     __shared__ double sAcc[kAttnWaves][kMaxGroupWidth];
@@ -714,6 +719,7 @@ gateup_geglu_block(const float *hidden, const float *normWeight, int width, floa
 __global__ __launch_bounds__(kGluThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void gateup_geglu_kernel(GateUpArgs a)
 {
+    GQ8_ARGS_EARLY("s"(a.q8), "s"(a.debug_activated));
     __shared__ RowQ8 row;
     __shared__ double sPartial[kGluWaves];
     __shared__ float sGate[kBlock], sUp[kBlock];
@@ -754,6 +760,7 @@ __global__ __launch_bounds__(kThreads) void final_norm_kernel(HeadArgs a)
 
 __global__ __launch_bounds__(kThreads) void lmhead_argmax_kernel(HeadArgs a)
 {
+    GQ8_ARGS_EARLY("s"(a.best), "s"(a.logits));
     __shared__ unsigned long long sBest[kWaves];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nb = a.width / kBlock;

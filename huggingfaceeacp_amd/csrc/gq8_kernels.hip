@@ -360,6 +360,7 @@ __global__ __launch_bounds__(kThreads) void q8_matvec_kernel(
     const uint8_t *__restrict__ x8, int64_t x_elements, int x_row, const uint8_t *__restrict__ w8,
     int inner, int outputs, float *__restrict__ y, int residual)
 {
+    GQ8_ARGS_EARLY("s"(y), "s"(residual));
     __shared__ double sPartial[kThreads / 64][U];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int group = wave / WPR, part = wave % WPR;

@@ -80,6 +80,12 @@ GQ8_HD int quantize_in_block(float x, uint16_t bits, float scale, float inverse)
     return quantize_value(x, scale, inverse) & (bits ? -1 : 0);
 }
 
+// Takes kernel arguments into scalar registers where it stands (kernel entry):
+// left to itself the compiler loads an argument just before its first use,
+// and a use late in a kernel then waits on a fresh scalar-cache line of the
+// argument segment, which a weight stream may have pushed out of the L2.
+#define GQ8_ARGS_EARLY(...) asm volatile("" ::__VA_ARGS__)
+
 // The candidate hint of quantize_value on the device: a reciprocal of the
 // fp16 scale good to an ulp (v_rcp_f32).  The exact boundary compares above
 // make the quantized value independent of the hint as long as the candidate
