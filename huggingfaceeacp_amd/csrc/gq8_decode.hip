@@ -292,9 +292,12 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a)
             values[half] = half_bits(fHi);
         }
     }
+    // the tag of the attention launch after this one
+    if (blockIdx.x == 0 && threadIdx.x == 0 && a.tag_epoch)
+        a.tag_epoch[0] += 1;
 }
 
-// ---- split-key attention, merged per head group by its last workgroup ---------
+// ---- split-key attention, merged per head group by its live splits -------------
 // The grid is (key split, head group).  A workgroup of eight waves owns the
 // keys [k0, k0 + n) of one split and the G heads of one group (G = 1 when a
 // head is at least a 32-element block wide, else the heads of one block).
@@ -307,22 +310,27 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a)
 //   softmax  wave g takes head g: the split's maximum, exp(s - max) and sum;
 //   values   the same keys (the first round's values still in registers);
 //            the eight waves' sums are added in LDS, in wave order.
-// The split's partial (double) is stored with agent-scope stores, which are
-// coherent across the chip's L2s, and the workgroup waits for them to
-// complete before taking its group's ticket; the last workgroup of a group
-// reads the partials with agent-scope loads.  No L2 write-back fence is
-// needed, which with hundreds of workgroups would cost more than the work.
-// The last workgroup merges the splits (MultiQueryAttention.h:43-49: every
-// split rescaled to the row maximum, the sums divided by the total), rounds
-// to fp32 and quantizes the group's 32-element blocks.  Scores, weights and
-// sums are double throughout.
+// The split's partial (double) and its (max, sum) are stored as tagged words
+// (a 32-bit half and the launch's tag in one single-copy-atomic agent-scope
+// store, coherent across the chip's L2s); the tag is an epoch the q|k|v
+// launch before advances, so no word is ever cleared.  The group's live
+// splits then merge its 32-channel blocks among themselves (split s takes
+// blocks s, s + splits, ...; a wave a block, a lane a channel): each polls
+// the words it needs until they carry the tag, with a bounded wait that sets
+// the error word when it gives up.  No workgroup takes a ticket or reads the
+// whole group's partials.  The merge (MultiQueryAttention.h:43-49: every
+// split rescaled to the row maximum in split order, the sums divided by the
+// total) rounds to fp32 and quantizes the block.  The splits of a launch
+// wait on each other, so its workgroups must be resident together: one a
+// compute unit at most, at the launch sizes used.  Scores, weights and sums
+// are double throughout.
 constexpr int kAttnThreads = 512;
 constexpr int kAttnWaves = kAttnThreads / 64;
 constexpr int kScoreBatch = 8;                          // keys a wave takes a round
 constexpr int kRoundKeys = kAttnWaves * kScoreBatch;    // 64
 constexpr int kMaxSplitKeys = 256;                      // so the window is at most 16384
 constexpr int kMaxGroupWidth = 256;                     // G * head_dim
-constexpr int kMergeBatch = 32;
+constexpr int kPollSplits = 16; // split partials a merging lane polls at once
 
 struct SplitPlan {
     int splits, perSplit;
@@ -375,27 +383,16 @@ __device__ inline double word_half(const uint32_t (&w)[(C + 1) / 2], int i)
     return (double) half_value((uint16_t) (w[i >> 1] >> (16 * (i & 1))));
 }
 
-__device__ inline void store_agent(double *p, double v)
-{
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ inline double load_agent(const double *p)
-{
-    return __hip_atomic_load(const_cast<double *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 template <int C, int G>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a)
 {
-    GQ8_ARGS_EARLY("s"(a.grid_splits), "s"(a.scale), "s"(a.ws_o), "s"(a.ws_ml), "s"(a.counter),
-                   "s"(a.out), "s"(a.q8));
+    GQ8_ARGS_EARLY("s"(a.grid_splits), "s"(a.scale), "s"(a.part_ll), "s"(a.ml_ll), "s"(a.tag_epoch),
+                   "s"(a.error), "s"(a.out), "s"(a.q8));
     constexpr int kRows = kScoreBatch * G; // reduce_rows width: (key, head) pairs
     __shared__ double sScore[G][kMaxSplitKeys];
     __shared__ double sAcc[kAttnWaves][kMaxGroupWidth];
     __shared__ double sMax[G], sSum[G];
     __shared__ double sSplitMax[G][kDecodeSplits];
-    __shared__ int sLast;
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int hd = a.head_dim, kvWidth = a.kv_heads * hd;
@@ -566,42 +563,74 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
                 sAcc[wave][g * hd + c0 + i] = acc[g][i];
     __syncthreads();
 
-    // the split's partial: the waves' sums in wave order, then (max, sum)
+    // the split's partial: the waves' sums in wave order, then (max, sum), as
+    // tagged words (two a double) that the merging workgroups poll
+    const uint32_t tag = a.tag_epoch[0];
     if (t < groupWidth) {
         double o = 0.0;
         for (int w = 0; w < kAttnWaves; ++w)
             o += sAcc[w][t];
-        store_agent(a.ws_o + (int64_t) split * qWidth + h0 * hd + t, o);
+        uint64_t *dst = a.part_ll + ((int64_t) split * qWidth + h0 * hd + t) * 2;
+        const uint64_t bits = (uint64_t) __double_as_longlong(o);
+        ll_put(dst, (uint32_t) bits, tag);
+        ll_put(dst + 1, (uint32_t) (bits >> 32), tag);
     }
     if (t < G) {
-        store_agent(a.ws_ml + (split * heads + h0 + t) * 2, sMax[t]);
-        store_agent(a.ws_ml + (split * heads + h0 + t) * 2 + 1, sSum[t]);
+        uint64_t *dst = a.ml_ll + ((int64_t) split * heads + h0 + t) * 4;
+        const uint64_t m = (uint64_t) __double_as_longlong(sMax[t]);
+        const uint64_t sum = (uint64_t) __double_as_longlong(sSum[t]);
+        ll_put(dst, (uint32_t) m, tag);
+        ll_put(dst + 1, (uint32_t) (m >> 32), tag);
+        ll_put(dst + 2, (uint32_t) sum, tag);
+        ll_put(dst + 3, (uint32_t) (sum >> 32), tag);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // the stores have completed
-    __syncthreads();
-    if (t == 0)
-        sLast = __hip_atomic_fetch_add(a.counter + group, 1, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT) == plan.splits - 1;
-    __syncthreads();
-    if (!sLast)
-        return;
 
-    // the merge of the group's splits: wave g takes head h0 + g.  The first
-    // batch of partials is requested together with the (max, sum) pairs, so
-    // the merge waits on one round trip.
+    // The merge (MultiQueryAttention.h:43-49: every split rescaled to the row
+    // maximum, in split order, the sums divided by the total), a 32-channel
+    // block a wave: the group's live splits share its blocks (split s takes
+    // blocks s, s + splits, ...), each polling the words it needs, so no
+    // workgroup waits on a ticket or reads the whole group's partials.
     const int splits = plan.splits;
-    const bool merging = t < ((groupWidth + 63) / 64) * 64; // whole waves, for the block reductions
-    double part[kMergeBatch];
-    if (merging)
+    const int blocks = groupWidth / kBlock;
+    const int mine = split < blocks ? (blocks - split + splits - 1) / splits : 0;
+    if (mine == 0)
+        return;
+    const uint32_t mlBytes = (uint32_t) (kDecodeSplits * heads * 4 * 8);
+    const uint32_t partBytes = (uint32_t) ((int64_t) kDecodeSplits * qWidth * 16);
+    // lanes 32..63 of a merging wave repeat lanes 0..31 (the cross-lane sums
+    // below take whole waves); lanes 0..31 store
+    const int b = split + wave * splits;              // a merging wave's block of the group
+    const int c = b * kBlock + (lane & (kBlock - 1)); // its channel in the group
+    // the merging waves request their first batch of partial words before
+    // the factors' wait: they land with the (max, sum) words
+    v4u w[kPollSplits];
+    auto request = [&](int s0) {
 #pragma unroll
-        for (int u = 0; u < kMergeBatch; ++u)
-            part[u] = (u < splits && t < groupWidth)
-                          ? load_agent(a.ws_o + (int64_t) u * qWidth + h0 * hd + t) : 0.0;
+        for (int u = 0; u < kPollSplits; ++u) {
+            const int sp = min(s0 + u, splits - 1);
+            w[u] = ld_agent_16(a.part_ll, (uint32_t) ((sp * qWidth + h0 * hd + c) * 16), partBytes);
+        }
+    };
+    if (wave < mine)
+        request(0);
+    // waves g < G: the split factors of head h0 + g, lane s taking split s
     if (wave < G) {
         const bool liveSplit = lane < splits;
         const int sp = liveSplit ? lane : 0;
-        const double m = load_agent(a.ws_ml + (sp * heads + h0 + wave) * 2);
-        const double sum = load_agent(a.ws_ml + (sp * heads + h0 + wave) * 2 + 1);
+        const uint32_t off = (uint32_t) ((sp * heads + h0 + wave) * 4 * 8);
+        double m = -INFINITY, sum = 0.0;
+        int spins = 0;
+        for (;;) {
+            const v4u w0 = ld_agent_16(a.ml_ll, off, mlBytes);
+            const v4u w1 = ld_agent_16(a.ml_ll, off + 16, mlBytes);
+            if (w0.y == tag && w0.w == tag && w1.y == tag && w1.w == tag) {
+                m = __longlong_as_double((long long) (((uint64_t) w0.z << 32) | w0.x));
+                sum = __longlong_as_double((long long) (((uint64_t) w1.z << 32) | w1.x));
+                break;
+            }
+            if (wait_give_up(a.error, spins))
+                break;
+        }
         double total;
         const double f = merge_factor(m, sum, liveSplit, total);
         if (liveSplit)
@@ -610,36 +639,53 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
             sSum[wave] = total;
     }
     __syncthreads();
-    if (!merging)
+    if (wave >= mine)
         return;
-    const int g = min(t / hd, G - 1);
+    const int g = c / hd;
     double weighted = 0.0;
-    for (int s0 = 0; s0 < splits; s0 += kMergeBatch) {
+    for (int s0 = 0; s0 < splits; s0 += kPollSplits) {
+        double part[kPollSplits];
+        int spins = 0;
         if (s0 > 0)
+            request(s0);
+        for (;;) {
+            bool all = true;
 #pragma unroll
-            for (int u = 0; u < kMergeBatch; ++u)
-                part[u] = (s0 + u < splits && t < groupWidth)
-                              ? load_agent(a.ws_o + (int64_t) (s0 + u) * qWidth + h0 * hd + t) : 0.0;
+            for (int u = 0; u < kPollSplits; ++u)
+                all = all && w[u].y == tag && w[u].w == tag;
+            if (all) {
 #pragma unroll
-        for (int u = 0; u < kMergeBatch; ++u)
+                for (int u = 0; u < kPollSplits; ++u)
+                    part[u] = __longlong_as_double((long long) (((uint64_t) w[u].z << 32) | w[u].x));
+                break;
+            }
+            if (wait_give_up(a.error, spins)) {
+#pragma unroll
+                for (int u = 0; u < kPollSplits; ++u)
+                    part[u] = 0.0;
+                break;
+            }
+            request(s0);
+        }
+#pragma unroll
+        for (int u = 0; u < kPollSplits; ++u)
             if (s0 + u < splits)
                 weighted += part[u] * sSplitMax[g][s0 + u];
     }
-    const int idx = h0 * hd + t;
-    const float v = t < groupWidth ? (float) (weighted / sSum[g]) : 0.f;
-    if (a.out && t < groupWidth)
-        a.out[idx] = v;
+    const int idx = h0 * hd + c;
+    const float v = (float) (weighted / sSum[g]);
     float amax = fabsf(v);
-    amax = max_lanes<16>(amax);
-    if (t < groupWidth) { // whole 32-blocks: groupWidth is a multiple of 32
-        const uint16_t bits = scale_bits_from_amax(amax);
-        const float sc = half_value(bits);
-        a.q8[idx] = (uint8_t) (int8_t) quantize_in_block(v, bits, sc, quantize_hint(sc));
-        if ((t & 31) == 0)
-            reinterpret_cast<uint16_t *>(a.q8 + qWidth)[idx / kBlock] = bits;
-    }
-    if (t == 0) // ready for the next launch
-        __hip_atomic_store(a.counter + group, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    amax = max_lanes<16>(amax); // lanes 0..31: the block
+    const uint16_t bits = scale_bits_from_amax(amax);
+    const float sc = half_value(bits);
+    const int byte = quantize_in_block(v, bits, sc, quantize_hint(sc));
+    if (lane >= kBlock)
+        return;
+    if (a.out)
+        a.out[idx] = v;
+    a.q8[idx] = (uint8_t) (int8_t) byte;
+    if (lane == 0)
+        reinterpret_cast<uint16_t *>(a.q8 + qWidth)[idx / kBlock] = bits;
 }
 
 // ---- gate|up + GeGLU + Q8 -----------------------------------------------------------
@@ -1763,17 +1809,13 @@ bool fused_decode_supported(int width, int heads, int kv_heads, int head_dim, in
     const int qWidth = heads * head_dim, kvWidth = kv_heads * head_dim;
     int channels = 0, group = 0;
     return attention_layout(head_dim, &channels, &group) && heads % group == 0
-           && heads / group <= kDecodeCounters && group <= kAttnWaves && group * head_dim <= kMaxGroupWidth
+           && group <= kAttnWaves && group * head_dim <= kMaxGroupWidth
            && width % kBlock == 0 && width <= kFusedMaxWidth && qWidth % kBlock == 0
            && heads % kv_heads == 0 && kvWidth % 8 == 0
            && max_positions <= kDecodeSplits * kMaxSplitKeys && intermediate % kBlock == 0
            && intermediate <= 16384;
 }
 
-size_t decode_workspace_bytes(int heads, int head_dim)
-{
-    return (size_t) kDecodeSplits * ((size_t) heads * head_dim + 2 * heads) * sizeof(double);
-}
 
 static int head_groups(int vocab)
 {
@@ -1810,7 +1852,7 @@ hipError_t launch_attention(const AttentionArgs &a, hipStream_t stream)
 {
     int channels = 0, group = 0;
     if (!attention_layout(a.head_dim, &channels, &group) || a.heads % group != 0 || !a.q8
-        || !a.counter)
+        || !a.part_ll || !a.ml_ll || !a.tag_epoch || !a.error)
         return hipErrorInvalidValue;
     if (a.grid_splits < 1 || a.grid_splits > kDecodeSplits)
         return hipErrorInvalidValue;

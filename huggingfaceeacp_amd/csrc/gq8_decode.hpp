@@ -12,7 +12,6 @@ namespace gq8 {
 
 constexpr int kFusedMaxWidth = 2048; // a normalised row held in LDS as Q8
 constexpr int kDecodeSplits = 64;    // attention workgroups over one row's keys
-constexpr int kDecodeCounters = 64; // attention head-group tickets
 constexpr int kHeadSlots = 64;       // lm_head argmax words (one wave folds them)
 constexpr int kHeadSlotStride = 16;  // 128 bytes between words
 
@@ -34,6 +33,7 @@ struct QkvArgs {
     uint16_t *key_cache, *value_cache; // this layer's [max_positions, KV * D]
     float *debug_normalised;  // optional
     uint8_t *debug_q8;        // optional
+    uint32_t *tag_epoch;      // advanced by one each launch (the attention launch's tag)
 };
 
 struct AttentionArgs {
@@ -43,8 +43,10 @@ struct AttentionArgs {
     int max_positions;        // rows of the cache (the bound of speculative reads)
     const int *position;      // keys [0, *position] are attended
     float scale;
-    double *ws_o, *ws_ml;     // kDecodeSplits partials
-    int *counter;             // one a head group (kDecodeCounters), zero between launches
+    uint64_t *part_ll;        // split partials as tagged words: [kDecodeSplits][H D][2]
+    uint64_t *ml_ll;          // their (max, sum): [kDecodeSplits][H][4] tagged words
+    const uint32_t *tag_epoch; // the launch's tag (advanced by the q|k|v launch before it)
+    int *error;               // set when a merge's wait gives up
     float *out;               // optional fp32 row
     uint8_t *q8;              // Q8 row for o_proj
     int grid_splits;          // the launch's key splits (attention_grid_splits of the step's
@@ -204,7 +206,6 @@ hipError_t launch_flow_step(const FlowArgs &a, hipStream_t stream);
 
 bool fused_decode_supported(int width, int heads, int kv_heads, int head_dim, int intermediate,
                             int max_positions);
-size_t decode_workspace_bytes(int heads, int head_dim);
 
 hipError_t launch_qkv_rope(const QkvArgs &a, hipStream_t stream);
 hipError_t launch_attention(const AttentionArgs &a, hipStream_t stream);

@@ -602,8 +602,11 @@ struct gq8_decoder {
              *persistMl = nullptr, *persistAttn = nullptr, *persistAct = nullptr, *persistCand = nullptr;
     uint32_t *persistEpoch = nullptr;
     int *persistError = nullptr;
-    double *decodeO = nullptr, *decodeMl = nullptr;
-    int *counters = nullptr; // attention head-group tickets
+    // the decode attention's tagged split partials, their tag epoch and the
+    // error word its bounded waits set
+    uint64_t *attnPart = nullptr, *attnMl = nullptr;
+    uint32_t *attnEpoch = nullptr;
+    int *attnError = nullptr;
     unsigned long long *headBest = nullptr; // the lm_head argmax slots
 
     // sampling (Gemma::setSampling, Gemma.cpp:198-202): the options, and the
@@ -968,10 +971,17 @@ extern "C" int gq8_decoder_create(const gq8_shape *shape, gq8_decoder **out)
     d->fusedSupported = gq8::fused_decode_supported(s.width, s.heads, s.kv_heads, s.head_dim,
                                                     s.intermediate, s.max_positions);
     {
-        const size_t wsBytes = gq8::decode_workspace_bytes(s.heads, s.head_dim);
-        GQ8_ALLOC(d->decodeO, wsBytes);
-        d->decodeMl = d->decodeO + (size_t) gq8::kDecodeSplits * s.heads * s.head_dim;
-        GQ8_ALLOC(d->counters, gq8::kDecodeCounters * sizeof(int));
+        const size_t partBytes = (size_t) gq8::kDecodeSplits * d->qWidth * 2 * sizeof(uint64_t);
+        const size_t mlBytes = (size_t) gq8::kDecodeSplits * s.heads * 4 * sizeof(uint64_t);
+        GQ8_ALLOC(d->attnPart, partBytes);
+        GQ8_ALLOC(d->attnMl, mlBytes);
+        GQ8_ALLOC(d->attnEpoch, 64 * sizeof(uint32_t));
+        GQ8_ALLOC(d->attnError, 64 * sizeof(int));
+        if (hipMemset(d->attnPart, 0, partBytes) != hipSuccess
+            || hipMemset(d->attnMl, 0, mlBytes) != hipSuccess
+            || hipMemset(d->attnEpoch, 0, 64 * sizeof(uint32_t)) != hipSuccess
+            || hipMemset(d->attnError, 0, 64 * sizeof(int)) != hipSuccess)
+            return cleanup(fail(GQ8_ERR_DEVICE, "attention state: initialisation failed"));
         GQ8_ALLOC(d->headBest, gq8::kHeadSlots * gq8::kHeadSlotStride * sizeof(unsigned long long));
     }
 #undef GQ8_ALLOC
@@ -979,7 +989,6 @@ extern "C" int gq8_decoder_create(const gq8_shape *shape, gq8_decoder **out)
         return cleanup(fail(GQ8_ERR_MEMORY, "pinned allocation failed"));
     if (hipMemset(d->sequence, 0, ((size_t) s.max_positions + 1) * sizeof(uint32_t)) != hipSuccess
         || hipMemset(d->position, 0, sizeof(int)) != hipSuccess
-        || hipMemset(d->counters, 0, gq8::kDecodeCounters * sizeof(int)) != hipSuccess
         || hipMemset(d->headBest, 0, gq8::kHeadSlots * gq8::kHeadSlotStride * sizeof(unsigned long long))
                != hipSuccess
         || hipMemset(d->keyCache, 0, cacheElements * sizeof(uint16_t)) != hipSuccess
@@ -1623,8 +1632,26 @@ int check_persist_error(gq8_decoder *d)
 int check_flow_error(gq8_decoder *d);
 
 // The error word of whichever one-launch step is on.
+// Reads and clears the decode attention's error word: a set word means a
+// merge's wait gave up and that step's results are invalid.
+int check_attention_error(gq8_decoder *d)
+{
+    if (!d->fusedSupported)
+        return GQ8_OK;
+    int error = 0;
+    GQ8_HIP(hipStreamSynchronize(d->stream));
+    GQ8_HIP(hipMemcpy(&error, d->attnError, sizeof(int), hipMemcpyDeviceToHost));
+    if (error == 0)
+        return GQ8_OK;
+    GQ8_HIP(hipMemset(d->attnError, 0, sizeof(int)));
+    return fail(GQ8_ERR_DEVICE, "decode attention: a split merge's wait gave up (the step's "
+                                "results are invalid)");
+}
+
 int check_step_error(gq8_decoder *d)
 {
+    if (int s = check_attention_error(d))
+        return s;
     if (d->usePersist)
         if (int s = check_persist_error(d))
             return s;
@@ -1654,7 +1681,6 @@ int check_flow_error(gq8_decoder *d)
     GQ8_HIP(hipMemset(d->flowTagged, 0, d->flowTaggedBytes));
     GQ8_HIP(hipMemset(d->flowCounters, 0, (size_t) gq8::kFlowCounterInts * sizeof(int)));
     GQ8_HIP(hipMemset(d->flowError, 0, sizeof(int)));
-    GQ8_HIP(hipMemset(d->counters, 0, gq8::kDecodeCounters * sizeof(int)));
     GQ8_HIP(hipMemset(d->headBest, 0, gq8::kHeadSlots * gq8::kHeadSlotStride * sizeof(unsigned long long)));
     if (int s = resync_position(d))
         return s;
@@ -1702,6 +1728,7 @@ int encode_fused_token(gq8_decoder *d, float *logits, bool sample)
         q.value_cache = d->valueCache + layerCache;
         q.debug_normalised = debugValues(0, l);
         q.debug_q8 = debugQ8(0, l);
+        q.tag_epoch = d->attnEpoch;
         GQ8_STAGE(kStageQkv, gq8::launch_qkv_rope(q, st));
 
         gq8::AttentionArgs at{};
@@ -1714,9 +1741,10 @@ int encode_fused_token(gq8_decoder *d, float *logits, bool sample)
         at.max_positions = s.max_positions;
         at.position = d->position;
         at.scale = 1.f / std::sqrt((float) s.head_dim);
-        at.ws_o = d->decodeO;
-        at.ws_ml = d->decodeMl;
-        at.counter = d->counters;
+        at.part_ll = d->attnPart;
+        at.ml_ll = d->attnMl;
+        at.tag_epoch = d->attnEpoch;
+        at.error = d->attnError;
         at.out = debugValues(1, l);
         at.q8 = d->x8;
         at.grid_splits = gq8::attention_grid_splits(d->capturing ? d->captureKeys
