@@ -394,13 +394,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
     __shared__ double sMax[G], sSum[G];
     __shared__ double sSplitMax[G][kDecodeSplits];
 
+    // a 1-D grid: the head groups' splits, a group's splits consecutive
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int hd = a.head_dim, kvWidth = a.kv_heads * hd;
     const int heads = a.heads, qWidth = heads * hd;
     const int perKv = heads / a.kv_heads;
-    const int group = blockIdx.y, h0 = group * G;
+    const int group = (int) blockIdx.x / a.grid_splits, h0 = group * G;
     const int groupWidth = G * hd;
-    const int split = blockIdx.x;
+    const int split = (int) blockIdx.x % a.grid_splits;
 
     // the query channels of this lane, before the position is known
     // (unconditional loads, masked: a selected load would be sunk into a
@@ -601,18 +602,6 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
     // below take whole waves); lanes 0..31 store
     const int b = split + wave * splits;              // a merging wave's block of the group
     const int c = b * kBlock + (lane & (kBlock - 1)); // its channel in the group
-    // the merging waves request their first batch of partial words before
-    // the factors' wait: they land with the (max, sum) words
-    v4u w[kPollSplits];
-    auto request = [&](int s0) {
-#pragma unroll
-        for (int u = 0; u < kPollSplits; ++u) {
-            const int sp = min(s0 + u, splits - 1);
-            w[u] = ld_agent_16(a.part_ll, (uint32_t) ((sp * qWidth + h0 * hd + c) * 16), partBytes);
-        }
-    };
-    if (wave < mine)
-        request(0);
     // waves g < G: the split factors of head h0 + g, lane s taking split s
     if (wave < G) {
         const bool liveSplit = lane < splits;
@@ -646,9 +635,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
     for (int s0 = 0; s0 < splits; s0 += kPollSplits) {
         double part[kPollSplits];
         int spins = 0;
-        if (s0 > 0)
-            request(s0);
         for (;;) {
+            v4u w[kPollSplits];
+#pragma unroll
+            for (int u = 0; u < kPollSplits; ++u) {
+                const int sp = min(s0 + u, splits - 1);
+                w[u] = ld_agent_16(a.part_ll, (uint32_t) ((sp * qWidth + h0 * hd + c) * 16), partBytes);
+            }
             bool all = true;
 #pragma unroll
             for (int u = 0; u < kPollSplits; ++u)
@@ -665,7 +658,6 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
                     part[u] = 0.0;
                 break;
             }
-            request(s0);
         }
 #pragma unroll
         for (int u = 0; u < kPollSplits; ++u)
@@ -1856,7 +1848,7 @@ hipError_t launch_attention(const AttentionArgs &a, hipStream_t stream)
         return hipErrorInvalidValue;
     if (a.grid_splits < 1 || a.grid_splits > kDecodeSplits)
         return hipErrorInvalidValue;
-    const dim3 grid(a.grid_splits, a.heads / group);
+    const dim3 grid(a.grid_splits * (a.heads / group));
     if (channels == 4)
         hipLaunchKernelGGL((attention_kernel<4, 1>), grid, dim3(kAttnThreads), 0, stream, a);
     else if (channels == 2)
