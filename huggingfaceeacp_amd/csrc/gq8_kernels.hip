@@ -18,10 +18,12 @@ namespace {
 constexpr int kThreads = 256;
 constexpr uint32_t kUnchosen = 0xFFFFFFFFu; // Argmax.h:45
 
+// The largest magnitude of a 32-lane group (lanes 32 g .. 32 g + 31); lanes
+// of the wave outside the group may be inactive.  fmaxf returns the other
+// operand for a NaN, as std::max(largest, |x|) keeps `largest`
+// (Int8Blocks.cpp:118-119).
 __device__ inline float group32_amax(float a)
 {
-    // fmaxf returns the other operand for a NaN, as std::max(largest, |x|)
-    // keeps `largest` (Int8Blocks.cpp:118-119).
     for (int mask = 16; mask >= 1; mask >>= 1)
         a = fmaxf(a, __shfl_xor(a, mask));
     return a;
@@ -29,18 +31,15 @@ __device__ inline float group32_amax(float a)
 
 // One element of a 32-element block held by 32 consecutive lanes: the block's
 // scale from the group's largest magnitude, the element's byte, and (lane 0
-// of the group) the scale's fp16 bits.
+// of the group) the scale's fp16 bits.  Without branches, so a thread's
+// elements interleave.
 __device__ inline void quantize_in_group(float value, int lane32, uint8_t *byte,
                                          uint16_t *scaleSlot)
 {
     const float amax = group32_amax(fabsf(value));
     const uint16_t bits = scale_bits_from_amax(amax);
-    int q = 0;
-    if (bits != 0) {
-        const float scale = half_value(bits);
-        q = quantize_value(value, scale, quantize_hint(scale));
-    }
-    *byte = (uint8_t) (int8_t) q;
+    const float scale = half_value(bits);
+    *byte = (uint8_t) (int8_t) quantize_in_block(value, bits, scale, quantize_hint(scale));
     if (lane32 == 0)
         *scaleSlot = bits;
 }
@@ -97,6 +96,33 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const uint32_t *__restr
 }
 
 // ---- RMSNorm, optionally fused with the activation quantization ---------
+// The normalized element i of a row and its Int8Blocks byte and block scale
+// (lane 0 of its 32-lane group stores the scale).  The whole wave is active:
+// the group's largest magnitude is the DPP form of group32_amax, same pairing.
+__device__ inline void norm_store(float x, float w, double scale, int64_t at, bool live,
+                                  int64_t elements, float *__restrict__ y, uint8_t *__restrict__ q8)
+{
+    const float v = norm_value(x, scale, w);
+    const float amax = max_lanes<16>(fabsf(v));
+    const uint16_t bits = scale_bits_from_amax(amax);
+    const float sc = half_value(bits);
+    const int byte = quantize_in_block(v, bits, sc, quantize_hint(sc));
+    if (!live)
+        return;
+    if (y)
+        y[at] = v;
+    if (q8) {
+        q8[at] = (uint8_t) (int8_t) byte;
+        if ((threadIdx.x & 31) == 0)
+            reinterpret_cast<uint16_t *>(q8 + elements)[at / kBlock] = bits;
+    }
+}
+
+// K: elements a thread holds (the row's width rounded up to K x kThreads),
+// loaded at once, or 0: rows of any width, streamed from memory twice.  Every
+// lane of a wave takes part in the group reductions (elements past the width
+// are computed from a clamped index and not stored).
+template <int K>
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restrict__ x,
                                                            const float *__restrict__ weight,
                                                            int rows, int width, float epsilon,
@@ -107,64 +133,57 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restri
     const int row = blockIdx.x;
     const float *xr = x + (int64_t) row * width;
 
-    // rows up to kThreads * kNormHeld wide are loaded once, all at once
-    constexpr int kNormHeld = 16;
-    const bool held = width <= kThreads * kNormHeld;
-    float xv[kNormHeld], wv[kNormHeld];
-    if (held) {
-#pragma unroll
-        for (int k = 0; k < kNormHeld; ++k) {
-            const int i = min(threadIdx.x + k * kThreads, width - 1); // clamped; masked below
-            xv[k] = xr[i];
-            wv[k] = weight[i];
-        }
-    }
-    double squares = 0.0;
-    if (held) {
-#pragma unroll
-        for (int k = 0; k < kNormHeld; ++k)
-            if (threadIdx.x + k * kThreads < width)
-                squares += (double) xv[k] * (double) xv[k]; // the square is exact in double
-    } else {
+    const int64_t elements = (int64_t) rows * width;
+    if constexpr (K == 0) {
+        double squares = 0.0;
         for (int i = threadIdx.x; i < width; i += kThreads) {
             const double v = (double) xr[i];
             squares += v * v;
         }
-    }
-    squares = wave_sum(squares);
-    if ((threadIdx.x & 63) == 0)
-        partial[threadIdx.x >> 6] = squares;
-    __syncthreads();
-    double total = 0.0;
-    for (int w = 0; w < kThreads / 64; ++w)
-        total += partial[w];
-    const double scale = norm_scale(total, width, epsilon);
-
-    const int64_t elements = (int64_t) rows * width;
-    if (held) {
+        squares = wave_sum(squares);
+        if ((threadIdx.x & 63) == 0)
+            partial[threadIdx.x >> 6] = squares;
+        __syncthreads();
+        double total = 0.0;
 #pragma unroll
-        for (int k = 0; k < kNormHeld; ++k) {
-            const int i = threadIdx.x + k * kThreads;
-            if (i >= width) // whole 32-element groups drop out together
-                break;
-            const int64_t at = (int64_t) row * width + i;
-            const float v = norm_value(xv[k], scale, wv[k]);
-            if (y)
-                y[at] = v;
-            if (q8)
-                quantize_in_group(v, threadIdx.x & 31, q8 + at,
-                                  reinterpret_cast<uint16_t *>(q8 + elements) + at / kBlock);
+        for (int w = 0; w < kThreads / 64; ++w)
+            total += partial[w];
+        const double scale = norm_scale(total, width, epsilon);
+        for (int base = 0; base < width; base += kThreads) { // uniform: whole waves
+            const int i = base + threadIdx.x;
+            const bool live = i < width;
+            const int c = live ? i : width - 1;
+            norm_store(xr[c], weight[c], scale, (int64_t) row * width + c, live, elements, y, q8);
         }
-        return;
-    }
-    for (int i = threadIdx.x; i < width; i += kThreads) {
-        const int64_t at = (int64_t) row * width + i;
-        const float v = norm_value(xr[i], scale, weight[i]);
-        if (y)
-            y[at] = v;
-        if (q8)
-            quantize_in_group(v, threadIdx.x & 31, q8 + at,
-                              reinterpret_cast<uint16_t *>(q8 + elements) + at / kBlock);
+    } else {
+        float xv[K], wv[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int i = min(threadIdx.x + k * kThreads, width - 1); // clamped; masked below
+            xv[k] = xr[i];
+            wv[k] = weight[i];
+        }
+        double squares = 0.0;
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+            if (threadIdx.x + k * kThreads < width)
+                squares += (double) xv[k] * (double) xv[k]; // the square is exact in double
+        squares = wave_sum(squares);
+        if ((threadIdx.x & 63) == 0)
+            partial[threadIdx.x >> 6] = squares;
+        __syncthreads();
+        double total = 0.0;
+#pragma unroll
+        for (int w = 0; w < kThreads / 64; ++w)
+            total += partial[w];
+        const double scale = norm_scale(total, width, epsilon);
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int i = threadIdx.x + k * kThreads;
+            const bool live = i < width; // whole 32-element groups are live together
+            norm_store(xv[k], wv[k], scale, (int64_t) row * width + (live ? i : 0), live, elements,
+                       y, q8);
+        }
     }
 }
 
@@ -828,8 +847,25 @@ hipError_t launch_rmsnorm(const float *x, const float *weight, int rows, int wid
 {
     if (rows <= 0 || width <= 0 || width % kBlock != 0)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, stream, x, weight, rows,
-                       width, epsilon, y, q8);
+    const int held = (width + kThreads - 1) / kThreads;
+    if (held <= 1)
+        hipLaunchKernelGGL(rmsnorm_kernel<1>, dim3(rows), dim3(kThreads), 0, stream, x, weight, rows,
+                           width, epsilon, y, q8);
+    else if (held <= 2)
+        hipLaunchKernelGGL(rmsnorm_kernel<2>, dim3(rows), dim3(kThreads), 0, stream, x, weight, rows,
+                           width, epsilon, y, q8);
+    else if (held <= 4)
+        hipLaunchKernelGGL(rmsnorm_kernel<4>, dim3(rows), dim3(kThreads), 0, stream, x, weight, rows,
+                           width, epsilon, y, q8);
+    else if (held <= 8)
+        hipLaunchKernelGGL(rmsnorm_kernel<8>, dim3(rows), dim3(kThreads), 0, stream, x, weight, rows,
+                           width, epsilon, y, q8);
+    else if (held <= 16)
+        hipLaunchKernelGGL(rmsnorm_kernel<16>, dim3(rows), dim3(kThreads), 0, stream, x, weight, rows,
+                           width, epsilon, y, q8);
+    else
+        hipLaunchKernelGGL(rmsnorm_kernel<0>, dim3(rows), dim3(kThreads), 0, stream, x, weight, rows,
+                           width, epsilon, y, q8);
     return hipGetLastError();
 }
 
