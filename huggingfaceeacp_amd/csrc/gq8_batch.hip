@@ -209,16 +209,6 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
     const uint8_t *wRow = a.w8 + (int64_t) n * a.inner + (lane >> 4) * 8;
     const uint16_t *wScale = reinterpret_cast<const uint16_t *>(a.w8 + (int64_t) a.outputs * a.inner)
                              + (int64_t) n * nb;
-    // up to kRowsPrefetch chunks of weights in flight a wave (issued before
-    // the staging below, so the first ones overlap it)
-    constexpr int P = V ? (NC < kRowsPrefetch ? NC : kRowsPrefetch) : 1;
-    WeightChunk buf[P];
-    if (b0 < b1) {
-#pragma unroll
-        for (int i = 0; i < P; ++i)
-            load_weight_chunk<V>(buf[i], wRow, wScale, V ? b0 + i * kChunkBlocks : b0, b1);
-    }
-
     // stage the workgroup's activation blocks in MFMA fragment order (lane l
     // of block b: sequence l % 16, bytes 8 (l / 16) .. + 8) and their scales
     const uint16_t *xScales = reinterpret_cast<const uint16_t *>(a.x8 + (int64_t) a.x_rows * a.inner);
@@ -257,6 +247,16 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
         const int e = t + i * kRowsThreads;
         if (e < scales)
             sSx[e] = half_value(scaleBits[i]);
+    }
+    // then up to kRowsPrefetch chunks of weights in flight a wave: behind
+    // the LDS writes, since once the weight stream fills the memory queues a
+    // wave's vector memory instructions issue only as fast as loads retire
+    constexpr int P = V ? (NC < kRowsPrefetch ? NC : kRowsPrefetch) : 1;
+    WeightChunk buf[P];
+    if (b0 < b1) {
+#pragma unroll
+        for (int i = 0; i < P; ++i)
+            load_weight_chunk<V>(buf[i], wRow, wScale, V ? b0 + i * kChunkBlocks : b0, b1);
     }
     __syncthreads();
 
@@ -369,6 +369,7 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
 // ---- attention of the lockstep rows ---------------------------------------------
 constexpr int kRowsTileKeys = 64;   // keys a tile (16 a key wave)
 constexpr int kRowsWaveKeys = 16;
+constexpr int kRowsHeadGroup = 4;   // query heads a workgroup
 
 // C consecutive fp16 channels kept packed, two a register.
 template <int C>
@@ -396,29 +397,41 @@ __device__ inline Halves<C> load_channels(const uint16_t *p)
     return h;
 }
 
-// C channels a lane (head width 64 C), H heads.  Scores: lane l takes key
-// t0 + l of a 64-key tile and wave w a quarter of the channels, every head
-// (no cross-lane sums; the query comes from LDS as doubles, the four
-// quarters are added in LDS).  Values: lane l takes channels C l .. C l + C - 1
-// and wave w keys t0 + 16 w .. + 15, every head.
-template <int C, int H>
-__global__ __launch_bounds__(kRowsThreads) void attention_rows_kernel(RowsAttentionArgs a)
+// C channels a lane (head width 64 C), H heads, G of them a workgroup
+// (blockIdx.z picks the group; the groups of one key tile share the tile's
+// rows through the L2).  Scores: wave w takes a quarter of the channels and
+// its lane l keys t0 + l % 16 + 16 j (j < 4) over the quarter's slice l / 16
+// of C channels... 4 C channels, every head of the group, so each query pair
+// read from LDS serves four keys (the LDS reads, not the fp64 products, bound
+// this phase); the sixteen slices' dots are added in LDS in channel order.
+// Values: lane l takes channels C l .. C l + C - 1 and wave w keys
+// t0 + 16 w .. + 15, every head of the group.
+template <int C, int H, int G>
+__global__ __launch_bounds__(kRowsThreads, 3) void attention_rows_kernel(RowsAttentionArgs a)
 {
+    static_assert(H % G == 0, "whole head groups");
     constexpr int hd = 64 * C, half = hd / 2, qW = H * hd;
     constexpr int hq = hd / kRowsWaves;        // channels a wave scores
-    constexpr int kKeyWords = hq / 2;          // their fp16 pairs
-    constexpr int kAccHeads = 4;               // heads a pass of the waves' LDS sum
-    constexpr int kRopePairs = ((H + 1) * half + kRowsThreads - 1) / kRowsThreads;
-    static_assert(hq % 8 == 0, "16-byte key loads");
-    __shared__ double sQd[H][hd];
+    constexpr int kSlices = 4;                 // channel slices of a wave's quarter
+    constexpr int kSliceCh = hq / kSlices;     // channels a lane scores (4 C)
+    constexpr int kSliceWords = kSliceCh / 2;  // their fp16 pairs
+    constexpr int kLaneKeys = kRowsTileKeys / 16; // keys a lane scores
+    constexpr int kParts = kRowsWaves * kSlices;  // partial dots of a score
+    constexpr int kAccHeads = G < 4 ? G : 4;   // heads a pass of the waves' LDS sum
+    constexpr int kRopePairs = ((G + 1) * half + kRowsThreads - 1) / kRowsThreads;
+    __shared__ double sQd[G][hd];
     __shared__ __attribute__((aligned(16))) uint16_t sKnew[hd], sVnew[hd];
-    __shared__ double sP[kRowsWaves][H][kRowsTileKeys];
-    __shared__ double sS[H][kRowsTileKeys];
-    __shared__ double sMax[H], sSum[H], sF[H];
-    __shared__ double sAcc[kRowsWaves][kAccHeads * hd];
+    // the partial dots, and after the last tile the waves' value sums
+    constexpr int kPartDoubles = kParts * G * kRowsTileKeys;
+    constexpr int kAccDoubles = kRowsWaves * kAccHeads * hd;
+    __shared__ double sShared[kPartDoubles > kAccDoubles ? kPartDoubles : kAccDoubles];
+    double (*sP)[G][kRowsTileKeys] = reinterpret_cast<double (*)[G][kRowsTileKeys]>(sShared);
+    double (*sAcc)[kAccHeads * hd] = reinterpret_cast<double (*)[kAccHeads * hd]>(sShared);
+    __shared__ double sS[G][kRowsTileKeys];
+    __shared__ double sMax[G], sSum[G], sF[G];
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int seq = blockIdx.y, split = blockIdx.x;
+    const int seq = blockIdx.y, split = blockIdx.x, hBase = blockIdx.z * G;
     const int k0 = split * a.per_split;
     // the position first: its wait then counts only the loads before it
     const int pos = a.positions[seq];
@@ -428,28 +441,43 @@ __global__ __launch_bounds__(kRowsThreads) void attention_rows_kernel(RowsAttent
     uint16_t *keys = a.key_cache + seq * a.cache_stride;
     uint16_t *values = a.value_cache + seq * a.cache_stride;
 
-    // Loads that do not need the position go first: the query and new key
-    // pairs, the new value, and the first tile's key and value rows (rows
+    // Loads that do not need the position go first: the group's query and
+    // the new key pairs (local head G: global head H, right after the
+    // queries), the new value, and the first tile's key and value rows (rows
     // past the position are read inside the cache and never used).  Their
     // round trip overlaps the position's.
     float lo[kRopePairs], hi[kRopePairs];
 #pragma unroll
     for (int k = 0; k < kRopePairs; ++k) {
-        const int idx = min(t + k * kRowsThreads, (H + 1) * half - 1);
+        const int idx = min(t + k * kRowsThreads, (G + 1) * half - 1);
         const int head = idx / half, i = idx % half;
-        lo[k] = row[head * hd + i];
-        hi[k] = row[head * hd + i + half];
+        const int global = head < G ? hBase + head : H;
+        lo[k] = row[global * hd + i];
+        hi[k] = row[global * hd + i + half];
     }
     const float newValue = row[qW + hd + min(t, hd - 1)];
-    uint32_t kq[kKeyWords];
+    // this lane's score slice: channels ch0 .. ch0 + kSliceCh - 1 of keys
+    // t0 + kg + 16 j
+    const int kg = lane & 15, ch0 = wave * hq + (lane >> 4) * kSliceCh;
+    uint32_t kq[kLaneKeys][kSliceWords];
     Halves<C> vh[kRowsWaveKeys];
-    auto load_keys = [&](int t0) {
-        const int j = min(t0 + lane, a.max_positions - 1);
-        const uint4 *src = reinterpret_cast<const uint4 *>(keys + (int64_t) j * hd + wave * hq);
+    auto load_key_slice = [&](uint32_t (&dst)[kSliceWords], const uint16_t *src) {
+        if constexpr (kSliceWords % 4 == 0) {
 #pragma unroll
-        for (int v = 0; v < kKeyWords / 4; ++v) {
-            const uint4 w = src[v];
-            kq[4 * v] = w.x; kq[4 * v + 1] = w.y; kq[4 * v + 2] = w.z; kq[4 * v + 3] = w.w;
+            for (int v = 0; v < kSliceWords / 4; ++v) {
+                const uint4 w = reinterpret_cast<const uint4 *>(src)[v];
+                dst[4 * v] = w.x; dst[4 * v + 1] = w.y; dst[4 * v + 2] = w.z; dst[4 * v + 3] = w.w;
+            }
+        } else {
+            const uint2 w = *reinterpret_cast<const uint2 *>(src);
+            dst[0] = w.x; dst[1] = w.y;
+        }
+    };
+    auto load_keys = [&](int t0) {
+#pragma unroll
+        for (int j = 0; j < kLaneKeys; ++j) {
+            const int key = min(t0 + kg + 16 * j, a.max_positions - 1);
+            load_key_slice(kq[j], keys + (int64_t) key * hd + ch0);
         }
     };
     auto load_values = [&](int t0) {
@@ -460,7 +488,6 @@ __global__ __launch_bounds__(kRowsThreads) void attention_rows_kernel(RowsAttent
         }
     };
     load_keys(k0);
-    load_values(k0);
     asm volatile("" ::: "memory"); // keeps the loads above the position-dependent exit
 
     const int keyCount = pos + 1;
@@ -469,14 +496,13 @@ __global__ __launch_bounds__(kRowsThreads) void attention_rows_kernel(RowsAttent
     const int k1 = min(k0 + a.per_split, keyCount);
     const bool holdsNew = k1 == keyCount; // this split ends at the new position
 
-    // RoPE (rope_kv_kernel's arithmetic) of the query heads and, in the
-    // split holding it, of the new key (head H, right after the queries); the
-    // new value rounded to fp16
+    // RoPE (rope_kv_kernel's arithmetic) of the group's query heads and, in
+    // the split holding it, of the new key; the new value rounded to fp16
     {
         float cs[kRopePairs], sn[kRopePairs];
 #pragma unroll
         for (int k = 0; k < kRopePairs; ++k) {
-            const int idx = min(t + k * kRowsThreads, (H + 1) * half - 1);
+            const int idx = min(t + k * kRowsThreads, (G + 1) * half - 1);
             const int64_t angle = (int64_t) pos * half + idx % half;
             cs[k] = a.cosines[angle];
             sn[k] = a.sines[angle];
@@ -484,12 +510,12 @@ __global__ __launch_bounds__(kRowsThreads) void attention_rows_kernel(RowsAttent
 #pragma unroll
         for (int k = 0; k < kRopePairs; ++k) {
             const int idx = t + k * kRowsThreads;
-            if (idx >= (H + 1) * half)
+            if (idx >= (G + 1) * half)
                 break;
             const int head = idx / half, i = idx % half;
             float rl, rh;
             rotate_pair(lo[k], hi[k], cs[k], sn[k], &rl, &rh);
-            if (head < H) {
+            if (head < G) {
                 sQd[head][i] = (double) rl;
                 sQd[head][i + half] = (double) rh;
             } else {
@@ -500,70 +526,75 @@ __global__ __launch_bounds__(kRowsThreads) void attention_rows_kernel(RowsAttent
         if (holdsNew && t < hd)
             sVnew[t] = half_bits(newValue);
     }
-    if (t < H) {
+    if (t < G) {
         sMax[t] = -INFINITY;
         sSum[t] = 0.0;
     }
     __syncthreads();
-    if (holdsNew && t < hd) {
+    if (holdsNew && t < hd && blockIdx.z == 0) { // one group appends the new rows
         keys[(int64_t) pos * hd + t] = sKnew[t];
         values[(int64_t) pos * hd + t] = sVnew[t];
     }
 
-    double acc[H][C];
+    double acc[G][C];
 #pragma unroll
-    for (int h = 0; h < H; ++h)
+    for (int h = 0; h < G; ++h)
 #pragma unroll
         for (int c = 0; c < C; ++c)
             acc[h][c] = 0.0;
 
     for (int t0 = k0; t0 < k1; t0 += kRowsTileKeys) {
         const int nk = min(kRowsTileKeys, k1 - t0);
-        if (t0 > k0) { // the first tile's rows are already in
+        if (t0 > k0) // the first tile's keys are already in
             load_keys(t0);
-            load_values(t0);
-        }
         if (holdsNew && t0 + nk == keyCount) { // the new position's rows from LDS
-            if (t0 + lane == pos) {
-                const uint4 *src = reinterpret_cast<const uint4 *>(sKnew + wave * hq);
 #pragma unroll
-                for (int v = 0; v < kKeyWords / 4; ++v) {
-                    const uint4 w = src[v];
-                    kq[4 * v] = w.x; kq[4 * v + 1] = w.y; kq[4 * v + 2] = w.z; kq[4 * v + 3] = w.w;
+            for (int j = 0; j < kLaneKeys; ++j)
+                if (t0 + kg + 16 * j == pos)
+                    load_key_slice(kq[j], sKnew + ch0);
+        }
+        // this lane's keys against every head of the group over its slice
+        double p[kLaneKeys][G];
+#pragma unroll
+        for (int j = 0; j < kLaneKeys; ++j)
+#pragma unroll
+            for (int h = 0; h < G; ++h)
+                p[j][h] = 0.0;
+#pragma unroll
+        for (int w = 0; w < kSliceWords; ++w) {
+            double ka[kLaneKeys], kb[kLaneKeys];
+#pragma unroll
+            for (int j = 0; j < kLaneKeys; ++j) {
+                ka[j] = (double) half_value((uint16_t) (kq[j][w] & 0xFFFFu));
+                kb[j] = (double) half_value((uint16_t) (kq[j][w] >> 16));
+            }
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                const double2 qq = *reinterpret_cast<const double2 *>(&sQd[h][ch0 + 2 * w]);
+#pragma unroll
+                for (int j = 0; j < kLaneKeys; ++j) {
+                    p[j][h] = fma(qq.x, ka[j], p[j][h]);
+                    p[j][h] = fma(qq.y, kb[j], p[j][h]);
                 }
             }
-            const Halves<C> vn = load_channels<C>(sVnew + c0);
-#pragma unroll
-            for (int i = 0; i < kRowsWaveKeys; ++i)
-                if (t0 + wave * kRowsWaveKeys + i == pos)
-                    vh[i] = vn;
         }
-        // this lane's key against every head over this wave's channels
-        double p[H];
+        const int part = wave * kSlices + (lane >> 4); // the slice's place in channel order
 #pragma unroll
-        for (int h = 0; h < H; ++h)
-            p[h] = 0.0;
+        for (int j = 0; j < kLaneKeys; ++j)
 #pragma unroll
-        for (int w = 0; w < kKeyWords; ++w) {
-            const double ka = (double) half_value((uint16_t) (kq[w] & 0xFFFFu));
-            const double kb = (double) half_value((uint16_t) (kq[w] >> 16));
-#pragma unroll
-            for (int h = 0; h < H; ++h) {
-                const double2 qq = *reinterpret_cast<const double2 *>(&sQd[h][wave * hq + 2 * w]);
-                p[h] = fma(qq.x, ka, p[h]);
-                p[h] = fma(qq.y, kb, p[h]);
-            }
-        }
-#pragma unroll
-        for (int h = 0; h < H; ++h)
-            sP[wave][h][lane] = p[h];
+            for (int h = 0; h < G; ++h)
+                sP[part][h][kg + 16 * j] = p[j][h];
+        // the tile's value rows: their round trip overlaps the softmax
+        load_values(t0);
         __syncthreads();
         // the tile's softmax against the running maximum, a wave a head; the
-        // four channel quarters added in order
-        for (int h = wave; h < H; h += kRowsWaves) {
-            const double sc = lane < nk ? (double) a.scale * (((sP[0][h][lane] + sP[1][h][lane])
-                                                               + sP[2][h][lane]) + sP[3][h][lane])
-                                        : -INFINITY;
+        // slices' dots added in channel order
+        for (int h = wave; h < G; h += kRowsWaves) {
+            double dot = sP[0][h][lane];
+#pragma unroll
+            for (int q = 1; q < kParts; ++q)
+                dot += sP[q][h][lane];
+            const double sc = lane < nk ? (double) a.scale * dot : -INFINITY;
             const double tileMax = wave_max_d(sc);
             const double previous = sMax[h];
             const double largest = fmax(previous, tileMax);
@@ -578,9 +609,16 @@ __global__ __launch_bounds__(kRowsThreads) void attention_rows_kernel(RowsAttent
             }
         }
         __syncthreads();
+        if (holdsNew && t0 + nk == keyCount) { // the new position's value from LDS
+            const Halves<C> vn = load_channels<C>(sVnew + c0);
+#pragma unroll
+            for (int i = 0; i < kRowsWaveKeys; ++i)
+                if (t0 + wave * kRowsWaveKeys + i == pos)
+                    vh[i] = vn;
+        }
         // rescaled running sums plus this wave's keys in order
 #pragma unroll
-        for (int h = 0; h < H; ++h) {
+        for (int h = 0; h < G; ++h) {
             const double f = sF[h];
 #pragma unroll
             for (int c = 0; c < C; ++c)
@@ -595,7 +633,7 @@ __global__ __launch_bounds__(kRowsThreads) void attention_rows_kernel(RowsAttent
             for (int c = 0; c < C; ++c)
                 v[c] = (double) vh[i].at(c);
 #pragma unroll
-            for (int h = 0; h < H; ++h) {
+            for (int h = 0; h < G; ++h) {
                 const double wi = sS[h][wave * kRowsWaveKeys + i];
 #pragma unroll
                 for (int c = 0; c < C; ++c)
@@ -605,31 +643,31 @@ __global__ __launch_bounds__(kRowsThreads) void attention_rows_kernel(RowsAttent
         __syncthreads(); // the next tile rewrites the scores
     }
 
-    // the split's partial: the four waves' sums in wave order, kAccHeads
-    // heads a pass
+    // the split's partial of the group's heads: the four waves' sums in wave
+    // order, kAccHeads heads a pass
     const int64_t slot = (int64_t) seq * kRowsMaxSplits + split;
 #pragma unroll
-    for (int h0 = 0; h0 < H; h0 += kAccHeads) {
+    for (int h0 = 0; h0 < G; h0 += kAccHeads) {
         if (h0 > 0)
             __syncthreads();
 #pragma unroll
-        for (int h = 0; h < kAccHeads && h0 + h < H; ++h)
+        for (int h = 0; h < kAccHeads && h0 + h < G; ++h)
 #pragma unroll
             for (int c = 0; c < C; ++c)
                 sAcc[wave][h * hd + c0 + c] = acc[h0 + h][c];
         __syncthreads();
-        const int width = min(kAccHeads, H - h0) * hd;
+        const int width = min(kAccHeads, G - h0) * hd;
         for (int o = t; o < width; o += kRowsThreads) {
             double v = sAcc[0][o];
 #pragma unroll
             for (int w = 1; w < kRowsWaves; ++w)
                 v += sAcc[w][o];
-            a.ws_o[slot * qW + h0 * hd + o] = v;
+            a.ws_o[slot * qW + (hBase + h0) * hd + o] = v;
         }
     }
-    if (t < H) {
-        a.ws_ml[(slot * H + t) * 2] = sMax[t];
-        a.ws_ml[(slot * H + t) * 2 + 1] = sSum[t];
+    if (t < G) {
+        a.ws_ml[(slot * H + hBase + t) * 2] = sMax[t];
+        a.ws_ml[(slot * H + hBase + t) * 2 + 1] = sSum[t];
     }
 }
 
@@ -807,10 +845,12 @@ hipError_t launch_rows_attention(const RowsAttentionArgs &a, int rows, int max_p
         || !rows_attention_supported(a.heads, 1, a.head_dim, max_positions)
         || a.per_split != rows_attention_split_keys(max_positions) || a.max_positions != max_positions)
         return hipErrorInvalidValue;
-    const dim3 grid((max_positions + a.per_split - 1) / a.per_split, rows);
+    const int groups = a.heads > kRowsHeadGroup ? a.heads / kRowsHeadGroup : 1;
+    const dim3 grid((max_positions + a.per_split - 1) / a.per_split, rows, groups);
     const int C = a.head_dim / 64;
 #define GQ8_ROWS_ATTENTION(CC, HH)                                                              \
-    hipLaunchKernelGGL((attention_rows_kernel<CC, HH>), grid, dim3(kRowsThreads), 0, stream, a)
+    hipLaunchKernelGGL((attention_rows_kernel<CC, HH, (HH > kRowsHeadGroup ? kRowsHeadGroup : HH)>), grid, \
+                       dim3(kRowsThreads), 0, stream, a)
     switch (a.heads * 8 + C) {
     case 2 * 8 + 1: GQ8_ROWS_ATTENTION(1, 2); break;
     case 2 * 8 + 2: GQ8_ROWS_ATTENTION(2, 2); break;
