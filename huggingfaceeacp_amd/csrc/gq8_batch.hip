@@ -73,6 +73,10 @@ RowsPlan rows_plan(int inner, int outputs)
     int per = (nb + kRowsWaves - 1) / kRowsWaves;
     if (per > kChunkBlocks)
         per = (per + kChunkBlocks - 1) / kChunkBlocks * kChunkBlocks;
+    // rows short enough that a tile's four waves hold all of its weight
+    // chunks in flight at once take no split: one round trip, no merge
+    if (per <= kRowsPrefetch * kChunkBlocks)
+        return {kRowsWaves, per, 1};
     while (kRowsWaves * per > kRowsMaxRange)
         per /= 2;
     int splits = (nb + kRowsWaves * per - 1) / (kRowsWaves * per);
@@ -149,6 +153,44 @@ __device__ inline void load_weight_chunk(WeightChunk &c, const uint8_t *wRow, co
     }
 }
 
+// One chunk of the activation rows for the direct path (no staging): 8
+// blocks of sequence (lane % 16)'s row at this lane's 8-byte slice (the MFMA
+// A fragment), and the fp16 scales of this lane's four accumulator rows
+// 4 (lane / 16) + r over the same 8 blocks.
+struct ActChunk {
+    long x[kChunkBlocks];
+    uint32_t s[4][kChunkBlocks / 2];
+};
+
+__device__ inline void load_act_chunk(ActChunk &c, const uint8_t *xRow, const uint16_t *const (&xs)[4],
+                                      int c0)
+{
+#pragma unroll
+    for (int k = 0; k < kChunkBlocks; ++k)
+        c.x[k] = *reinterpret_cast<const long *>(xRow + (int64_t) (c0 + k) * kBlock);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(xs[r] + c0);
+        c.s[r][0] = v.x; c.s[r][1] = v.y; c.s[r][2] = v.z; c.s[r][3] = v.w;
+    }
+}
+
+// The weight chunk against the activation chunk, in chunk_products'
+// arithmetic (its staged scales are these, converted to fp32 the same way).
+__device__ inline void chunk_products_direct(const WeightChunk &c, const ActChunk &x, double (&acc)[4])
+{
+#pragma unroll
+    for (int k = 0; k < kChunkBlocks; ++k) {
+        const float sw = half_of(c.s[k / 2], k & 1);
+        const v4i zero = {0, 0, 0, 0};
+        const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(x.x[k], c.w[k], zero, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            acc[r] = fma((double) d[r], (double) (sw * half_of(x.s[r][k / 2], k & 1)), acc[r]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 // The chunk against the staged activation blocks: one MFMA a block, then
 // acc[r] (sequence 4 (lane / 16) + r, output lane % 16) += dot * (sw * sx)
 // (the scale product exact in fp32, the product exact in double).
@@ -177,10 +219,14 @@ __device__ inline void chunk_products(const WeightChunk &c, const long *sX, cons
 
 // NC > 0: every wave takes exactly NC whole chunks (the loop unrolled, so
 // each chunk's wait counts only the loads before it); NC == 0: any range.
-template <int WPT, int NC>
+// Direct (WPT 4, whole chunks): no staging; each wave loads its activation
+// blocks next to its weight chunks (L2 hits: a quarter of a tile's blocks is
+// read by that tile's wave alone, so staging would buy no reuse).
+template <int WPT, int NC, bool Direct = false>
 __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
 {
     constexpr bool V = NC > 0;
+    static_assert(!Direct || (WPT == kRowsWaves && NC > 0), "direct: split tiles, whole chunks");
     constexpr int kTiles = kRowsWaves / WPT; // tiles a workgroup
     extern __shared__ __attribute__((aligned(16))) unsigned char rowsLds[];
     const int range = WPT * a.per;
@@ -209,9 +255,40 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
     const uint8_t *wRow = a.w8 + (int64_t) n * a.inner + (lane >> 4) * 8;
     const uint16_t *wScale = reinterpret_cast<const uint16_t *>(a.w8 + (int64_t) a.outputs * a.inner)
                              + (int64_t) n * nb;
+    const uint16_t *xScales = reinterpret_cast<const uint16_t *>(a.x8 + (int64_t) a.x_rows * a.inner);
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    if constexpr (Direct) {
+        const int grp = lane >> 4;
+        const uint8_t *xRow = a.x8 + (int64_t) min(col, a.rows - 1) * a.inner + grp * 8;
+        const uint16_t *const xs[4] = {xScales + (int64_t) min(4 * grp + 0, a.rows - 1) * nb,
+                                       xScales + (int64_t) min(4 * grp + 1, a.rows - 1) * nb,
+                                       xScales + (int64_t) min(4 * grp + 2, a.rows - 1) * nb,
+                                       xScales + (int64_t) min(4 * grp + 3, a.rows - 1) * nb};
+        constexpr int P = NC < kRowsPrefetch ? NC : kRowsPrefetch;
+        WeightChunk wb[P];
+        ActChunk xb[P];
+        if (b0 < b1) { // the last split's waves may have no blocks
+#pragma unroll
+            for (int i = 0; i < P; ++i) {
+                load_weight_chunk<true>(wb[i], wRow, wScale, b0 + i * kChunkBlocks, b1);
+                load_act_chunk(xb[i], xRow, xs, b0 + i * kChunkBlocks);
+            }
+#pragma unroll
+            for (int i = 0; i < NC; ++i) {
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_sched_barrier(0);
+                chunk_products_direct(wb[i % P], xb[i % P], acc);
+                __builtin_amdgcn_sched_barrier(0);
+                asm volatile("" ::: "memory");
+                if (i + P < NC) {
+                    load_weight_chunk<true>(wb[i % P], wRow, wScale, b0 + (i + P) * kChunkBlocks, b1);
+                    load_act_chunk(xb[i % P], xRow, xs, b0 + (i + P) * kChunkBlocks);
+                }
+            }
+        }
+    } else {
     // stage the workgroup's activation blocks in MFMA fragment order (lane l
     // of block b: sequence l % 16, bytes 8 (l / 16) .. + 8) and their scales
-    const uint16_t *xScales = reinterpret_cast<const uint16_t *>(a.x8 + (int64_t) a.x_rows * a.inner);
     // every load first (clamped into range), then the LDS writes; with whole
     // chunks the range is WPT NC chunks, so WPT NC pieces a thread
     constexpr int kMaxRange = V ? WPT * NC * kChunkBlocks : kRowsMaxRange;
@@ -260,7 +337,6 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
     }
     __syncthreads();
 
-    double acc[4] = {0.0, 0.0, 0.0, 0.0};
     // two weight buffers: the next chunk's loads are in flight while this
     // one computes
     if constexpr (V) {
@@ -286,6 +362,7 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
             chunk_products<false>(buf[0], sX, sSx, c0 - r0, c0, b1, lane, acc);
         }
     }
+    } // staged
 
     // a tile's sum over its waves (in block order), one (sequence, output)
     // cell a thread; tile k of the workgroup lands in sPart[k]
@@ -809,7 +886,25 @@ hipError_t launch_rows(const RowsArgs &a, const RowsPlan &plan, hipStream_t stre
     case 16: GQ8_ROWS(W, 16); break;                                                           \
     default: GQ8_ROWS(W, 0); break;                                                            \
     }
-    if (plan.wpt == 1) {
+    // split tiles of whole chunks with no split over workgroups (every chunk
+    // in flight at once) load their activation blocks directly (the scale
+    // rows 16-byte aligned: x8 aligned, nb a multiple of 8)
+    const bool direct = plan.wpt == kRowsWaves && plan.splits == 1 && whole && !a.geglu8
+                        && reinterpret_cast<uintptr_t>(a.x8) % 16 == 0;
+    if (direct) {
+        const size_t epilogue = (size_t) kRowsWaves * kBatchRows * (kRowsTile + 1) * sizeof(double);
+#define GQ8_ROWS_DIRECT(N)                                                                     \
+    hipLaunchKernelGGL((q8_rows_kernel<kRowsWaves, N, true>), grid, dim3(kRowsThreads), epilogue, \
+                       stream, a)
+        switch (nc) {
+        case 1: GQ8_ROWS_DIRECT(1); break;
+        case 2: GQ8_ROWS_DIRECT(2); break;
+        case 4: GQ8_ROWS_DIRECT(4); break;
+        case 8: GQ8_ROWS_DIRECT(8); break;
+        default: GQ8_ROWS_DIRECT(16); break;
+        }
+#undef GQ8_ROWS_DIRECT
+    } else if (plan.wpt == 1) {
         GQ8_ROWS_NC(1);
     } else {
         GQ8_ROWS_NC(kRowsWaves);
