@@ -48,6 +48,8 @@ constexpr int kChunkBlocks = 8;       // blocks a wave's weight loads cover at o
 constexpr int kRowsMaxRange = 128;    // blocks of the activation rows a workgroup stages
 constexpr int kRowsManyTiles = 1024;  // products this wide give each wave whole rows
 constexpr int kRowsPrefetch = 2;      // weight chunks in flight a wave
+constexpr int kRowsStreamGroups = 512; // workgroups of a streamed product (two a compute unit)
+constexpr int kRowsStreamAhead = 4;    // weight chunks in flight a wave of a streamed product
 
 // A workgroup stages `range` blocks of the activation rows in LDS and its
 // waves stream weight rows against them.  Wide products (tiles >= 1024: gate
@@ -187,6 +189,7 @@ __device__ inline void chunk_products_direct(const WeightChunk &c, const ActChun
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             acc[r] = fma((double) d[r], (double) (sw * half_of(x.s[r][k / 2], k & 1)), acc[r]);
+        asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
         __builtin_amdgcn_sched_barrier(0);
     }
 }
@@ -212,8 +215,55 @@ __device__ inline void chunk_products(const WeightChunk &c, const long *sX, cons
         acc[2] = fma((double) d[2], (double) (sw * sx.z), acc[2]);
         acc[3] = fma((double) d[3], (double) (sw * sx.w), acc[3]);
         // one block at a time: the results of hoisted products would hold
-        // accumulation registers that cost occupancy
+        // accumulation registers that cost occupancy (the sums are pinned
+        // here, so they cannot sink to the end of a tile either)
+        asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
         __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Stages blocks [r0, rEnd) (at most kMaxRange) of the activation rows in LDS
+// in MFMA fragment order (lane l of block b: sequence l % 16, bytes
+// 8 (l / 16) .. + 8) and their scales as fp32: every load first (clamped into
+// range), then the LDS writes.  No barrier.
+template <int kMaxRange>
+__device__ inline void stage_activation(const RowsArgs &a, int r0, int rEnd, long *sX, float *sSx,
+                                        int t)
+{
+    constexpr int kPieces = kMaxRange * kBatchRows * 2 / kRowsThreads; // 16-byte pieces
+    constexpr int kScales = (kMaxRange * kBatchRows + kRowsThreads - 1) / kRowsThreads;
+    const int nb = a.inner / kBlock;
+    const uint16_t *xScales = reinterpret_cast<const uint16_t *>(a.x8 + (int64_t) a.x_rows * a.inner);
+    const int pieces = (rEnd - r0) * kBatchRows * 2, scales = (rEnd - r0) * kBatchRows;
+    uint4 piece[kPieces];
+    uint16_t scaleBits[kScales];
+#pragma unroll
+    for (int i = 0; i < kPieces; ++i) {
+        const int p = min(t + i * kRowsThreads, pieces - 1);
+        const int rb = p >> 5, m = (p >> 1) & 15, h = p & 1;
+        piece[i] = *reinterpret_cast<const uint4 *>(a.x8 + (int64_t) min(m, a.rows - 1) * a.inner
+                                                    + (int64_t) (r0 + rb) * kBlock + h * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < kScales; ++i) {
+        const int e = min(t + i * kRowsThreads, scales - 1);
+        scaleBits[i] = xScales[(int64_t) min(e & 15, a.rows - 1) * nb + r0 + (e >> 4)];
+    }
+#pragma unroll
+    for (int i = 0; i < kPieces; ++i) {
+        const int p = t + i * kRowsThreads;
+        if (p < pieces) {
+            const int rb = p >> 5, m = (p >> 1) & 15, h = p & 1;
+            uint2 *dst = reinterpret_cast<uint2 *>(sX) + rb * 64 + m;
+            dst[(2 * h) * 16] = make_uint2(piece[i].x, piece[i].y);
+            dst[(2 * h + 1) * 16] = make_uint2(piece[i].z, piece[i].w);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kScales; ++i) {
+        const int e = t + i * kRowsThreads;
+        if (e < scales)
+            sSx[e] = half_value(scaleBits[i]);
     }
 }
 
@@ -287,44 +337,8 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
             }
         }
     } else {
-    // stage the workgroup's activation blocks in MFMA fragment order (lane l
-    // of block b: sequence l % 16, bytes 8 (l / 16) .. + 8) and their scales
-    // every load first (clamped into range), then the LDS writes; with whole
-    // chunks the range is WPT NC chunks, so WPT NC pieces a thread
-    constexpr int kMaxRange = V ? WPT * NC * kChunkBlocks : kRowsMaxRange;
-    constexpr int kPieces = kMaxRange * kBatchRows * 2 / kRowsThreads; // 16-byte pieces
-    constexpr int kScales = (kMaxRange * kBatchRows + kRowsThreads - 1) / kRowsThreads;
-    const int pieces = (rEnd - r0) * kBatchRows * 2, scales = (rEnd - r0) * kBatchRows;
-    uint4 piece[kPieces];
-    uint16_t scaleBits[kScales];
-#pragma unroll
-    for (int i = 0; i < kPieces; ++i) {
-        const int p = min(t + i * kRowsThreads, pieces - 1);
-        const int rb = p >> 5, m = (p >> 1) & 15, h = p & 1;
-        piece[i] = *reinterpret_cast<const uint4 *>(a.x8 + (int64_t) min(m, a.rows - 1) * a.inner
-                                                    + (int64_t) (r0 + rb) * kBlock + h * 16);
-    }
-#pragma unroll
-    for (int i = 0; i < kScales; ++i) {
-        const int e = min(t + i * kRowsThreads, scales - 1);
-        scaleBits[i] = xScales[(int64_t) min(e & 15, a.rows - 1) * nb + r0 + (e >> 4)];
-    }
-#pragma unroll
-    for (int i = 0; i < kPieces; ++i) {
-        const int p = t + i * kRowsThreads;
-        if (p < pieces) {
-            const int rb = p >> 5, m = (p >> 1) & 15, h = p & 1;
-            uint2 *dst = reinterpret_cast<uint2 *>(sX) + rb * 64 + m;
-            dst[(2 * h) * 16] = make_uint2(piece[i].x, piece[i].y);
-            dst[(2 * h + 1) * 16] = make_uint2(piece[i].z, piece[i].w);
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < kScales; ++i) {
-        const int e = t + i * kRowsThreads;
-        if (e < scales)
-            sSx[e] = half_value(scaleBits[i]);
-    }
+    // with whole chunks the range is WPT NC chunks
+    stage_activation<V ? WPT * NC * kChunkBlocks : kRowsMaxRange>(a, r0, rEnd, sX, sSx, t);
     // then up to kRowsPrefetch chunks of weights in flight a wave: behind
     // the LDS writes, since once the weight stream fills the memory queues a
     // wave's vector memory instructions issue only as fast as loads retire
@@ -441,6 +455,101 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
     }
     if (t == 0) // ready for the next launch
         __hip_atomic_store(a.tickets + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wide products with no GeGLU (the lm_head): a workgroup stages the whole
+// activation rows (nb = NC chunks) once, then takes groups of four tiles
+// (one a wave) from a shared counter until none is left, so a workgroup that
+// the memory system serves faster takes more of them.  Each wave's weight
+// chunks stream across the group boundaries, P ahead (the next group is
+// claimed when a group starts and published at the workgroup barrier P
+// chunks before its end); a tile's 16 x 16 outputs go straight from its
+// accumulators to y.  counters[0] is the next group, counters[1] the
+// workgroups done; the last one done zeroes both for the next launch.  The
+// arithmetic is q8_rows_kernel's.
+template <int NC>
+__global__ __launch_bounds__(kRowsThreads) void q8_rows_stream_kernel(RowsArgs a)
+{
+    constexpr int nb = NC * kChunkBlocks;
+    constexpr int P = NC < kRowsStreamAhead ? NC : kRowsStreamAhead;
+    __shared__ __attribute__((aligned(16))) long sX[nb * 64];
+    __shared__ __attribute__((aligned(16))) float sSx[nb * kBatchRows];
+    __shared__ int sGroup[2];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int tiles = (a.outputs + kRowsTile - 1) / kRowsTile;
+    const int groups = (tiles + kRowsWaves - 1) / kRowsWaves;
+    int *counters = a.tickets;
+    const uint16_t *wScales = reinterpret_cast<const uint16_t *>(a.w8 + (int64_t) a.outputs * a.inner);
+    auto row_of = [&](int g) { return min((g * kRowsWaves + wave) * kRowsTile + col, a.outputs - 1); };
+    auto claim = [&]() {
+        return __hip_atomic_fetch_add(counters, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+
+    if (t == 0)
+        sGroup[0] = claim();
+    stage_activation<nb>(a, 0, nb, sX, sSx, t);
+    __syncthreads();
+    int g = sGroup[0];
+    WeightChunk buf[P];
+    if (g < groups) {
+        const int n = row_of(g);
+#pragma unroll
+        for (int i = 0; i < P; ++i)
+            load_weight_chunk<true>(buf[i], a.w8 + (int64_t) n * a.inner + grp * 8,
+                                    wScales + (int64_t) n * nb, i * kChunkBlocks, nb);
+    }
+    int slot = 1;
+#pragma nounroll
+    while (g < groups) {
+        if (t == 0)
+            sGroup[slot] = claim(); // the next group, in flight while this one streams
+        const int n = row_of(g);
+        const uint8_t *wRow = a.w8 + (int64_t) n * a.inner + grp * 8;
+        const uint16_t *sRow = wScales + (int64_t) n * nb;
+        int next = groups;
+        double acc[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            chunk_products<true>(buf[i % P], sX, sSx, i * kChunkBlocks, i * kChunkBlocks, nb, lane, acc);
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("" ::: "memory");
+            if (i + P < NC) {
+                load_weight_chunk<true>(buf[i % P], wRow, sRow, (i + P) * kChunkBlocks, nb);
+            } else {
+                if (i + P == NC) { // the next group's index, published
+                    __syncthreads();
+                    next = sGroup[slot];
+                }
+                if (next < groups) {
+                    const int m = row_of(next);
+                    load_weight_chunk<true>(buf[i % P], a.w8 + (int64_t) m * a.inner + grp * 8,
+                                            wScales + (int64_t) m * nb, (i + P - NC) * kChunkBlocks,
+                                            nb);
+                }
+            }
+        }
+        const int on = (g * kRowsWaves + wave) * kRowsTile + col;
+        if (on < a.outputs) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = 4 * grp + r;
+                if (m < a.rows)
+                    a.y[(int64_t) m * a.y_stride + on] = (float) acc[r];
+            }
+        }
+        g = next;
+        slot ^= 1;
+    }
+    if (t == 0
+        && __hip_atomic_fetch_add(counters + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+               == (int) gridDim.x - 1) {
+        // every workgroup has claimed its last group: ready for the next launch
+        __hip_atomic_store(counters, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(counters + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // ---- attention of the lockstep rows ---------------------------------------------
@@ -891,7 +1000,20 @@ hipError_t launch_rows(const RowsArgs &a, const RowsPlan &plan, hipStream_t stre
     // rows 16-byte aligned: x8 aligned, nb a multiple of 8)
     const bool direct = plan.wpt == kRowsWaves && plan.splits == 1 && whole && !a.geglu8
                         && reinterpret_cast<uintptr_t>(a.x8) % 16 == 0;
-    if (direct) {
+    // wide products with whole rows of whole chunks and no GeGLU stream
+    // their tiles through about two workgroups a compute unit
+    const int groups = (rows_ticket_count(outputs) + kRowsWaves - 1) / kRowsWaves;
+    const bool streamed = plan.wpt == 1 && plan.splits == 1 && whole && !a.geglu8 && plan.per == nb
+                          && (nc == 4 || nc == 8) && groups > kRowsStreamGroups;
+    if (streamed) {
+        if (!a.tickets)
+            return hipErrorInvalidValue;
+        const dim3 sgrid(kRowsStreamGroups);
+        if (nc == 4)
+            hipLaunchKernelGGL((q8_rows_stream_kernel<4>), sgrid, dim3(kRowsThreads), 0, stream, a);
+        else
+            hipLaunchKernelGGL((q8_rows_stream_kernel<8>), sgrid, dim3(kRowsThreads), 0, stream, a);
+    } else if (direct) {
         const size_t epilogue = (size_t) kRowsWaves * kBatchRows * (kRowsTile + 1) * sizeof(double);
 #define GQ8_ROWS_DIRECT(N)                                                                     \
     hipLaunchKernelGGL((q8_rows_kernel<kRowsWaves, N, true>), grid, dim3(kRowsThreads), epilogue, \
