@@ -101,6 +101,7 @@ struct RowsArgs {
     const uint8_t *x8;
     int x_rows, rows;
     const uint8_t *w8;
+    const uint8_t *w8t; // non-null: w8 in fragment order (tile_weights_kernel), read instead
     int inner, outputs, per;
     float *y;
     int y_stride, residual;
@@ -131,19 +132,49 @@ struct WeightChunk {
     uint32_t s[kChunkBlocks / 2];
 };
 
+// A wave's weight stream: this lane's slice of block 0 of the wave's tile
+// (rows 16 tile .. 16 tile + 15; lane l takes row l % 16 at byte 8 (l / 16)
+// of a block) and the tile's scales.  Tiled: the fragment-ordered copy, where
+// block b of a tile is 512 contiguous bytes (lane l's 8 at 8 l) and chunk c's
+// scales 256 (row r's 8 at 16 r); the row-major layout puts a tile's block
+// at 16 places 2 KB and more apart, which streams about a third slower.
+template <bool Tiled>
+struct WeightRows {
+    const uint8_t *bytes;
+    const uint16_t *scales;
+    __device__ WeightRows(const RowsArgs &a, int tile, int lane)
+    {
+        const int nb = a.inner / kBlock, tiles = (a.outputs + kRowsTile - 1) / kRowsTile;
+        if constexpr (Tiled) {
+            const int tt = min(tile, tiles - 1); // clamped into range; never stored
+            bytes = a.w8t + (int64_t) tt * nb * 512 + lane * 8;
+            scales = reinterpret_cast<const uint16_t *>(a.w8t + (int64_t) tiles * kRowsTile * a.inner)
+                     + (int64_t) tt * nb * kRowsTile + (lane & 15) * kChunkBlocks;
+        } else {
+            const int n = min(tile * kRowsTile + (lane & 15), a.outputs - 1);
+            bytes = a.w8 + (int64_t) n * a.inner + (lane >> 4) * 8;
+            scales = reinterpret_cast<const uint16_t *>(a.w8 + (int64_t) a.outputs * a.inner)
+                     + (int64_t) n * nb;
+        }
+    }
+};
+
 // V: whole chunks (the block count and every range a multiple of 8), the
-// scales one 16-byte load; else blocks past `end` are loaded clamped.
-template <bool V>
-__device__ inline void load_weight_chunk(WeightChunk &c, const uint8_t *wRow, const uint16_t *wScale,
-                                         int c0, int end)
+// scales one 16-byte load; else (row-major only) blocks past `end` are
+// loaded clamped.
+template <bool V, bool Tiled = false>
+__device__ inline void load_weight_chunk(WeightChunk &c, const WeightRows<Tiled> &ws, int c0, int end)
 {
+    static_assert(V || !Tiled, "the fragment-ordered copy is read in whole chunks");
+    const uint8_t *wRow = ws.bytes;
+    const uint16_t *wScale = ws.scales;
 #pragma unroll
     for (int k = 0; k < kChunkBlocks; ++k) {
         const int b = V ? c0 + k : min(c0 + k, end - 1);
-        c.w[k] = *reinterpret_cast<const long *>(wRow + (int64_t) b * kBlock);
+        c.w[k] = *reinterpret_cast<const long *>(wRow + (int64_t) b * (Tiled ? 512 : kBlock));
     }
     if constexpr (V) {
-        const uint4 v = *reinterpret_cast<const uint4 *>(wScale + c0);
+        const uint4 v = *reinterpret_cast<const uint4 *>(wScale + (Tiled ? (c0 >> 3) * 128 : c0));
         c.s[0] = v.x; c.s[1] = v.y; c.s[2] = v.z; c.s[3] = v.w;
     } else {
 #pragma unroll
@@ -272,11 +303,12 @@ __device__ inline void stage_activation(const RowsArgs &a, int r0, int rEnd, lon
 // Direct (WPT 4, whole chunks): no staging; each wave loads its activation
 // blocks next to its weight chunks (L2 hits: a quarter of a tile's blocks is
 // read by that tile's wave alone, so staging would buy no reuse).
-template <int WPT, int NC, bool Direct = false>
+template <int WPT, int NC, bool Direct = false, bool Tiled = false>
 __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
 {
     constexpr bool V = NC > 0;
     static_assert(!Direct || (WPT == kRowsWaves && NC > 0), "direct: split tiles, whole chunks");
+    static_assert(!Tiled || V, "the fragment-ordered copy is read in whole chunks");
     constexpr int kTiles = kRowsWaves / WPT; // tiles a workgroup
     extern __shared__ __attribute__((aligned(16))) unsigned char rowsLds[];
     const int range = WPT * a.per;
@@ -301,10 +333,7 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
     const int b1 = min(b0 + a.per, nb);
 
     // this wave's weight rows (clamped into range; never stored)
-    const int n = min(n0 + col, a.outputs - 1);
-    const uint8_t *wRow = a.w8 + (int64_t) n * a.inner + (lane >> 4) * 8;
-    const uint16_t *wScale = reinterpret_cast<const uint16_t *>(a.w8 + (int64_t) a.outputs * a.inner)
-                             + (int64_t) n * nb;
+    const WeightRows<Tiled> ws(a, tile, lane);
     const uint16_t *xScales = reinterpret_cast<const uint16_t *>(a.x8 + (int64_t) a.x_rows * a.inner);
     double acc[4] = {0.0, 0.0, 0.0, 0.0};
     if constexpr (Direct) {
@@ -320,7 +349,7 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
         if (b0 < b1) { // the last split's waves may have no blocks
 #pragma unroll
             for (int i = 0; i < P; ++i) {
-                load_weight_chunk<true>(wb[i], wRow, wScale, b0 + i * kChunkBlocks, b1);
+                load_weight_chunk<true, Tiled>(wb[i], ws, b0 + i * kChunkBlocks, b1);
                 load_act_chunk(xb[i], xRow, xs, b0 + i * kChunkBlocks);
             }
 #pragma unroll
@@ -331,7 +360,7 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
                 __builtin_amdgcn_sched_barrier(0);
                 asm volatile("" ::: "memory");
                 if (i + P < NC) {
-                    load_weight_chunk<true>(wb[i % P], wRow, wScale, b0 + (i + P) * kChunkBlocks, b1);
+                    load_weight_chunk<true, Tiled>(wb[i % P], ws, b0 + (i + P) * kChunkBlocks, b1);
                     load_act_chunk(xb[i % P], xRow, xs, b0 + (i + P) * kChunkBlocks);
                 }
             }
@@ -347,7 +376,7 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
     if (b0 < b1) {
 #pragma unroll
         for (int i = 0; i < P; ++i)
-            load_weight_chunk<V>(buf[i], wRow, wScale, V ? b0 + i * kChunkBlocks : b0, b1);
+            load_weight_chunk<V, Tiled>(buf[i], ws, V ? b0 + i * kChunkBlocks : b0, b1);
     }
     __syncthreads();
 
@@ -366,13 +395,13 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
                 __builtin_amdgcn_sched_barrier(0);
                 asm volatile("" ::: "memory");
                 if (i + P < NC) // the buffer just consumed takes the chunk P ahead
-                    load_weight_chunk<true>(buf[i % P], wRow, wScale, b0 + (i + P) * kChunkBlocks, b1);
+                    load_weight_chunk<true, Tiled>(buf[i % P], ws, b0 + (i + P) * kChunkBlocks, b1);
             }
         }
     } else {
         for (int c0 = b0; c0 < b1; c0 += kChunkBlocks) {
             if (c0 > b0)
-                load_weight_chunk<false>(buf[0], wRow, wScale, c0, b1);
+                load_weight_chunk<false>(buf[0], WeightRows<false>(a, tile, lane), c0, b1);
             chunk_products<false>(buf[0], sX, sSx, c0 - r0, c0, b1, lane, acc);
         }
     }
@@ -467,7 +496,7 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
 // accumulators to y.  counters[0] is the next group, counters[1] the
 // workgroups done; the last one done zeroes both for the next launch.  The
 // arithmetic is q8_rows_kernel's.
-template <int NC>
+template <int NC, bool Tiled>
 __global__ __launch_bounds__(kRowsThreads) void q8_rows_stream_kernel(RowsArgs a)
 {
     constexpr int nb = NC * kChunkBlocks;
@@ -480,8 +509,6 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_stream_kernel(RowsArgs a
     const int tiles = (a.outputs + kRowsTile - 1) / kRowsTile;
     const int groups = (tiles + kRowsWaves - 1) / kRowsWaves;
     int *counters = a.tickets;
-    const uint16_t *wScales = reinterpret_cast<const uint16_t *>(a.w8 + (int64_t) a.outputs * a.inner);
-    auto row_of = [&](int g) { return min((g * kRowsWaves + wave) * kRowsTile + col, a.outputs - 1); };
     auto claim = [&]() {
         return __hip_atomic_fetch_add(counters, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
@@ -493,20 +520,17 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_stream_kernel(RowsArgs a
     int g = sGroup[0];
     WeightChunk buf[P];
     if (g < groups) {
-        const int n = row_of(g);
+        const WeightRows<Tiled> ws(a, g * kRowsWaves + wave, lane);
 #pragma unroll
         for (int i = 0; i < P; ++i)
-            load_weight_chunk<true>(buf[i], a.w8 + (int64_t) n * a.inner + grp * 8,
-                                    wScales + (int64_t) n * nb, i * kChunkBlocks, nb);
+            load_weight_chunk<true, Tiled>(buf[i], ws, i * kChunkBlocks, nb);
     }
     int slot = 1;
 #pragma nounroll
     while (g < groups) {
         if (t == 0)
             sGroup[slot] = claim(); // the next group, in flight while this one streams
-        const int n = row_of(g);
-        const uint8_t *wRow = a.w8 + (int64_t) n * a.inner + grp * 8;
-        const uint16_t *sRow = wScales + (int64_t) n * nb;
+        const WeightRows<Tiled> ws(a, g * kRowsWaves + wave, lane);
         int next = groups;
         double acc[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
@@ -517,18 +541,16 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_stream_kernel(RowsArgs a
             __builtin_amdgcn_sched_barrier(0);
             asm volatile("" ::: "memory");
             if (i + P < NC) {
-                load_weight_chunk<true>(buf[i % P], wRow, sRow, (i + P) * kChunkBlocks, nb);
+                load_weight_chunk<true, Tiled>(buf[i % P], ws, (i + P) * kChunkBlocks, nb);
             } else {
                 if (i + P == NC) { // the next group's index, published
                     __syncthreads();
                     next = sGroup[slot];
                 }
-                if (next < groups) {
-                    const int m = row_of(next);
-                    load_weight_chunk<true>(buf[i % P], a.w8 + (int64_t) m * a.inner + grp * 8,
-                                            wScales + (int64_t) m * nb, (i + P - NC) * kChunkBlocks,
-                                            nb);
-                }
+                if (next < groups)
+                    load_weight_chunk<true, Tiled>(buf[i % P],
+                                                   WeightRows<Tiled>(a, next * kRowsWaves + wave, lane),
+                                                   (i + P - NC) * kChunkBlocks, nb);
             }
         }
         const int on = (g * kRowsWaves + wave) * kRowsTile + col;
@@ -549,6 +571,42 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_stream_kernel(RowsArgs a
         // every workgroup has claimed its last group: ready for the next launch
         __hip_atomic_store(counters, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(counters + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// The fragment-ordered copy of an Int8Blocks weight (WeightRows<true>'s
+// layout): thread i of the bytes writes lane (i % 64)'s 8 bytes of block
+// (i / 64) % nb of tile i / (64 nb); rows past `outputs` are zero.  Then the
+// scales, 8 (one chunk of one row) a thread.
+__global__ __launch_bounds__(kRowsThreads) void tile_weights_kernel(const uint8_t *__restrict__ w8,
+                                                                   int outputs, int inner,
+                                                                   uint8_t *__restrict__ out)
+{
+    const int nb = inner / kBlock, tiles = (outputs + kRowsTile - 1) / kRowsTile;
+    const int64_t pieces = (int64_t) tiles * nb * 64, chunks = (int64_t) tiles * kRowsTile * (nb / 8);
+    const uint16_t *scales = reinterpret_cast<const uint16_t *>(w8 + (int64_t) outputs * inner);
+    uint16_t *scalesOut = reinterpret_cast<uint16_t *>(out + (int64_t) tiles * kRowsTile * inner);
+    for (int64_t i = blockIdx.x * (int64_t) blockDim.x + threadIdx.x; i < pieces + chunks;
+         i += (int64_t) gridDim.x * blockDim.x) {
+        if (i < pieces) {
+            const int lane = (int) (i % 64), b = (int) ((i / 64) % nb);
+            const int64_t tile = i / (64 * (int64_t) nb);
+            const int64_t row = tile * kRowsTile + lane % 16;
+            long v = 0;
+            if (row < outputs)
+                v = *reinterpret_cast<const long *>(w8 + row * inner + (int64_t) b * kBlock
+                                                    + (lane / 16) * 8);
+            reinterpret_cast<long *>(out)[i] = v;
+        } else {
+            const int64_t j = i - pieces; // (tile, chunk, row)
+            const int r = (int) (j % kRowsTile), c = (int) ((j / kRowsTile) % (nb / 8));
+            const int64_t tile = j / (kRowsTile * (int64_t) (nb / 8));
+            const int64_t row = tile * kRowsTile + r;
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (row < outputs)
+                v = *reinterpret_cast<const uint4 *>(scales + row * nb + c * 8);
+            reinterpret_cast<uint4 *>(scalesOut)[j] = v;
+        }
     }
 }
 
@@ -933,10 +991,38 @@ namespace {
 hipError_t launch_rows(const RowsArgs &a, const RowsPlan &plan, hipStream_t stream);
 }
 
+bool rows_tiled_supported(int inner, int outputs)
+{
+    return inner > 0 && inner % (kChunkBlocks * kBlock) == 0 && outputs > 0;
+}
+
+size_t rows_tiled_bytes(int inner, int outputs)
+{
+    if (!rows_tiled_supported(inner, outputs))
+        return 0;
+    const size_t rowsPadded = (size_t) rows_ticket_count(outputs) * kRowsTile;
+    return rowsPadded * inner + rowsPadded * (inner / kBlock) * sizeof(uint16_t);
+}
+
+hipError_t launch_tile_weights(const uint8_t *w8, int inner, int outputs, uint8_t *out,
+                               hipStream_t stream)
+{
+    if (!w8 || !out || !rows_tiled_supported(inner, outputs)
+        || reinterpret_cast<uintptr_t>(w8) % 16 != 0 || reinterpret_cast<uintptr_t>(out) % 16 != 0
+        || ((size_t) outputs * inner) % 16 != 0)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(tile_weights_kernel, dim3(4096), dim3(kRowsThreads), 0, stream, w8, outputs,
+                       inner, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_q8_rows(const uint8_t *x8, int x_rows, int rows, const uint8_t *w8, int inner,
                           int outputs, float *y, int y_stride, int residual, double *partials,
-                          size_t partial_bytes, int *tickets, hipStream_t stream)
+                          size_t partial_bytes, int *tickets, hipStream_t stream,
+                          const uint8_t *w8_tiled)
 {
+    if (w8_tiled && !rows_tiled_supported(inner, outputs))
+        return hipErrorInvalidValue;
     if (rows <= 0 || rows > kBatchRows || x_rows < rows || inner <= 0 || inner % kBlock != 0
         || outputs <= 0 || y_stride < outputs)
         return hipErrorInvalidValue;
@@ -944,8 +1030,8 @@ hipError_t launch_q8_rows(const uint8_t *x8, int x_rows, int rows, const uint8_t
     if (plan.splits > 1
         && (!partials || !tickets || partial_bytes < rows_workspace_bytes(inner, outputs)))
         return hipErrorInvalidValue;
-    const RowsArgs a{x8, x_rows, rows, w8, inner, outputs, plan.per, y, y_stride, residual,
-                     partials, tickets, nullptr};
+    const RowsArgs a{x8, x_rows, rows, w8, w8_tiled, inner, outputs, plan.per, y, y_stride,
+                     residual, partials, tickets, nullptr};
     return launch_rows(a, plan, stream);
 }
 
@@ -958,43 +1044,29 @@ bool rows_geglu_supported(int inner, int intermediate)
 }
 
 hipError_t launch_q8_rows_geglu(const uint8_t *x8, int x_rows, int rows, const uint8_t *w8,
-                                int inner, int intermediate, uint8_t *geglu8, hipStream_t stream)
+                                int inner, int intermediate, uint8_t *geglu8, hipStream_t stream,
+                                const uint8_t *w8_tiled)
 {
     if (rows <= 0 || rows > kBatchRows || x_rows < rows || !geglu8
-        || !rows_geglu_supported(inner, intermediate))
+        || !rows_geglu_supported(inner, intermediate)
+        || (w8_tiled && !rows_tiled_supported(inner, 2 * intermediate)))
         return hipErrorInvalidValue;
     const RowsPlan plan = rows_plan(inner, 2 * intermediate);
-    const RowsArgs a{x8, x_rows, rows, w8, inner, 2 * intermediate, plan.per, nullptr, 0, 0,
-                     nullptr, nullptr, geglu8};
+    const RowsArgs a{x8, x_rows, rows, w8, w8_tiled, inner, 2 * intermediate, plan.per, nullptr, 0,
+                     0, nullptr, nullptr, geglu8};
     return launch_rows(a, plan, stream);
 }
 
 namespace {
-hipError_t launch_rows(const RowsArgs &a, const RowsPlan &plan, hipStream_t stream)
+// Tiled: the whole-chunk kernels read the fragment-ordered copy (a.w8t).
+template <bool Tiled>
+hipError_t launch_rows_as(const RowsArgs &a, const RowsPlan &plan, int nc, bool whole,
+                          hipStream_t stream)
 {
-    const int inner = a.inner, outputs = a.outputs;
-    const uint8_t *w8 = a.w8;
-    const int nb = inner / kBlock;
-    const uintptr_t wScales = reinterpret_cast<uintptr_t>(w8) + (uintptr_t) outputs * inner;
-    // whole chunks: every wave's range a multiple of 8 blocks inside the row
-    // (the last split's waves may hold fewer, or none: nb a multiple of per)
-    const int nc = plan.per / kChunkBlocks;
-    const bool whole = plan.per % kChunkBlocks == 0 && nb % plan.per == 0 && wScales % 16 == 0
-                       && (nc == 1 || nc == 2 || nc == 4 || nc == 8 || nc == 16);
+    const int inner = a.inner, outputs = a.outputs, nb = inner / kBlock;
     const int tilesPerGroup = kRowsWaves / plan.wpt;
     const dim3 grid((rows_ticket_count(outputs) + tilesPerGroup - 1) / tilesPerGroup, plan.splits);
     const size_t lds = rows_lds_bytes(plan);
-#define GQ8_ROWS(W, N)                                                                         \
-    hipLaunchKernelGGL((q8_rows_kernel<W, N>), grid, dim3(kRowsThreads), lds, stream, a)
-#define GQ8_ROWS_NC(W)                                                                         \
-    switch (whole ? nc : 0) {                                                                  \
-    case 1: GQ8_ROWS(W, 1); break;                                                             \
-    case 2: GQ8_ROWS(W, 2); break;                                                             \
-    case 4: GQ8_ROWS(W, 4); break;                                                             \
-    case 8: GQ8_ROWS(W, 8); break;                                                             \
-    case 16: GQ8_ROWS(W, 16); break;                                                           \
-    default: GQ8_ROWS(W, 0); break;                                                            \
-    }
     // split tiles of whole chunks with no split over workgroups (every chunk
     // in flight at once) load their activation blocks directly (the scale
     // rows 16-byte aligned: x8 aligned, nb a multiple of 8)
@@ -1010,14 +1082,16 @@ hipError_t launch_rows(const RowsArgs &a, const RowsPlan &plan, hipStream_t stre
             return hipErrorInvalidValue;
         const dim3 sgrid(kRowsStreamGroups);
         if (nc == 4)
-            hipLaunchKernelGGL((q8_rows_stream_kernel<4>), sgrid, dim3(kRowsThreads), 0, stream, a);
+            hipLaunchKernelGGL((q8_rows_stream_kernel<4, Tiled>), sgrid, dim3(kRowsThreads), 0, stream, a);
         else
-            hipLaunchKernelGGL((q8_rows_stream_kernel<8>), sgrid, dim3(kRowsThreads), 0, stream, a);
-    } else if (direct) {
+            hipLaunchKernelGGL((q8_rows_stream_kernel<8, Tiled>), sgrid, dim3(kRowsThreads), 0, stream, a);
+        return hipGetLastError();
+    }
+    if (direct) {
         const size_t epilogue = (size_t) kRowsWaves * kBatchRows * (kRowsTile + 1) * sizeof(double);
 #define GQ8_ROWS_DIRECT(N)                                                                     \
-    hipLaunchKernelGGL((q8_rows_kernel<kRowsWaves, N, true>), grid, dim3(kRowsThreads), epilogue, \
-                       stream, a)
+    hipLaunchKernelGGL((q8_rows_kernel<kRowsWaves, N, true, Tiled>), grid, dim3(kRowsThreads),   \
+                       epilogue, stream, a)
         switch (nc) {
         case 1: GQ8_ROWS_DIRECT(1); break;
         case 2: GQ8_ROWS_DIRECT(2); break;
@@ -1026,6 +1100,25 @@ hipError_t launch_rows(const RowsArgs &a, const RowsPlan &plan, hipStream_t stre
         default: GQ8_ROWS_DIRECT(16); break;
         }
 #undef GQ8_ROWS_DIRECT
+        return hipGetLastError();
+    }
+#define GQ8_ROWS(W, N)                                                                         \
+    hipLaunchKernelGGL((q8_rows_kernel<W, N, false, Tiled>), grid, dim3(kRowsThreads), lds, stream, a)
+#define GQ8_ROWS_NC(W)                                                                         \
+    switch (nc) {                                                                              \
+    case 1: GQ8_ROWS(W, 1); break;                                                             \
+    case 2: GQ8_ROWS(W, 2); break;                                                             \
+    case 4: GQ8_ROWS(W, 4); break;                                                             \
+    case 8: GQ8_ROWS(W, 8); break;                                                             \
+    default: GQ8_ROWS(W, 16); break;                                                           \
+    }
+    if (!whole) { // row-major, any range
+        if constexpr (Tiled)
+            return hipErrorInvalidValue;
+        if (plan.wpt == 1)
+            hipLaunchKernelGGL((q8_rows_kernel<1, 0>), grid, dim3(kRowsThreads), lds, stream, a);
+        else
+            hipLaunchKernelGGL((q8_rows_kernel<kRowsWaves, 0>), grid, dim3(kRowsThreads), lds, stream, a);
     } else if (plan.wpt == 1) {
         GQ8_ROWS_NC(1);
     } else {
@@ -1034,6 +1127,23 @@ hipError_t launch_rows(const RowsArgs &a, const RowsPlan &plan, hipStream_t stre
 #undef GQ8_ROWS_NC
 #undef GQ8_ROWS
     return hipGetLastError();
+}
+
+hipError_t launch_rows(const RowsArgs &a, const RowsPlan &plan, hipStream_t stream)
+{
+    const int inner = a.inner, outputs = a.outputs;
+    const int nb = inner / kBlock;
+    const uintptr_t wScales = reinterpret_cast<uintptr_t>(a.w8) + (uintptr_t) outputs * inner;
+    // whole chunks: every wave's range a multiple of 8 blocks inside the row
+    // (the last split's waves may hold fewer, or none: nb a multiple of per)
+    const int nc = plan.per / kChunkBlocks;
+    const bool whole = plan.per % kChunkBlocks == 0 && nb % plan.per == 0 && wScales % 16 == 0
+                       && (nc == 1 || nc == 2 || nc == 4 || nc == 8 || nc == 16);
+    if (a.w8t && whole)
+        return launch_rows_as<true>(a, plan, nc, whole, stream);
+    RowsArgs rowMajor = a;
+    rowMajor.w8t = nullptr;
+    return launch_rows_as<false>(rowMajor, plan, nc, whole, stream);
 }
 } // namespace
 

@@ -557,6 +557,7 @@ struct gq8_decoder {
     int64_t normStride = 0;                                                 // floats
     float *finalNorm = nullptr;
     std::vector<char> present;
+    uint64_t weightVersion = 0; // bumped by every weight upload (copies made from them go stale)
 
     uint16_t *keyCache = nullptr, *valueCache = nullptr;
     float *cosines = nullptr, *sines = nullptr;
@@ -1057,6 +1058,7 @@ Placement placement(gq8_decoder *d, int index)
 int mark_present(gq8_decoder *d, int index)
 {
     d->present[index] = 1;
+    ++d->weightVersion;
     return GQ8_OK;
 }
 } // namespace
@@ -2361,6 +2363,13 @@ struct gq8_batch {
     double *partials = nullptr;
     size_t partialBytes = 0;
     int *tickets = nullptr;
+    // the products' weights in fragment order (rows_tiled_bytes), per layer
+    // q|k|v, o, gate|up, down and the tied lm_head, made from the decoder's
+    // weights of version tiledVersion
+    std::vector<uint8_t *> tiledQkv, tiledO, tiledGateUp, tiledDown;
+    uint8_t *tiledHead = nullptr;
+    uint64_t tiledVersion = 0;
+    bool tiled = false;
     void *argmaxWorkspace = nullptr;
     size_t argmaxWorkspaceBytes = 0;
     hipGraphExec_t graph = nullptr;
@@ -2417,12 +2426,35 @@ struct SequenceLoan {
     }
 };
 
-int batch_product(gq8_batch *b, int inner, int outputs, const uint8_t *w, float *y, int yStride,
-                  int residual)
+int batch_product(gq8_batch *b, int inner, int outputs, const uint8_t *w, const uint8_t *wTiled,
+                  float *y, int yStride, int residual)
 {
     GQ8_LAUNCH(gq8::launch_q8_rows(b->x8, b->sequences, b->sequences, w, inner, outputs, y, yStride,
-                                   residual, b->partials, b->partialBytes, b->tickets,
-                                   b->d->stream));
+                                   residual, b->partials, b->partialBytes, b->tickets, b->d->stream,
+                                   wTiled));
+    return GQ8_OK;
+}
+
+// The fragment-ordered copies, remade when the decoder's weights changed
+// since they were made (the copies sit at fixed addresses, so a captured step
+// stays valid).
+int refresh_tiled(gq8_batch *b)
+{
+    gq8_decoder *d = b->d;
+    if (!b->tiled || b->tiledVersion == d->weightVersion)
+        return GQ8_OK;
+    const gq8_shape &s = d->shape;
+    const int W = s.width, F = s.intermediate;
+    hipStream_t st = d->stream;
+    for (int l = 0; l < s.layers; ++l) {
+        GQ8_LAUNCH(gq8::launch_tile_weights(d->qkv[l], W, d->qkvWidth, b->tiledQkv[l], st));
+        GQ8_LAUNCH(gq8::launch_tile_weights(d->out[l], d->qWidth, W, b->tiledO[l], st));
+        GQ8_LAUNCH(gq8::launch_tile_weights(d->gateUp[l], W, 2 * F, b->tiledGateUp[l], st));
+        GQ8_LAUNCH(gq8::launch_tile_weights(d->down[l], F, W, b->tiledDown[l], st));
+    }
+    GQ8_LAUNCH(gq8::launch_tile_weights(d->embedding, W, s.vocab, b->tiledHead, st));
+    GQ8_HIP(hipStreamSynchronize(st));
+    b->tiledVersion = d->weightVersion;
     return GQ8_OK;
 }
 
@@ -2449,7 +2481,8 @@ int encode_batch_step(gq8_batch *b)
         const int64_t layerCache = (int64_t) l * s.max_positions * d->kvWidth;
         GQ8_STAGE(kStageNorm, gq8::launch_rmsnorm(b->hidden, d->inputNorm[l], S, W, s.rms_epsilon,
                                                   nullptr, b->x8, st));
-        GQ8_BATCH_STAGE(kStageQkv, batch_product(b, W, d->qkvWidth, d->qkv[l], b->qkvRows,
+        GQ8_BATCH_STAGE(kStageQkv, batch_product(b, W, d->qkvWidth, d->qkv[l],
+                                                 b->tiled ? b->tiledQkv[l] : nullptr, b->qkvRows,
                                                  d->qkvWidth, 0));
         gq8::RowsAttentionArgs at{};
         at.qkv = b->qkvRows;
@@ -2470,22 +2503,30 @@ int encode_batch_step(gq8_batch *b)
         at.q8 = b->x8;
         at.q8_rows = S;
         GQ8_STAGE(kStageAttention, gq8::launch_rows_attention(at, S, s.max_positions, st));
-        GQ8_BATCH_STAGE(kStageO, batch_product(b, d->qWidth, W, d->out[l], b->hidden, W, 1));
+        GQ8_BATCH_STAGE(kStageO, batch_product(b, d->qWidth, W, d->out[l],
+                                               b->tiled ? b->tiledO[l] : nullptr, b->hidden, W, 1));
         GQ8_STAGE(kStageNorm, gq8::launch_rmsnorm(b->hidden, d->postNorm[l], S, W, s.rms_epsilon,
                                                   nullptr, b->x8, st));
         if (gq8::rows_geglu_supported(W, F)) { // GeGLU in the gate | up product's epilogue
             GQ8_STAGE(kStageGateUp, gq8::launch_q8_rows_geglu(b->x8, S, S, d->gateUp[l], W, F,
-                                                               b->x8b, st));
+                                                               b->x8b, st,
+                                                               b->tiled ? b->tiledGateUp[l]
+                                                                        : nullptr));
         } else {
-            GQ8_BATCH_STAGE(kStageGateUp, batch_product(b, W, 2 * F, d->gateUp[l], b->fused, 2 * F, 0));
+            GQ8_BATCH_STAGE(kStageGateUp, batch_product(b, W, 2 * F, d->gateUp[l],
+                                                        b->tiled ? b->tiledGateUp[l] : nullptr,
+                                                        b->fused, 2 * F, 0));
             GQ8_STAGE(kStageGeglu, gq8::launch_geglu(b->fused, S, F, nullptr, b->x8b, st));
         }
         GQ8_STAGE(kStageDown, gq8::launch_q8_rows(b->x8b, S, S, d->down[l], F, W, b->hidden, W, 1,
-                                                  b->partials, b->partialBytes, b->tickets, st));
+                                                  b->partials, b->partialBytes, b->tickets, st,
+                                                  b->tiled ? b->tiledDown[l] : nullptr));
     }
     GQ8_STAGE(kStageNorm, gq8::launch_rmsnorm(b->hidden, d->finalNorm, S, W, s.rms_epsilon, nullptr,
                                               b->x8, st));
-    GQ8_BATCH_STAGE(kStageLogits, batch_product(b, W, s.vocab, d->embedding, b->logits, s.vocab, 0));
+    GQ8_BATCH_STAGE(kStageLogits, batch_product(b, W, s.vocab, d->embedding,
+                                                b->tiled ? b->tiledHead : nullptr, b->logits,
+                                                s.vocab, 0));
     GQ8_STAGE(kStageArgmax, gq8::launch_argmax(b->logits, nullptr, S, s.vocab, b->chosen, nullptr, 0,
                                                b->argmaxWorkspace, b->argmaxWorkspaceBytes, st));
     GQ8_LAUNCH(gq8::launch_batch_advance(b->chosen, b->slots, b->slotStride, b->positions, S, st));
@@ -2599,6 +2640,30 @@ extern "C" int gq8_batch_create(gq8_decoder *d, int sequences, gq8_batch **out)
         if (hipMemset(b->tickets, 0, (size_t) tickets * sizeof(int)) != hipSuccess)
             return cleanup(fail(GQ8_ERR_DEVICE, "batch tickets: initialisation failed"));
     }
+    // the fragment-ordered weight copies, when every product's rows are whole
+    // chunks (made at the first decode)
+    auto aligned = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    b->tiled = gq8::rows_tiled_supported(W, d->qkvWidth) && gq8::rows_tiled_supported(d->qWidth, W)
+               && gq8::rows_tiled_supported(W, 2 * F) && gq8::rows_tiled_supported(F, W)
+               && gq8::rows_tiled_supported(W, s.vocab) && aligned(d->embedding);
+    for (int l = 0; l < s.layers && b->tiled; ++l)
+        b->tiled = aligned(d->qkv[l]) && aligned(d->out[l]) && aligned(d->gateUp[l])
+                   && aligned(d->down[l]);
+    if (b->tiled) {
+        for (int l = 0; l < s.layers; ++l) {
+            uint8_t *p = nullptr;
+            GQ8_BATCH_ALLOC(p, gq8::rows_tiled_bytes(W, d->qkvWidth));
+            b->tiledQkv.push_back(p);
+            GQ8_BATCH_ALLOC(p, gq8::rows_tiled_bytes(d->qWidth, W));
+            b->tiledO.push_back(p);
+            GQ8_BATCH_ALLOC(p, gq8::rows_tiled_bytes(W, 2 * F));
+            b->tiledGateUp.push_back(p);
+            GQ8_BATCH_ALLOC(p, gq8::rows_tiled_bytes(F, W));
+            b->tiledDown.push_back(p);
+        }
+        GQ8_BATCH_ALLOC(b->tiledHead, gq8::rows_tiled_bytes(W, s.vocab));
+        b->tiledVersion = d->weightVersion - 1; // made at the first decode
+    }
     b->argmaxWorkspaceBytes = gq8::argmax_workspace_bytes(S, s.vocab);
     if (b->argmaxWorkspaceBytes)
         GQ8_BATCH_ALLOC(b->argmaxWorkspace, b->argmaxWorkspaceBytes);
@@ -2670,6 +2735,8 @@ extern "C" int gq8_batch_decode(gq8_batch *b, int steps, int use_graph)
     }
     if (steps == 0)
         return GQ8_OK;
+    if (int st = refresh_tiled(b))
+        return st;
     if (use_graph)
         if (int st = ensure_batch_graph(b))
             return st;
