@@ -48,17 +48,20 @@ constexpr int kChunkBlocks = 8;       // blocks a wave's weight loads cover at o
 constexpr int kRowsMaxRange = 128;    // blocks of the activation rows a workgroup stages
 constexpr int kRowsManyTiles = 1024;  // products this wide give each wave whole rows
 constexpr int kRowsPrefetch = 2;      // weight chunks in flight a wave
+constexpr int kMergeBatch = 8;        // split partials a merge requests at once
 constexpr int kRowsStreamGroups = 512; // workgroups of a streamed product (two a compute unit)
 constexpr int kRowsStreamAhead = 4;    // weight chunks in flight a wave of a streamed product
 
 // A workgroup stages `range` blocks of the activation rows in LDS and its
 // waves stream weight rows against them.  Wide products (tiles >= 1024: gate
 // | up, the lm_head) give a workgroup four tiles and each wave a tile's whole
-// rows (WPT 1); narrow ones give a workgroup one tile, its four waves consecutive
-// quarters of the staged blocks (WPT 4), and split the blocks over `splits`
-// workgroups until the chip has about 512.
+// rows (WPT 1).  Narrow ones give a tile's consecutive quarters of the blocks
+// to four waves (WPT 4) when those hold every chunk in flight at once (q|k|v,
+// o: one workgroup a tile, loading its activation blocks directly); longer
+// rows (down) split their blocks over `splits` workgroups until the chip has
+// about 512, two tiles a workgroup and two waves a tile (WPT 2).
 struct RowsPlan {
-    int wpt;    // waves a tile: 1 or 4
+    int wpt;    // waves a tile: 1, 2 or 4
     int per;    // blocks a wave takes
     int splits; // workgroups over one tile's blocks
     int range() const { return wpt * per; }
@@ -85,6 +88,13 @@ RowsPlan rows_plan(int inner, int outputs)
     while (tiles * splits < 512 && per >= 2 * kChunkBlocks && per % (2 * kChunkBlocks) == 0) {
         per /= 2;
         splits = (nb + kRowsWaves * per - 1) / (kRowsWaves * per);
+    }
+    if (splits > 1 && tiles % 2 == 0) {
+        // split over workgroups: two tiles a workgroup, two waves a tile, so
+        // each staged block serves two tiles (the staging, not the weights,
+        // had bound these launches)
+        const int pairs = 2 * per;
+        return {2, per, (nb + pairs - 1) / pairs};
     }
     return {kRowsWaves, per, splits};
 }
@@ -470,17 +480,44 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
     __syncthreads();
     if (!sLast)
         return;
-    for (int cell = t; cell < kTiles * kBatchRows * kRowsTile; cell += kRowsThreads) {
+    // the splits' partials of this thread's cells, kMergeBatch splits
+    // requested at once (cells and splits past the ends read a clamped, live
+    // slot), added in split order
+    constexpr int kCells = kTiles * kBatchRows * kRowsTile / kRowsThreads;
+    const int splits = (int) gridDim.y;
+    double total[kCells];
+#pragma unroll
+    for (int i = 0; i < kCells; ++i)
+        total[i] = 0.0;
+    for (int s0 = 0; s0 < splits; s0 += kMergeBatch) {
+        double part[kCells][kMergeBatch];
+#pragma unroll
+        for (int i = 0; i < kCells; ++i) {
+            const int cell = t + i * kRowsThreads;
+            const int k = cell >> 8, m = min((cell >> 4) & 15, a.rows - 1), c = cell & 15;
+            const int on = min((blockIdx.x * kTiles + k) * kRowsTile + c, a.outputs - 1);
+#pragma unroll
+            for (int j = 0; j < kMergeBatch; ++j)
+                part[i][j] = load_agent_d(a.partials + ((int64_t) min(s0 + j, splits - 1) * kBatchRows + m)
+                                                           * a.outputs + on);
+        }
+#pragma unroll
+        for (int i = 0; i < kCells; ++i)
+#pragma unroll
+            for (int j = 0; j < kMergeBatch; ++j)
+                if (s0 + j < splits)
+                    total[i] += part[i][j];
+    }
+#pragma unroll
+    for (int i = 0; i < kCells; ++i) {
+        const int cell = t + i * kRowsThreads;
         const int k = cell >> 8, m = (cell >> 4) & 15, c = cell & 15;
         const int on = (blockIdx.x * kTiles + k) * kRowsTile + c;
         if (m >= a.rows || on >= a.outputs)
             continue;
-        double total = 0.0;
-        for (int s = 0; s < (int) gridDim.y; ++s)
-            total += load_agent_d(a.partials + ((int64_t) s * kBatchRows + m) * a.outputs + on);
         float *dst = a.y + (int64_t) m * a.y_stride + on;
         const double old = a.residual ? (double) *dst : 0.0;
-        *dst = (float) (total + old);
+        *dst = (float) (total[i] + old);
     }
     if (t == 0) // ready for the next launch
         __hip_atomic_store(a.tickets + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1117,10 +1154,14 @@ hipError_t launch_rows_as(const RowsArgs &a, const RowsPlan &plan, int nc, bool 
             return hipErrorInvalidValue;
         if (plan.wpt == 1)
             hipLaunchKernelGGL((q8_rows_kernel<1, 0>), grid, dim3(kRowsThreads), lds, stream, a);
+        else if (plan.wpt == 2)
+            hipLaunchKernelGGL((q8_rows_kernel<2, 0>), grid, dim3(kRowsThreads), lds, stream, a);
         else
             hipLaunchKernelGGL((q8_rows_kernel<kRowsWaves, 0>), grid, dim3(kRowsThreads), lds, stream, a);
     } else if (plan.wpt == 1) {
         GQ8_ROWS_NC(1);
+    } else if (plan.wpt == 2) {
+        GQ8_ROWS_NC(2);
     } else {
         GQ8_ROWS_NC(kRowsWaves);
     }
