@@ -420,11 +420,4 @@ def main() -> int:
 
 
 if __name__ == "__main__":
-    rc = main()
-    # every decoder and batch is closed and the JSON line flushed; leave at
-    # once rather than through interpreter teardown (the OpenMP pool of the
-    # CPU baseline and the HIP runtime otherwise keep the process alive for
-    # a while after the result is out)
-    sys.stdout.flush()
-    sys.stderr.flush()
-    os._exit(rc)
+    sys.exit(main())
