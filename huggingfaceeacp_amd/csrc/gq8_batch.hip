@@ -118,6 +118,7 @@ struct RowsArgs {
     double *partials; // [splits][kBatchRows][outputs]
     int *tickets;     // one a workgroup column
     uint8_t *geglu8;  // non-null: outputs are gate | up rows; GeGLU's Q8 rows land here
+    int split_major;  // grid (splits, columns) instead of (columns, splits)
 };
 
 __device__ inline void store_agent_d(double *p, double v)
@@ -333,11 +334,17 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
     // GeGLU's pairing (four tiles a workgroup): waves 0 and 1 take gate
     // tiles 2 x, 2 x + 1, waves 2 and 3 the up tiles of the same outputs
     const int upTiles = a.outputs / (2 * kRowsTile);
-    const int tile = a.geglu8 ? (wave >> 1) * upTiles + 2 * blockIdx.x + (wave & 1)
-                              : blockIdx.x * kTiles + wave / WPT;
+    // split products launch split-major (blockIdx.x the split), so each XCD
+    // (workgroups go to the eight in turn) takes one block range and its L2
+    // holds only that range of the activation rows
+    const int colIdx = a.split_major ? (int) blockIdx.y : (int) blockIdx.x;
+    const int splitIdx = a.split_major ? (int) blockIdx.x : (int) blockIdx.y;
+    const int nSplits = a.split_major ? (int) gridDim.x : (int) gridDim.y;
+    const int tile = a.geglu8 ? (wave >> 1) * upTiles + 2 * colIdx + (wave & 1)
+                              : colIdx * kTiles + wave / WPT;
     const int part = wave % WPT;
     const int n0 = tile * kRowsTile;
-    const int r0 = blockIdx.y * range;             // the workgroup's first block
+    const int r0 = splitIdx * range;             // the workgroup's first block
     const int rEnd = min(r0 + range, nb);
     const int b0 = r0 + part * a.per;              // this wave's blocks
     const int b1 = min(b0 + a.per, nb);
@@ -442,7 +449,7 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
             const float amax = max_lanes<16>(fabsf(v));
             const uint16_t bits = scale_bits_from_amax(amax);
             const float sc = half_value(bits);
-            const int j = blockIdx.x * 2 * kRowsTile + jj;
+            const int j = colIdx * 2 * kRowsTile + jj;
             if (m < a.rows) {
                 a.geglu8[(int64_t) m * F + j] = (uint8_t) (int8_t) quantize_in_block(v, bits, sc, quantize_hint(sc));
                 if (jj == 0)
@@ -457,26 +464,26 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
 #pragma unroll
         for (int w = 0; w < WPT; ++w)
             sum += sPart[((size_t) (k * WPT + w) * kBatchRows + m) * (kRowsTile + 1) + c];
-        const int on = (blockIdx.x * kTiles + k) * kRowsTile + c;
+        const int on = (colIdx * kTiles + k) * kRowsTile + c;
         if (m >= a.rows || on >= a.outputs)
             continue;
-        if (gridDim.y == 1) {
+        if (nSplits == 1) {
             float *dst = a.y + (int64_t) m * a.y_stride + on;
             const double old = a.residual ? (double) *dst : 0.0;
             *dst = (float) (sum + old);
         } else {
-            // the blocks are split over gridDim.y workgroups: agent-scope
+            // the blocks are split over nSplits workgroups: agent-scope
             // stores (coherent across the L2s), completed before the ticket
-            store_agent_d(a.partials + ((int64_t) blockIdx.y * kBatchRows + m) * a.outputs + on, sum);
+            store_agent_d(a.partials + ((int64_t) splitIdx * kBatchRows + m) * a.outputs + on, sum);
         }
     }
-    if (gridDim.y == 1)
+    if (nSplits == 1)
         return;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (t == 0)
-        sLast = __hip_atomic_fetch_add(a.tickets + blockIdx.x, 1, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT) == (int) gridDim.y - 1;
+        sLast = __hip_atomic_fetch_add(a.tickets + colIdx, 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT) == nSplits - 1;
     __syncthreads();
     if (!sLast)
         return;
@@ -484,7 +491,7 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
     // requested at once (cells and splits past the ends read a clamped, live
     // slot), added in split order
     constexpr int kCells = kTiles * kBatchRows * kRowsTile / kRowsThreads;
-    const int splits = (int) gridDim.y;
+    const int splits = nSplits;
     double total[kCells];
 #pragma unroll
     for (int i = 0; i < kCells; ++i)
@@ -495,7 +502,7 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
         for (int i = 0; i < kCells; ++i) {
             const int cell = t + i * kRowsThreads;
             const int k = cell >> 8, m = min((cell >> 4) & 15, a.rows - 1), c = cell & 15;
-            const int on = min((blockIdx.x * kTiles + k) * kRowsTile + c, a.outputs - 1);
+            const int on = min((colIdx * kTiles + k) * kRowsTile + c, a.outputs - 1);
 #pragma unroll
             for (int j = 0; j < kMergeBatch; ++j)
                 part[i][j] = load_agent_d(a.partials + ((int64_t) min(s0 + j, splits - 1) * kBatchRows + m)
@@ -512,7 +519,7 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
     for (int i = 0; i < kCells; ++i) {
         const int cell = t + i * kRowsThreads;
         const int k = cell >> 8, m = (cell >> 4) & 15, c = cell & 15;
-        const int on = (blockIdx.x * kTiles + k) * kRowsTile + c;
+        const int on = (colIdx * kTiles + k) * kRowsTile + c;
         if (m >= a.rows || on >= a.outputs)
             continue;
         float *dst = a.y + (int64_t) m * a.y_stride + on;
@@ -520,7 +527,7 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
         *dst = (float) (total[i] + old);
     }
     if (t == 0) // ready for the next launch
-        __hip_atomic_store(a.tickets + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.tickets + colIdx, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Wide products with no GeGLU (the lm_head): a workgroup stages the whole
@@ -1102,7 +1109,8 @@ hipError_t launch_rows_as(const RowsArgs &a, const RowsPlan &plan, int nc, bool 
 {
     const int inner = a.inner, outputs = a.outputs, nb = inner / kBlock;
     const int tilesPerGroup = kRowsWaves / plan.wpt;
-    const dim3 grid((rows_ticket_count(outputs) + tilesPerGroup - 1) / tilesPerGroup, plan.splits);
+    const int columns = (rows_ticket_count(outputs) + tilesPerGroup - 1) / tilesPerGroup;
+    const dim3 grid = a.split_major ? dim3(plan.splits, columns) : dim3(columns, plan.splits);
     const size_t lds = rows_lds_bytes(plan);
     // split tiles of whole chunks with no split over workgroups (every chunk
     // in flight at once) load their activation blocks directly (the scale
@@ -1180,11 +1188,12 @@ hipError_t launch_rows(const RowsArgs &a, const RowsPlan &plan, hipStream_t stre
     const int nc = plan.per / kChunkBlocks;
     const bool whole = plan.per % kChunkBlocks == 0 && nb % plan.per == 0 && wScales % 16 == 0
                        && (nc == 1 || nc == 2 || nc == 4 || nc == 8 || nc == 16);
+    RowsArgs b = a;
+    b.split_major = plan.splits > 1;
     if (a.w8t && whole)
-        return launch_rows_as<true>(a, plan, nc, whole, stream);
-    RowsArgs rowMajor = a;
-    rowMajor.w8t = nullptr;
-    return launch_rows_as<false>(rowMajor, plan, nc, whole, stream);
+        return launch_rows_as<true>(b, plan, nc, whole, stream);
+    b.w8t = nullptr;
+    return launch_rows_as<false>(b, plan, nc, whole, stream);
 }
 } // namespace
 
