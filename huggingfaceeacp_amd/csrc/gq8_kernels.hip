@@ -177,12 +177,37 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restri
         for (int w = 0; w < kThreads / 64; ++w)
             total += partial[w];
         const double scale = norm_scale(total, width, epsilon);
+        // every element's value, block scale and byte first (no branches, so
+        // the K chains interleave), then the stores
+        float v[K], amax[K];
+        uint16_t bits[K];
+        int bytes[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            v[k] = norm_value(xv[k], scale, wv[k]);
+            amax[k] = fabsf(v[k]);
+        }
+        max_lanes_each<16>(amax); // each 32-lane group's largest magnitude
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            bits[k] = scale_bits_from_amax(amax[k]);
+            const float sc = half_value(bits[k]);
+            bytes[k] = quantize_in_block(v[k], bits[k], sc, quantize_hint(sc));
+        }
+        uint16_t *scales = q8 ? reinterpret_cast<uint16_t *>(q8 + elements) : nullptr;
 #pragma unroll
         for (int k = 0; k < K; ++k) {
             const int i = threadIdx.x + k * kThreads;
-            const bool live = i < width; // whole 32-element groups are live together
-            norm_store(xv[k], wv[k], scale, (int64_t) row * width + (live ? i : 0), live, elements,
-                       y, q8);
+            if (i >= width) // whole 32-element groups are live together
+                continue;
+            const int64_t at = (int64_t) row * width + i;
+            if (y)
+                y[at] = v[k];
+            if (q8) {
+                q8[at] = (uint8_t) (int8_t) bytes[k];
+                if ((threadIdx.x & 31) == 0)
+                    scales[at / kBlock] = bits[k];
+            }
         }
     }
 }

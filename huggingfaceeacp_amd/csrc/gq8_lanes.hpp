@@ -103,6 +103,24 @@ __device__ inline float max_lanes(float v)
         return v;
 }
 
+// max_lanes<D> of K values at once, one exchange distance at a time across
+// all K (the same pairing and order for each value), so the K chains
+// interleave instead of running one after another.
+template <int D, int K>
+__device__ inline void max_lanes_each(float (&v)[K])
+{
+    if constexpr (D >= 1) {
+        float other[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+            other[k] = xor_lane<D>(v[k]);
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+            v[k] = fmaxf(v[k], other[k]);
+        max_lanes_each<D / 2, K>(v);
+    }
+}
+
 template <int D>
 __device__ inline unsigned long long max_lanes(unsigned long long v)
 {

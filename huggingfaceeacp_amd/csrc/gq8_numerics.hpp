@@ -37,11 +37,17 @@ GQ8_HD float half_value(uint16_t bits)
 
 // blockScaleBits (Lib/HuggingFaceEACP/Kernels/Int8Blocks.cpp:114-125) from a
 // block's largest magnitude: amax / 127 as a float division, narrowed to fp16;
-// a scale that is zero, infinite or NaN is stored as zero.
+// a scale that is zero, infinite or NaN is stored as zero.  The quotient is
+// found without a division: the double product amax * (1 / 127) is within
+// 2^-52 (relative) of the exact quotient, and the exact quotient lies at least
+// 2^-32 (relative) from every fp32 rounding midpoint (its distance from one is
+// |t - 127 (2 j + 1)| / (127 2^24) of the fp32 spacing, with t an even
+// integer), so both round to the same fp32: the correctly rounded quotient.
 GQ8_HD uint16_t scale_bits_from_amax(float amax)
 {
 #pragma clang fp contract(off)
-    const uint16_t bits = half_bits(amax / kLargestQuantized);
+    const float quotient = (float) ((double) amax * (1.0 / (double) kLargestQuantized));
+    const uint16_t bits = half_bits(quotient);
     const float scale = half_value(bits);
     return (scale > 0.f && scale <= 65504.f) ? bits : (uint16_t) 0;
 }
