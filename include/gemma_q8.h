@@ -406,8 +406,12 @@ int gq8_decoder_load_safetensors(gq8_decoder *decoder, gq8_safetensors *const *s
 typedef struct gq8_batch gq8_batch;
 /* S in [1, 16] sequences, each with its own fp16 cache and max_positions + 1
  * token slots; the decoder's weights are shared, so the decoder must outlive
- * the batch.  GQ8_ERR_SHAPE where the one-token attention layout does not
- * cover the decoder's shape. */
+ * the batch.  Where every product's inner size is a multiple of 256 the batch
+ * also keeps a copy of the weights in the products' MFMA fragment order
+ * (about the size of the weights: 2.98 GB for Gemma-2B), made at its first
+ * decode and again at a decode after any weight upload to the decoder.
+ * GQ8_ERR_SHAPE where the one-token attention layout does not cover the
+ * decoder's shape. */
 int gq8_batch_create(gq8_decoder *decoder, int sequences, gq8_batch **out);
 void gq8_batch_destroy(gq8_batch *batch);
 /* Gemma::generate's prefill (Gemma.cpp:350-380, 402-424) of one sequence,
