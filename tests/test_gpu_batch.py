@@ -91,6 +91,33 @@ def test_batch_two_layer_gemma(torch_cuda):
     check_rows(torch, decoder, histories, logits, "gemma 2-layer")
 
 
+def test_batch_follows_weight_uploads(torch_cuda):
+    """A batch's products read its own fragment-ordered copy of the weights
+    (Gemma dims): after new down weights of the last layer and a new tied
+    embedding are uploaded to the decoder, the same batch's next steps
+    follow them, holding the one-sequence path's ids and logits."""
+    torch = torch_cuda
+    shape, decoder, _ = gemma_pair(2, 128, max_step_rows=64)
+    prompts = [O.prompt_ids(0xFEED0 + i, shape.vocab, n) for i, n in enumerate((5, 9, 16, 24))]
+    batch = G.Batch(decoder, len(prompts))
+    for s, prompt in enumerate(prompts):
+        batch.prefill(s, prompt)
+    batch.decode(2, use_graph=True)
+    down = 1 + (shape.layers - 1) * G.PER_LAYER + G.T_DOWN
+    decoder.load_tensor(down, O.normal_fill(0xD0A1, 0.05, shape.tensor_elements(down)))
+    decoder.load_tensor(0, O.normal_fill(0xE3B0, 0.03, shape.tensor_elements(0)))
+    for s, prompt in enumerate(prompts):
+        batch.prefill(s, prompt)
+    batch.decode(3, use_graph=True)
+    histories = [batch.tokens(s, 0, len(p) + 3) for s, p in enumerate(prompts)]
+    logits = batch.logits()
+    for s, prompt in enumerate(prompts):
+        single, _ = decoder.generate(prompt, 4, eos=-1)
+        assert list(batch.tokens(s, len(prompt), 4)) == list(single), s
+    check_rows(torch, decoder, histories, logits, "after weight uploads")
+    batch.close()
+
+
 def test_batch_refusals(torch_cuda):
     """Batch size, unprefilled sequences and the window are refused before
     anything runs; a refused decode leaves every sequence where it was."""
