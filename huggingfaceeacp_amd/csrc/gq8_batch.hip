@@ -264,48 +264,63 @@ __device__ inline void chunk_products(const WeightChunk &c, const long *sX, cons
     }
 }
 
-// Stages blocks [r0, rEnd) (at most kMaxRange) of the activation rows in LDS
-// in MFMA fragment order (lane l of block b: sequence l % 16, bytes
-// 8 (l / 16) .. + 8) and their scales as fp32: every load first (clamped into
-// range), then the LDS writes.  No barrier.
+// Blocks [r0, rEnd) (at most kMaxRange) of the activation rows, staged in
+// LDS in MFMA fragment order (lane l of block b: sequence l % 16, bytes
+// 8 (l / 16) .. + 8) with their scales as fp32.  stage_load issues every
+// load (clamped into range) and stage_write makes the LDS writes (no
+// barrier).  A workgroup issues its first weight loads between the two: the
+// staging loads are ahead of them in the memory queues, and the weights are
+// in flight while the staged rows arrive and are written.
 template <int kMaxRange>
-__device__ inline void stage_activation(const RowsArgs &a, int r0, int rEnd, long *sX, float *sSx,
-                                        int t)
+struct StagePieces {
+    static constexpr int kPieces = kMaxRange * kBatchRows * 2 / kRowsThreads; // 16-byte pieces
+    static constexpr int kScales = (kMaxRange * kBatchRows + kRowsThreads - 1) / kRowsThreads;
+    uint4 piece[kPieces];
+    uint16_t scaleBits[kScales];
+};
+
+template <int kMaxRange>
+__device__ inline void stage_load(const RowsArgs &a, int r0, int rEnd, StagePieces<kMaxRange> &sp, int t)
 {
-    constexpr int kPieces = kMaxRange * kBatchRows * 2 / kRowsThreads; // 16-byte pieces
-    constexpr int kScales = (kMaxRange * kBatchRows + kRowsThreads - 1) / kRowsThreads;
+    using S = StagePieces<kMaxRange>;
     const int nb = a.inner / kBlock;
     const uint16_t *xScales = reinterpret_cast<const uint16_t *>(a.x8 + (int64_t) a.x_rows * a.inner);
     const int pieces = (rEnd - r0) * kBatchRows * 2, scales = (rEnd - r0) * kBatchRows;
-    uint4 piece[kPieces];
-    uint16_t scaleBits[kScales];
 #pragma unroll
-    for (int i = 0; i < kPieces; ++i) {
+    for (int i = 0; i < S::kPieces; ++i) {
         const int p = min(t + i * kRowsThreads, pieces - 1);
         const int rb = p >> 5, m = (p >> 1) & 15, h = p & 1;
-        piece[i] = *reinterpret_cast<const uint4 *>(a.x8 + (int64_t) min(m, a.rows - 1) * a.inner
-                                                    + (int64_t) (r0 + rb) * kBlock + h * 16);
+        sp.piece[i] = *reinterpret_cast<const uint4 *>(a.x8 + (int64_t) min(m, a.rows - 1) * a.inner
+                                                       + (int64_t) (r0 + rb) * kBlock + h * 16);
     }
 #pragma unroll
-    for (int i = 0; i < kScales; ++i) {
+    for (int i = 0; i < S::kScales; ++i) {
         const int e = min(t + i * kRowsThreads, scales - 1);
-        scaleBits[i] = xScales[(int64_t) min(e & 15, a.rows - 1) * nb + r0 + (e >> 4)];
+        sp.scaleBits[i] = xScales[(int64_t) min(e & 15, a.rows - 1) * nb + r0 + (e >> 4)];
     }
+}
+
+template <int kMaxRange>
+__device__ inline void stage_write(int r0, int rEnd, const StagePieces<kMaxRange> &sp, long *sX,
+                                   float *sSx, int t)
+{
+    using S = StagePieces<kMaxRange>;
+    const int pieces = (rEnd - r0) * kBatchRows * 2, scales = (rEnd - r0) * kBatchRows;
 #pragma unroll
-    for (int i = 0; i < kPieces; ++i) {
+    for (int i = 0; i < S::kPieces; ++i) {
         const int p = t + i * kRowsThreads;
         if (p < pieces) {
             const int rb = p >> 5, m = (p >> 1) & 15, h = p & 1;
             uint2 *dst = reinterpret_cast<uint2 *>(sX) + rb * 64 + m;
-            dst[(2 * h) * 16] = make_uint2(piece[i].x, piece[i].y);
-            dst[(2 * h + 1) * 16] = make_uint2(piece[i].z, piece[i].w);
+            dst[(2 * h) * 16] = make_uint2(sp.piece[i].x, sp.piece[i].y);
+            dst[(2 * h + 1) * 16] = make_uint2(sp.piece[i].z, sp.piece[i].w);
         }
     }
 #pragma unroll
-    for (int i = 0; i < kScales; ++i) {
+    for (int i = 0; i < S::kScales; ++i) {
         const int e = t + i * kRowsThreads;
         if (e < scales)
-            sSx[e] = half_value(scaleBits[i]);
+            sSx[e] = half_value(sp.scaleBits[i]);
     }
 }
 
@@ -384,10 +399,13 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
         }
     } else {
     // with whole chunks the range is WPT NC chunks
-    stage_activation<V ? WPT * NC * kChunkBlocks : kRowsMaxRange>(a, r0, rEnd, sX, sSx, t);
-    // then up to kRowsPrefetch chunks of weights in flight a wave: behind
-    // the LDS writes, since once the weight stream fills the memory queues a
-    // wave's vector memory instructions issue only as fast as loads retire
+    // the staging loads, then up to kRowsPrefetch chunks of weights in
+    // flight a wave: behind the staging loads, since once the weight stream
+    // fills the memory queues a wave's vector memory instructions issue only
+    // as fast as loads retire; then the LDS writes
+    constexpr int kRange = V ? WPT * NC * kChunkBlocks : kRowsMaxRange;
+    StagePieces<kRange> staged;
+    stage_load<kRange>(a, r0, rEnd, staged, t);
     constexpr int P = V ? (NC < kRowsPrefetch ? NC : kRowsPrefetch) : 1;
     WeightChunk buf[P];
     if (b0 < b1) {
@@ -395,6 +413,8 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
         for (int i = 0; i < P; ++i)
             load_weight_chunk<V, Tiled>(buf[i], ws, V ? b0 + i * kChunkBlocks : b0, b1);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    stage_write<kRange>(r0, rEnd, staged, sX, sSx, t);
     __syncthreads();
 
     // two weight buffers: the next chunk's loads are in flight while this
@@ -531,15 +551,15 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
 }
 
 // Wide products with no GeGLU (the lm_head): a workgroup stages the whole
-// activation rows (nb = NC chunks) once, then takes groups of four tiles
-// (one a wave) from a shared counter until none is left, so a workgroup that
-// the memory system serves faster takes more of them.  Each wave's weight
-// chunks stream across the group boundaries, P ahead (the next group is
-// claimed when a group starts and published at the workgroup barrier P
-// chunks before its end); a tile's 16 x 16 outputs go straight from its
-// accumulators to y.  counters[0] is the next group, counters[1] the
-// workgroups done; the last one done zeroes both for the next launch.  The
-// arithmetic is q8_rows_kernel's.
+// activation rows (nb = NC chunks) once, starts on group blockIdx.x of four
+// tiles (one a wave), then takes groups from a shared counter until none is
+// left, so a workgroup that the memory system serves faster takes more of
+// them.  Each wave's weight chunks stream across the group boundaries, P
+// ahead (the next group is claimed when a group starts and published at the
+// workgroup barrier P chunks before its end); a tile's 16 x 16 outputs go
+// straight from its accumulators to y.  counters[0] counts the claims (group
+// gridDim.x + claim), counters[1] the workgroups done; the last one done
+// zeroes both for the next launch.  The arithmetic is q8_rows_kernel's.
 template <int NC, bool Tiled>
 __global__ __launch_bounds__(kRowsThreads) void q8_rows_stream_kernel(RowsArgs a)
 {
@@ -557,11 +577,10 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_stream_kernel(RowsArgs a
         return __hip_atomic_fetch_add(counters, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
 
-    if (t == 0)
-        sGroup[0] = claim();
-    stage_activation<nb>(a, 0, nb, sX, sSx, t);
-    __syncthreads();
-    int g = sGroup[0];
+    // the first group is the workgroup's own; later ones are claimed
+    StagePieces<nb> staged;
+    stage_load<nb>(a, 0, nb, staged, t);
+    int g = blockIdx.x;
     WeightChunk buf[P];
     if (g < groups) {
         const WeightRows<Tiled> ws(a, g * kRowsWaves + wave, lane);
@@ -569,11 +588,14 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_stream_kernel(RowsArgs a
         for (int i = 0; i < P; ++i)
             load_weight_chunk<true, Tiled>(buf[i], ws, i * kChunkBlocks, nb);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    stage_write<nb>(0, nb, staged, sX, sSx, t);
+    __syncthreads();
     int slot = 1;
 #pragma nounroll
     while (g < groups) {
-        if (t == 0)
-            sGroup[slot] = claim(); // the next group, in flight while this one streams
+        if (t == 0) // the next group, in flight while this one streams
+            sGroup[slot] = (int) gridDim.x + claim();
         const WeightRows<Tiled> ws(a, g * kRowsWaves + wave, lane);
         int next = groups;
         double acc[4] = {0.0, 0.0, 0.0, 0.0};
