@@ -29,6 +29,7 @@
 #include "gq8_device.hpp"
 #include "gq8_numerics.hpp"
 
+#include <algorithm>
 #include <cfloat>
 
 #include "gq8_lanes.hpp"
@@ -421,19 +422,27 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
     for (int g = 0; g < G; ++g)
         kvOffset[g] = ((h0 + g) / perKv) * hd + c0;
 
-    // While at most grid_splits rounds of keys are attended, split s is the
-    // one round [64 s, 64 s + 64): its rows are loaded before the position
-    // arrives (rows past the position are read, inside the cache, and never
-    // used), so the two loads do not wait on each other.
+    // Split s is expected to be the keys [s S, s S + S) (S = spec_keys: one
+    // round of 64 while at most grid_splits rounds are attended, two while at
+    // most 2 grid_splits are): its rows are loaded before the position arrives
+    // (rows past the position are read, inside the cache, and never used), so
+    // the two loads do not wait on each other.
     constexpr int CW = (C + 1) / 2; // words of a lane's channels of one row
     uint32_t kh[kScoreBatch][G][CW], vh[kScoreBatch][G][CW];
+    uint32_t kh2[kScoreBatch][G][CW], vh2[kScoreBatch][G][CW];
+    const bool specTwo = a.spec_keys == 2 * kRoundKeys;
 #pragma unroll
     for (int b = 0; b < kScoreBatch; ++b) {
-        const int j = min(split * kRoundKeys + wave + b * kAttnWaves, a.max_positions - 1);
+        const int j = min(split * a.spec_keys + wave + b * kAttnWaves, a.max_positions - 1);
+        const int j2 = min(j + kRoundKeys, a.max_positions - 1);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             load_words<C>(a.key_cache + (int64_t) j * kvWidth + kvOffset[g], kh[b][g]);
             load_words<C>(a.value_cache + (int64_t) j * kvWidth + kvOffset[g], vh[b][g]);
+            if (specTwo) { // uniform: the launch's
+                load_words<C>(a.key_cache + (int64_t) j2 * kvWidth + kvOffset[g], kh2[b][g]);
+                load_words<C>(a.value_cache + (int64_t) j2 * kvWidth + kvOffset[g], vh2[b][g]);
+            }
         }
     }
     // keeps the loads above the position-dependent exit: the compiler would
@@ -462,17 +471,16 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
                 load_words<C>(base + (int64_t) j * kvWidth + kvOffset[g], dst[b][g]);
         }
     };
-    if (plan.perSplit != kRoundKeys) { // longer splits: the first round again, from k0
-        load_round(keys, 0, kh);
-        load_round(values, 0, vh);
-    }
     // a two-round split (a window of 4097 .. 8192 keys) has its second round's
     // rows in flight with the first's
     const bool twoRounds = plan.perSplit == 2 * kRoundKeys;
-    uint32_t kh2[kScoreBatch][G][CW], vh2[kScoreBatch][G][CW];
-    if (twoRounds) {
-        load_round(keys, kRoundKeys, kh2);
-        load_round(values, kRoundKeys, vh2);
+    if (plan.perSplit != a.spec_keys) { // not the split expected: its rows again, from k0
+        load_round(keys, 0, kh);
+        load_round(values, 0, vh);
+        if (twoRounds) {
+            load_round(keys, kRoundKeys, kh2);
+            load_round(values, kRoundKeys, vh2);
+        }
     }
 
     auto score_round = [&](const uint32_t (&k)[kScoreBatch][G][CW], int r0) {
@@ -1834,10 +1842,27 @@ int attention_grid_splits(int keyCount)
     return kDecodeSplits;
 }
 
+int attention_spec_keys(int keyCount)
+{
+    return keyCount > kDecodeSplits * kRoundKeys ? 2 * kRoundKeys : kRoundKeys;
+}
+
+int attention_graph_range(int keyCount)
+{
+    const int splits = attention_grid_splits(keyCount);
+    if (splits < kDecodeSplits)
+        return splits == 16 ? 0 : 1;
+    return attention_spec_keys(keyCount) == kRoundKeys ? 2 : 3;
+}
+
 int attention_key_range(int keyCount, int maxPositions)
 {
     const int splits = attention_grid_splits(keyCount);
-    return splits < kDecodeSplits ? splits * kRoundKeys : maxPositions;
+    if (splits < kDecodeSplits)
+        return splits * kRoundKeys;
+    if (attention_spec_keys(keyCount) == kRoundKeys)
+        return std::min(kDecodeSplits * kRoundKeys, maxPositions);
+    return maxPositions;
 }
 
 hipError_t launch_attention(const AttentionArgs &a, hipStream_t stream)
@@ -1846,7 +1871,8 @@ hipError_t launch_attention(const AttentionArgs &a, hipStream_t stream)
     if (!attention_layout(a.head_dim, &channels, &group) || a.heads % group != 0 || !a.q8
         || !a.part_ll || !a.ml_ll || !a.tag_epoch || !a.error)
         return hipErrorInvalidValue;
-    if (a.grid_splits < 1 || a.grid_splits > kDecodeSplits)
+    if (a.grid_splits < 1 || a.grid_splits > kDecodeSplits
+        || (a.spec_keys != kRoundKeys && a.spec_keys != 2 * kRoundKeys))
         return hipErrorInvalidValue;
     const dim3 grid(a.grid_splits * (a.heads / group));
     if (channels == 4)

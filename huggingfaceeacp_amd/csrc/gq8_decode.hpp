@@ -51,6 +51,8 @@ struct AttentionArgs {
     uint8_t *q8;              // Q8 row for o_proj
     int grid_splits;          // the launch's key splits (attention_grid_splits of the step's
                               // key-count range)
+    int spec_keys;            // keys of a split loaded before the position is known
+                              // (attention_spec_keys of the same range)
 };
 
 // Key splits of the one-token attention launch for steps of at most
@@ -60,7 +62,16 @@ struct AttentionArgs {
 // sized to the range keeps those loads few.  A captured step replays within
 // the range it was captured for (attention_key_range).
 int attention_grid_splits(int keyCount);
-// The largest key count of the range that `keyCount` falls in.
+// The keys a split of that launch covers when the step has `keyCount` keys
+// and the split takes its rounds of 64 at once (128 past 4096 keys): the rows
+// its workgroups load before the position arrives.  A split of another size
+// loads its rows again once the position is known.
+int attention_spec_keys(int keyCount);
+// The key-count ranges a captured step serves (attention_graph_range of a
+// key count: 16, 32 and 64 splits of one round, 64 splits of two), and the
+// largest key count of the range that `keyCount` falls in.
+constexpr int kAttentionRanges = 4;
+int attention_graph_range(int keyCount);
 int attention_key_range(int keyCount, int maxPositions);
 
 struct GateUpArgs {

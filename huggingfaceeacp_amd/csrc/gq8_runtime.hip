@@ -620,7 +620,7 @@ struct gq8_decoder {
 
     // the captured one-token step, one a key-count range (the attention
     // launch is sized to its range: gq8::attention_grid_splits)
-    static constexpr int kGraphRanges = 3;
+    static constexpr int kGraphRanges = gq8::kAttentionRanges;
     hipGraphExec_t graphs[kGraphRanges] = {};
     bool capturing = false;
     int captureKeys = 0; // while capturing: the largest key count of the range
@@ -1749,8 +1749,9 @@ int encode_fused_token(gq8_decoder *d, float *logits, bool sample)
         at.error = d->attnError;
         at.out = debugValues(1, l);
         at.q8 = d->x8;
-        at.grid_splits = gq8::attention_grid_splits(d->capturing ? d->captureKeys
-                                                                  : d->hostPosition + 1);
+        const int rangeKeys = d->capturing ? d->captureKeys : d->hostPosition + 1;
+        at.grid_splits = gq8::attention_grid_splits(rangeKeys);
+        at.spec_keys = gq8::attention_spec_keys(rangeKeys);
         GQ8_STAGE(kStageAttention, gq8::launch_attention(at, st));
         if (dbg && copy_last_q8_row(d, d->x8, 1, d->qWidth, debugQ8(1, l)))
             return GQ8_ERR_DEVICE;
@@ -1984,12 +1985,8 @@ namespace {
 // range, captured on first use.
 int graph_range(const gq8_decoder *d, int keyCount)
 {
-    const int splits = gq8::attention_grid_splits(keyCount);
-    int range = 0;
-    for (int s = 16; s < splits && range + 1 < gq8_decoder::kGraphRanges; s *= 2)
-        ++range;
     (void) d;
-    return range;
+    return gq8::attention_graph_range(keyCount);
 }
 
 int ensure_graph(gq8_decoder *d, int keyCount)
