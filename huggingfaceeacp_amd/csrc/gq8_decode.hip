@@ -331,7 +331,7 @@ constexpr int kScoreBatch = 8;                          // keys a wave takes a r
 constexpr int kRoundKeys = kAttnWaves * kScoreBatch;    // 64
 constexpr int kMaxSplitKeys = 256;                      // so the window is at most 16384
 constexpr int kMaxGroupWidth = 256;                     // G * head_dim
-constexpr int kPollSplits = 16; // split partials a merging lane polls at once
+constexpr int kPollSplits = 8; // split partials a merging lane polls at once (a run of at most 64 / 8)
 
 struct SplitPlan {
     int splits, perSplit;
@@ -385,7 +385,8 @@ __device__ inline double word_half(const uint32_t (&w)[(C + 1) / 2], int i)
 }
 
 template <int C, int G>
-__global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a)
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void attention_kernel(AttentionArgs a)
 {
     GQ8_ARGS_EARLY("s"(a.grid_splits), "s"(a.scale), "s"(a.part_ll), "s"(a.ml_ll), "s"(a.tag_epoch),
                    "s"(a.error), "s"(a.out), "s"(a.q8));
@@ -595,10 +596,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
     }
 
     // The merge (MultiQueryAttention.h:43-49: every split rescaled to the row
-    // maximum, in split order, the sums divided by the total), a 32-channel
-    // block a wave: the group's live splits share its blocks (split s takes
-    // blocks s, s + splits, ...), each polling the words it needs, so no
-    // workgroup waits on a ticket or reads the whole group's partials.
+    // maximum, in split order, the sums divided by the total): the group's
+    // live splits share its 32-channel blocks (split s takes blocks s,
+    // s + splits, ...), each polling the words it needs, so no workgroup
+    // waits on a ticket or reads the whole group's partials.  A merging
+    // workgroup's waves share its blocks: wpb waves a block, each taking a
+    // run of consecutive splits in one round of polls; the runs' sums are
+    // added in LDS in split order.
     const int splits = plan.splits;
     const int blocks = groupWidth / kBlock;
     const int mine = split < blocks ? (blocks - split + splits - 1) / splits : 0;
@@ -608,8 +612,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
     const uint32_t partBytes = (uint32_t) ((int64_t) kDecodeSplits * qWidth * 16);
     // lanes 32..63 of a merging wave repeat lanes 0..31 (the cross-lane sums
     // below take whole waves); lanes 0..31 store
-    const int b = split + wave * splits;              // a merging wave's block of the group
-    const int c = b * kBlock + (lane & (kBlock - 1)); // its channel in the group
+    const int wpb = kAttnWaves / mine;                // waves a block (mine <= 8 blocks)
+    const int bi = wave / wpb, ci = wave % wpb;       // this wave's block and run
+    const bool merging = bi < mine;
+    const int b = split + bi * splits;                // the block of the group
+    const int c = b * kBlock + (lane & (kBlock - 1)); // this lane's channel in the group
+    const int run = (splits + wpb - 1) / wpb;
+    const int sBegin = min(ci * run, splits), sEnd = min(sBegin + run, splits);
     // waves g < G: the split factors of head h0 + g, lane s taking split s
     if (wave < G) {
         const bool liveSplit = lane < splits;
@@ -635,45 +644,55 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttentionArgs a
         if (lane == 0)
             sSum[wave] = total;
     }
+    // the partial sums above have been read out of sAcc: it takes the runs'
     __syncthreads();
-    if (wave >= mine)
-        return;
     const int g = c / hd;
     double weighted = 0.0;
-    for (int s0 = 0; s0 < splits; s0 += kPollSplits) {
-        double part[kPollSplits];
-        int spins = 0;
-        for (;;) {
-            v4u w[kPollSplits];
+    if (merging) {
+        for (int s0 = sBegin; s0 < sEnd; s0 += kPollSplits) {
+            double part[kPollSplits];
+            int spins = 0;
+            for (;;) {
+                v4u w[kPollSplits];
 #pragma unroll
-            for (int u = 0; u < kPollSplits; ++u) {
-                const int sp = min(s0 + u, splits - 1);
-                w[u] = ld_agent_16(a.part_ll, (uint32_t) ((sp * qWidth + h0 * hd + c) * 16), partBytes);
+                for (int u = 0; u < kPollSplits; ++u) {
+                    const int sp = min(s0 + u, sEnd - 1);
+                    w[u] = ld_agent_16(a.part_ll, (uint32_t) ((sp * qWidth + h0 * hd + c) * 16), partBytes);
+                }
+                bool all = true;
+#pragma unroll
+                for (int u = 0; u < kPollSplits; ++u)
+                    all = all && w[u].y == tag && w[u].w == tag;
+                if (all) {
+#pragma unroll
+                    for (int u = 0; u < kPollSplits; ++u)
+                        part[u] = __longlong_as_double((long long) (((uint64_t) w[u].z << 32) | w[u].x));
+                    break;
+                }
+                if (wait_give_up(a.error, spins)) {
+#pragma unroll
+                    for (int u = 0; u < kPollSplits; ++u)
+                        part[u] = 0.0;
+                    break;
+                }
             }
-            bool all = true;
 #pragma unroll
             for (int u = 0; u < kPollSplits; ++u)
-                all = all && w[u].y == tag && w[u].w == tag;
-            if (all) {
-#pragma unroll
-                for (int u = 0; u < kPollSplits; ++u)
-                    part[u] = __longlong_as_double((long long) (((uint64_t) w[u].z << 32) | w[u].x));
-                break;
-            }
-            if (wait_give_up(a.error, spins)) {
-#pragma unroll
-                for (int u = 0; u < kPollSplits; ++u)
-                    part[u] = 0.0;
-                break;
-            }
+                if (s0 + u < sEnd)
+                    weighted += part[u] * sSplitMax[g][s0 + u];
         }
-#pragma unroll
-        for (int u = 0; u < kPollSplits; ++u)
-            if (s0 + u < splits)
-                weighted += part[u] * sSplitMax[g][s0 + u];
     }
+    double *sRun = &sAcc[0][0]; // [kAttnWaves][kBlock]: each wave's run sums
+    if (merging && lane < kBlock)
+        sRun[wave * kBlock + lane] = weighted;
+    __syncthreads();
+    if (!merging || ci != 0)
+        return;
+    double total = sRun[wave * kBlock + (lane & (kBlock - 1))];
+    for (int k = 1; k < wpb; ++k)
+        total += sRun[(wave + k) * kBlock + (lane & (kBlock - 1))];
     const int idx = h0 * hd + c;
-    const float v = (float) (weighted / sSum[g]);
+    const float v = (float) (total / sSum[g]);
     float amax = fabsf(v);
     amax = max_lanes<16>(amax); // lanes 0..31: the block
     const uint16_t bits = scale_bits_from_amax(amax);
