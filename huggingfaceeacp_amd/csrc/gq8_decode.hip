@@ -338,11 +338,11 @@ struct SplitPlan {
 };
 
 // Whole rounds a split, as few as the launch's gridSplits splits allow.
-__device__ inline SplitPlan plan_splits(int keyCount, int gridSplits)
+__device__ inline SplitPlan plan_splits(int keyCount, int gridSplits, int roundKeys)
 {
     const int roundsPerSplit =
-        (keyCount + kRoundKeys * gridSplits - 1) / (kRoundKeys * gridSplits);
-    const int perSplit = roundsPerSplit * kRoundKeys;
+        (keyCount + roundKeys * gridSplits - 1) / (roundKeys * gridSplits);
+    const int perSplit = roundsPerSplit * roundKeys;
     return {(keyCount + perSplit - 1) / perSplit, perSplit};
 }
 
@@ -384,13 +384,14 @@ __device__ inline double word_half(const uint32_t (&w)[(C + 1) / 2], int i)
     return (double) half_value((uint16_t) (w[i >> 1] >> (16 * (i & 1))));
 }
 
-template <int C, int G>
+template <int C, int G, int B>
 __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void attention_kernel(AttentionArgs a)
 {
     GQ8_ARGS_EARLY("s"(a.grid_splits), "s"(a.scale), "s"(a.part_ll), "s"(a.ml_ll), "s"(a.tag_epoch),
                    "s"(a.error), "s"(a.out), "s"(a.q8));
-    constexpr int kRows = kScoreBatch * G; // reduce_rows width: (key, head) pairs
+    constexpr int kRound = kAttnWaves * B; // keys a round: B a wave
+    constexpr int kRows = B * G; // reduce_rows width: (key, head) pairs
     __shared__ double sScore[G][kMaxSplitKeys];
     __shared__ double sAcc[kAttnWaves][kMaxGroupWidth];
     __shared__ double sMax[G], sSum[G];
@@ -429,13 +430,13 @@ void attention_kernel(AttentionArgs a)
     // (rows past the position are read, inside the cache, and never used), so
     // the two loads do not wait on each other.
     constexpr int CW = (C + 1) / 2; // words of a lane's channels of one row
-    uint32_t kh[kScoreBatch][G][CW], vh[kScoreBatch][G][CW];
-    uint32_t kh2[kScoreBatch][G][CW], vh2[kScoreBatch][G][CW];
-    const bool specTwo = a.spec_keys == 2 * kRoundKeys;
+    uint32_t kh[B][G][CW], vh[B][G][CW];
+    uint32_t kh2[B][G][CW], vh2[B][G][CW];
+    const bool specTwo = a.spec_keys == 2 * kRound;
 #pragma unroll
-    for (int b = 0; b < kScoreBatch; ++b) {
+    for (int b = 0; b < B; ++b) {
         const int j = min(split * a.spec_keys + wave + b * kAttnWaves, a.max_positions - 1);
-        const int j2 = min(j + kRoundKeys, a.max_positions - 1);
+        const int j2 = min(j + kRound, a.max_positions - 1);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             load_words<C>(a.key_cache + (int64_t) j * kvWidth + kvOffset[g], kh[b][g]);
@@ -451,7 +452,7 @@ void attention_kernel(AttentionArgs a)
     asm volatile("" ::: "memory");
 
     const int keyCount = *a.position + 1;
-    const SplitPlan plan = plan_splits(keyCount, a.grid_splits);
+    const SplitPlan plan = plan_splits(keyCount, a.grid_splits, kRound);
     // a launch too small for its step's keys (the host sizes it to the range:
     // attention_grid_splits) would overrun sScore; it does nothing instead
     if (split >= plan.splits || plan.perSplit > kMaxSplitKeys)
@@ -463,9 +464,9 @@ void attention_kernel(AttentionArgs a)
 
     // a round's rows for this wave: keys r0 + wave + 8 b, clamped into range
     // (the clamped duplicates are masked where they are used)
-    auto load_round = [&](const uint16_t *base, int r0, uint32_t (&dst)[kScoreBatch][G][CW]) {
+    auto load_round = [&](const uint16_t *base, int r0, uint32_t (&dst)[B][G][CW]) {
 #pragma unroll
-        for (int b = 0; b < kScoreBatch; ++b) {
+        for (int b = 0; b < B; ++b) {
             const int j = min(r0 + wave + b * kAttnWaves, n - 1);
 #pragma unroll
             for (int g = 0; g < G; ++g)
@@ -474,20 +475,20 @@ void attention_kernel(AttentionArgs a)
     };
     // a two-round split (a window of 4097 .. 8192 keys) has its second round's
     // rows in flight with the first's
-    const bool twoRounds = plan.perSplit == 2 * kRoundKeys;
+    const bool twoRounds = plan.perSplit == 2 * kRound;
     if (plan.perSplit != a.spec_keys) { // not the split expected: its rows again, from k0
         load_round(keys, 0, kh);
         load_round(values, 0, vh);
         if (twoRounds) {
-            load_round(keys, kRoundKeys, kh2);
-            load_round(values, kRoundKeys, vh2);
+            load_round(keys, kRound, kh2);
+            load_round(values, kRound, vh2);
         }
     }
 
-    auto score_round = [&](const uint32_t (&k)[kScoreBatch][G][CW], int r0) {
+    auto score_round = [&](const uint32_t (&k)[B][G][CW], int r0) {
         double y[kRows];
 #pragma unroll
-        for (int b = 0; b < kScoreBatch; ++b)
+        for (int b = 0; b < B; ++b)
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 double p = 0.0;
@@ -506,9 +507,9 @@ void attention_kernel(AttentionArgs a)
     };
     score_round(kh, 0);
     if (twoRounds) {
-        score_round(kh2, kRoundKeys);
+        score_round(kh2, kRound);
     } else {
-        for (int r0 = kRoundKeys; r0 < n; r0 += kRoundKeys) {
+        for (int r0 = kRound; r0 < n; r0 += kRound) {
             load_round(keys, r0, kh);
             score_round(kh, r0);
         }
@@ -541,9 +542,9 @@ void attention_kernel(AttentionArgs a)
 #pragma unroll
         for (int i = 0; i < C; ++i)
             acc[g][i] = 0.0;
-    auto value_round = [&](const uint32_t (&v)[kScoreBatch][G][CW], int r0) {
+    auto value_round = [&](const uint32_t (&v)[B][G][CW], int r0) {
 #pragma unroll
-        for (int b = 0; b < kScoreBatch; ++b) {
+        for (int b = 0; b < B; ++b) {
             const int j = r0 + wave + b * kAttnWaves;
             if (j >= n)
                 break;
@@ -558,9 +559,9 @@ void attention_kernel(AttentionArgs a)
     };
     value_round(vh, 0);
     if (twoRounds) {
-        value_round(vh2, kRoundKeys);
+        value_round(vh2, kRound);
     } else {
-        for (int r0 = kRoundKeys; r0 < n; r0 += kRoundKeys) {
+        for (int r0 = kRound; r0 < n; r0 += kRound) {
             load_round(values, r0, vh);
             value_round(vh, r0);
         }
@@ -1853,35 +1854,44 @@ hipError_t launch_qkv_rope(const QkvArgs &a, hipStream_t stream)
     return hipGetLastError();
 }
 
+// The one-token attention launch for each key-count range: its splits, the
+// keys of a round (4 or 8 a wave), and the keys a split is expected to cover
+// (its rows loaded before the position).  Short contexts take half rounds,
+// so twice the workgroups share the keys; past 4096 keys a split takes two
+// rounds at once.
+struct AttentionRange {
+    int lastKeys, splits, roundKeys, specKeys;
+};
+constexpr AttentionRange kAttentionTable[kAttentionRanges] = {
+    {512, 16, 32, 32}, {1024, 32, 32, 32}, {2048, 64, 32, 32}, {4096, 64, 64, 64},
+    {INT32_MAX, 64, 64, 128}};
+
+int attention_graph_range(int keyCount)
+{
+    int r = 0;
+    while (r + 1 < kAttentionRanges && keyCount > kAttentionTable[r].lastKeys)
+        ++r;
+    return r;
+}
+
 int attention_grid_splits(int keyCount)
 {
-    for (int splits = 16; splits < kDecodeSplits; splits *= 2)
-        if (keyCount <= splits * kRoundKeys)
-            return splits;
-    return kDecodeSplits;
+    return kAttentionTable[attention_graph_range(keyCount)].splits;
+}
+
+int attention_round_keys(int keyCount)
+{
+    return kAttentionTable[attention_graph_range(keyCount)].roundKeys;
 }
 
 int attention_spec_keys(int keyCount)
 {
-    return keyCount > kDecodeSplits * kRoundKeys ? 2 * kRoundKeys : kRoundKeys;
-}
-
-int attention_graph_range(int keyCount)
-{
-    const int splits = attention_grid_splits(keyCount);
-    if (splits < kDecodeSplits)
-        return splits == 16 ? 0 : 1;
-    return attention_spec_keys(keyCount) == kRoundKeys ? 2 : 3;
+    return kAttentionTable[attention_graph_range(keyCount)].specKeys;
 }
 
 int attention_key_range(int keyCount, int maxPositions)
 {
-    const int splits = attention_grid_splits(keyCount);
-    if (splits < kDecodeSplits)
-        return splits * kRoundKeys;
-    if (attention_spec_keys(keyCount) == kRoundKeys)
-        return std::min(kDecodeSplits * kRoundKeys, maxPositions);
-    return maxPositions;
+    return std::min(kAttentionTable[attention_graph_range(keyCount)].lastKeys, maxPositions);
 }
 
 hipError_t launch_attention(const AttentionArgs &a, hipStream_t stream)
@@ -1891,17 +1901,26 @@ hipError_t launch_attention(const AttentionArgs &a, hipStream_t stream)
         || !a.part_ll || !a.ml_ll || !a.tag_epoch || !a.error)
         return hipErrorInvalidValue;
     if (a.grid_splits < 1 || a.grid_splits > kDecodeSplits
-        || (a.spec_keys != kRoundKeys && a.spec_keys != 2 * kRoundKeys))
+        || (a.round_keys != 32 && a.round_keys != 64)
+        || (a.spec_keys != a.round_keys && a.spec_keys != 2 * a.round_keys))
         return hipErrorInvalidValue;
     const dim3 grid(a.grid_splits * (a.heads / group));
+#define GQ8_ATTENTION(CC, GG)                                                                  \
+    do {                                                                                       \
+        if (a.round_keys == 32)                                                                \
+            hipLaunchKernelGGL((attention_kernel<CC, GG, 4>), grid, dim3(kAttnThreads), 0, stream, a); \
+        else                                                                                   \
+            hipLaunchKernelGGL((attention_kernel<CC, GG, 8>), grid, dim3(kAttnThreads), 0, stream, a); \
+    } while (0)
     if (channels == 4)
-        hipLaunchKernelGGL((attention_kernel<4, 1>), grid, dim3(kAttnThreads), 0, stream, a);
+        GQ8_ATTENTION(4, 1);
     else if (channels == 2)
-        hipLaunchKernelGGL((attention_kernel<2, 1>), grid, dim3(kAttnThreads), 0, stream, a);
+        GQ8_ATTENTION(2, 1);
     else if (group == 1)
-        hipLaunchKernelGGL((attention_kernel<1, 1>), grid, dim3(kAttnThreads), 0, stream, a);
+        GQ8_ATTENTION(1, 1);
     else
-        hipLaunchKernelGGL((attention_kernel<1, 2>), grid, dim3(kAttnThreads), 0, stream, a);
+        GQ8_ATTENTION(1, 2);
+#undef GQ8_ATTENTION
     return hipGetLastError();
 }
 

@@ -51,27 +51,26 @@ struct AttentionArgs {
     uint8_t *q8;              // Q8 row for o_proj
     int grid_splits;          // the launch's key splits (attention_grid_splits of the step's
                               // key-count range)
+    int round_keys;           // keys a round of the launch (attention_round_keys: 32 or 64)
     int spec_keys;            // keys of a split loaded before the position is known
                               // (attention_spec_keys of the same range)
 };
 
-// Key splits of the one-token attention launch for steps of at most
-// `keyCount` keys: the fewest of 16, 32 and kDecodeSplits that give every
-// split at most one 64-key round (64 past 4096 keys).  Splits past the
-// step's keys exit after their speculative first-round loads, so a launch
-// sized to the range keeps those loads few.  A captured step replays within
-// the range it was captured for (attention_key_range).
-int attention_grid_splits(int keyCount);
-// The keys a split of that launch covers when the step has `keyCount` keys
-// and the split takes its rounds of 64 at once (128 past 4096 keys): the rows
-// its workgroups load before the position arrives.  A split of another size
-// loads its rows again once the position is known.
-int attention_spec_keys(int keyCount);
-// The key-count ranges a captured step serves (attention_graph_range of a
-// key count: 16, 32 and 64 splits of one round, 64 splits of two), and the
-// largest key count of the range that `keyCount` falls in.
-constexpr int kAttentionRanges = 4;
+// The one-token attention launch for steps of `keyCount` keys, by key-count
+// range (attention_graph_range: at most 512, 1024, 2048, 4096 keys, and
+// beyond): its key splits (16, 32, 64, 64, 64), the keys of its rounds (32
+// while at most 2048 keys, then 64: 4 or 8 keys a wave), and the keys a split
+// is expected to cover, whose rows its workgroups load before the position
+// arrives (one round; two past 4096 keys).  A split of another size loads its
+// rows again once the position is known.  Splits past the step's keys exit
+// after their speculative loads, so a launch sized to the range keeps those
+// loads few.  A captured step replays within the range it was captured for;
+// attention_key_range is the largest key count of that range.
+constexpr int kAttentionRanges = 5;
 int attention_graph_range(int keyCount);
+int attention_grid_splits(int keyCount);
+int attention_round_keys(int keyCount);
+int attention_spec_keys(int keyCount);
 int attention_key_range(int keyCount, int maxPositions);
 
 struct GateUpArgs {

@@ -1751,6 +1751,7 @@ int encode_fused_token(gq8_decoder *d, float *logits, bool sample)
         at.q8 = d->x8;
         const int rangeKeys = d->capturing ? d->captureKeys : d->hostPosition + 1;
         at.grid_splits = gq8::attention_grid_splits(rangeKeys);
+        at.round_keys = gq8::attention_round_keys(rangeKeys);
         at.spec_keys = gq8::attention_spec_keys(rangeKeys);
         GQ8_STAGE(kStageAttention, gq8::launch_attention(at, st));
         if (dbg && copy_last_q8_row(d, d->x8, 1, d->qWidth, debugQ8(1, l)))
