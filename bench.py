@@ -51,7 +51,7 @@ METRIC = "Gemma-2B Q8_0 decode tok/s (b=1, ctx 512) + % of HBM roofline"
 STAGE_LABELS = {
     "gate_up": "gateup_geglu_kernel (post-attention norm + gate|up 2048 -> 2x16384 + GeGLU + Q8)",
     "lm_head": "lmhead_argmax_kernel (tied lm_head 2048 -> 256000 + first-maximum fold)",
-    "down": "q8_matvec_kernel<1,4,2> (down 16384 -> 2048 + residual)",
+    "down": "q8_matvec_kernel<4,4,2> (down 16384 -> 2048 + residual)",
 }
 DATA = ("synthetic: seeded N(0,0.02) weights / N(0,0.1) norms quantized to Int8Blocks, "
         "seeded uniform prompt ids")
