@@ -756,7 +756,7 @@ __global__ __launch_bounds__(kRowsThreads, 3) void attention_rows_kernel(RowsAtt
     // queries), the new value, and the first tile's key and value rows (rows
     // past the position are read inside the cache and never used).  Their
     // round trip overlaps the position's.
-    float lo[kRopePairs], hi[kRopePairs];
+    float lo[kRopePairs], hi[kRopePairs], cs[kRopePairs], sn[kRopePairs];
 #pragma unroll
     for (int k = 0; k < kRopePairs; ++k) {
         const int idx = min(t + k * kRowsThreads, (G + 1) * half - 1);
@@ -764,6 +764,10 @@ __global__ __launch_bounds__(kRowsThreads, 3) void attention_rows_kernel(RowsAtt
         const int global = head < G ? hBase + head : H;
         lo[k] = row[global * hd + i];
         hi[k] = row[global * hd + i + half];
+        // the angles of the row's position, copied for the step by its embed
+        // launch: no wait on the position
+        cs[k] = a.row_angles[(int64_t) seq * 2 * half + i];
+        sn[k] = a.row_angles[(int64_t) (seq * 2 + 1) * half + i];
     }
     const float newValue = row[qW + hd + min(t, hd - 1)];
     // this lane's score slice: channels ch0 .. ch0 + kSliceCh - 1 of keys
@@ -809,14 +813,6 @@ __global__ __launch_bounds__(kRowsThreads, 3) void attention_rows_kernel(RowsAtt
     // RoPE (rope_kv_kernel's arithmetic) of the group's query heads and, in
     // the split holding it, of the new key; the new value rounded to fp16
     {
-        float cs[kRopePairs], sn[kRopePairs];
-#pragma unroll
-        for (int k = 0; k < kRopePairs; ++k) {
-            const int idx = min(t + k * kRowsThreads, (G + 1) * half - 1);
-            const int64_t angle = (int64_t) pos * half + idx % half;
-            cs[k] = a.cosines[angle];
-            sn[k] = a.sines[angle];
-        }
 #pragma unroll
         for (int k = 0; k < kRopePairs; ++k) {
             const int idx = t + k * kRowsThreads;
@@ -1240,7 +1236,7 @@ size_t rows_attention_workspace_doubles(int rows, int heads, int head_dim)
 hipError_t launch_rows_attention(const RowsAttentionArgs &a, int rows, int max_positions,
                                  hipStream_t stream)
 {
-    if (rows <= 0 || rows > kBatchRows || a.q8_rows < rows
+    if (rows <= 0 || rows > kBatchRows || a.q8_rows < rows || !a.row_angles
         || !rows_attention_supported(a.heads, 1, a.head_dim, max_positions)
         || a.per_split != rows_attention_split_keys(max_positions) || a.max_positions != max_positions)
         return hipErrorInvalidValue;

@@ -70,16 +70,27 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_kernel(const float *__
 // ---- embedding gather (Embed.h:45-82) ------------------------------------
 // Row r embeds tokens[*pos_ptr + r] (one sequence), or with row_positions
 // tokens[r * slot_stride + row_positions[r]] (row r of a lockstep batch, each
-// sequence's slots slot_stride apart).
+// sequence's slots slot_stride apart).  With row_angles, the first workgroup
+// of row r also copies the RoPE table rows of its position (RoPE.cpp:7-34):
+// cosines to row_angles[2 r half ..], sines to row_angles[(2 r + 1) half ..].
 __global__ __launch_bounds__(kThreads) void embed_kernel(const uint32_t *__restrict__ tokens,
                                                          const int *pos_ptr,
                                                          const int *row_positions,
                                                          int64_t slot_stride,
                                                          const uint8_t *__restrict__ table,
                                                          int64_t vocab, int width, float scale,
-                                                         float *__restrict__ out)
+                                                         float *__restrict__ out,
+                                                         const float *__restrict__ cosines,
+                                                         const float *__restrict__ sines, int half,
+                                                         float *__restrict__ row_angles)
 {
     const int row = blockIdx.y;
+    if (row_angles && blockIdx.x == 0 && (int) threadIdx.x < 2 * half) {
+        const int i = threadIdx.x % half;
+        const int64_t angle = (int64_t) row_positions[row] * half + i;
+        row_angles[(int64_t) row * 2 * half + threadIdx.x] =
+            (int) threadIdx.x < half ? cosines[angle] : sines[angle];
+    }
     const int c = blockIdx.x * kThreads + threadIdx.x;
     if (c >= width)
         return;
@@ -851,19 +862,21 @@ hipError_t launch_embed(const uint32_t *tokens, const int *pos_ptr, int rows,
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(embed_kernel, dim3(blocks_for(width, kThreads), rows), dim3(kThreads), 0,
                        stream, tokens, pos_ptr, nullptr, (int64_t) 0, table, (int64_t) vocab, width,
-                       scale, out);
+                       scale, out, nullptr, nullptr, 0, nullptr);
     return hipGetLastError();
 }
 
 hipError_t launch_embed_slots(const uint32_t *slots, int64_t slot_stride, const int *positions,
                               int rows, const uint8_t *table, int vocab, int width, float scale,
-                              float *out, hipStream_t stream)
+                              float *out, const float *cosines, const float *sines, int half,
+                              float *row_angles, hipStream_t stream)
 {
-    if (rows <= 0 || width <= 0 || width % kBlock != 0 || !positions || slot_stride <= 0)
+    if (rows <= 0 || width <= 0 || width % kBlock != 0 || !positions || slot_stride <= 0
+        || (row_angles && (!cosines || !sines || half <= 0 || 2 * half > kThreads)))
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(embed_kernel, dim3(blocks_for(width, kThreads), rows), dim3(kThreads), 0,
                        stream, slots, nullptr, positions, slot_stride, table, (int64_t) vocab,
-                       width, scale, out);
+                       width, scale, out, cosines, sines, half, row_angles);
     return hipGetLastError();
 }
 

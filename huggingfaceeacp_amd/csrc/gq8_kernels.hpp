@@ -112,9 +112,12 @@ hipError_t launch_advance(int *pos_ptr, int amount, hipStream_t stream);
 // slots + r * slot_stride.
 constexpr int kBatchRows = 16;
 
+// With row_angles, also the RoPE table rows (half pairs, cosines then sines)
+// of each row's position, for the step's attention (RowsAttentionArgs).
 hipError_t launch_embed_slots(const uint32_t *slots, int64_t slot_stride, const int *positions,
                               int rows, const uint8_t *table, int vocab, int width, float scale,
-                              float *out, hipStream_t stream);
+                              float *out, const float *cosines, const float *sines, int half,
+                              float *row_angles, hipStream_t stream);
 
 // y[m, n] (+)= the Int8Blocks product of up to kBatchRows activation rows (a
 // Q8 row buffer of x_rows rows, rows [0, rows) used) on int8 MFMA.  Products
@@ -150,7 +153,7 @@ struct RowsAttentionArgs {
     const float *qkv;
     int qkv_stride;
     const int *positions;
-    const float *cosines, *sines;
+    const float *row_angles;  // row r's RoPE cosines [2 r half ..] and sines [(2 r + 1) half ..]
     uint16_t *key_cache, *value_cache;
     int64_t cache_stride;
     int max_positions;        // rows of each cache (the bound of speculative reads)

@@ -2358,6 +2358,7 @@ struct gq8_batch {
     uint8_t *x8b = nullptr; // Q8 rows of GeGLU (gate | up reads x8 while they are written)
     uint32_t *chosen = nullptr;
     double *attnO = nullptr, *attnMl = nullptr;
+    float *rowAngles = nullptr; // each row's RoPE cosines and sines for the step
     double *partials = nullptr;
     size_t partialBytes = 0;
     int *tickets = nullptr;
@@ -2474,7 +2475,8 @@ int encode_batch_step(gq8_batch *b)
 
     GQ8_STAGE(kStageEmbed, gq8::launch_embed_slots(b->slots, b->slotStride, b->positions, S,
                                                    d->embedding, s.vocab, W, s.embedding_scale,
-                                                   b->hidden, st));
+                                                   b->hidden, d->cosines, d->sines, s.head_dim / 2,
+                                                   b->rowAngles, st));
     for (int l = 0; l < s.layers; ++l) {
         const int64_t layerCache = (int64_t) l * s.max_positions * d->kvWidth;
         GQ8_STAGE(kStageNorm, gq8::launch_rmsnorm(b->hidden, d->inputNorm[l], S, W, s.rms_epsilon,
@@ -2486,8 +2488,7 @@ int encode_batch_step(gq8_batch *b)
         at.qkv = b->qkvRows;
         at.qkv_stride = d->qkvWidth;
         at.positions = b->positions;
-        at.cosines = d->cosines;
-        at.sines = d->sines;
+        at.row_angles = b->rowAngles;
         at.key_cache = b->keyCache + layerCache;
         at.value_cache = b->valueCache + layerCache;
         at.cache_stride = b->cacheStride;
@@ -2619,6 +2620,7 @@ extern "C" int gq8_batch_create(gq8_decoder *d, int sequences, gq8_batch **out)
     GQ8_BATCH_ALLOC(b->x8, gq8::q8_bytes(S, d->maxInner));
     GQ8_BATCH_ALLOC(b->x8b, gq8::q8_bytes(S, F));
     GQ8_BATCH_ALLOC(b->chosen, S * sizeof(uint32_t));
+    GQ8_BATCH_ALLOC(b->rowAngles, (size_t) S * s.head_dim * sizeof(float));
     GQ8_BATCH_ALLOC(b->attnO, gq8::rows_attention_workspace_doubles(S, s.heads, s.head_dim)
                                   * sizeof(double));
     b->attnMl = b->attnO + (size_t) S * gq8::kRowsMaxSplits * d->qWidth;
