@@ -132,8 +132,11 @@ __device__ inline void norm_store(float x, float w, double scale, int64_t at, bo
 // K: elements a thread holds (the row's width rounded up to K x kThreads),
 // loaded at once, or 0: rows of any width, streamed from memory twice.  Every
 // lane of a wave takes part in the group reductions (elements past the width
-// are computed from a clamped index and not stored).
-template <int K>
+// are computed from a clamped index and not stored).  P > 1 (K > 0): the row
+// is P workgroups (blockIdx.y); each sums the squares of the whole row and
+// normalizes its K / P elements a thread, so a few rows fill more of the
+// chip and each thread's chain is shorter.
+template <int K, int P>
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restrict__ x,
                                                            const float *__restrict__ weight,
                                                            int rows, int width, float epsilon,
@@ -167,11 +170,20 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restri
             norm_store(xr[c], weight[c], scale, (int64_t) row * width + c, live, elements, y, q8);
         }
     } else {
-        float xv[K], wv[K];
+        static_assert(K % P == 0, "whole parts of a row");
+        constexpr int KP = K / P;
+        const int k0 = (int) blockIdx.y * KP; // this workgroup's part: elements t + k kThreads, k >= k0
+        float xv[K], xn[KP], wv[KP];
 #pragma unroll
-        for (int k = 0; k < K; ++k) {
-            const int i = min(threadIdx.x + k * kThreads, width - 1); // clamped; masked below
-            xv[k] = xr[i];
+        for (int k = 0; k < K; ++k)
+            xv[k] = xr[min((int) threadIdx.x + k * kThreads, width - 1)]; // clamped; masked below
+#pragma unroll
+        for (int k = 0; k < KP; ++k) {
+            const int i = min((int) threadIdx.x + (k0 + k) * kThreads, width - 1);
+            if constexpr (P == 1)
+                xn[k] = xv[k];
+            else
+                xn[k] = xr[i];
             wv[k] = weight[i];
         }
         double squares = 0.0;
@@ -190,25 +202,25 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restri
         const double scale = norm_scale(total, width, epsilon);
         // every element's value, block scale and byte first (no branches, so
         // the K chains interleave), then the stores
-        float v[K], amax[K];
-        uint16_t bits[K];
-        int bytes[K];
+        float v[KP], amax[KP];
+        uint16_t bits[KP];
+        int bytes[KP];
 #pragma unroll
-        for (int k = 0; k < K; ++k) {
-            v[k] = norm_value(xv[k], scale, wv[k]);
+        for (int k = 0; k < KP; ++k) {
+            v[k] = norm_value(xn[k], scale, wv[k]);
             amax[k] = fabsf(v[k]);
         }
         max_lanes_each<16>(amax); // each 32-lane group's largest magnitude
 #pragma unroll
-        for (int k = 0; k < K; ++k) {
+        for (int k = 0; k < KP; ++k) {
             bits[k] = scale_bits_from_amax(amax[k]);
             const float sc = half_value(bits[k]);
             bytes[k] = quantize_in_block(v[k], bits[k], sc, quantize_hint(sc));
         }
         uint16_t *scales = q8 ? reinterpret_cast<uint16_t *>(q8 + elements) : nullptr;
 #pragma unroll
-        for (int k = 0; k < K; ++k) {
-            const int i = threadIdx.x + k * kThreads;
+        for (int k = 0; k < KP; ++k) {
+            const int i = threadIdx.x + (k0 + k) * kThreads;
             if (i >= width) // whole 32-element groups are live together
                 continue;
             const int64_t at = (int64_t) row * width + i;
@@ -886,24 +898,32 @@ hipError_t launch_rmsnorm(const float *x, const float *weight, int rows, int wid
     if (rows <= 0 || width <= 0 || width % kBlock != 0)
         return hipErrorInvalidValue;
     const int held = (width + kThreads - 1) / kThreads;
+    // a few rows (a lockstep step's) take a workgroup for each element a
+    // thread holds
+    const bool split = rows <= 64;
+#define GQ8_RMSNORM(KK)                                                                          \
+    do {                                                                                         \
+        if (split)                                                                               \
+            hipLaunchKernelGGL((rmsnorm_kernel<KK, KK>), dim3(rows, KK), dim3(kThreads), 0, stream, \
+                               x, weight, rows, width, epsilon, y, q8);                          \
+        else                                                                                     \
+            hipLaunchKernelGGL((rmsnorm_kernel<KK, 1>), dim3(rows), dim3(kThreads), 0, stream, x,  \
+                               weight, rows, width, epsilon, y, q8);                             \
+    } while (0)
     if (held <= 1)
-        hipLaunchKernelGGL(rmsnorm_kernel<1>, dim3(rows), dim3(kThreads), 0, stream, x, weight, rows,
-                           width, epsilon, y, q8);
+        GQ8_RMSNORM(1);
     else if (held <= 2)
-        hipLaunchKernelGGL(rmsnorm_kernel<2>, dim3(rows), dim3(kThreads), 0, stream, x, weight, rows,
-                           width, epsilon, y, q8);
+        GQ8_RMSNORM(2);
     else if (held <= 4)
-        hipLaunchKernelGGL(rmsnorm_kernel<4>, dim3(rows), dim3(kThreads), 0, stream, x, weight, rows,
-                           width, epsilon, y, q8);
+        GQ8_RMSNORM(4);
     else if (held <= 8)
-        hipLaunchKernelGGL(rmsnorm_kernel<8>, dim3(rows), dim3(kThreads), 0, stream, x, weight, rows,
-                           width, epsilon, y, q8);
+        GQ8_RMSNORM(8);
     else if (held <= 16)
-        hipLaunchKernelGGL(rmsnorm_kernel<16>, dim3(rows), dim3(kThreads), 0, stream, x, weight, rows,
-                           width, epsilon, y, q8);
+        GQ8_RMSNORM(16);
     else
-        hipLaunchKernelGGL(rmsnorm_kernel<0>, dim3(rows), dim3(kThreads), 0, stream, x, weight, rows,
-                           width, epsilon, y, q8);
+        hipLaunchKernelGGL((rmsnorm_kernel<0, 1>), dim3(rows), dim3(kThreads), 0, stream, x, weight,
+                           rows, width, epsilon, y, q8);
+#undef GQ8_RMSNORM
     return hipGetLastError();
 }
 
