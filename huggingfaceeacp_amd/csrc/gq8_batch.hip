@@ -977,25 +977,27 @@ __global__ __launch_bounds__(kRowsThreads, 3) void attention_rows_kernel(RowsAtt
     }
 }
 
-// The merge of a row's key splits, one workgroup a (head, sequence), one
-// channel a thread: every split rescaled to the row maximum, in split order,
-// the sum divided by the total (MultiQueryAttention.h:43-49), rounded to fp32
-// and quantized in 32-channel blocks for o_proj.  Every split's partial is
-// loaded at once.
-__global__ __launch_bounds__(kRowsThreads) void attention_merge_rows_kernel(RowsAttentionArgs a)
+// The merge of a row's key splits, one wave a (64 channels of a head,
+// sequence), one channel a lane: every split rescaled to the row maximum, in
+// split order, the sum divided by the total (MultiQueryAttention.h:43-49),
+// rounded to fp32 and quantized in 32-channel blocks for o_proj.  Every
+// split's partial is loaded at once, and each wave computes its head's split
+// factors itself, so a workgroup moves 16 KB of partials, not a head's 64 KB.
+__global__ __launch_bounds__(64) void attention_merge_rows_kernel(RowsAttentionArgs a)
 {
     __shared__ double sF[kRowsMaxSplits];
     __shared__ double sTotal;
-    const int head = blockIdx.x, seq = blockIdx.y, t = threadIdx.x;
     const int hd = a.head_dim, H = a.heads, qW = H * hd;
+    const int quarters = hd / 64; // waves a head
+    const int head = blockIdx.x / quarters, seq = blockIdx.y, t = threadIdx.x;
     const int splits = (a.positions[seq] + a.per_split) / a.per_split; // keys: position + 1
     const int64_t first = (int64_t) seq * kRowsMaxSplits;
-    const int o = head * hd + t;
+    const int o = head * hd + (blockIdx.x % quarters) * 64 + t;
     double part[kRowsMaxSplits];
 #pragma unroll
     for (int u = 0; u < kRowsMaxSplits; ++u)
         part[u] = a.ws_o[(first + min(u, splits - 1)) * qW + o];
-    if (t < 64) {
+    {
         const bool live = t < splits;
         const int sp = live ? t : 0;
         const double m = a.ws_ml[((first + sp) * H + head) * 2];
@@ -1261,8 +1263,8 @@ hipError_t launch_rows_attention(const RowsAttentionArgs &a, int rows, int max_p
 #undef GQ8_ROWS_ATTENTION
     if (hipError_t e = hipGetLastError(); e != hipSuccess)
         return e;
-    hipLaunchKernelGGL(attention_merge_rows_kernel, dim3(a.heads, rows), dim3(a.head_dim), 0, stream,
-                       a);
+    hipLaunchKernelGGL(attention_merge_rows_kernel, dim3(a.heads * (a.head_dim / 64), rows), dim3(64), 0,
+                       stream, a);
     return hipGetLastError();
 }
 
