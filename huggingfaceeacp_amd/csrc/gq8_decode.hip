@@ -15,7 +15,7 @@
 //   (o_proj, down)       q8_matvec_kernel with the residual add;
 //   gateup_geglu_kernel  norm + Q8 prologue, the gate|up product, GeGLU and
 //                        the Q8 row for down_proj;
-//   final_norm_kernel    the final norm and its Q8 row (one workgroup);
+//   (final norm)         rmsnorm_kernel: the final norm and its Q8 row;
 //   lmhead_argmax_kernel the tied lm_head over the whole vocabulary, each
 //                        workgroup's first maximum merged into one packed
 //                        64-bit word by atomicMax;
@@ -820,14 +820,6 @@ constexpr int kHeadRows = 8;
 constexpr int kHeadThreads = 512;
 constexpr int kHeadWaves = kHeadThreads / 64;
 
-__global__ __launch_bounds__(kThreads) void final_norm_kernel(HeadArgs a)
-{
-    __shared__ RowQ8 row;
-    __shared__ double sPartial[kWaves];
-    const RowSlice<8> slice = load_row_slice<8>(a.hidden, nullptr, nullptr, 0, 0.f, nullptr,
-                                                a.norm_weight, a.width);
-    norm_q8_finish(slice, a.width, a.epsilon, row, sPartial, a.normalised_out, a.q8);
-}
 
 __global__ __launch_bounds__(kHeadThreads) void lmhead_argmax_kernel(HeadArgs a)
 {
@@ -1936,10 +1928,14 @@ hipError_t launch_gateup_geglu(const GateUpArgs &a, hipStream_t stream)
     return hipGetLastError();
 }
 
+// The final norm of the step's row: the row-norm kernel, whose one row takes
+// a workgroup for each element a thread holds (each sums the whole row's
+// squares and normalizes its share), so the chain after the row arrives is
+// one element long.
 hipError_t launch_final_norm(const HeadArgs &a, hipStream_t stream)
 {
-    hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(kThreads), 0, stream, a);
-    return hipGetLastError();
+    return launch_rmsnorm(a.hidden, a.norm_weight, 1, a.width, a.epsilon, a.normalised_out, a.q8,
+                          stream);
 }
 
 hipError_t launch_lmhead_argmax(const HeadArgs &a, hipStream_t stream)
