@@ -48,7 +48,9 @@ constexpr int kChunkBlocks = 8;       // blocks a wave's weight loads cover at o
 constexpr int kRowsMaxRange = 128;    // blocks of the activation rows a workgroup stages
 constexpr int kRowsManyTiles = 1024;  // products this wide give each wave whole rows
 constexpr int kRowsPrefetch = 2;      // weight chunks in flight a wave
-constexpr int kMergeBatch = 8;        // split partials a merge requests at once
+constexpr int kMergeBatch = 8;
+constexpr int kRowsBestSlots = 32;   // a row's greedy-pick slots (atomicMax targets)
+constexpr int kRowsBestStride = 16;  // 128 bytes between slots        // split partials a merge requests at once
 constexpr int kRowsStreamGroups = 512; // workgroups of a streamed product (two a compute unit)
 constexpr int kRowsStreamAhead = 4;    // weight chunks in flight a wave of a streamed product
 
@@ -119,6 +121,7 @@ struct RowsArgs {
     int *tickets;     // one a workgroup column
     uint8_t *geglu8;  // non-null: outputs are gate | up rows; GeGLU's Q8 rows land here
     int split_major;  // grid (splits, columns) instead of (columns, splits)
+    unsigned long long *best; // streamed only, non-null: each row's greedy pick (see below)
 };
 
 __device__ inline void store_agent_d(double *p, double v)
@@ -591,6 +594,9 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_stream_kernel(RowsArgs a
     __builtin_amdgcn_sched_barrier(0);
     stage_write<nb>(0, nb, staged, sX, sSx, t);
     __syncthreads();
+    // with a.best: the largest (logit key, complemented column) of each of
+    // this lane's accumulator rows 4 grp + r over the workgroup's tiles
+    unsigned long long runBest[4] = {0ull, 0ull, 0ull, 0ull};
     int slot = 1;
 #pragma nounroll
     while (g < groups) {
@@ -628,8 +634,33 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_stream_kernel(RowsArgs a
                     a.y[(int64_t) m * a.y_stride + on] = (float) acc[r];
             }
         }
+        if (a.best) { // uniform
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                unsigned long long key = on < a.outputs ? candidate_key((float) acc[r], (uint32_t) on) : 0ull;
+                key = max_lanes<8>(key); // the tile's 16 columns (lanes of one row of 16)
+                runBest[r] = key > runBest[r] ? key : runBest[r];
+            }
+        }
         g = next;
         slot ^= 1;
+    }
+    if (a.best) { // the workgroup's best of each row into one of the row's slots
+        __shared__ unsigned long long sRowBest[kRowsWaves][kBatchRows];
+        if (col == 0)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                sRowBest[wave][4 * grp + r] = runBest[r];
+        __syncthreads();
+        if (t < a.rows) {
+            unsigned long long c = sRowBest[0][t];
+#pragma unroll
+            for (int w = 1; w < kRowsWaves; ++w)
+                c = sRowBest[w][t] > c ? sRowBest[w][t] : c;
+            if (c != 0)
+                atomicMax(a.best + ((int64_t) t * kRowsBestSlots + blockIdx.x % kRowsBestSlots)
+                                       * kRowsBestStride, c);
+        }
     }
     if (t == 0
         && __hip_atomic_fetch_add(counters + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
@@ -1025,6 +1056,29 @@ __global__ __launch_bounds__(64) void attention_merge_rows_kernel(RowsAttentionA
                                                                       + o / kBlock] = bits;
 }
 
+// Row r's greedy pick from its slots (the largest key: the largest logit,
+// the lowest column among equal ones, as Sampler.cpp:60-76), stored in
+// chosen[r] and in the row's slot after its position, which advances; the
+// slots are cleared for the next step.  A wave a row.
+__global__ __launch_bounds__(64) void batch_pick_advance_kernel(unsigned long long *best,
+                                                                uint32_t *chosen, uint32_t *slots,
+                                                                int64_t slot_stride, int *positions)
+{
+    const int r = blockIdx.x, lane = threadIdx.x;
+    unsigned long long *mine = best + ((int64_t) r * kRowsBestSlots + lane) * kRowsBestStride;
+    unsigned long long c = lane < kRowsBestSlots ? *mine : 0ull;
+    if (lane < kRowsBestSlots)
+        *mine = 0ull;
+    c = max_lanes<32>(c);
+    if (lane == 0) {
+        const uint32_t token = c == 0 ? 0u : 0xFFFFFFFFu - (uint32_t) (c & 0xFFFFFFFFull);
+        const int p = positions[r];
+        chosen[r] = token;
+        slots[r * slot_stride + p + 1] = token;
+        positions[r] = p + 1;
+    }
+}
+
 __global__ void batch_advance_kernel(const uint32_t *__restrict__ chosen, uint32_t *slots,
                                      int64_t slot_stride, int *positions, int rows)
 {
@@ -1083,7 +1137,7 @@ hipError_t launch_tile_weights(const uint8_t *w8, int inner, int outputs, uint8_
 hipError_t launch_q8_rows(const uint8_t *x8, int x_rows, int rows, const uint8_t *w8, int inner,
                           int outputs, float *y, int y_stride, int residual, double *partials,
                           size_t partial_bytes, int *tickets, hipStream_t stream,
-                          const uint8_t *w8_tiled)
+                          const uint8_t *w8_tiled, unsigned long long *best)
 {
     if (w8_tiled && !rows_tiled_supported(inner, outputs))
         return hipErrorInvalidValue;
@@ -1094,9 +1148,41 @@ hipError_t launch_q8_rows(const uint8_t *x8, int x_rows, int rows, const uint8_t
     if (plan.splits > 1
         && (!partials || !tickets || partial_bytes < rows_workspace_bytes(inner, outputs)))
         return hipErrorInvalidValue;
-    const RowsArgs a{x8, x_rows, rows, w8, w8_tiled, inner, outputs, plan.per, y, y_stride,
-                     residual, partials, tickets, nullptr};
+    RowsArgs a{x8, x_rows, rows, w8, w8_tiled, inner, outputs, plan.per, y, y_stride,
+               residual, partials, tickets, nullptr};
+    a.best = best;
     return launch_rows(a, plan, stream);
+}
+
+bool rows_pick_supported(const uint8_t *w8, const uint8_t *w8_tiled, int inner, int outputs)
+{
+    if (inner <= 0 || inner % kBlock != 0 || outputs <= 0)
+        return false;
+    const RowsPlan plan = rows_plan(inner, outputs);
+    const int nb = inner / kBlock, nc = plan.per / kChunkBlocks;
+    const uintptr_t wScales = reinterpret_cast<uintptr_t>(w8) + (uintptr_t) outputs * inner;
+    const bool whole = plan.per % kChunkBlocks == 0 && nb % plan.per == 0 && wScales % 16 == 0
+                       && (nc == 1 || nc == 2 || nc == 4 || nc == 8 || nc == 16);
+    (void) w8_tiled;
+    const int groups = (rows_ticket_count(outputs) + kRowsWaves - 1) / kRowsWaves;
+    return plan.wpt == 1 && plan.splits == 1 && whole && plan.per == nb && (nc == 4 || nc == 8)
+           && groups > kRowsStreamGroups;
+}
+
+size_t rows_pick_bytes()
+{
+    return (size_t) kBatchRows * kRowsBestSlots * kRowsBestStride * sizeof(unsigned long long);
+}
+
+hipError_t launch_batch_pick_advance(unsigned long long *best, uint32_t *chosen, uint32_t *slots,
+                                     int64_t slot_stride, int *positions, int rows,
+                                     hipStream_t stream)
+{
+    if (!best || rows <= 0 || rows > kBatchRows || slot_stride <= 0)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(batch_pick_advance_kernel, dim3(rows), dim3(64), 0, stream, best, chosen,
+                       slots, slot_stride, positions);
+    return hipGetLastError();
 }
 
 bool rows_geglu_supported(int inner, int intermediate)
@@ -1142,6 +1228,8 @@ hipError_t launch_rows_as(const RowsArgs &a, const RowsPlan &plan, int nc, bool 
     const int groups = (rows_ticket_count(outputs) + kRowsWaves - 1) / kRowsWaves;
     const bool streamed = plan.wpt == 1 && plan.splits == 1 && whole && !a.geglu8 && plan.per == nb
                           && (nc == 4 || nc == 8) && groups > kRowsStreamGroups;
+    if (a.best && !streamed) // the pick rides on the streamed product only
+        return hipErrorInvalidValue;
     if (streamed) {
         if (!a.tickets)
             return hipErrorInvalidValue;

@@ -129,7 +129,18 @@ int rows_ticket_count(int outputs);
 hipError_t launch_q8_rows(const uint8_t *x8, int x_rows, int rows, const uint8_t *w8, int inner,
                           int outputs, float *y, int y_stride, int residual, double *partials,
                           size_t partial_bytes, int *tickets, hipStream_t stream,
-                          const uint8_t *w8_tiled = nullptr);
+                          const uint8_t *w8_tiled = nullptr, unsigned long long *best = nullptr);
+// The greedy pick fused into a streamed product (rows_pick_supported: the
+// lm_head's shape): with best (rows_pick_bytes, zero between steps), every
+// workgroup folds its tiles' (logit key, complemented column) maxima of each
+// row into one of the row's slots; launch_batch_pick_advance then takes each
+// row's largest (the lowest column among equal logits), stores it in chosen
+// and in the row's next slot, advances the position and clears the slots.
+bool rows_pick_supported(const uint8_t *w8, const uint8_t *w8_tiled, int inner, int outputs);
+size_t rows_pick_bytes();
+hipError_t launch_batch_pick_advance(unsigned long long *best, uint32_t *chosen, uint32_t *slots,
+                                     int64_t slot_stride, int *positions, int rows,
+                                     hipStream_t stream);
 
 // The fragment-ordered copy of an [outputs, inner] Int8Blocks weight that
 // the lockstep products stream about a third faster than the row-major

@@ -2359,6 +2359,7 @@ struct gq8_batch {
     uint32_t *chosen = nullptr;
     double *attnO = nullptr, *attnMl = nullptr;
     float *rowAngles = nullptr; // each row's RoPE cosines and sines for the step
+    unsigned long long *pick = nullptr; // the lm_head's greedy-pick slots, zero between steps
     double *partials = nullptr;
     size_t partialBytes = 0;
     int *tickets = nullptr;
@@ -2426,11 +2427,11 @@ struct SequenceLoan {
 };
 
 int batch_product(gq8_batch *b, int inner, int outputs, const uint8_t *w, const uint8_t *wTiled,
-                  float *y, int yStride, int residual)
+                  float *y, int yStride, int residual, unsigned long long *pick = nullptr)
 {
     GQ8_LAUNCH(gq8::launch_q8_rows(b->x8, b->sequences, b->sequences, w, inner, outputs, y, yStride,
                                    residual, b->partials, b->partialBytes, b->tickets, b->d->stream,
-                                   wTiled));
+                                   wTiled, pick));
     return GQ8_OK;
 }
 
@@ -2523,9 +2524,16 @@ int encode_batch_step(gq8_batch *b)
     }
     GQ8_STAGE(kStageNorm, gq8::launch_rmsnorm(b->hidden, d->finalNorm, S, W, s.rms_epsilon, nullptr,
                                               b->x8, st));
-    GQ8_BATCH_STAGE(kStageLogits, batch_product(b, W, s.vocab, d->embedding,
-                                                b->tiled ? b->tiledHead : nullptr, b->logits,
-                                                s.vocab, 0));
+    // the greedy pick rides on the streamed lm_head where it streams
+    const uint8_t *headTiled = b->tiled ? b->tiledHead : nullptr;
+    const bool pick = gq8::rows_pick_supported(d->embedding, headTiled, W, s.vocab);
+    GQ8_BATCH_STAGE(kStageLogits, batch_product(b, W, s.vocab, d->embedding, headTiled, b->logits,
+                                                s.vocab, 0, pick ? b->pick : nullptr));
+    if (pick) {
+        GQ8_STAGE(kStageArgmax, gq8::launch_batch_pick_advance(b->pick, b->chosen, b->slots,
+                                                               b->slotStride, b->positions, S, st));
+        return GQ8_OK;
+    }
     GQ8_STAGE(kStageArgmax, gq8::launch_argmax(b->logits, nullptr, S, s.vocab, b->chosen, nullptr, 0,
                                                b->argmaxWorkspace, b->argmaxWorkspaceBytes, st));
     GQ8_LAUNCH(gq8::launch_batch_advance(b->chosen, b->slots, b->slotStride, b->positions, S, st));
@@ -2621,6 +2629,9 @@ extern "C" int gq8_batch_create(gq8_decoder *d, int sequences, gq8_batch **out)
     GQ8_BATCH_ALLOC(b->x8b, gq8::q8_bytes(S, F));
     GQ8_BATCH_ALLOC(b->chosen, S * sizeof(uint32_t));
     GQ8_BATCH_ALLOC(b->rowAngles, (size_t) S * s.head_dim * sizeof(float));
+    GQ8_BATCH_ALLOC(b->pick, gq8::rows_pick_bytes());
+    if (hipMemset(b->pick, 0, gq8::rows_pick_bytes()) != hipSuccess)
+        return cleanup(fail(GQ8_ERR_DEVICE, "batch pick slots: initialisation failed"));
     GQ8_BATCH_ALLOC(b->attnO, gq8::rows_attention_workspace_doubles(S, s.heads, s.head_dim)
                                   * sizeof(double));
     b->attnMl = b->attnO + (size_t) S * gq8::kRowsMaxSplits * d->qWidth;
