@@ -8,8 +8,9 @@ Int8Blocks quantizes a row's 32-element blocks on their own, so the two rows
 hold the same bytes and every step gives u and w the same logit.  Feeding u
 instead of w embeds the same row, so the expected run is the untouched run
 with every w replaced by u; the oracle (whose argmax keeps the first maximum)
-must agree.  u is taken in the same wave's eight rows as w, or in another
-workgroup (another of the 64 argmax slots), and the run goes through every
+must agree.  u is taken in the same wave's eight rows as w, or in the
+previous workgroup's 64 rows (another of the 64 argmax slots), and the run
+goes through every
 decode path that chooses ids: the fused kernels (plain and graph replay),
 the dataflow and persistent one-launch steps, and a one-sequence lockstep
 batch."""
@@ -28,12 +29,12 @@ LAYERS, POSITIONS, STEPS = 2, 96, 12
 def tied_pair(winners, used, placement):
     """(step, w, u): the first step whose winner w has an unused lower row u in
     the same eight-row wave group (placement "wave") or in the previous
-    32-row workgroup (placement "slot")."""
+    64-row workgroup (placement "slot")."""
     for step, w in enumerate(winners):
         if placement == "wave":
             candidates = range(w & ~7, w)
         else:
-            candidates = [w - 32] if w >= 32 else []
+            candidates = [w - 64] if w >= 64 else []
         for u in candidates:
             if u not in used:
                 return step, int(w), int(u)
