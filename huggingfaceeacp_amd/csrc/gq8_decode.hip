@@ -303,9 +303,10 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a)
 // keys [k0, k0 + n) of one split and the G heads of one group (G = 1 when a
 // head is at least a 32-element block wide, else the heads of one block).
 // Lane l owns channels [C l, C l + C) of a head, so the query lives in
-// registers and no LDS staging is needed.  Keys go in rounds of 64, wave w
-// taking keys w, w + 8, ..., w + 56 of a round:
-//   scores   the round's keys and values are loaded at once; the eight keys'
+// registers and no LDS staging is needed.  Keys go in rounds of 8 B (B = 4
+// or 8 keys a wave, by the launch's key-count range), wave w taking keys w,
+// w + 8, ..., w + 8 (B - 1) of a round:
+//   scores   the round's keys and values are loaded at once; the B keys'
 //            per-lane partial dots (C channels, every head of the group) are
 //            summed across the wave together (reduce_rows);
 //   softmax  wave g takes head g: the split's maximum, exp(s - max) and sum;
@@ -322,9 +323,10 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a)
 // whole group's partials.  The merge (MultiQueryAttention.h:43-49: every
 // split rescaled to the row maximum in split order, the sums divided by the
 // total) rounds to fp32 and quantizes the block.  The splits of a launch
-// wait on each other, so its workgroups must be resident together: one a
-// compute unit at most, at the launch sizes used.  Scores, weights and sums
-// are double throughout.
+// wait on each other, so its workgroups must be resident together: the
+// kernel is held to four waves a SIMD (at most 128 VGPRs), two 512-thread
+// workgroups a compute unit, and the largest launch is 64 splits x 8 heads =
+// 512 workgroups.  Scores, weights and sums are double throughout.
 constexpr int kAttnThreads = 512;
 constexpr int kAttnWaves = kAttnThreads / 64;
 constexpr int kScoreBatch = 8;                          // keys a wave takes a round
