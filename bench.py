@@ -100,8 +100,6 @@ def linear_ops(shape) -> int:
 # ---- the headline: config 2 decode ---------------------------------------------------
 def headline_decode(args, G, torch, decoder, shape, use_graph):
     prompt = G.prompt_ids(0xC0FFEE + 2, shape.vocab, args.prompt)
-    decoder.set_flow(args.flow)
-    decoder.set_persistent(args.persistent)
     # warmup: its own sequence (graph instantiation, first launches)
     decoder.generate(prompt, args.warmup + 1, eos=-1, use_graph=use_graph)
     # timed: prefill + first token untimed, then exactly K decode steps
@@ -124,8 +122,6 @@ def headline_decode(args, G, torch, decoder, shape, use_graph):
     # the stage breakdown: every launch group of K more steps bracketed by HIP
     # events on the decoder's stream (the event packets add about a
     # microsecond to each bracket)
-    decoder.set_flow(False)
-    decoder.set_persistent(False)
     decoder.generate(prompt, 1, eos=-1, use_graph=False)
     decoder.set_timing(True)
     decoder.decode(args.steps, use_graph=False)
@@ -326,10 +322,6 @@ def main() -> int:
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the prefill, long-context and lockstep configurations")
     ap.add_argument("--no-graph", action="store_true", help="launch steps without hipGraph replay")
-    ap.add_argument("--flow", action="store_true",
-                    help="decode steps as one dataflow launch a token")
-    ap.add_argument("--persistent", action="store_true",
-                    help="decode steps as one persistent launch a token (one workgroup a compute unit)")
     ap.add_argument("--mode", choices=("all", "decode", "prefill", "long", "batch"), default="all",
                     help="all: the headline decode and the other configurations; the others run "
                          "one configuration alone (for profiles)")
@@ -403,8 +395,7 @@ def main() -> int:
                                f"{args.prompt}-token prompt, {args.steps} timed decode steps, "
                                "fp16 KV cache, batch 1",
                    "layers": args.layers, "prompt_tokens": args.prompt,
-                   "decode_steps": args.steps, "graph": use_graph, "flow": args.flow,
-                   "persistent": args.persistent},
+                   "decode_steps": args.steps, "graph": use_graph},
         "step_hbm": {"bytes_per_token": int(head["step_bytes"]),
                      "achieved_gbs": round(head["step_gbs"], 1),
                      "frac": round(head["step_gbs"] / HBM_PEAK_GBS, 4)},

@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIBRARY = os.path.join(HERE, "libgemma_q8.so")
 
-SOURCES = ["gq8_kernels.hip", "gq8_decode.hip", "gq8_persist.hip", "gq8_gemm.hip",
+SOURCES = ["gq8_kernels.hip", "gq8_decode.hip", "gq8_gemm.hip",
            "gq8_batch.hip", "gq8_prefill_attention.hip", "gq8_checkpoint.hip", "gq8_sample.hip",
            "gq8_tokenizer.cpp", "gq8_gemma.cpp",
            "gq8_runtime.hip"]

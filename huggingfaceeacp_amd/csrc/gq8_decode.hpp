@@ -51,27 +51,37 @@ struct AttentionArgs {
     uint8_t *q8;              // Q8 row for o_proj
     int grid_splits;          // the launch's key splits (attention_grid_splits of the step's
                               // key-count range)
-    int round_keys;           // keys a round of the launch (attention_round_keys: 32 or 64)
-    int spec_keys;            // keys of a split loaded before the position is known
-                              // (attention_spec_keys of the same range)
+    int rounds;               // 32-key rounds a split takes at most (attention_rounds)
+    int spec_keys;            // rounds * 32: the keys of a split loaded before the position
+                              // is known
 };
 
 // The one-token attention launch for steps of `keyCount` keys, by key-count
 // range (attention_graph_range: at most 512, 1024, 2048, 4096 keys, and
-// beyond): its key splits (16, 32, 64, 64, 64), the keys of its rounds (32
-// while at most 2048 keys, then 64: 4 or 8 keys a wave), and the keys a split
-// is expected to cover, whose rows its workgroups load before the position
-// arrives (one round; two past 4096 keys).  A split of another size loads its
-// rows again once the position is known.  Splits past the step's keys exit
-// after their speculative loads, so a launch sized to the range keeps those
-// loads few.  A captured step replays within the range it was captured for;
-// attention_key_range is the largest key count of that range.
+// beyond): its key splits (16, 32, 64, 64, 64) and the 32-key rounds a split
+// takes at most (1, 1, 1, 2, 4), whose rows its workgroups load before the
+// position arrives.  A captured step replays within the range it was
+// captured for; attention_key_range is the largest key count of that range.
 constexpr int kAttentionRanges = 5;
 int attention_graph_range(int keyCount);
 int attention_grid_splits(int keyCount);
-int attention_round_keys(int keyCount);
-int attention_spec_keys(int keyCount);
+int attention_rounds(int keyCount);
 int attention_key_range(int keyCount, int maxPositions);
+// Query heads a workgroup of the split attention (2 of a KV head's, or 1).
+int attention_group_heads(int heads, int kv_heads);
+// Workgroups of the split attention's launch for steps of keyCount keys.
+int attention_grid(int heads, int kv_heads, int keyCount);
+// Whether the split attention takes the shape (head width 64, 128 or 256, a
+// window of at most 64 splits of 128 keys).
+bool split_attention_supported(int heads, int kv_heads, int head_dim, int max_positions);
+// Whether every launch the window reaches fits the workgroups that can be
+// resident at once, by range: the launch's workgroups wait on each other.
+bool split_attention_fits(int heads, int kv_heads, int head_dim, int max_positions,
+                          const int (&resident)[kAttentionRanges]);
+// The resident workgroups of each range's kernel on `device` (occupancy of
+// the instance times the compute units); false if unknown.
+bool split_attention_resident(int device, int heads, int kv_heads, int head_dim, int max_positions,
+                              int (&resident)[kAttentionRanges]);
 
 struct GateUpArgs {
     const float *hidden;
@@ -101,121 +111,10 @@ struct HeadArgs {
     int advance;              // nonzero: *position += 1 after the argmax
 };
 
-// ---- the dataflow decode step: one launch a token --------------------------------
-// Every piece of work of a one-token step (the q|k|v rows, the attention
-// splits, the o, gate|up and down rows of every layer, the final norm, the
-// lm_head rows and the id) is one workgroup, in dependency order; a workgroup
-// issues its weight loads, then waits (a bounded spin) until the phase it
-// reads from has finished, computes and publishes its outputs with
-// agent-scope (cross-L2 coherent) stores before counting itself done.
-constexpr int kFlowThreads = 512;
-constexpr int kFlowCounters = 2;       // the lm_head items, the idle attention splits
-// A counter is a tree of 128-byte lines: a top line, kFlowFlagLines completion
-// flags (waiters spread their polling over them) and kFlowSubLines
-// sub-counters of at most kFlowFanIn arrivals each.
-constexpr int kFlowLineInts = 32;
-constexpr int kFlowFanIn = 16;
-constexpr int kFlowFlagLines = 16;
-constexpr int kFlowSubLines = 1024;
-constexpr int kFlowCounterLines = 1 + kFlowFlagLines + kFlowSubLines;
-constexpr int64_t kFlowCounterInts = (int64_t) kFlowCounters * kFlowCounterLines * kFlowLineInts;
-constexpr int kFlowMaxLayers = 127;    // residual-row versions 0 .. 2 layers fit a tag's 8 bits
-
-struct FlowArgs {
-    int layers, width, heads, kv_heads, head_dim, intermediate, vocab, max_positions;
-    float epsilon, embed_scale, attn_scale;
-    const uint8_t *embedding;                 // Int8Blocks [vocab, width], also the lm_head
-    // layer l of a kind at base + l * stride (bytes for the Int8Blocks
-    // tensors, floats for the norms): addresses the compiler knows are global
-    const uint8_t *qkv, *out, *gate_up, *down; // fused q|k|v, o, fused gate|up, down
-    int64_t qkv_stride, out_stride, gate_up_stride, down_stride;
-    const float *input_norm, *post_norm;
-    int64_t norm_stride;
-    const float *final_norm;
-    uint16_t *key_cache, *value_cache;        // [layers][max_positions][kv_heads * head_dim]
-    const float *cosines, *sines;
-    uint32_t *sequence;
-    int *position;
-    uint32_t *epoch;                          // the launch's tag epoch (never 0)
-    // rows handed between items, one tagged word (value | tag << 32) an element
-    uint64_t *hidden_ll;                      // the residual row [width]
-    uint64_t *q_ll;                           // the rotated q row [heads * head_dim]
-    uint64_t *k_ll, *v_ll;                    // this step's fp16 K and V rows, two halves a word
-    uint64_t *part_ll;                        // attention partial outputs [kDecodeSplits][q width] doubles
-    uint64_t *part_ml_ll;                     // their max and sum [kDecodeSplits][heads] double pairs
-    uint64_t *attn_ll, *act_ll, *head_ll;     // Q8 rows: bytes (four a word), then one scale word a block
-    float *logits;
-    unsigned long long *best;                 // argmax slots
-    int *counters;                            // kFlowCounters counter trees
-    int *error;                               // nonzero after a wait gave up
-    int attn_splits;                          // attention split items a head group
-    int sample;                               // nonzero: the id goes to sequence[position + 1]
-    int qkv_items, attn_items, o_items, gate_up_items, down_items, head_items;
-};
-
-// ---- the persistent decode step: one launch a token, one workgroup a CU -------
-// Every workgroup runs the whole step's program on its share of every phase
-// (gq8_persist.hip).  Four prefetch waves stream its share of the gate|up,
-// down and lm_head weights into an LDS ring; four compute waves run the
-// dependent chain and hand rows on in tagged words.
-constexpr int kPersistThreads = 512;
-constexpr int kPersistMaxSplits = 64;   // attention key splits of a row
-constexpr int kPersistMaxLayers = 127;  // residual-row versions 0 .. 2 layers fit a tag's 8 bits
-
-struct PersistArgs {
-    int layers, width, heads, kv_heads, head_dim, intermediate, vocab, max_positions;
-    float epsilon, embed_scale, attn_scale;
-    const uint8_t *embedding;                 // Int8Blocks [vocab, width], also the lm_head
-    // layer l of a kind at base + l * stride (bytes for the Int8Blocks
-    // tensors, floats for the norms)
-    const uint8_t *qkv, *out, *gate_up, *down;
-    int64_t qkv_stride, out_stride, gate_up_stride, down_stride;
-    const float *input_norm, *post_norm;
-    int64_t norm_stride;
-    const float *final_norm;
-    uint16_t *key_cache, *value_cache;        // [layers][max_positions][kv_heads * head_dim]
-    const float *cosines, *sines;
-    uint32_t *sequence;
-    int *position;
-    uint32_t *epoch;                          // the launch's tag epoch (never 0)
-    // tagged rows (value | tag << 32, one element a word)
-    uint64_t *hid_ll;                         // the residual row [width]
-    uint64_t *q_ll;                           // the rotated q row [heads * head_dim]
-    uint64_t *kv_ll;                          // this step's k then v row, fp16 bits [2 kv width]
-    uint64_t *part_ll;                        // attention partials [split][head][head_dim], doubles as
-                                              // (low, high) word pairs
-    uint64_t *ml_ll;                          // their (max, sum) [split][head], four words
-    uint64_t *attn_ll, *act_ll;               // Q8 rows: bytes four a word, then a scale word a block
-    uint64_t *cand_ll;                        // a workgroup's argmax candidate, two words
-    float *logits;                            // fp32 [vocab]
-    int *error;                               // nonzero after a wait gave up
-    int sample;                               // nonzero: the id goes to sequence[position + 1]
-    int grid;                                 // workgroups: one a compute unit, all resident
-};
-
-// Tagged words the persistent step needs, by row (the runtime carves them
-// from one allocation).
-struct PersistWords {
-    int64_t hid, q, kv, part, ml, attn, act, cand;
-};
-PersistWords persist_words(int width, int heads, int kv_heads, int head_dim, int intermediate, int grid);
-// Whether the shape fits the persistent step's partition on `grid` workgroups.
-bool persist_decode_supported(int layers, int width, int heads, int kv_heads, int head_dim,
-                              int intermediate, int vocab, int max_positions, int grid);
-// The workgroups of the persistent step on `device` (its compute units, when
-// one workgroup fits a unit), or 0.
-int persist_grid(int device);
-hipError_t launch_persist_step(const PersistArgs &a, hipStream_t stream);
-
-bool flow_decode_supported(int layers, int width, int heads, int kv_heads, int head_dim, int intermediate,
-                           int vocab, int max_positions);
-int flow_attention_splits(int max_positions);
-// Fills the item counts of a; returns the grid size.
-int flow_items(FlowArgs &a);
-hipError_t launch_flow_step(const FlowArgs &a, hipStream_t stream);
-
-bool fused_decode_supported(int width, int heads, int kv_heads, int head_dim, int intermediate,
-                            int max_positions);
+// Whether the fused one-token kernels (q|k|v + RoPE, gate|up + GeGLU, the
+// head) take the shape; the attention between them is the split attention
+// where it fits, else the partial/merge pair of gq8_kernels.hip.
+bool fused_decode_supported(int width, int heads, int kv_heads, int head_dim, int intermediate);
 
 hipError_t launch_qkv_rope(const QkvArgs &a, hipStream_t stream);
 hipError_t launch_attention(const AttentionArgs &a, hipStream_t stream);

@@ -221,6 +221,28 @@ __device__ inline v4u ld_agent_16(const void *base, uint32_t offset, uint32_t by
     return __builtin_amdgcn_raw_buffer_load_b128(r, (int) offset, 0, kCoherentLoad);
 }
 
+// 16 bytes to byte `offset` of a `bytes`-long buffer with an agent-coherent
+// (sc1) buffer store; a store past the end is dropped.
+__device__ inline void st_agent_16(void *base, uint32_t offset, uint32_t bytes, v4u value)
+{
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, (int) bytes, 0x00020000);
+    __builtin_amdgcn_raw_buffer_store_b128(value, r, (int) offset, 0, kCoherentLoad);
+}
+
+// A double and the tag as two tagged words in one 16-byte store: (low half,
+// tag, high half, tag).  A reader checks both tags, so a store seen half
+// done is read again.
+__device__ inline v4u tagged_double(double d, uint32_t tag)
+{
+    const uint64_t bits = (uint64_t) __double_as_longlong(d);
+    v4u v;
+    v.x = (uint32_t) bits;
+    v.y = tag;
+    v.z = (uint32_t) (bits >> 32);
+    v.w = tag;
+    return v;
+}
+
 // ---- tagged words -----------------------------------------------------------
 // tag = epoch << 8 | version.  Versions of the residual row: 0 the embedding
 // row, 2 l + 1 after layer l's o projection, 2 l + 2 after its down

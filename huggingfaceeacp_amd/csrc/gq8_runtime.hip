@@ -582,27 +582,7 @@ struct gq8_decoder {
     // the fused one-token path
     bool useFused = true;
     bool fusedSupported = false;
-    // the dataflow step (one launch a token)
-    bool useFlow = false;
-    bool flowSupported = false;
-    uint64_t *flowTagged = nullptr;  // the tagged rows, one allocation
-    size_t flowTaggedBytes = 0;
-    uint64_t *flowHidden = nullptr, *flowQ = nullptr, *flowK = nullptr, *flowV = nullptr;
-    uint64_t *flowPart = nullptr, *flowPartMl = nullptr, *flowAttn = nullptr, *flowAct = nullptr,
-             *flowHead = nullptr;
-    uint32_t *flowEpoch = nullptr;
-    int *flowCounters = nullptr;
-    int *flowError = nullptr;
-    // the persistent step (one launch a token, one workgroup a compute unit)
-    bool usePersist = false;
-    bool persistSupported = false;
-    int persistGrid = 0;
-    uint64_t *persistTagged = nullptr; // the tagged rows, one allocation
-    size_t persistTaggedBytes = 0;
-    uint64_t *persistHid = nullptr, *persistQ = nullptr, *persistKv = nullptr, *persistPart = nullptr,
-             *persistMl = nullptr, *persistAttn = nullptr, *persistAct = nullptr, *persistCand = nullptr;
-    uint32_t *persistEpoch = nullptr;
-    int *persistError = nullptr;
+    bool splitAttention = false; // its attention is the split kernel (else partial/merge)
     // the decode attention's tagged split partials, their tag epoch and the
     // error word its bounded waits set
     uint64_t *attnPart = nullptr, *attnMl = nullptr;
@@ -905,72 +885,18 @@ extern "C" int gq8_decoder_create(const gq8_shape *shape, gq8_decoder **out)
     GQ8_ALLOC(d->debugNormalised, R * W * sizeof(float));
     GQ8_ALLOC(d->debugAttended, R * d->qWidth * sizeof(float));
     GQ8_ALLOC(d->debugActivated, R * (int64_t) s.intermediate * sizeof(float));
-    d->flowSupported = gq8::flow_decode_supported(s.layers, s.width, s.heads, s.kv_heads, s.head_dim,
-                                                  s.intermediate, s.vocab, s.max_positions);
-    {
-        // tagged rows (one 8-byte word an element), carved from one allocation
-        const auto q8Words = [](int64_t n) { return n / 4 + n / gq8::kBlock + 2; };
-        const int64_t sizes[] = {
-            W, d->qWidth, d->kvWidth / 2 + 2, d->kvWidth / 2 + 2,
-            (int64_t) gq8::kDecodeSplits * d->qWidth * 2, (int64_t) gq8::kDecodeSplits * s.heads * 4,
-            q8Words(d->qWidth), q8Words(s.intermediate), q8Words(W)};
-        int64_t total = 0;
-        for (int64_t n : sizes)
-            total += (n + 1) / 2 * 2; // 16-byte aligned parts
-        d->flowTaggedBytes = (size_t) total * sizeof(uint64_t);
-        GQ8_ALLOC(d->flowTagged, d->flowTaggedBytes);
-        uint64_t *part = d->flowTagged;
-        uint64_t **dst[] = {&d->flowHidden, &d->flowQ, &d->flowK, &d->flowV, &d->flowPart,
-                            &d->flowPartMl, &d->flowAttn, &d->flowAct, &d->flowHead};
-        for (int k = 0; k < 9; ++k) {
-            *dst[k] = part;
-            part += (sizes[k] + 1) / 2 * 2;
-        }
-        GQ8_ALLOC(d->flowEpoch, 64 * sizeof(uint32_t));
-        GQ8_ALLOC(d->flowCounters, (size_t) gq8::kFlowCounterInts * sizeof(int));
-        GQ8_ALLOC(d->flowError, 64 * sizeof(int));
-        const uint32_t one = 1;
-        if (hipMemset(d->flowTagged, 0, d->flowTaggedBytes) != hipSuccess
-            || hipMemcpy(d->flowEpoch, &one, sizeof(one), hipMemcpyHostToDevice) != hipSuccess
-            || hipMemset(d->flowCounters, 0, (size_t) gq8::kFlowCounterInts * sizeof(int)) != hipSuccess
-            || hipMemset(d->flowError, 0, sizeof(int)) != hipSuccess)
-            return cleanup(fail(GQ8_ERR_DEVICE, "flow state: initialisation failed"));
-    }
-    {
-        int device = 0;
-        if (hipGetDevice(&device) != hipSuccess)
-            return cleanup(fail(GQ8_ERR_DEVICE, "persistent step: no current device"));
-        d->persistGrid = gq8::persist_grid(device);
-        d->persistSupported = d->persistGrid > 0
-                              && gq8::persist_decode_supported(s.layers, s.width, s.heads, s.kv_heads,
-                                                               s.head_dim, s.intermediate, s.vocab,
-                                                               s.max_positions, d->persistGrid);
-        const int grid = d->persistGrid > 0 ? d->persistGrid : 1;
-        const gq8::PersistWords pw = gq8::persist_words(s.width, s.heads, s.kv_heads, s.head_dim,
-                                                        s.intermediate, grid);
-        const int64_t sizes[] = {pw.hid, pw.q, pw.kv, pw.part, pw.ml, pw.attn, pw.act, pw.cand};
-        int64_t total = 0;
-        for (int64_t n : sizes)
-            total += (n + 1) / 2 * 2; // 16-byte aligned parts
-        d->persistTaggedBytes = (size_t) total * sizeof(uint64_t);
-        GQ8_ALLOC(d->persistTagged, d->persistTaggedBytes);
-        uint64_t *part = d->persistTagged;
-        uint64_t **dst[] = {&d->persistHid, &d->persistQ, &d->persistKv, &d->persistPart,
-                            &d->persistMl, &d->persistAttn, &d->persistAct, &d->persistCand};
-        for (int k = 0; k < 8; ++k) {
-            *dst[k] = part;
-            part += (sizes[k] + 1) / 2 * 2;
-        }
-        GQ8_ALLOC(d->persistEpoch, 64 * sizeof(uint32_t));
-        GQ8_ALLOC(d->persistError, 64 * sizeof(int));
-        const uint32_t one = 1;
-        if (hipMemset(d->persistTagged, 0, d->persistTaggedBytes) != hipSuccess
-            || hipMemcpy(d->persistEpoch, &one, sizeof(one), hipMemcpyHostToDevice) != hipSuccess
-            || hipMemset(d->persistError, 0, sizeof(int)) != hipSuccess)
-            return cleanup(fail(GQ8_ERR_DEVICE, "persistent step state: initialisation failed"));
-    }
     d->fusedSupported = gq8::fused_decode_supported(s.width, s.heads, s.kv_heads, s.head_dim,
-                                                    s.intermediate, s.max_positions);
+                                                    s.intermediate);
+    {
+        // the split attention's workgroups wait on each other: it is taken
+        // only where every launch the window reaches fits on the device at once
+        int device = 0, resident[gq8::kAttentionRanges] = {};
+        d->splitAttention = d->fusedSupported && hipGetDevice(&device) == hipSuccess
+                            && gq8::split_attention_resident(device, s.heads, s.kv_heads, s.head_dim,
+                                                             s.max_positions, resident)
+                            && gq8::split_attention_fits(s.heads, s.kv_heads, s.head_dim,
+                                                         s.max_positions, resident);
+    }
     {
         const size_t partBytes = (size_t) gq8::kDecodeSplits * d->qWidth * 2 * sizeof(uint64_t);
         const size_t mlBytes = (size_t) gq8::kDecodeSplits * s.heads * 4 * sizeof(uint64_t);
@@ -1348,25 +1274,47 @@ extern "C" int gq8_decoder_position(const gq8_decoder *d)
     return d ? d->hostPosition : -1;
 }
 
-extern "C" int gq8_decoder_set_flow(gq8_decoder *d, int enabled)
+extern "C" int gq8_decoder_device_position(gq8_decoder *d)
 {
     if (!d)
-        return fail(GQ8_ERR_ARGUMENT, "null decoder");
-    if (enabled && !d->flowSupported)
-        return fail(GQ8_ERR_SHAPE, "decoder_set_flow: the shape has no dataflow step");
-    d->useFlow = enabled != 0;
-    drop_graphs(d); // a captured step follows the path it was captured with
-    return GQ8_OK;
+        return fail(GQ8_ERR_ARGUMENT, "decoder_device_position: null decoder");
+    int position = 0;
+    GQ8_HIP(hipStreamSynchronize(d->stream));
+    GQ8_HIP(hipMemcpy(&position, d->position, sizeof(int), hipMemcpyDeviceToHost));
+    return position;
 }
 
-extern "C" int gq8_decoder_set_persistent(gq8_decoder *d, int enabled)
+extern "C" int gq8_decoder_attention_path(const gq8_decoder *d)
 {
     if (!d)
-        return fail(GQ8_ERR_ARGUMENT, "null decoder");
-    if (enabled && !d->persistSupported)
-        return fail(GQ8_ERR_SHAPE, "decoder_set_persistent: the shape or device has no persistent step");
-    d->usePersist = enabled != 0;
-    drop_graphs(d); // a captured step follows the path it was captured with
+        return fail(GQ8_ERR_ARGUMENT, "decoder_attention_path: null decoder");
+    return d->fusedSupported ? (d->splitAttention ? 1 : 0) : -1;
+}
+
+extern "C" int gq8_decode_attention_fits(const gq8_shape *shape, int resident_workgroups)
+{
+    if (int s = gq8_shape_validate(shape))
+        return s;
+    const gq8_shape &s = *shape;
+    int resident[gq8::kAttentionRanges];
+    for (int &r : resident)
+        r = resident_workgroups;
+    return gq8::fused_decode_supported(s.width, s.heads, s.kv_heads, s.head_dim, s.intermediate)
+                   && gq8::split_attention_fits(s.heads, s.kv_heads, s.head_dim, s.max_positions,
+                                                resident)
+               ? 1
+               : 0;
+}
+
+extern "C" int gq8_decoder_inject_wait_failure(gq8_decoder *d)
+{
+    if (!d)
+        return fail(GQ8_ERR_ARGUMENT, "decoder_inject_wait_failure: null decoder");
+    if (!d->splitAttention)
+        return fail(GQ8_ERR_SHAPE, "decoder_inject_wait_failure: the attention is not the split kernel");
+    const int one = 1;
+    GQ8_HIP(hipStreamSynchronize(d->stream));
+    GQ8_HIP(hipMemcpy(d->attnError, &one, sizeof(int), hipMemcpyHostToDevice));
     return GQ8_OK;
 }
 
@@ -1486,159 +1434,14 @@ int encode_sample(gq8_decoder *d, const float *row, int offset)
 }
 
 
-// The one-token step as one dataflow launch (gq8_decode.hip).
-int encode_flow_token(gq8_decoder *d, float *logits, bool sample)
+// Reads and clears the split attention's error word.  A set word means a
+// bounded wait of a split merge gave up (or a launch was too small for its
+// keys), so the steps enqueued since the last check are invalid: the device
+// and host positions go back to `rollback`, the position before those steps,
+// and the caller can run them again (their cache rows are rewritten).
+int check_step_error(gq8_decoder *d, int rollback)
 {
-    const gq8_shape &s = d->shape;
-    gq8::FlowArgs a{};
-    a.layers = s.layers;
-    a.width = s.width;
-    a.heads = s.heads;
-    a.kv_heads = s.kv_heads;
-    a.head_dim = s.head_dim;
-    a.intermediate = s.intermediate;
-    a.vocab = s.vocab;
-    a.max_positions = s.max_positions;
-    a.epsilon = s.rms_epsilon;
-    a.embed_scale = s.embedding_scale;
-    a.attn_scale = 1.f / std::sqrt((float) s.head_dim);
-    a.embedding = d->embedding;
-    a.qkv = d->qkv[0];
-    a.qkv_stride = d->qkvStride;
-    a.out = d->out[0];
-    a.out_stride = d->outStride;
-    a.gate_up = d->gateUp[0];
-    a.gate_up_stride = d->gateUpStride;
-    a.down = d->down[0];
-    a.down_stride = d->downStride;
-    a.input_norm = d->inputNorm[0];
-    a.post_norm = d->postNorm[0];
-    a.norm_stride = d->normStride;
-    a.final_norm = d->finalNorm;
-    a.key_cache = d->keyCache;
-    a.value_cache = d->valueCache;
-    a.cosines = d->cosines;
-    a.sines = d->sines;
-    a.sequence = d->sequence;
-    a.position = d->position;
-    a.epoch = d->flowEpoch;
-    a.hidden_ll = d->flowHidden;
-    a.q_ll = d->flowQ;
-    a.k_ll = d->flowK;
-    a.v_ll = d->flowV;
-    a.part_ll = d->flowPart;
-    a.part_ml_ll = d->flowPartMl;
-    a.attn_ll = d->flowAttn;
-    a.act_ll = d->flowAct;
-    a.head_ll = d->flowHead;
-    a.logits = logits;
-    a.best = d->headBest;
-    a.counters = d->flowCounters;
-    a.error = d->flowError;
-    a.attn_splits = gq8::flow_attention_splits(s.max_positions);
-    a.sample = sample ? 1 : 0;
-    GQ8_STAGE(kStageLogits, gq8::launch_flow_step(a, d->stream));
-    return GQ8_OK;
-}
-
-// The one-token step as one persistent launch (gq8_persist.hip).
-int encode_persist_token(gq8_decoder *d, float *logits, bool sample)
-{
-    const gq8_shape &s = d->shape;
-    gq8::PersistArgs a{};
-    a.layers = s.layers;
-    a.width = s.width;
-    a.heads = s.heads;
-    a.kv_heads = s.kv_heads;
-    a.head_dim = s.head_dim;
-    a.intermediate = s.intermediate;
-    a.vocab = s.vocab;
-    a.max_positions = s.max_positions;
-    a.epsilon = s.rms_epsilon;
-    a.embed_scale = s.embedding_scale;
-    a.attn_scale = 1.f / std::sqrt((float) s.head_dim);
-    a.embedding = d->embedding;
-    a.qkv = d->qkv[0];
-    a.qkv_stride = d->qkvStride;
-    a.out = d->out[0];
-    a.out_stride = d->outStride;
-    a.gate_up = d->gateUp[0];
-    a.gate_up_stride = d->gateUpStride;
-    a.down = d->down[0];
-    a.down_stride = d->downStride;
-    a.input_norm = d->inputNorm[0];
-    a.post_norm = d->postNorm[0];
-    a.norm_stride = d->normStride;
-    a.final_norm = d->finalNorm;
-    a.key_cache = d->keyCache;
-    a.value_cache = d->valueCache;
-    a.cosines = d->cosines;
-    a.sines = d->sines;
-    a.sequence = d->sequence;
-    a.position = d->position;
-    a.epoch = d->persistEpoch;
-    a.hid_ll = d->persistHid;
-    a.q_ll = d->persistQ;
-    a.kv_ll = d->persistKv;
-    a.part_ll = d->persistPart;
-    a.ml_ll = d->persistMl;
-    a.attn_ll = d->persistAttn;
-    a.act_ll = d->persistAct;
-    a.cand_ll = d->persistCand;
-    a.logits = logits;
-    a.error = d->persistError;
-    a.sample = sample ? 1 : 0;
-    a.grid = d->persistGrid;
-    GQ8_STAGE(kStageLogits, gq8::launch_persist_step(a, d->stream));
-    return GQ8_OK;
-}
-
-// After a one-launch step gave up, the steps enqueued behind it gave up too
-// and none of them advanced the device position: the host's count of enqueued
-// steps is set back to the device's, so the next step writes its slot at the
-// position the device actually holds.
-int resync_position(gq8_decoder *d)
-{
-    int position = 0;
-    GQ8_HIP(hipMemcpy(&position, d->position, sizeof(int), hipMemcpyDeviceToHost));
-    if (position < 0 || position > d->shape.max_positions)
-        return fail(GQ8_ERR_DEVICE, "one-launch step: the device position is out of range");
-    d->hostPosition = position;
-    return GQ8_OK;
-}
-
-// Reads and clears the persistent step's error word, as check_flow_error does
-// for the dataflow step.
-int check_persist_error(gq8_decoder *d)
-{
-    if (!d->persistSupported)
-        return GQ8_OK;
-    int error = 0;
-    GQ8_HIP(hipStreamSynchronize(d->stream));
-    GQ8_HIP(hipMemcpy(&error, d->persistError, sizeof(int), hipMemcpyDeviceToHost));
-    if (error == 0)
-        return GQ8_OK;
-    uint32_t epoch = 0;
-    GQ8_HIP(hipMemcpy(&epoch, d->persistEpoch, sizeof(epoch), hipMemcpyDeviceToHost));
-    epoch = (epoch + 1) & 0xFFFFFFu;
-    if (epoch == 0)
-        epoch = 1;
-    GQ8_HIP(hipMemcpy(d->persistEpoch, &epoch, sizeof(epoch), hipMemcpyHostToDevice));
-    GQ8_HIP(hipMemset(d->persistTagged, 0, d->persistTaggedBytes));
-    GQ8_HIP(hipMemset(d->persistError, 0, sizeof(int)));
-    if (int s = resync_position(d))
-        return s;
-    return fail(GQ8_ERR_DEVICE, "persistent step: a wait gave up (the step's results are invalid)");
-}
-
-int check_flow_error(gq8_decoder *d);
-
-// The error word of whichever one-launch step is on.
-// Reads and clears the decode attention's error word: a set word means a
-// merge's wait gave up and that step's results are invalid.
-int check_attention_error(gq8_decoder *d)
-{
-    if (!d->fusedSupported)
+    if (!d->splitAttention)
         return GQ8_OK;
     int error = 0;
     GQ8_HIP(hipStreamSynchronize(d->stream));
@@ -1646,47 +1449,10 @@ int check_attention_error(gq8_decoder *d)
     if (error == 0)
         return GQ8_OK;
     GQ8_HIP(hipMemset(d->attnError, 0, sizeof(int)));
-    return fail(GQ8_ERR_DEVICE, "decode attention: a split merge's wait gave up (the step's "
-                                "results are invalid)");
-}
-
-int check_step_error(gq8_decoder *d)
-{
-    if (int s = check_attention_error(d))
-        return s;
-    if (d->usePersist)
-        if (int s = check_persist_error(d))
-            return s;
-    if (d->useFlow)
-        return check_flow_error(d);
-    return GQ8_OK;
-}
-
-// Reads and clears the dataflow step's error word.  A set word means a step
-// gave up waiting: the counters and tagged rows are cleared and the epoch
-// moves on, so that nothing the failed step put is taken as current.
-int check_flow_error(gq8_decoder *d)
-{
-    if (!d->flowSupported)
-        return GQ8_OK;
-    int error = 0;
-    GQ8_HIP(hipStreamSynchronize(d->stream));
-    GQ8_HIP(hipMemcpy(&error, d->flowError, sizeof(int), hipMemcpyDeviceToHost));
-    if (error == 0)
-        return GQ8_OK;
-    uint32_t epoch = 0;
-    GQ8_HIP(hipMemcpy(&epoch, d->flowEpoch, sizeof(epoch), hipMemcpyDeviceToHost));
-    epoch = (epoch + 1) & 0xFFFFFFu;
-    if (epoch == 0)
-        epoch = 1;
-    GQ8_HIP(hipMemcpy(d->flowEpoch, &epoch, sizeof(epoch), hipMemcpyHostToDevice));
-    GQ8_HIP(hipMemset(d->flowTagged, 0, d->flowTaggedBytes));
-    GQ8_HIP(hipMemset(d->flowCounters, 0, (size_t) gq8::kFlowCounterInts * sizeof(int)));
-    GQ8_HIP(hipMemset(d->flowError, 0, sizeof(int)));
-    GQ8_HIP(hipMemset(d->headBest, 0, gq8::kHeadSlots * gq8::kHeadSlotStride * sizeof(unsigned long long)));
-    if (int s = resync_position(d))
-        return s;
-    return fail(GQ8_ERR_DEVICE, "dataflow step: a wait gave up (the step's results are invalid)");
+    GQ8_HIP(hipMemcpy(d->position, &rollback, sizeof(int), hipMemcpyHostToDevice));
+    d->hostPosition = rollback;
+    return fail(GQ8_ERR_DEVICE, "decode attention: a split merge's wait gave up (the steps since "
+                                "position " + std::to_string(rollback) + " are undone)");
 }
 
 // The one-token step through the fused kernels (gq8_decode.hip): five
@@ -1751,9 +1517,17 @@ int encode_fused_token(gq8_decoder *d, float *logits, bool sample)
         at.q8 = d->x8;
         const int rangeKeys = d->capturing ? d->captureKeys : d->hostPosition + 1;
         at.grid_splits = gq8::attention_grid_splits(rangeKeys);
-        at.round_keys = gq8::attention_round_keys(rangeKeys);
-        at.spec_keys = gq8::attention_spec_keys(rangeKeys);
-        GQ8_STAGE(kStageAttention, gq8::launch_attention(at, st));
+        at.rounds = gq8::attention_rounds(rangeKeys);
+        at.spec_keys = at.rounds * 32;
+        if (d->splitAttention) {
+            GQ8_STAGE(kStageAttention, gq8::launch_attention(at, st));
+        } else {
+            GQ8_STAGE(kStageAttention, gq8::launch_mqa(d->qkvRows, d->qWidth, q.key_cache, q.value_cache,
+                                                       s.heads, s.kv_heads, s.head_dim, 1, d->position, 0,
+                                                       s.max_positions, at.scale, at.out, d->x8,
+                                                       d->attentionWorkspace,
+                                                       d->attentionWorkspaceBytes, st));
+        }
         if (dbg && copy_last_q8_row(d, d->x8, 1, d->qWidth, debugQ8(1, l)))
             return GQ8_ERR_DEVICE;
 
@@ -1821,14 +1595,6 @@ int encode_step(gq8_decoder *d, int rows, float *logits, int logitsRows, bool sa
     hipStream_t st = d->stream;
     const float attentionScale = 1.f / std::sqrt((float) s.head_dim);
     const bool dbg = d->debug;
-    // the one-launch steps choose by argmax inside the launch
-    const bool oneLaunch = !(sample && sampled(d));
-    if (oneLaunch && rows == 1 && logits && logitsRows == 1 && d->usePersist && d->persistSupported
-        && !(d->debug && !d->capturing))
-        return encode_persist_token(d, logits, sample);
-    if (oneLaunch && rows == 1 && logits && logitsRows == 1 && d->useFlow && d->flowSupported
-        && !(d->debug && !d->capturing))
-        return encode_flow_token(d, logits, sample);
     if (rows == 1 && logits && logitsRows == 1 && d->useFused && d->fusedSupported)
         return encode_fused_token(d, logits, sample);
 
@@ -1946,7 +1712,7 @@ extern "C" int gq8_decoder_step(gq8_decoder *d, const uint32_t *tokens, int n, f
     if (int s = encode_step(d, n, logits, logits ? logits_rows : 0, false))
         return s;
     GQ8_HIP(hipStreamSynchronize(d->stream));
-    if (int s = check_step_error(d))
+    if (int s = check_step_error(d, d->hostPosition))
         return s;
     d->hostPosition += n;
     return GQ8_OK;
@@ -2130,7 +1896,7 @@ extern "C" int gq8_generate_streaming(gq8_decoder *d, const int32_t *prompt, int
             ++steps;
         }
         GQ8_HIP(hipStreamSynchronize(d->stream));
-        if (int st = check_step_error(d))
+        if (int st = check_step_error(d, 0)) // the run is void
             return st;
         std::vector<uint32_t> ids(limit);
         GQ8_HIP(hipMemcpy(ids.data(), d->sequence + prompt_length, limit * sizeof(uint32_t),
@@ -2192,7 +1958,7 @@ extern "C" int gq8_generate_streaming(gq8_decoder *d, const int32_t *prompt, int
             }
         }
         finish(GQ8_OK);
-        if (int st = check_step_error(d))
+        if (int st = check_step_error(d, 0)) // the run is void
             return st;
     }
     local.decode_seconds = std::chrono::duration<double>(Clock::now() - decodeStart).count();
@@ -2209,6 +1975,7 @@ extern "C" int gq8_decoder_decode(gq8_decoder *d, int steps, int use_graph)
         return fail(GQ8_ERR_ARGUMENT, "decoder_decode: bad arguments");
     if (d->hostPosition + steps > d->shape.max_positions)
         return fail(GQ8_ERR_WINDOW, "decoder_decode: the steps would pass the window");
+    const int start = d->hostPosition;
     if (use_graph)
         if (int st = ensure_graphs(d, d->hostPosition + 1, d->hostPosition + steps))
             return st;
@@ -2216,7 +1983,7 @@ extern "C" int gq8_decoder_decode(gq8_decoder *d, int steps, int use_graph)
         if (int st = decode_one(d, use_graph != 0))
             return st;
     GQ8_HIP(hipStreamSynchronize(d->stream));
-    return check_step_error(d);
+    return check_step_error(d, start);
 }
 
 extern "C" int gq8_decoder_tokens(gq8_decoder *d, int first, int count, int32_t *host_out)
@@ -2725,7 +2492,7 @@ extern "C" int gq8_batch_prefill(gq8_batch *b, int sequence, const int32_t *prom
             d->hostPosition += rows;
         }
         GQ8_HIP(hipStreamSynchronize(d->stream));
-        if (int st = check_step_error(d))
+        if (int st = check_step_error(d, 0)) // the run is void
             return st;
     }
     b->hostPositions[sequence] = prompt_length;

@@ -144,12 +144,14 @@ def library() -> ctypes.CDLL:
         "gq8_decoder_read_tensor": (i32, [P, i32, P, sz]),
         "gq8_decoder_begin_sequence": (i32, [P]),
         "gq8_decoder_position": (i32, [P]),
+        "gq8_decoder_device_position": (i32, [P]),
         "gq8_decoder_step": (i32, [P, P, i32, P, i32]),
         "gq8_decoder_hidden": (i32, [P, P, i32]),
         "gq8_decoder_set_debug": (i32, [P, i32]),
         "gq8_decoder_set_fused": (i32, [P, i32]),
-        "gq8_decoder_set_flow": (i32, [P, i32]),
-        "gq8_decoder_set_persistent": (i32, [P, i32]),
+        "gq8_decoder_attention_path": (i32, [P]),
+        "gq8_decode_attention_fits": (i32, [P, i32]),
+        "gq8_decoder_inject_wait_failure": (i32, [P]),
         "gq8_decoder_debug": (i32, [P, i32, i32, P, P]),
         "gq8_generate": (i32, [P, P, i32, i32, i32, i32, P, ctypes.POINTER(_RunStats)]),
         "gq8_decoder_decode": (i32, [P, i32, i32]),
@@ -410,6 +412,15 @@ class DecoderShape:
         c = self.as_c()
         return bool(library().gq8_tensor_is_norm(ctypes.byref(c), index))
 
+    def attention_fits(self, resident_workgroups: int) -> bool:
+        """Whether one-token steps of this shape take the split attention kernel
+        when `resident_workgroups` of its workgroups fit on the device at once."""
+        c = self.as_c()
+        status = int(library().gq8_decode_attention_fits(ctypes.byref(c), resident_workgroups))
+        if status < 0:
+            check(status)
+        return status == 1
+
 
 @dataclass
 class RunStats:
@@ -471,6 +482,14 @@ class Decoder:
     def position(self) -> int:
         return int(library().gq8_decoder_position(self.handle))
 
+    @property
+    def device_position(self) -> int:
+        """The position word on the device, once the decoder's stream is idle."""
+        value = int(library().gq8_decoder_device_position(self.handle))
+        if value < 0:
+            check(value)
+        return value
+
     def step(self, tokens_ptr: int, n: int, logits_ptr: int | None, logits_rows: int | None = None):
         rows = n if logits_rows is None else logits_rows
         check(library().gq8_decoder_step(self.handle, tokens_ptr, n, logits_ptr or None,
@@ -481,14 +500,15 @@ class Decoder:
         check(library().gq8_decoder_hidden(self.handle, _host(out), rows))
         return out
 
-    def set_flow(self, enabled: bool) -> None:
-        """Run one-token steps as one dataflow launch (off by default)."""
-        check(library().gq8_decoder_set_flow(self.handle, int(enabled)))
+    @property
+    def attention_path(self) -> int:
+        """1: the split attention kernel; 0: the partial/merge pair; -1: no fused step."""
+        return int(library().gq8_decoder_attention_path(self.handle))
 
-    def set_persistent(self, enabled: bool) -> None:
-        """Run one-token steps as one persistent launch (one workgroup a compute
-        unit); raises when the shape or device has no persistent step."""
-        check(library().gq8_decoder_set_persistent(self.handle, int(enabled)))
+    def inject_wait_failure(self) -> None:
+        """Sets the split attention's error word: the next step's bounded waits
+        give up, and its check reports ERR_DEVICE and undoes the step."""
+        check(library().gq8_decoder_inject_wait_failure(self.handle))
 
     def set_sampling(self, options: SamplingOptions) -> None:
         """Gemma::setSampling: how generate and decode choose each id (on the device)."""

@@ -233,6 +233,11 @@ int gq8_decoder_read_tensor(gq8_decoder *decoder, int index, void *host_out, siz
 /* Decoder::beginSequence / position (Decoder.h:93-104). */
 int gq8_decoder_begin_sequence(gq8_decoder *decoder);
 int gq8_decoder_position(const gq8_decoder *decoder);
+/* The position word on the device, after the decoder's stream has finished
+ * (steps advance it on the device; it equals gq8_decoder_position after every
+ * synchronous call).  Decoder::position (Decoder.h:101-104) read where the
+ * steps keep it. */
+int gq8_decoder_device_position(gq8_decoder *decoder);
 
 /* Decoder::step (Decoder.cpp:644-706): n token ids (device, uint32) at
  * positions position .. position + n - 1; logits (device, fp32) receives
@@ -244,32 +249,36 @@ int gq8_decoder_step(gq8_decoder *decoder, const uint32_t *tokens, int n, float 
  * when the shape allows; 0 selects the unfused kernels (both compute the same
  * arithmetic).  On by default. */
 int gq8_decoder_set_fused(gq8_decoder *decoder, int enabled);
-/* One-token steps as one dataflow launch (every phase of every layer a set of
- * workgroups that wait on the phase they read from) when the shape allows;
- * the same arithmetic as the fused kernels.  Off by default.  A step that
- * gave up waiting is reported by the next synchronous call as GQ8_ERR_DEVICE.
- * No reference counterpart: it replaces the per-kernel dispatch of
- * Decoder::step (Decoder.cpp:644-706) for one-token steps. */
-int gq8_decoder_set_flow(gq8_decoder *decoder, int enabled);
-/* One-token steps as one persistent launch when the shape and the device
- * allow: one workgroup a compute unit runs the whole step, prefetch waves
- * streaming the gate|up, down and lm_head weights into LDS while compute waves
- * run the dependent chain.  The products have the fused kernels' arithmetic
- * and summation order; attention splits its keys its own way (double sums
- * throughout).  A step that gave up waiting is reported by the next
- * synchronous call as GQ8_ERR_DEVICE.  No reference counterpart: it replaces
- * the per-kernel dispatch of Decoder::step (Decoder.cpp:644-706) for
- * one-token steps.  GQ8_ERR_SHAPE when the shape or device has none. */
-int gq8_decoder_set_persistent(gq8_decoder *decoder, int enabled);
+/* The attention of the fused one-token step: 1 when it is the split kernel
+ * (one workgroup a key split and group of query heads loads the split's K/V
+ * rows once for all the heads, and the workgroups of a launch merge each
+ * other's partials), 0 when it is the two-launch partial/merge pair (no
+ * waits between workgroups), -1 when the shape has no fused step.  Replaces
+ * MultiQueryDecodeAttention's dispatch (MultiQueryAttention.cpp:66-77). */
+int gq8_decoder_attention_path(const gq8_decoder *decoder);
+/* The choice behind gq8_decoder_attention_path for a shape, on the host:
+ * 1 when the shape takes the split kernel and each of its launches (up to 64
+ * key splits x KV heads x query-head groups workgroups, by key-count range)
+ * fits `resident_workgroups` workgroups resident at once, else 0; negative
+ * for a shape gq8_shape_validate refuses.  The decoder passes the kernel's
+ * occupancy times the device's compute units.  No reference counterpart:
+ * the reference's attention workgroups never wait on each other
+ * (MultiQueryAttention.cpp:66-77). */
+int gq8_decode_attention_fits(const gq8_shape *shape, int resident_workgroups);
+/* Sets the split attention's error word, as a bounded wait does when it gives
+ * up: the next step's waits give up at once, every kernel still exits, and
+ * the check after it reports GQ8_ERR_DEVICE and puts the device and host
+ * positions back to where that step began.  For tests of that path;
+ * GQ8_ERR_SHAPE when the decoder's attention is not the split kernel.  No
+ * reference counterpart (the reference has no waits between workgroups). */
+int gq8_decoder_inject_wait_failure(gq8_decoder *decoder);
 /* Gemma::setSampling (Generation/Gemma.cpp:198-202): how gq8_generate and
  * gq8_decoder_decode choose each id.  Temperature 0 (the default) is the
  * argmax; above it, each id is drawn on the device (gq8_sample_row's rule)
  * and written to its sequence slot, so no logits come back to the host
  * (Gemma::generateBySampling, Gemma.cpp:546-595, reads them back).  Every
  * sequence draws from the seed afresh (Gemma.cpp:549), one draw a sampled
- * token.  The one-launch steps (set_flow, set_persistent) choose by argmax
- * only and stand aside while a temperature is set.  GQ8_ERR_ARGUMENT as
- * SamplingError. */
+ * token.  GQ8_ERR_ARGUMENT as SamplingError. */
 int gq8_decoder_set_sampling(gq8_decoder *decoder, const gq8_sampling *options);
 /* Decoder::hiddenStates (Decoder.h:119-121): the last step's rows after the
  * final norm, [rows, width] fp32, copied to the host. */

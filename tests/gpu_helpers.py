@@ -48,3 +48,31 @@ def worst_error(actual: np.ndarray, expected: np.ndarray) -> float:
     actual = np.asarray(actual, dtype=np.float64)
     expected = np.asarray(expected, dtype=np.float64)
     return float(np.max(np.abs(actual - expected) / (1.0 + np.abs(expected))))
+
+
+def small_heads_shape(max_positions=256, max_step_rows=16):
+    """Width 128, two heads of 64 over one KV head, FFN 256, vocabulary 1000:
+    the smallest head width the split attention kernel takes."""
+    from huggingfaceeacp_amd import gemma_q8 as G
+    return G.DecoderShape(128, 2, 1, 64, 2, 256, 1000, max_positions, max_step_rows)
+
+
+def seeded_weights(shape):
+    """N(0, sigma) as Tests/Decoder/Common.h:164-237 draws them, with wider
+    spreads: embedding 0.1, norms 1.0, projections 4/sqrt(fan in).  With the
+    reference's (0.2, 0.1, 1/sqrt(fan in)) the tied embedding dominates and
+    every greedy id repeats the prompt's last one; with these 36 of 40 ids
+    differ and the smallest top-2 margin is about 1.5e-2."""
+    from huggingfaceeacp_amd import gemma_q8 as G
+    tensors = []
+    for i in range(shape.tensor_count()):
+        if i == 0:
+            sigma = 0.1
+        elif shape.tensor_is_norm(i):
+            sigma = 1.0
+        else:
+            role = (i - 1) % G.PER_LAYER
+            fan_in = {G.T_O: shape.query_width, G.T_DOWN: shape.intermediate}.get(role, shape.width)
+            sigma = 4.0 / np.sqrt(fan_in)
+        tensors.append(O.normal_fill(0x9100 + i, sigma, shape.tensor_elements(i)))
+    return tensors

@@ -10,10 +10,13 @@ instead of w embeds the same row, so the expected run is the untouched run
 with every w replaced by u; the oracle (whose argmax keeps the first maximum)
 must agree.  u is taken in the same wave's eight rows as w, or in the
 previous workgroup's 64 rows (another of the 64 argmax slots), and the run
-goes through every
-decode path that chooses ids: the fused kernels (plain and graph replay),
-the dataflow and persistent one-launch steps, and a one-sequence lockstep
-batch."""
+goes through every decode path that chooses ids: the fused kernels (plain
+and graph replay), the unfused kernels, and a one-sequence lockstep batch.
+
++0 and -0 compare equal, so between them too the lower id must win: a model
+whose embedding rows are all zero bytes has logits of exactly zero, signed by
+the row's fp16 scale bits (0x8000 is -0), and every path must pick id 0
+whichever sign the low rows carry."""
 import numpy as np
 import pytest
 
@@ -70,18 +73,52 @@ def test_lm_head_ties_go_to_the_lower_id(torch_cuda, placement):
     decoder = G.Decoder(shape)
     for i, values in enumerate(tensors):
         decoder.load_tensor(i, values)
-    for label, graph, flow, persistent in (("plain", False, False, False),
-                                           ("graph", True, False, False),
-                                           ("flow", True, True, False),
-                                           ("persistent", True, False, True)):
-        decoder.set_flow(flow)
-        decoder.set_persistent(persistent)
+    for label, graph, fused in (("plain", False, True), ("graph", True, True),
+                                ("unfused", False, False)):
+        decoder.set_fused(fused)
         tokens, _ = decoder.generate(prompt, STEPS, eos=-1, use_graph=graph)
         assert list(tokens) == expected, label
-    decoder.set_flow(False)
-    decoder.set_persistent(False)
+    decoder.set_fused(True)
     batch = G.Batch(decoder, 1)
     batch.prefill(0, prompt)
     batch.decode(STEPS - 1, use_graph=True)
     assert list(batch.tokens(0, prompt.size, STEPS)) == expected, "lockstep"
     batch.close()
+
+
+@pytest.mark.parametrize("low_sign", [0x8000, 0x0000])
+def test_signed_zero_logits_tie_to_the_lower_id(torch_cuda, low_sign):
+    """Rows 0..9 of the tied embedding carry scale bits `low_sign`, the rest
+    the other sign, every byte zero: the hidden rows stay zero, every logit is
+    +0 or -0, and the first maximum is id 0 (a key that ordered -0 below +0
+    would pick id 10 for one of the two placements)."""
+    from gpu_helpers import seeded_weights, small_heads_shape
+    shape = small_heads_shape(max_positions=32)
+    tensors = seeded_weights(shape)
+    decoder = G.Decoder(shape)
+    for i, values in enumerate(tensors):
+        if i != 0:
+            decoder.load_tensor(i, values)
+    rows, width = shape.vocab, shape.width
+    scales = np.full((rows, width // 32), low_sign ^ 0x8000, np.uint16)
+    scales[:10] = low_sign
+    stored = np.concatenate([np.zeros(rows * width, np.uint8), scales.ravel().view(np.uint8)])
+    decoder.load_tensor_q8(0, stored)
+    prompt = np.array([3, 500, 999], np.int32)
+    expected = [0] * 6
+    for label, graph, fused in (("plain", False, True), ("graph", True, True),
+                                ("unfused", False, False)):
+        decoder.set_fused(fused)
+        tokens, _ = decoder.generate(prompt, 6, eos=-1, use_graph=graph)
+        assert list(tokens) == expected, (label, list(tokens))
+    decoder.set_fused(True)
+    batch = G.Batch(decoder, 1)
+    batch.prefill(0, prompt)
+    batch.decode(5, use_graph=True)
+    assert list(batch.tokens(0, prompt.size, 6)) == expected, "lockstep"
+    batch.close()
+    # the oracle's first maximum agrees on a row of signed zeros
+    row = np.zeros(rows, np.float32)
+    row[:10] = -0.0 if low_sign else 0.0
+    row[10:] = 0.0 if low_sign else -0.0
+    assert O.argmax(row) == 0

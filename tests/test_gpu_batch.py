@@ -16,7 +16,7 @@ import oracle as O
 from gpu_helpers import exact_fraction, worst_error
 from huggingfaceeacp_amd import gemma_q8 as G
 from test_gpu_decoder import build_pair, gemma_pair, gpu_step
-from test_gpu_persist import persist_shape, seeded_weights
+from gpu_helpers import seeded_weights, small_heads_shape
 
 pytestmark = pytest.mark.gpu
 
@@ -61,7 +61,7 @@ def test_batch_small_shape(torch_cuda):
     """Five sequences of a small shape (every product on the unaligned
     path): the oracle's ids, plain steps and graph replay."""
     torch = torch_cuda
-    shape = persist_shape(max_positions=64)
+    shape = small_heads_shape(max_positions=64)
     decoder, model = build_pair(shape, seeded_weights(shape))
     rng = np.random.default_rng(7)
     prompts = [rng.integers(0, shape.vocab, n).astype(np.int32) for n in (3, 7, 1, 12, 20)]
@@ -121,7 +121,7 @@ def test_batch_follows_weight_uploads(torch_cuda):
 def test_batch_refusals(torch_cuda):
     """Batch size, unprefilled sequences and the window are refused before
     anything runs; a refused decode leaves every sequence where it was."""
-    shape = persist_shape(max_positions=32)
+    shape = small_heads_shape(max_positions=32)
     decoder, _ = build_pair(shape, seeded_weights(shape))
     for bad in (0, 17):
         with pytest.raises(G.Gq8Error) as e:

@@ -18,7 +18,7 @@ import pytest
 import oracle as O
 from huggingfaceeacp_amd import gemma_q8 as G
 from test_gpu_decoder import to_oracle_shape
-from test_gpu_persist import persist_shape, seeded_weights
+from gpu_helpers import seeded_weights, small_heads_shape
 
 pytestmark = pytest.mark.gpu
 
@@ -87,7 +87,7 @@ def small_checkpoint(tmp_path, shape, tensors):
 
 
 def test_checkpoint_loads_like_the_values(torch_cuda, tmp_path):
-    shape = persist_shape(max_positions=64)
+    shape = small_heads_shape(max_positions=64)
     config = {"model_type": "gemma", "vocab_size": shape.vocab, "hidden_size": shape.width,
               "intermediate_size": shape.intermediate, "num_hidden_layers": shape.layers,
               "num_attention_heads": shape.heads, "num_key_value_heads": shape.kv_heads,
@@ -121,7 +121,7 @@ def test_checkpoint_loads_like_the_values(torch_cuda, tmp_path):
 
 
 def test_checkpoint_refusals(torch_cuda, tmp_path):
-    shape = persist_shape(max_positions=64)
+    shape = small_heads_shape(max_positions=64)
     tensors = seeded_weights(shape)
     paths, _ = small_checkpoint(tmp_path, shape, tensors)
     files = [G.SafeTensors.open(p) for p in paths]

@@ -120,9 +120,9 @@ def stepwise(torch, decoder, f, digest_steps=()):
 
 
 def test_config2_headline_512_plus_256(torch_cuda):
-    """18 layers, the 512-token prompt, 256 greedy tokens: the plain loop, the
-    graph replay and the persistent step all give the oracle's ids; every
-    step's top-8 logits and the last prompt row's Q8 bytes are the oracle's."""
+    """18 layers, the 512-token prompt, 256 greedy tokens: the plain loop and
+    the graph replay give the oracle's ids; every step's top-8 logits and the
+    last prompt row's Q8 bytes are the oracle's."""
     torch = torch_cuda
     f = fixture("gemma_ctx512.npz")
     print("config 2: 18 layers, 512 + 256", flush=True)
@@ -130,13 +130,11 @@ def test_config2_headline_512_plus_256(torch_cuda):
     decoder = G.Decoder(shape)
     decoder.fill_synthetic(16)
     expected = list(f["ids"])
-    for label, graph, persistent in (("graph", True, False), ("plain", False, False),
-                                     ("persistent", True, True)):
-        decoder.set_persistent(persistent)
+    assert decoder.attention_path == 1
+    for label, graph in (("graph", True), ("plain", False)):
         tokens, stats = decoder.generate(f["prompt"], 256, eos=-1, use_graph=graph)
         print(f"  {label}: {len(tokens)} ids, decode {stats.decode_seconds * 1e3:.1f} ms", flush=True)
         assert list(tokens) == expected, label
-    decoder.set_persistent(False)
     exact = stepwise(torch, decoder, f)
     print(f"  top-8 logits bit-identical in {exact:.4f} of places; smallest top-2 margin "
           f"{f['margins'].min():.3g}; distinct ids {len(set(expected))}")
@@ -242,16 +240,12 @@ def test_varied_ids_18_layers(torch_cuda):
     shape, decoder = varied_decoder(18, 256)
     expected = list(f["ids"])
     assert len(set(expected)) > 40
-    for label, graph, persistent, flow in (("graph", True, False, False),
-                                           ("plain", False, False, False),
-                                           ("persistent", True, True, False),
-                                           ("flow", True, False, True)):
-        decoder.set_persistent(persistent)
-        decoder.set_flow(flow)
+    for label, graph, fused in (("graph", True, True), ("plain", False, True),
+                                ("unfused", False, False)):
+        decoder.set_fused(fused)
         tokens, _ = decoder.generate(f["prompt"], 48, eos=-1, use_graph=graph)
         assert list(tokens) == expected, label
-    decoder.set_persistent(False)
-    decoder.set_flow(False)
+    decoder.set_fused(True)
     exact = stepwise(torch, decoder, f, digest_steps=tuple(int(s) for s in f["digest_steps"]))
     print(f"  distinct ids {len(set(expected))}, smallest top-2 margin {f['margins'].min():.3g}, "
           f"top-8 logits bit-identical in {exact:.4f} of places")

@@ -280,58 +280,3 @@ def test_full_gemma_short_run(torch_cuda):
     count, ref, margins = model.generate(prompt, 4, eos=1)
     print(f"18-layer greedy: gpu {list(tokens)}, oracle {list(ref)}, margins {margins}")
     assert list(tokens) == list(ref)
-
-
-def flow_runs(torch, decoder, prompt, count):
-    """Greedy ids (graph and plain loop) and the last prompt token's logits as
-    a one-token step, with the dataflow step on and off."""
-    runs = {}
-    for flow in (True, False):
-        decoder.set_flow(flow)
-        plain, _ = decoder.generate(prompt, count, eos=-1, use_graph=False)
-        graph, _ = decoder.generate(prompt, count, eos=-1, use_graph=True)
-        decoder.begin_sequence()
-        capacity = decoder.shape.step_capacity()
-        for start in range(0, len(prompt) - 1, capacity):
-            gpu_step(torch, decoder, prompt[start:min(start + capacity, len(prompt) - 1)], 1)
-        logits = gpu_step(torch, decoder, prompt[-1:])[0]
-        runs[flow] = (list(plain), list(graph), logits)
-    decoder.set_flow(False)
-    return runs
-
-
-def test_flow_step_small_model(torch_cuda):
-    """The dataflow step (one launch a token) at the small quantizable config
-    (head width 16: two heads a workgroup; 15 of 16 attention splits idle):
-    the oracle's greedy ids, and the fused kernels' logits."""
-    torch = torch_cuda
-    shape = small_shape(max_step_rows=8)
-    decoder, model = build_pair(shape, small_weights(shape))
-    runs = flow_runs(torch, decoder, PROMPT, 8)
-    _, ref, _ = model.generate(np.array(PROMPT), 8, eos=-1)
-    for flow, (plain, graph, _) in runs.items():
-        assert plain == list(ref), (flow, plain, list(ref))
-        assert graph == list(ref), (flow, graph, list(ref))
-    assert worst_error(runs[True][2], runs[False][2]) <= 1e-6
-    print(f"small model flow/fused logits exact {exact_fraction(runs[True][2], runs[False][2]):.4f}")
-
-
-@pytest.mark.parametrize("prompt_length,max_positions", [(9, 64), (700, 1024)])
-def test_flow_step_two_layer_gemma(torch_cuda, prompt_length, max_positions):
-    """The dataflow step at Gemma-2B dims (2 layers): identical greedy ids to
-    the fused kernels and the oracle; logits equal to the fused kernels' (the
-    same arithmetic in the same order).  The long prompt spreads the keys over
-    several attention splits, which the merge folds."""
-    torch = torch_cuda
-    shape, decoder, model = gemma_pair(2, max_positions, max_step_rows=min(256, max_positions))
-    prompt = O.prompt_ids(0xC0FFEE + 3, shape.vocab, prompt_length)
-    runs = flow_runs(torch, decoder, prompt, 12)
-    assert runs[True][0] == runs[False][0] == runs[True][1] == runs[False][1]
-    if prompt_length < 64:
-        _, ref, _ = model.generate(prompt, 12, eos=-1)
-        assert runs[True][0] == list(ref)
-    err = worst_error(runs[True][2], runs[False][2])
-    exact = exact_fraction(runs[True][2], runs[False][2])
-    print(f"gemma flow/fused ({prompt_length} tokens): worst {err:.3g}, exact {exact:.4f}")
-    assert err <= 1e-6
-    assert exact >= 0.999

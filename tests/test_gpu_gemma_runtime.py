@@ -18,7 +18,7 @@ from huggingfaceeacp_amd import gemma_q8 as G
 from test_gemma_runtime import GOLDEN_TOKENIZER, config_for
 from test_gpu_checkpoint import small_checkpoint
 from test_gpu_decoder import to_oracle_shape
-from test_gpu_persist import persist_shape, seeded_weights
+from gpu_helpers import seeded_weights, small_heads_shape
 
 pytestmark = pytest.mark.gpu
 
@@ -51,7 +51,7 @@ def cut_at(ids, eos):
 
 
 def test_gemma_directory_generates_the_oracle_ids(torch_cuda, tmp_path):
-    shape = persist_shape(max_positions=WINDOW)
+    shape = small_heads_shape(max_positions=WINDOW)
     prompt = [2, 5, 41, 3, 17, 28, 9, 60]
     # the oracle's run without a stop picks the EOS: its sixth id, where the
     # five before it differ from it
@@ -110,7 +110,7 @@ def test_gemma_directory_generates_the_oracle_ids(torch_cuda, tmp_path):
 
 
 def test_gemma_directory_sampling_matches_the_decoder(torch_cuda, tmp_path):
-    shape = persist_shape(max_positions=WINDOW)
+    shape = small_heads_shape(max_positions=WINDOW)
     root = tmp_path / "model"
     widened = write_directory(root, shape, eos=-1)
     options = G.SamplingOptions(temperature=0.8, top_k=40, top_p=0.9, seed=1234)

@@ -5,15 +5,16 @@ The oracle's full prefill at this length is minutes of CPU time, so parity
 here rests on properties the window fixes and on independent GPU paths:
 - the run returns exactly max_positions - prompt = 128 ids (Gemma.cpp:395-400)
   and the window's last position is refused after the run's last step;
-- the plain loop, hipGraph replay and the one-launch persistent step give the
+- the plain loop and the hipGraph replay of the split attention, and the
+  plain loop of the partial/merge attention (the unfused kernels), give the
   same ids;
 - the logits of the window's last position agree between the one-token
   decode kernels (split-key attention over 8191 keys) and a multi-row step
   (prefill attention on fp64 MFMA and the int8 MFMA GEMM) that recomputes the
   last rows from the cache, to the double-sum order (1e-6 relative, >= 99 %
   bit-identical).
-The oracle pins the same kernels at shorter lengths (test_gpu_decoder.py,
-test_gpu_persist.py)."""
+The oracle pins the same kernels at every launch range of the split
+attention, 4111 keys included, in test_gpu_attention_ranges.py."""
 import numpy as np
 import pytest
 
@@ -33,15 +34,16 @@ def test_long_context_window(torch_cuda):
     prompt = O.prompt_ids(0xC0FFEE + 4, shape.vocab, PROMPT)
     print("long_context: 8064 + 128, 2 layers", flush=True)
     runs = {}
-    for label, persistent, graph in (("graph", False, True), ("plain", False, False),
-                                     ("persistent", True, True)):
-        decoder.set_persistent(persistent)
+    assert decoder.attention_path == 1
+    for label, fused, graph in (("graph", True, True), ("plain", True, False),
+                                ("unfused", False, False)):
+        decoder.set_fused(fused)
         tokens, stats = decoder.generate(prompt, 1000, eos=-1, use_graph=graph)
         runs[label] = list(tokens)
         print(f"  {label}: {len(tokens)} ids, decode {stats.decode_seconds * 1e3:.1f} ms", flush=True)
-    decoder.set_persistent(False)
+    decoder.set_fused(True)
     assert len(runs["graph"]) == WINDOW - PROMPT
-    assert runs["graph"] == runs["plain"] == runs["persistent"]
+    assert runs["graph"] == runs["plain"] == runs["unfused"]
 
     # the run's last step left the position at 8191: one more step fills the
     # window's extra slot, a second is refused

@@ -23,7 +23,7 @@ import pytest
 
 import oracle as O
 from huggingfaceeacp_amd import gemma_q8 as G
-from test_gpu_persist import persist_shape, seeded_weights
+from gpu_helpers import seeded_weights, small_heads_shape
 
 pytestmark = pytest.mark.gpu
 
@@ -169,7 +169,7 @@ OPTIONS = [S(0.8, seed=101), S(1.0, top_k=5, seed=102), S(0.7, top_p=0.9, seed=1
 @pytest.mark.parametrize("options", OPTIONS,
                          ids=["temperature", "top_k", "top_p", "both", "hot", "hot_top_k"])
 def test_sampled_generation_matches_the_host_loop(torch_cuda, options):
-    shape = persist_shape(max_positions=96)
+    shape = small_heads_shape(max_positions=96)
     decoder = loaded_decoder(shape)
     prompt = np.array([5, 41, 3, 17, 28, 9, 60], np.int32)
     limit = 40
@@ -196,25 +196,8 @@ def test_sampled_generation_matches_the_host_loop(torch_cuda, options):
     assert list(greedy) == host_loop(torch_cuda, decoder, prompt, limit, -1, S.greedy())
 
 
-def test_sampling_sets_the_one_launch_step_aside(torch_cuda):
-    shape = persist_shape(max_positions=96)
-    decoder = loaded_decoder(shape)
-    prompt = np.array([7, 8, 9], np.int32)
-    options = S(1.0, top_k=20, seed=77)
-    want = host_loop(torch_cuda, decoder, prompt, 24, -1, options)
-    decoder.set_sampling(options)
-    for switch in (decoder.set_persistent, decoder.set_flow):
-        try:
-            switch(True)
-        except G.Gq8Error:
-            continue
-        got, _ = decoder.generate(prompt, 24, eos=-1)
-        assert list(got) == want
-        switch(False)
-
-
 def test_each_run_reseeds(torch_cuda):
-    shape = persist_shape(max_positions=96)
+    shape = small_heads_shape(max_positions=96)
     decoder = loaded_decoder(shape)
     prompt = np.array([11, 12], np.int32)
     # a temperature this high spreads the draws over most of the vocabulary
