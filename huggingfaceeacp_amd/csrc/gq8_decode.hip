@@ -329,8 +329,7 @@ __global__ __launch_bounds__(kThreads) void qkv_rope_kernel(QkvArgs a)
 // Scores, weights and sums are double throughout.
 constexpr int kAttnThreads = 512;
 constexpr int kAttnWaves = kAttnThreads / 64;
-constexpr int kKeysPerWave = 4;                          // a wave's keys in a round
-constexpr int kRoundKeys = kAttnWaves * kKeysPerWave;    // 32
+constexpr int kRoundKeys = 32;                           // keys a round: four a wave
 constexpr int kMaxRounds = 4;
 constexpr int kMaxSplitKeys = kRoundKeys * kMaxRounds;   // 128: a window of 64 x 128 = 8192
 constexpr int kPollSplits = 8; // split partials a merging lane polls (a run of at most 16)
@@ -347,41 +346,92 @@ __device__ inline SplitPlan plan_splits(int keyCount, int gridSplits)
     return {(keyCount + perSplit - 1) / perSplit, perSplit};
 }
 
-// C consecutive halves of an fp16 row kept as loaded, (C + 1) / 2 words, and
-// half i of them.
-template <int C>
-__device__ inline void load_words(const uint16_t *p, uint32_t (&w)[(C + 1) / 2])
+// SC consecutive halves of an fp16 row as SC / 2 words (8-, 16- or 32-byte
+// loads), half i of them, and the same words stored to LDS.
+template <int SC>
+__device__ inline void load_row(const uint16_t *p, uint32_t (&w)[SC / 2])
 {
-    if constexpr (C == 4) {
+    static_assert(SC == 4 || SC == 8 || SC == 16, "4, 8 or 16 halves");
+    if constexpr (SC == 4) {
         const uint2 v = *reinterpret_cast<const uint2 *>(p);
         w[0] = v.x;
         w[1] = v.y;
-    } else if constexpr (C == 2) {
-        w[0] = *reinterpret_cast<const uint32_t *>(p);
     } else {
-        w[0] = *p;
+#pragma unroll
+        for (int k = 0; k < SC / 8; ++k) {
+            const uint4 v = reinterpret_cast<const uint4 *>(p)[k];
+            w[4 * k] = v.x;
+            w[4 * k + 1] = v.y;
+            w[4 * k + 2] = v.z;
+            w[4 * k + 3] = v.w;
+        }
     }
 }
 
-template <int C>
-__device__ inline double word_half(const uint32_t (&w)[(C + 1) / 2], int i)
+template <int SC>
+__device__ inline void store_row(uint16_t *p, const uint32_t (&w)[SC / 2])
 {
-    return (double) half_value((uint16_t) (w[i >> 1] >> (16 * (i & 1))));
-}
-
-template <int C>
-__device__ inline void store_words(uint16_t *p, const uint32_t (&w)[(C + 1) / 2])
-{
-    if constexpr (C == 4)
+    if constexpr (SC == 4) {
         *reinterpret_cast<uint2 *>(p) = make_uint2(w[0], w[1]);
-    else if constexpr (C == 2)
-        *reinterpret_cast<uint32_t *>(p) = w[0];
-    else
-        *p = (uint16_t) w[0];
+    } else {
+#pragma unroll
+        for (int k = 0; k < SC / 8; ++k)
+            reinterpret_cast<uint4 *>(p)[k] = make_uint4(w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]);
+    }
 }
 
-// C: channels a lane in the score layout (head width 64 C); G: query heads a
-// workgroup; R: rounds a split at most (the launch's key-count range).
+__device__ inline double half_word(uint32_t w, int i)
+{
+    return (double) half_value((uint16_t) (w >> (16 * i)));
+}
+
+// The sum over a value-layout channel's key partitions (lane bits from
+// log2(CPW) up), every lane ending with the same total.
+template <int CPW>
+__device__ inline double sum_partitions(double v)
+{
+    if constexpr (CPW < 64) {
+        v += xor_lane<CPW>(v);
+        return sum_partitions<CPW * 2>(v);
+    } else {
+        return v;
+    }
+}
+
+// The (key, head) row a lane holds after reduce_halving<G, 8, G> over a
+// key's 16 lanes (lane bits 3, 2, ... give the upper half of the rows), and
+// whether it is the lowest lane holding it.
+template <int U>
+__device__ inline int row_of_lane16(int lane)
+{
+    int row = 0, n = U, bit = 8;
+    while (n > 1) {
+        n /= 2;
+        if (lane & bit)
+            row += n;
+        bit >>= 1;
+    }
+    return row;
+}
+
+template <int U>
+__device__ inline bool stores_row16(int lane)
+{
+    int bits = 0, n = U, bit = 8;
+    while (n > 1) {
+        n /= 2;
+        bits |= bit;
+        bit >>= 1;
+    }
+    return (lane & 15 & ~bits) == 0;
+}
+
+// C: the head width is 64 C; G: query heads a workgroup; R: 32-key rounds a
+// split at most (the launch's key-count range).  Score layout: 16 lanes a
+// key, lane l the channels [SC (l % 16), SC (l % 16) + SC) of every head of
+// the group, wave w the keys 4 w .. 4 w + 3 of a round.  Value layout: lane
+// l of wave w the channel w CPW + l % CPW of every head of the group and the
+// keys of partition l / CPW (keys j = partition + KP t).
 template <int C, int G, int R>
 __global__ __launch_bounds__(kAttnThreads)
 void attention_kernel(AttentionArgs a)
@@ -389,16 +439,14 @@ void attention_kernel(AttentionArgs a)
     GQ8_ARGS_EARLY("s"(a.grid_splits), "s"(a.scale), "s"(a.part_ll), "s"(a.ml_ll), "s"(a.tag_epoch),
                    "s"(a.error), "s"(a.out), "s"(a.q8));
     constexpr int kHd = 64 * C;
-    constexpr int CW = (C + 1) / 2;              // words of a lane's channels of one row
-    constexpr int kRows = kKeysPerWave * G;      // (key, head) dots reduced together
-    constexpr int VT = kHd * G >= 512 ? kHd * G / 512 : 1; // value-layout channels a lane
-    constexpr int kLanesPerHead = 64 / G;        // value layout: a wave's lanes of one head
-    constexpr int kSlice = kLanesPerHead * VT;   // a wave's channels of each head
-    constexpr int kWavesUsed = kHd / kSlice;     // waves of the value phase
+    constexpr int SC = kHd / 16;                 // score layout: channels a lane
+    constexpr int SW = SC / 2;                   // their words
+    constexpr int KP = 512 / kHd;                // value layout: key partitions
+    constexpr int CPW = 64 / KP;                 // value layout: channels a wave
     constexpr int kBlocks = G * kHd / kBlock;    // the group's 32-channel blocks
-    static_assert(kWavesUsed >= 1 && kWavesUsed <= kAttnWaves && kWavesUsed * kSlice == kHd,
-                  "the value layout covers the head width");
-    __shared__ double sScore[G][kMaxSplitKeys];
+    static_assert(kAttnWaves * 4 == kRoundKeys, "a round is one key a 16-lane group");
+    static_assert(CPW * kAttnWaves == kHd, "the value layout covers the head width");
+    __shared__ __attribute__((aligned(16))) double sScore[kMaxSplitKeys][G];
     __shared__ __attribute__((aligned(16))) uint16_t sV[kMaxSplitKeys * kHd];
     __shared__ double sMax[G], sSum[G];
     constexpr int kTasks = kBlocks > kAttnWaves ? kBlocks : kAttnWaves;
@@ -421,33 +469,39 @@ void attention_kernel(AttentionArgs a)
     const int kvh = unit / gridSplits, split = unit % gridSplits;
     const int h0 = kvh * perKv + grp * G; // the group's first query head
     const int kvWidth = kvHeads * kHd, qWidth = heads * kHd;
-    const int c0 = lane * C;
+    const int sub = lane >> 4;            // score layout: the wave's key of four
+    const int c0 = (lane & 15) * SC;      // and the lane's first channel
     const int kvOffset = kvh * kHd + c0;
 
-    double q[G][C];
+    // the position first: its round trip runs beside the rows' loads, which
+    // would otherwise all have to return before it
+    const int positionLoaded = ld_agent_i(a.position);
+    double q[G][SC];
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int i = 0; i < C; ++i)
-            q[g][i] = (double) a.query[(h0 + g) * kHd + c0 + i];
+        for (int i = 0; i < SC; i += 4) {
+            const float4 f = *reinterpret_cast<const float4 *>(a.query + (h0 + g) * kHd + c0 + i);
+            q[g][i] = f.x;
+            q[g][i + 1] = f.y;
+            q[g][i + 2] = f.z;
+            q[g][i + 3] = f.w;
+        }
 
     // The split expected for the launch's range (spec_keys keys from
     // split * spec_keys) has its rows loaded before the position arrives (rows
     // past the position are read, inside the cache, and never used).
-    uint32_t kh[R][kKeysPerWave][CW], vh[R][kKeysPerWave][CW];
+    uint32_t kh[R][SW], vh[R][SW];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int k = 0; k < kKeysPerWave; ++k) {
-            const int j = min(split * a.spec_keys + r * kRoundKeys + wave + k * kAttnWaves,
-                              a.max_positions - 1);
-            load_words<C>(a.key_cache + (int64_t) j * kvWidth + kvOffset, kh[r][k]);
-            load_words<C>(a.value_cache + (int64_t) j * kvWidth + kvOffset, vh[r][k]);
-        }
+    for (int r = 0; r < R; ++r) {
+        const int j = min(split * a.spec_keys + r * kRoundKeys + 4 * wave + sub, a.max_positions - 1);
+        load_row<SC>(a.key_cache + (int64_t) j * kvWidth + kvOffset, kh[r]);
+        load_row<SC>(a.value_cache + (int64_t) j * kvWidth + kvOffset, vh[r]);
+    }
     // keeps the loads above the position-dependent code
     asm volatile("" ::: "memory");
 
-    const int keyCount = *a.position + 1;
+    const int keyCount = __builtin_amdgcn_readfirstlane(positionLoaded) + 1;
     const SplitPlan plan = plan_splits(keyCount, gridSplits);
     if (plan.perSplit > R * kRoundKeys) {
         // a launch too small for its step's keys (the host sizes it to the
@@ -464,41 +518,35 @@ void attention_kernel(AttentionArgs a)
         const int rounds = (n + kRoundKeys - 1) / kRoundKeys;
         if (plan.perSplit != a.spec_keys) { // not the split expected: its rows again, from k0
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-                for (int k = 0; k < kKeysPerWave; ++k) {
-                    const int j = k0 + min(r * kRoundKeys + wave + k * kAttnWaves, n - 1);
-                    load_words<C>(a.key_cache + (int64_t) j * kvWidth + kvOffset, kh[r][k]);
-                    load_words<C>(a.value_cache + (int64_t) j * kvWidth + kvOffset, vh[r][k]);
-                }
+            for (int r = 0; r < R; ++r) {
+                const int j = k0 + min(r * kRoundKeys + 4 * wave + sub, n - 1);
+                load_row<SC>(a.key_cache + (int64_t) j * kvWidth + kvOffset, kh[r]);
+                load_row<SC>(a.value_cache + (int64_t) j * kvWidth + kvOffset, vh[r]);
+            }
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             if (r >= rounds) // uniform
                 break;
-            double y[kRows];
+            // the lane's share of each head's dot, in two sums (even and odd
+            // channels), then the key's 16 lanes summed together
+            double y[G];
 #pragma unroll
-            for (int k = 0; k < kKeysPerWave; ++k)
+            for (int g = 0; g < G; ++g) {
+                double p0 = 0.0, p1 = 0.0;
 #pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    double p = 0.0;
-#pragma unroll
-                    for (int i = 0; i < C; ++i)
-                        p += q[g][i] * word_half<C>(kh[r][k], i);
-                    y[k * G + g] = p;
+                for (int i = 0; i < SC; i += 2) {
+                    p0 += q[g][i] * half_word(kh[r][i / 2], 0);
+                    p1 += q[g][i + 1] * half_word(kh[r][i / 2], 1);
                 }
-            const double total = reduce_rows<kRows>(y, lane);
-            if (stores_row<kRows>(lane)) {
-                const int row = row_of_lane<kRows>(lane);
-                const int j = r * kRoundKeys + wave + (row / G) * kAttnWaves;
-                if (j < n)
-                    sScore[row % G][j] = (double) a.scale * total;
+                y[g] = p0 + p1;
             }
-#pragma unroll
-            for (int k = 0; k < kKeysPerWave; ++k) {
-                const int j = r * kRoundKeys + wave + k * kAttnWaves;
-                if (j < n)
-                    store_words<C>(sV + j * kHd + c0, vh[r][k]);
+            reduce_halving<G, 8, G>(y, lane);
+            const int j = r * kRoundKeys + 4 * wave + sub;
+            if (j < n) {
+                if (stores_row16<G>(lane))
+                    sScore[j][row_of_lane16<G>(lane)] = (double) a.scale * y[0];
+                store_row<SC>(sV + j * kHd + c0, vh[r]);
             }
         }
         __syncthreads();
@@ -507,12 +555,12 @@ void attention_kernel(AttentionArgs a)
         if (wave < G) {
             double largest = -INFINITY;
             for (int j = lane; j < n; j += 64)
-                largest = fmax(largest, sScore[wave][j]);
+                largest = fmax(largest, sScore[j][wave]);
             largest = wave_max_d(largest);
             double sum = 0.0;
             for (int j = lane; j < n; j += 64) {
-                const double w = exp(sScore[wave][j] - largest);
-                sScore[wave][j] = w;
+                const double w = exp(sScore[j][wave] - largest);
+                sScore[j][wave] = w;
                 sum += w;
             }
             sum = wave_sum_d(sum);
@@ -524,53 +572,60 @@ void attention_kernel(AttentionArgs a)
         __syncthreads();
         // the split's (max, sum) go out before its values are weighted, so
         // the merging splits have them (and their factors) early
+        // (the stored words stay in their registers until the partials are
+        // stored: reusing them would wait for these stores to complete)
+        const v4u mlMax = tagged_double(sMax[t < G ? t : 0], tag);
+        const v4u mlSum = tagged_double(sSum[t < G ? t : 0], tag);
         if (t < G) {
             const uint32_t mlBytes = (uint32_t) (kDecodeSplits * heads * 4 * 8);
             const uint32_t off = (uint32_t) ((split * heads + h0 + t) * 4 * 8);
-            st_agent_16(a.ml_ll, off, mlBytes, tagged_double(sMax[t], tag));
-            st_agent_16(a.ml_ll, off + 16, mlBytes, tagged_double(sSum[t], tag));
+            st_agent_16(a.ml_ll, off, mlBytes, mlMax);
+            st_agent_16(a.ml_ll, off + 16, mlBytes, mlSum);
         }
 
-        // the weighted values, in key order: wave w < kWavesUsed holds channels
-        // [w kSlice, (w + 1) kSlice) of every head of the group
-        if (wave < kWavesUsed) {
-            const int g = lane / kLanesPerHead;
-            const int c = wave * kSlice + (lane % kLanesPerHead) * VT;
-            double acc[VT];
+        // the weighted values: each lane its channel of every head over its
+        // partition's keys, four keys a batch in two sums a head; the
+        // partitions' sums are then added across lanes in a fixed order
+        {
+            const int part = lane / CPW;
+            const int c = wave * CPW + lane % CPW;
+            double acc[2][G];
 #pragma unroll
-            for (int i = 0; i < VT; ++i)
-                acc[i] = 0.0;
-            // eight keys a batch, their LDS reads issued together; past n the
-            // weight is zero and the row is row n - 1's (finite halves)
-            for (int j0 = 0; j0 < n; j0 += 8) {
-                double w[8];
-                uint32_t v[8][(VT + 1) / 2];
+            for (int k = 0; k < 2; ++k)
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int j = min(j0 + u, n - 1);
-                    w[u] = j0 + u < n ? sScore[g][j] : 0.0;
-                    if constexpr (VT == 4) {
-                        const uint2 pair = *reinterpret_cast<const uint2 *>(sV + j * kHd + c);
-                        v[u][0] = pair.x;
-                        v[u][1] = pair.y;
-                    } else if constexpr (VT == 2) {
-                        v[u][0] = *reinterpret_cast<const uint32_t *>(sV + j * kHd + c);
-                    } else {
-                        v[u][0] = sV[j * kHd + c];
-                    }
+                for (int g = 0; g < G; ++g)
+                    acc[k][g] = 0.0;
+            for (int t0 = 0; t0 < n; t0 += 4 * KP) { // the same trip count in every lane
+                double w[4][G];
+                uint16_t v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int j = t0 + u * KP + part;
+                    const int jj = min(j, n - 1); // past n: a zero value (reads unconditional)
+#pragma unroll
+                    for (int g = 0; g < G; ++g)
+                        w[u][g] = sScore[jj][g];
+                    const uint16_t h = sV[jj * kHd + c];
+                    v[u] = j < n ? h : (uint16_t) 0;
                 }
 #pragma unroll
-                for (int u = 0; u < 8; ++u)
+                for (int u = 0; u < 4; ++u) {
+                    const double x = (double) half_value(v[u]);
 #pragma unroll
-                    for (int i = 0; i < VT; ++i)
-                        acc[i] += w[u] * (double) half_value((uint16_t) (v[u][i >> 1] >> (16 * (i & 1))));
+                    for (int g = 0; g < G; ++g)
+                        acc[u & 1][g] += w[u][g] * x;
+                }
             }
-            // the split's partial as tagged words (two a double, one store)
+            asm volatile("" ::"v"(mlMax), "v"(mlSum));
             const uint32_t partBytes = (uint32_t) ((int64_t) kDecodeSplits * qWidth * 16);
 #pragma unroll
-            for (int i = 0; i < VT; ++i)
-                st_agent_16(a.part_ll, (uint32_t) (((int64_t) split * qWidth + (h0 + g) * kHd + c + i) * 16),
-                            partBytes, tagged_double(acc[i], tag));
+            for (int g = 0; g < G; ++g) {
+                const double total = sum_partitions<CPW>(acc[0][g] + acc[1][g]);
+                // the split's partial as tagged words (two a double, one store)
+                if (lane < CPW)
+                    st_agent_16(a.part_ll, (uint32_t) (((int64_t) split * qWidth + (h0 + g) * kHd + c) * 16),
+                                partBytes, tagged_double(total, tag));
+            }
         }
     }
 
