@@ -441,11 +441,12 @@ void attention_kernel(AttentionArgs a)
     constexpr int kHd = 64 * C;
     constexpr int SC = kHd / 16;                 // score layout: channels a lane
     constexpr int SW = SC / 2;                   // their words
-    constexpr int KP = 512 / kHd;                // value layout: key partitions
-    constexpr int CPW = 64 / KP;                 // value layout: channels a wave
+    constexpr int VC = 2;                        // value layout: channels a lane
+    constexpr int KP = 512 * VC / kHd;           // value layout: key partitions
+    constexpr int CPW = 64 / KP;                 // value layout: lanes of a partition in a wave
     constexpr int kBlocks = G * kHd / kBlock;    // the group's 32-channel blocks
     static_assert(kAttnWaves * 4 == kRoundKeys, "a round is one key a 16-lane group");
-    static_assert(CPW * kAttnWaves == kHd, "the value layout covers the head width");
+    static_assert(CPW * VC * kAttnWaves == kHd, "the value layout covers the head width");
     __shared__ __attribute__((aligned(16))) double sScore[kMaxSplitKeys][G];
     __shared__ __attribute__((aligned(16))) uint16_t sV[kMaxSplitKeys * kHd];
     __shared__ double sMax[G], sSum[G];
@@ -583,49 +584,56 @@ void attention_kernel(AttentionArgs a)
             st_agent_16(a.ml_ll, off + 16, mlBytes, mlSum);
         }
 
-        // the weighted values: each lane its channel of every head over its
+        // the weighted values: each lane two channels of every head over its
         // partition's keys, four keys a batch in two sums a head; the
         // partitions' sums are then added across lanes in a fixed order
         {
             const int part = lane / CPW;
-            const int c = wave * CPW + lane % CPW;
-            double acc[2][G];
+            const int c = (wave * CPW + lane % CPW) * VC;
+            double acc[2][G][VC];
 #pragma unroll
             for (int k = 0; k < 2; ++k)
 #pragma unroll
                 for (int g = 0; g < G; ++g)
-                    acc[k][g] = 0.0;
+#pragma unroll
+                    for (int i = 0; i < VC; ++i)
+                        acc[k][g][i] = 0.0;
             for (int t0 = 0; t0 < n; t0 += 4 * KP) { // the same trip count in every lane
                 double w[4][G];
-                uint16_t v[4];
+                uint32_t v[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const int j = t0 + u * KP + part;
-                    const int jj = min(j, n - 1); // past n: a zero value (reads unconditional)
+                    const int jj = min(j, n - 1); // past n: zero values (reads unconditional)
 #pragma unroll
                     for (int g = 0; g < G; ++g)
                         w[u][g] = sScore[jj][g];
-                    const uint16_t h = sV[jj * kHd + c];
-                    v[u] = j < n ? h : (uint16_t) 0;
+                    const uint32_t h = *reinterpret_cast<const uint32_t *>(sV + jj * kHd + c);
+                    v[u] = j < n ? h : 0u;
                 }
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const double x = (double) half_value(v[u]);
+                for (int u = 0; u < 4; ++u)
 #pragma unroll
-                    for (int g = 0; g < G; ++g)
-                        acc[u & 1][g] += w[u][g] * x;
-                }
+                    for (int i = 0; i < VC; ++i) {
+                        const double x = half_word(v[u], i);
+#pragma unroll
+                        for (int g = 0; g < G; ++g)
+                            acc[u & 1][g][i] += w[u][g] * x;
+                    }
             }
             asm volatile("" ::"v"(mlMax), "v"(mlSum));
             const uint32_t partBytes = (uint32_t) ((int64_t) kDecodeSplits * qWidth * 16);
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const double total = sum_partitions<CPW>(acc[0][g] + acc[1][g]);
-                // the split's partial as tagged words (two a double, one store)
-                if (lane < CPW)
-                    st_agent_16(a.part_ll, (uint32_t) (((int64_t) split * qWidth + (h0 + g) * kHd + c) * 16),
-                                partBytes, tagged_double(total, tag));
-            }
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int i = 0; i < VC; ++i) {
+                    const double total = sum_partitions<CPW>(acc[0][g][i] + acc[1][g][i]);
+                    // the split's partial as tagged words (two a double, one store)
+                    if (lane < CPW)
+                        st_agent_16(a.part_ll,
+                                    (uint32_t) (((int64_t) split * qWidth + (h0 + g) * kHd + c + i) * 16),
+                                    partBytes, tagged_double(total, tag));
+                }
         }
     }
 
@@ -633,10 +641,10 @@ void attention_kernel(AttentionArgs a)
     // maximum, in split order, the sums divided by the total): every
     // live split of the group takes blocks split, split + splits, ...; a
     // block's waves each take a run of consecutive splits (lanes 32..63 the
-    // second half of the run).  A wave polls every split's (max, sum) of the
-    // block's head (stored before the split weighs its values), then requests
-    // its run's partial words and computes the split factors while they
-    // travel.  The runs' sums are added in LDS in split order.
+    // second half of the run) and poll every split's (max, sum) of the
+    // block's head (stored before the split weighs its values) and their run's
+    // partial words, a lane loading again only the words it lacks.  The runs'
+    // sums are added in LDS in split order.
     const int splits = plan.splits;
     if (!live)
         return;
@@ -665,28 +673,45 @@ void attention_kernel(AttentionArgs a)
         const int lo = lane < 32 ? lo0 : lo1, hi = lane < 32 ? lo1 : sEnd;
         const bool liveSplit = lane < splits;
         const uint32_t mlOff = (uint32_t) (((liveSplit ? lane : 0) * heads + h0 + g) * 4 * 8);
-        double m = -INFINITY, sum = 0.0;
-        int spins = 0;
-        for (;;) { // every split's (max, sum), stored before its values are weighted
-            const v4u m0 = ld_agent_16(a.ml_ll, mlOff, mlBytes);
-            const v4u m1 = ld_agent_16(a.ml_ll, mlOff + 16, mlBytes);
-            const bool ready = !liveSplit || (m0.y == tag && m0.w == tag && m1.y == tag && m1.w == tag);
-            if (__all(ready)) {
-                m = __longlong_as_double((long long) (((uint64_t) m0.z << 32) | m0.x));
-                sum = __longlong_as_double((long long) (((uint64_t) m1.z << 32) | m1.x));
-                break;
-            }
-            if (wait_give_up(a.error, spins))
-                break;
-        }
-        // the run's partial words are requested, and the factors computed
-        // while they travel
+        // every split's (max, sum) and the run's partial words, each lane
+        // loading again only the words it still lacks, so that after the last
+        // split stores, one trip through the memory system is left
+        v4u m0 = v4u{0u, 0u, 0u, 0u}, m1 = m0;
         v4u w[kPollSplits];
 #pragma unroll
-        for (int u = 0; u < kPollSplits; ++u) {
-            const int sp = min(lo + u, max(hi - 1, 0));
-            w[u] = ld_agent_16(a.part_ll, (uint32_t) ((sp * qWidth + h0 * kHd + cg) * 16), partBytes);
+        for (int u = 0; u < kPollSplits; ++u)
+            w[u] = v4u{0u, 0u, 0u, 0u};
+        bool mlReady = !liveSplit;
+        uint32_t pending = 0; // the run's words not yet seen with the tag
+#pragma unroll
+        for (int u = 0; u < kPollSplits; ++u)
+            pending |= (lo + u < hi ? 1u : 0u) << u;
+        int spins = 0;
+        for (;;) {
+            if (!mlReady) {
+                m0 = ld_agent_16(a.ml_ll, mlOff, mlBytes);
+                m1 = ld_agent_16(a.ml_ll, mlOff + 16, mlBytes);
+            }
+#pragma unroll
+            for (int u = 0; u < kPollSplits; ++u)
+                if (pending & (1u << u))
+                    w[u] = ld_agent_16(a.part_ll, (uint32_t) (((lo + u) * qWidth + h0 * kHd + cg) * 16), partBytes);
+            mlReady = mlReady || (m0.y == tag && m0.w == tag && m1.y == tag && m1.w == tag);
+#pragma unroll
+            for (int u = 0; u < kPollSplits; ++u)
+                if (w[u].y == tag && w[u].w == tag)
+                    pending &= ~(1u << u);
+            if (__all(mlReady && pending == 0))
+                break;
+            if (wait_give_up(a.error, spins)) {
+#pragma unroll
+                for (int u = 0; u < kPollSplits; ++u)
+                    w[u] = v4u{0u, tag, 0u, tag};
+                break;
+            }
         }
+        const double m = __longlong_as_double((long long) (((uint64_t) m0.z << 32) | m0.x));
+        const double sum = __longlong_as_double((long long) (((uint64_t) m1.z << 32) | m1.x));
         double total;
         const double f = merge_factor(m, sum, liveSplit, total);
         // this lane's splits' factors, read from the lanes holding them (the
@@ -697,25 +722,6 @@ void attention_kernel(AttentionArgs a)
             const double f0 = lane_value(f, min(lo0 + u, 63));
             const double f1 = lane_value(f, min(lo1 + u, 63));
             fu[u] = lane < 32 ? f0 : f1;
-        }
-        for (;;) {
-            bool ready = true;
-#pragma unroll
-            for (int u = 0; u < kPollSplits; ++u)
-                ready = ready && (lo + u >= hi || (w[u].y == tag && w[u].w == tag));
-            if (__all(ready))
-                break;
-            if (wait_give_up(a.error, spins)) {
-#pragma unroll
-                for (int u = 0; u < kPollSplits; ++u)
-                    w[u] = v4u{0u, tag, 0u, tag};
-                break;
-            }
-#pragma unroll
-            for (int u = 0; u < kPollSplits; ++u) {
-                const int sp = min(lo + u, max(hi - 1, 0));
-                w[u] = ld_agent_16(a.part_ll, (uint32_t) ((sp * qWidth + h0 * kHd + cg) * 16), partBytes);
-            }
         }
         double weighted = 0.0;
 #pragma unroll
