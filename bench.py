@@ -55,8 +55,8 @@ STAGE_LABELS = {
 }
 DATA = ("synthetic: seeded N(0,0.02) weights / N(0,0.1) norms quantized to Int8Blocks, "
         "seeded uniform prompt ids")
-ORACLE_BUILD = ("gcc -O3 -fopenmp -ffp-contract=off -march=x86-64-v2, the int8 block dot "
-                "built for AVX-512F / AVX2 / baseline and picked at load time")
+ORACLE_BUILD = ("gcc -O3 -fopenmp -ffp-contract=off -march=x86-64-v2, the int8 block dot and "
+                "the fp32 row dot built for AVX-512F / AVX2 / baseline and picked at load time")
 
 
 def log(*args):
@@ -252,7 +252,9 @@ def lockstep_config(args, G, torch, decoder, shape, sequences=16, prompt_len=102
 def cpu_baseline(args, threads: int, decode_bytes) -> dict:
     """The oracle's Q8 decoder (C, OpenMP over the host cores): config 2's
     decode after its 512-token prefill (a bounded sample of decode steps), and
-    the two-layer workload (16-token prompt, 32 greedy tokens) end to end."""
+    the two-layer workload (16-token prompt, 32 greedy tokens) end to end;
+    beside it the reference's own arithmetic (fp32 activations and KV cache,
+    the weights dequantized in the product) on a bounded decode sample."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     O.lib()
@@ -305,6 +307,39 @@ def cpu_baseline(args, threads: int, decode_bytes) -> dict:
               "config1_end_to_end_s": round(config1_s, 3),
               "config1_tok_s": round(count / config1_s, 2)}
     result["achieved_gbs"] = round(step_bytes * decode_tok_s / 1e9, 2)
+
+    # The reference's own arithmetic (Linear.h:128-357: fp32 activations
+    # against Int8Blocks weights dequantized in the product, an fp32 KV
+    # cache): the oracle's fp32-activation mode.  It has no blocked prefill,
+    # so its sample follows a 16-token prompt; at that length the attention
+    # is a sliver of a step whose cost is the 2.66 GB of weights.
+    f32 = O.Model(O.gemma_2b_shape(layers=args.layers, max_positions=1024), O.MODE_Q8_PATH_F32)
+    assert f32.fill_synthetic() == 0
+    prompt16 = O.prompt_ids(0xC0FFEE + 2, shape.vocab, 16)
+    status, logits, _ = f32.step(prompt16)
+    assert status == 0
+    token = O.argmax(logits[-1])
+    f32_steps = 0
+    t0 = time.perf_counter()
+    while f32_steps < 4 or (time.perf_counter() - t0 < args.cpu_seconds and f32_steps < 1000):
+        status, logits, _ = f32.step(np.array([token], dtype=np.int32))
+        assert status == 0
+        token = O.argmax(logits[0])
+        f32_steps += 1
+    f32_seconds = time.perf_counter() - t0
+    f32.close()
+    f32_tok_s = f32_steps / f32_seconds
+    f32_bytes = sum(decode_bytes(L) for L in range(17, 17 + f32_steps)) / f32_steps
+    log(f"cpu baseline, fp32 activations: {f32_steps} decode steps in {f32_seconds:.2f} s "
+        f"({f32_tok_s:.2f} tok/s)")
+    result["fp32_activations"] = {
+        "value": round(f32_tok_s, 3), "unit": "tok/s", "cores": threads,
+        "achieved_gbs": round(f32_bytes * f32_tok_s / 1e9, 2),
+        "sample": f"oracle C decoder in its fp32-activation mode (the reference's arithmetic: "
+                  f"fp32 activations, Int8Blocks weights dequantized in the product, fp32 KV "
+                  f"cache; {ORACLE_BUILD}; OpenMP, {threads} threads), {args.layers} layers: a "
+                  f"16-token seeded prompt, then {f32_steps} greedy decode steps timed "
+                  f"(positions 16..{15 + f32_steps}, {f32_seconds:.1f} s)"}
     return result
 
 

@@ -932,6 +932,34 @@ static void product_input(const gor_model *model, const float *x, int n, int8_t 
     }
 }
 
+/* The fp32 row against one dequantized weight row (Linear.h:128-357 with
+ * the Int8Blocks read of WeightStorage.h:80-191), a block at a time: the
+ * products x * q are exact in double, a block's 32 are summed in eight
+ * partial sums (element k in sum k % 8, combined in a fixed tree), then
+ * scaled by the block's fp16 scale and summed over the blocks in double.
+ * Built for three instruction sets like q8_row_dot. */
+__attribute__((target_clones("avx512f", "avx2", "default")))
+static double f32_row_dot(const float *x, const uint8_t *weights, int64_t elements, int64_t inner,
+                          int64_t row)
+{
+    const int64_t blocks = inner / GOR_BLOCK;
+    const int8_t *q = (const int8_t *) weights + row * inner;
+    const uint8_t *scales = weights + elements + 2 * row * blocks;
+    double total = 0.0;
+    for (int64_t b = 0; b < blocks; ++b) {
+        const float *xb = x + b * GOR_BLOCK;
+        const int8_t *qb = q + b * GOR_BLOCK;
+        double p[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+        for (int k = 0; k < GOR_BLOCK; k += 8)
+            for (int u = 0; u < 8; ++u)
+                p[u] += (double) xb[k + u] * (double) qb[k + u];
+        const double block = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+        const uint16_t bits = (uint16_t) (scales[2 * b] | ((uint32_t) scales[2 * b + 1] << 8));
+        total += block * (double) g_half_table[bits];
+    }
+    return total;
+}
+
 static void product(const gor_model *model, const float *x, const int8_t *xq,
                     const uint16_t *xs, const uint8_t *weights, int64_t rows, int64_t inner,
                     double *out)
@@ -942,12 +970,8 @@ static void product(const gor_model *model, const float *x, const int8_t *xq,
     }
     const int64_t elements = rows * inner;
 #pragma omp parallel for schedule(static)
-    for (int64_t r = 0; r < rows; ++r) {
-        double total = 0.0;
-        for (int64_t i = 0; i < inner; ++i)
-            total += (double) x[i] * dequantized(weights, elements, r * inner + i);
-        out[r] = total;
-    }
+    for (int64_t r = 0; r < rows; ++r)
+        out[r] = f32_row_dot(x, weights, elements, inner, r);
 }
 
 static void q8_token(gor_model *model, int32_t token, float *logits, float *hiddenOut)
