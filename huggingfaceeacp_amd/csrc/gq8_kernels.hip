@@ -21,7 +21,7 @@ constexpr uint32_t kUnchosen = 0xFFFFFFFFu; // Argmax.h:45
 // The largest magnitude of a 32-lane group (lanes 32 g .. 32 g + 31); lanes
 // of the wave outside the group may be inactive.  fmaxf returns the other
 // operand for a NaN, as std::max(largest, |x|) keeps `largest`
-// (Int8Blocks.cpp:118-119).
+// (Int8Blocks.cpp:29-30).
 __device__ inline float group32_amax(float a)
 {
     for (int mask = 16; mask >= 1; mask >>= 1)

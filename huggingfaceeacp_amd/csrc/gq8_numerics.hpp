@@ -35,7 +35,7 @@ GQ8_HD float half_value(uint16_t bits)
     return (float) __builtin_bit_cast(_Float16, bits);
 }
 
-// blockScaleBits (Lib/HuggingFaceEACP/Kernels/Int8Blocks.cpp:114-125) from a
+// blockScaleBits (Lib/HuggingFaceEACP/Kernels/Int8Blocks.cpp:25-36) from a
 // block's largest magnitude: amax / 127 as a float division, narrowed to fp16;
 // a scale that is zero, infinite or NaN is stored as zero.  The quotient is
 // found without a division: the double product amax * (1 / 127) is within
@@ -52,7 +52,7 @@ GQ8_HD uint16_t scale_bits_from_amax(float amax)
     return (scale > 0.f && scale <= 65504.f) ? bits : (uint16_t) 0;
 }
 
-// quantizedByte (Int8Blocks.cpp:130-136): nearbyint((double) x / (double) s)
+// quantizedByte (Int8Blocks.cpp:41-47): nearbyint((double) x / (double) s)
 // clamped to [-127, 127], with s the fp16 scale (positive, finite).  The double
 // quotient of two such numbers never lands on or across a half-integer the
 // exact quotient is not on (the exact distance from a tie is at least 2^-25,

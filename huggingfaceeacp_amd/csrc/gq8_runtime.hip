@@ -81,7 +81,7 @@ void parallel_for(int64_t count, int threads, F body)
         thread.join();
 }
 
-// ---- host Int8Blocks (Int8Blocks.cpp:114-213), the same numerics as the GPU
+// ---- host Int8Blocks (Int8Blocks.cpp:25-124), the same numerics as the GPU
 void quantize_block_host(const float *block, uint8_t *bytes, uint16_t *scale)
 {
     float largest = 0.f;
@@ -421,6 +421,8 @@ extern "C" int gq8_mqa_decode_noalloc(const float *query, const uint16_t *key_ca
         return s;
     if (!query || !key_cache || !value_cache || !out || key_count < 1)
         return fail(GQ8_ERR_ARGUMENT, "mqa_decode_noalloc: bad arguments");
+    // check_attention_shape (at most 16 heads, a 2048-wide query row) keeps
+    // every accepted shape's partials within the array: a guard, not a rule
     const size_t needed = gq8::mqa_workspace_bytes(1, heads, head_dim, key_count);
     if (needed > kNoAllocScratchBytes)
         return fail(GQ8_ERR_ARGUMENT, "mqa_decode_noalloc: the split partials need "

@@ -40,7 +40,7 @@ typedef enum gq8_status {
     GQ8_ERR_CAPACITY = -3,      /* rows past the step capacity (Decoder.cpp:655-664) */
     GQ8_ERR_WINDOW = -4,        /* position + rows past maxPositions (Decoder.cpp:666-675) */
     GQ8_ERR_TOKEN = -5,         /* token id outside the vocabulary (Gemma.cpp:418-424) */
-    GQ8_ERR_UNQUANTIZABLE = -6, /* quantizesAsInt8Blocks refusal (Int8Blocks.cpp:169-174) */
+    GQ8_ERR_UNQUANTIZABLE = -6, /* quantizesAsInt8Blocks refusal (Int8Blocks.cpp:80-85) */
     GQ8_ERR_NOT_PREPARED = -7,  /* weights missing (Decoder.cpp:286-300) */
     GQ8_ERR_EMPTY = -8,         /* a step or prompt of zero tokens (Decoder.cpp:650-651) */
     GQ8_ERR_DEVICE = -9,        /* a HIP call failed */
@@ -79,7 +79,7 @@ int gq8_rotary_table_host(int max_positions, int head_dim, double theta, float *
 /* ======================================================================= */
 
 /* Int8Blocks quantization of rows x inner fp32 values into one Q8 row
- * buffer; bit-exact with quantizeInt8Blocks (Int8Blocks.cpp:181-199).  Used
+ * buffer; bit-exact with quantizeInt8Blocks (Int8Blocks.cpp:87-110).  Used
  * for activations and for quantize-on-upload of weights. */
 int gq8_quantize_rows(const float *x, int64_t rows, int64_t inner, uint8_t *q8, void *stream);
 
@@ -129,7 +129,9 @@ int gq8_mqa_decode(const float *query, const uint16_t *key_cache, const uint16_t
  * forbid hipMalloc).  The split partials live in a static device array of
  * gq8_mqa_decode_noalloc_limit_bytes() bytes per GPU (1 064 960: one query
  * row of at most 16 heads and 2048 channels), held until the process ends;
- * a shape needing more is refused with GQ8_ERR_ARGUMENT.  Every call on one
+ * a shape past 16 heads or a 2048-wide query row is refused with
+ * GQ8_ERR_SHAPE (the shape check every attention entry point makes, which
+ * keeps the partials within the array).  Every call on one
  * GPU shares that array, so calls that overlap on one GPU (two streams, two
  * threads) race. */
 size_t gq8_mqa_decode_noalloc_limit_bytes(void);

@@ -22,7 +22,7 @@
 /* IEEE binary16, written from IEEE 754-2008 section 3.6 (binary16: 1 sign,  */
 /* 5 exponent bits biased by 15, 10 fraction bits) with round to nearest,    */
 /* ties to even -- the conversion eacp's halfFromFloat/halfToFloat perform   */
-/* (used at Lib/HuggingFaceEACP/Kernels/Int8Blocks.cpp:121-122, 190, 211).   */
+/* (used at Lib/HuggingFaceEACP/Kernels/Int8Blocks.cpp:32-33, 101, 121).   */
 /* ======================================================================== */
 uint16_t gor_half_from_float(float value)
 {
@@ -115,11 +115,11 @@ static void ensure_half_table(void)
 
 /* ======================================================================== */
 /* Int8Blocks (Lib/HuggingFaceEACP/Kernels/Int8Blocks.h:9-88,                */
-/* Int8Blocks.cpp:97-213).                                                   */
+/* Int8Blocks.cpp:70-124).                                                   */
 /* ======================================================================== */
 int64_t gor_int8_block_count(int64_t element_count)
 {
-    return element_count / GOR_BLOCK; /* Int8Blocks.cpp:159-162 */
+    return element_count / GOR_BLOCK; /* Int8Blocks.cpp:70-73 */
 }
 
 int64_t gor_int8_blocks_byte_count(int64_t element_count)
@@ -129,13 +129,13 @@ int64_t gor_int8_blocks_byte_count(int64_t element_count)
 
 int gor_quantizes_as_int8_blocks(int64_t contiguous_extent, int64_t element_count)
 {
-    /* Int8Blocks.cpp:169-174 */
+    /* Int8Blocks.cpp:80-85 */
     return contiguous_extent > 0 && element_count > 0
            && contiguous_extent % GOR_BLOCK == 0
            && element_count % (2 * GOR_BLOCK) == 0;
 }
 
-/* blockScaleBits, Int8Blocks.cpp:114-125: the largest magnitude over 127 as a
+/* blockScaleBits, Int8Blocks.cpp:25-36: the largest magnitude over 127 as a
  * float division, narrowed to fp16; a scale that is zero, infinite or NaN is
  * stored as zero.  std::max(largest, |x|) keeps `largest` when |x| is a NaN,
  * which is what the comparison below does too. */
@@ -155,7 +155,7 @@ uint16_t gor_block_scale_bits(const float *block)
     return (scale > 0.f && isfinite(scale)) ? bits : (uint16_t) 0u;
 }
 
-/* quantizedByte, Int8Blocks.cpp:130-136: round to nearest, ties to even, of
+/* quantizedByte, Int8Blocks.cpp:41-47: round to nearest, ties to even, of
  * the double quotient by the narrowed scale, clamped to [-127, 127].  The
  * reference leaves a NaN element undefined (a NaN cast to an integer); here it
  * is stored as zero. */
@@ -172,7 +172,7 @@ int8_t gor_quantized_byte(float value, float scale)
     return (int8_t) rounded;
 }
 
-/* quantizeInt8Blocks, Int8Blocks.cpp:181-199: `values` holds value_count
+/* quantizeInt8Blocks, Int8Blocks.cpp:87-110: `values` holds value_count
  * elements beginning at element `first` of a tensor of element_count, whose
  * bytes are `destination` in the two-region layout. */
 void gor_quantize_int8_blocks(const float *values, int64_t value_count, int64_t first,
@@ -194,7 +194,7 @@ void gor_quantize_int8_blocks(const float *values, int64_t value_count, int64_t 
     }
 }
 
-/* dequantizeInt8Blocks, Int8Blocks.cpp:201-213: the widened fp16 scale times
+/* dequantizeInt8Blocks, Int8Blocks.cpp:112-124: the widened fp16 scale times
  * the sign-extended byte, as an fp32 product. */
 void gor_dequantize_int8_blocks(const uint8_t *stored, int64_t element_count,
                                 float *values)

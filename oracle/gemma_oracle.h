@@ -12,7 +12,7 @@
  *
  *   - activation Q8: every product input row is quantized with the
  *     reference's own Int8Blocks rule (Lib/HuggingFaceEACP/Kernels/
- *     Int8Blocks.cpp:114-136) before the product, and the product is the
+ *     Int8Blocks.cpp:25-47) before the product, and the product is the
  *     exact int8 dot per 32-block times (weight scale * activation scale);
  *   - an fp16 key/value cache (IEEE binary16, round to nearest even).
  *
@@ -41,7 +41,7 @@ extern "C" {
 uint16_t gor_half_from_float(float value);
 float gor_half_to_float(uint16_t bits);
 
-/* ---- Int8Blocks format (Int8Blocks.h:56-88, Int8Blocks.cpp:114-213) -- */
+/* ---- Int8Blocks format (Int8Blocks.h:56-88, Int8Blocks.cpp:25-124) -- */
 enum { GOR_BLOCK = 32 };
 int64_t gor_int8_block_count(int64_t element_count);
 int64_t gor_int8_blocks_byte_count(int64_t element_count);

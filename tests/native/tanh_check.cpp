@@ -39,4 +39,23 @@ int main(int argc, char **argv) {
         differ += geglu(gq8::tanh_from_exp(inner), g, u) != geglu(std::tanh(inner), g, u);
     }
     printf("geglu fp32 differing from libm: %lld of %lld\n", (long long) differ, (long long) total);
+    // Where 1 + tanh cancels (tanh argument in [-10, -3]) every fp32 gate,
+    // against several up values (large ones included): the GeGLU as both
+    // sides round it, (float) ((0.5 g (1 + t)) u)
+    const double rootTwoOverPi = 0.7978845608028654;
+    const float ups[] = {1.f, -1.f, 3.7f, -0.001f, 1000.f, -12345.678f, 65504.f};
+    int64_t sweepDiffer = 0, sweepTotal = 0;
+    for (float g = -3.7f; g <= -2.2f; g = std::nextafter(g, 0.f)) {
+        const double x = (double) g;
+        const double inner = rootTwoOverPi * (x + 0.044715 * x * x * x);
+        if (inner < -10.0 || inner > -3.0) continue;
+        const double ta = gq8::tanh_from_exp(inner), tb = std::tanh(inner);
+        const double ga = 0.5 * x * (1.0 + ta), gb = 0.5 * x * (1.0 + tb);
+        for (float u : ups) {
+            ++sweepTotal;
+            sweepDiffer += (float) (ga * (double) u) != (float) (gb * (double) u);
+        }
+    }
+    printf("dense sweep (tanh argument in [-10, -3]) geglu fp32 differing from libm: %lld of %lld\n",
+           (long long) sweepDiffer, (long long) sweepTotal);
 }

@@ -74,13 +74,12 @@ def test_long_context_window(torch_cuda):
     assert exact >= 0.99
 
 
-def test_split_merge_moves_into_attention(torch_cuda):
-    """Up to 16 key splits the o product merges the attention splits itself;
-    past that the attention kernel merges them once and the o product reads
-    its Q8 row.  One-token steps across the change (keys 1017 .. 1040, 16 then
-    17 .. 17 splits of 64 keys) give the oracle's logits and greedy ids at
-    Gemma-2B dims (2 layers), and the graph replay of a captured step switches
-    with the device position."""
+def test_attention_range_change_at_1024_keys(torch_cuda):
+    """One-token steps across the split attention's change of launch at 1024
+    -> 1025 keys (32 splits of 32 keys, then 64) give the oracle's logits and
+    greedy ids at Gemma-2B dims (2 layers, seeded N(0, 0.02) weights), and the
+    graph replay crosses the change with the device position (its captured
+    steps of two key-count ranges) to the plain loop's ids."""
     torch = torch_cuda
     shape, decoder, model = gemma_pair(2, 1152, max_step_rows=256)
     prompt = O.prompt_ids(0xC0FFEE + 7, shape.vocab, 1016)

@@ -1,5 +1,5 @@
 """The block-scale quotient without a division (gq8_numerics.hpp
-scale_bits_from_amax): amax / 127 rounded to fp32, as Int8Blocks.cpp:114-125
+scale_bits_from_amax): amax / 127 rounded to fp32, as Int8Blocks.cpp:25-36
 computes it, equals the double product amax * (1 / 127) rounded to fp32 for
 every non-negative finite fp32 amax.  The argument in the source (the exact
 quotient stays at least 2^-32 from any fp32 rounding midpoint, the double

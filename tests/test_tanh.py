@@ -1,7 +1,9 @@
 """The GeGLU's tanh (huggingfaceeacp_amd/csrc/gq8_tanh.hpp, built for the host
 with g++) against libm's tanh, which the oracle's GeGLU uses (Gelu.h:27-46 in
 double): within 4 ulps over [-10, 10], and fp32 GeGLU outputs identical on
-two million seeded (gate, up) pairs."""
+two million seeded (gate, up) pairs and on every fp32 gate whose tanh
+argument lies in [-10, -3] (where 1 + tanh cancels and a tanh error is
+magnified most), against seven up values from 1e-3 to 65504."""
 import os
 import re
 import shutil
@@ -24,5 +26,8 @@ def test_tanh_from_exp_against_libm(tmp_path):
     print(out)
     worst = int(re.search(r"worst (\d+) ulp", out).group(1))
     differ = int(re.search(r"differing from libm: (\d+)", out).group(1))
+    sweep = re.search(r"dense sweep .* differing from libm: (\d+) of (\d+)", out)
     assert worst <= 4
     assert differ == 0
+    assert int(sweep.group(2)) > 20_000_000
+    assert int(sweep.group(1)) == 0
