@@ -623,17 +623,25 @@ void attention_kernel(AttentionArgs a)
             }
             asm volatile("" ::"v"(mlMax), "v"(mlSum));
             const uint32_t partBytes = (uint32_t) ((int64_t) kDecodeSplits * qWidth * 16);
+            static_assert(VC * CPW <= 64, "a head's channels of the wave in one store");
+            const int i = lane / CPW; // lanes i CPW .. i CPW + CPW - 1 store channel c + i
 #pragma unroll
-            for (int g = 0; g < G; ++g)
+            for (int g = 0; g < G; ++g) {
+                double total[VC];
 #pragma unroll
-                for (int i = 0; i < VC; ++i) {
-                    const double total = sum_partitions<CPW>(acc[0][g][i] + acc[1][g][i]);
-                    // the split's partial as tagged words (two a double, one store)
-                    if (lane < CPW)
-                        st_agent_16(a.part_ll,
-                                    (uint32_t) (((int64_t) split * qWidth + (h0 + g) * kHd + c + i) * 16),
-                                    partBytes, tagged_double(total, tag));
-                }
+                for (int k = 0; k < VC; ++k)
+                    total[k] = sum_partitions<CPW>(acc[0][g][k] + acc[1][g][k]);
+                double mine = total[0];
+#pragma unroll
+                for (int k = 1; k < VC; ++k)
+                    mine = i == k ? total[k] : mine;
+                // the split's partials as tagged words (two a double): the
+                // wave's VC CPW channels of the head, contiguous, in one store
+                if (lane < VC * CPW)
+                    st_agent_16(a.part_ll,
+                                (uint32_t) (((int64_t) split * qWidth + (h0 + g) * kHd + c + i) * 16),
+                                partBytes, tagged_double(mine, tag));
+            }
         }
     }
 
