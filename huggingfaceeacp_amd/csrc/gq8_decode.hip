@@ -9,9 +9,12 @@
 //                        the fused q|k|v product, RoPE on q and k, k and v
 //                        stored fp16 at the step's cache row (layer 0 also
 //                        gathers the embedding row);
-//   attention_kernel     split-key attention over the fp16 cache with an
-//                        online softmax; the last workgroup of a row merges
-//                        the splits and writes the Q8 row for o_proj;
+//   attention_kernel     split-key attention over the fp16 cache, a
+//                        workgroup per (KV head, key split, query-head
+//                        group) reading its split's rows once for the group;
+//                        every live split merges a share of the channel
+//                        blocks from the others' tagged partials and writes
+//                        them as the Q8 row for o_proj;
 //   (o_proj, down)       q8_matvec_kernel with the residual add;
 //   gateup_geglu_kernel  norm + Q8 prologue, the gate|up product, GeGLU and
 //                        the Q8 row for down_proj;
@@ -346,20 +349,35 @@ __device__ inline SplitPlan plan_splits(int keyCount, int gridSplits)
     return {(keyCount + perSplit - 1) / perSplit, perSplit};
 }
 
-// SC consecutive halves of an fp16 row as SC / 2 words (8-, 16- or 32-byte
-// loads), half i of them, and the same words stored to LDS.
+// The channels of a head row that lane l of a key's 16 lanes holds: SC of
+// them, in pieces of at most eight halves (16 bytes) with the 16 lanes'
+// pieces side by side, so that each load instruction reads whole lines of
+// the row (a lane's 32 contiguous bytes would use half of every line an
+// instruction touches).  Half i of the lane's slice is channel
+// row_channel<SC>(l, i).
 template <int SC>
-__device__ inline void load_row(const uint16_t *p, uint32_t (&w)[SC / 2])
+__device__ inline int row_channel(int l, int i)
 {
     static_assert(SC == 4 || SC == 8 || SC == 16, "4, 8 or 16 halves");
+    if constexpr (SC == 4)
+        return 4 * l + i;
+    else
+        return (i / 8) * 128 + 8 * l + i % 8;
+}
+
+// The lane's SC halves of the fp16 row at p as SC / 2 words (half i in word
+// i / 2), and the same words stored to a row in LDS.
+template <int SC>
+__device__ inline void load_row(const uint16_t *p, int l, uint32_t (&w)[SC / 2])
+{
     if constexpr (SC == 4) {
-        const uint2 v = *reinterpret_cast<const uint2 *>(p);
+        const uint2 v = *reinterpret_cast<const uint2 *>(p + row_channel<SC>(l, 0));
         w[0] = v.x;
         w[1] = v.y;
     } else {
 #pragma unroll
         for (int k = 0; k < SC / 8; ++k) {
-            const uint4 v = reinterpret_cast<const uint4 *>(p)[k];
+            const uint4 v = *reinterpret_cast<const uint4 *>(p + row_channel<SC>(l, 8 * k));
             w[4 * k] = v.x;
             w[4 * k + 1] = v.y;
             w[4 * k + 2] = v.z;
@@ -369,14 +387,15 @@ __device__ inline void load_row(const uint16_t *p, uint32_t (&w)[SC / 2])
 }
 
 template <int SC>
-__device__ inline void store_row(uint16_t *p, const uint32_t (&w)[SC / 2])
+__device__ inline void store_row(uint16_t *p, int l, const uint32_t (&w)[SC / 2])
 {
     if constexpr (SC == 4) {
-        *reinterpret_cast<uint2 *>(p) = make_uint2(w[0], w[1]);
+        *reinterpret_cast<uint2 *>(p + row_channel<SC>(l, 0)) = make_uint2(w[0], w[1]);
     } else {
 #pragma unroll
         for (int k = 0; k < SC / 8; ++k)
-            reinterpret_cast<uint4 *>(p)[k] = make_uint4(w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]);
+            *reinterpret_cast<uint4 *>(p + row_channel<SC>(l, 8 * k))
+                = make_uint4(w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]);
     }
 }
 
@@ -471,8 +490,8 @@ void attention_kernel(AttentionArgs a)
     const int h0 = kvh * perKv + grp * G; // the group's first query head
     const int kvWidth = kvHeads * kHd, qWidth = heads * kHd;
     const int sub = lane >> 4;            // score layout: the wave's key of four
-    const int c0 = (lane & 15) * SC;      // and the lane's first channel
-    const int kvOffset = kvh * kHd + c0;
+    const int l16 = lane & 15;            // and the lane's slice of a row
+    const int kvOffset = kvh * kHd;
 
     // the position first: its round trip runs beside the rows' loads, which
     // would otherwise all have to return before it
@@ -482,7 +501,8 @@ void attention_kernel(AttentionArgs a)
     for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int i = 0; i < SC; i += 4) {
-            const float4 f = *reinterpret_cast<const float4 *>(a.query + (h0 + g) * kHd + c0 + i);
+            const float4 f = *reinterpret_cast<const float4 *>(a.query + (h0 + g) * kHd
+                                                               + row_channel<SC>(l16, i));
             q[g][i] = f.x;
             q[g][i + 1] = f.y;
             q[g][i + 2] = f.z;
@@ -496,8 +516,8 @@ void attention_kernel(AttentionArgs a)
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int j = min(split * a.spec_keys + r * kRoundKeys + 4 * wave + sub, a.max_positions - 1);
-        load_row<SC>(a.key_cache + (int64_t) j * kvWidth + kvOffset, kh[r]);
-        load_row<SC>(a.value_cache + (int64_t) j * kvWidth + kvOffset, vh[r]);
+        load_row<SC>(a.key_cache + (int64_t) j * kvWidth + kvOffset, l16, kh[r]);
+        load_row<SC>(a.value_cache + (int64_t) j * kvWidth + kvOffset, l16, vh[r]);
     }
     // keeps the loads above the position-dependent code
     asm volatile("" ::: "memory");
@@ -521,8 +541,8 @@ void attention_kernel(AttentionArgs a)
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const int j = k0 + min(r * kRoundKeys + 4 * wave + sub, n - 1);
-                load_row<SC>(a.key_cache + (int64_t) j * kvWidth + kvOffset, kh[r]);
-                load_row<SC>(a.value_cache + (int64_t) j * kvWidth + kvOffset, vh[r]);
+                load_row<SC>(a.key_cache + (int64_t) j * kvWidth + kvOffset, l16, kh[r]);
+                load_row<SC>(a.value_cache + (int64_t) j * kvWidth + kvOffset, l16, vh[r]);
             }
         }
 #pragma unroll
@@ -547,7 +567,7 @@ void attention_kernel(AttentionArgs a)
             if (j < n) {
                 if (stores_row16<G>(lane))
                     sScore[j][row_of_lane16<G>(lane)] = (double) a.scale * y[0];
-                store_row<SC>(sV + j * kHd + c0, vh[r]);
+                store_row<SC>(sV + j * kHd, l16, vh[r]);
             }
         }
         __syncthreads();
