@@ -620,8 +620,17 @@ struct gq8_decoder {
 
 namespace {
 
+// Destroys the captured steps once the decoder's stream has finished every
+// replay it holds (a replay still in flight keeps using its executable graph).
 void drop_graphs(gq8_decoder *d)
 {
+    bool any = false;
+    for (hipGraphExec_t g : d->graphs)
+        any = any || g != nullptr;
+    if (!any)
+        return;
+    if (d->stream)
+        (void) hipStreamSynchronize(d->stream);
     for (hipGraphExec_t &g : d->graphs)
         if (g) {
             (void) hipGraphExecDestroy(g);
