@@ -156,6 +156,8 @@ void q8_gemm_kernel(
                 sc[i] = (i < 2 ? aScales : wScales)[scaleOff[i] + c0];
         }
         const uint8_t *ops = sOps[0];
+        // a block's four MFMAs go out together, then their double epilogue, so
+        // the later MFMAs run while the first one's results are scaled
 #pragma unroll 1
         for (int kb = 0; kb < kChunk; ++kb) {
             long af[2], bf[2];
@@ -168,6 +170,14 @@ void q8_gemm_kernel(
 #pragma unroll
             for (int j = 0; j < 2; ++j)
                 sw[j] = sScales[0][kTileM + wn + j * 16 + (lane & 15)][kb];
+            v4i d[2][2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const v4i zero = {0, 0, 0, 0};
+                    d[i][j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[i], bf[j], zero, 0, 0, 0);
+                }
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 double sx[4];
@@ -175,13 +185,10 @@ void q8_gemm_kernel(
                 for (int r = 0; r < 4; ++r)
                     sx[r] = sScales[0][wm + i * 16 + (lane >> 4) * 4 + r][kb];
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const v4i zero = {0, 0, 0, 0};
-                    const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[i], bf[j], zero, 0, 0, 0);
+                for (int j = 0; j < 2; ++j)
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        acc[i][j][r] += (double) d[r] * (sw[j] * sx[r]);
-                }
+                        acc[i][j][r] += (double) d[i][j][r] * (sw[j] * sx[r]);
             }
         }
     }
