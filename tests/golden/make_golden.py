@@ -19,7 +19,8 @@ are held to fixed bytes:
                     and every 1000th logit of the last prompt row.
 
 The full-size fixtures take minutes of CPU each and are written on request
-(`python tests/golden/make_golden.py ctx512 prefill2048 varied18 long8192`):
+(`python tests/golden/make_golden.py ctx512 prefill2048 varied18 varied18_ctx560
+long8192`):
 
   gemma_ctx512.npz  18 layers, seeded N(0, 0.02) weights, the 512-token
                     prompt of seed 0xC0FFEE + 2, 256 greedy tokens (no EOS
@@ -36,6 +37,10 @@ The full-size fixtures take minutes of CPU each and are written on request
                     64-token prompt of seed 0xC0FFEE + 7, 48 greedy tokens:
                     ids, top-8 ids and logits, margins, and the Q8 digests of
                     the last prompt row and of the 24th generated step;
+  gemma_varied18_ctx560.npz  the same weights past 512 keys: the 560-token
+                    prompt of seed 0xC0FFEE + 9, 24 greedy tokens, with the Q8
+                    digests of the last prompt row and of generated steps 1,
+                    12 and 23 (561, 572 and 583 keys);
   gemma_long8192.npz  18 layers, seeded N(0, 0.02) weights, the 8064-token
                     prompt of seed 0xC0FFEE + 4, greedy decode to the end of
                     the 8192-position window (128 ids): ids, top-8 ids and
@@ -230,6 +235,16 @@ def gemma_varied18():
     return greedy(model, prompt, 48, digest_steps=(24,))
 
 
+def gemma_varied18_ctx560():
+    model = O.Model(O.gemma_2b_shape(layers=18, max_positions=1024), O.MODE_Q8)
+    for index in range(model.tensor_count):
+        values = O.normal_fill(VARIED_SEED + index, varied_sigma(model, index),
+                               model.tensor_elements(index))
+        assert model.set_tensor(index, values) == 0
+    prompt = O.prompt_ids(0xC0FFEE + 9, model.shape.vocab, 560)
+    return greedy(model, prompt, 24, digest_steps=(1, 12, 23))
+
+
 def gemma_long8192():
     model = synthetic_gemma(18, 8192)
     prompt = O.prompt_ids(0xC0FFEE + 4, model.shape.vocab, 8064)
@@ -239,7 +254,8 @@ def gemma_long8192():
 
 
 FULL_SIZE = {"ctx512": gemma_ctx512, "prefill2048": gemma_prefill2048,
-             "varied18": gemma_varied18, "long8192": gemma_long8192}
+             "varied18": gemma_varied18, "varied18_ctx560": gemma_varied18_ctx560,
+             "long8192": gemma_long8192}
 
 
 def main():

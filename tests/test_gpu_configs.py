@@ -251,6 +251,26 @@ def test_varied_ids_18_layers(torch_cuda):
           f"top-8 logits bit-identical in {exact:.4f} of places")
 
 
+def test_varied_ids_18_layers_past_512_keys(torch_cuda):
+    """The same weights past 512 keys, where a step's attention is the
+    launch of 513-1024 keys (32 splits): the oracle's 24 ids through the
+    graph and the plain loop, each step's top-8 logits, and every layer's Q8
+    bytes at the last prompt row (560 keys) and at generated steps 1, 12
+    and 23 (561, 572 and 583 keys)."""
+    torch = torch_cuda
+    f = fixture("gemma_varied18_ctx560.npz")
+    print("varied spreads: 18 layers, 560 + 24", flush=True)
+    shape, decoder = varied_decoder(18, 1024)
+    expected = list(f["ids"])
+    assert len(set(expected)) > 16
+    for label, graph in (("graph", True), ("plain", False)):
+        tokens, _ = decoder.generate(f["prompt"], len(expected), eos=-1, use_graph=graph)
+        assert list(tokens) == expected, label
+    exact = stepwise(torch, decoder, f, digest_steps=tuple(int(s) for s in f["digest_steps"]))
+    print(f"  distinct ids {len(set(expected))}, smallest top-2 margin {f['margins'].min():.3g}, "
+          f"top-8 logits bit-identical in {exact:.4f} of places")
+
+
 def test_varied_ids_two_layers_q8_bytes(torch_cuda):
     """2 layers, the same spreads, against the live oracle: every Q8 byte of
     every layer's product inputs (counted, not hashed), the ids and logits."""
