@@ -11,8 +11,11 @@
 // waves take the key tiles (16 keys) round robin, each keeping an online
 // softmax state (row maximum, sum and the 16 x head_dim sums), and the states
 // are merged in LDS at the end.  The grid starts the longest row blocks
-// first, so the short ones fill in behind them.  A wave loads its next tile's
-// keys and values (16-byte loads) before it works on the current one.
+// first, so the short ones fill in behind them.  A wave requests a tile's
+// values (16-byte loads) before its scores and the next tile's keys right
+// after them, so no tile's operands wait in registers a whole tile ahead; the
+// kernel is held to two waves a SIMD (256 registers a wave), and one wave's
+// MFMAs run while the other waits on its loads or works on its softmax.
 //
 // Per tile a wave computes S^T = K Q^T with v_mfma_f64_16x16x4f64, so the
 // result holds row j of the block on lanes j, j + 16, j + 32, j + 48 and is
@@ -91,7 +94,8 @@ __device__ inline double half_at(const uint32_t (&w)[N], int i)
 
 // E channels a lane group, T = head_dim / 16 output column tiles.
 template <int E>
-__global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillArgs a)
+__global__ __launch_bounds__(kPaThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void prefill_attention_kernel(PrefillArgs a)
 {
     constexpr int HD = 4 * E, T = HD / 16;
     constexpr int KW = E / 2, VW = T / 2; // words of a lane's key channels / value channels
@@ -129,9 +133,12 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillAr
     const uint16_t *values = a.value_cache + kvh * HD + j * T;
     // a tile's operands: key k0 + j's channels, and keys k0 + g + 4 st's value channels
     // (keys past the block's last are clamped to it and masked)
-    auto load_tile = [&](int tile, uint32_t (&kw)[KW], uint32_t (&vw)[4][VW]) {
+    auto load_keys = [&](int tile, uint32_t (&kw)[KW]) {
         const int k0 = tile * kPaKeys;
         load_halves<E>(keys + (int64_t) min(k0 + j, lastKey) * kvWidth, kw);
+    };
+    auto load_values = [&](int tile, uint32_t (&vw)[4][VW]) {
+        const int k0 = tile * kPaKeys;
 #pragma unroll
         for (int st = 0; st < 4; ++st)
             load_halves<T>(values + (int64_t) min(k0 + g + 4 * st, lastKey) * kvWidth, vw[st]);
@@ -145,10 +152,9 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillAr
 
     uint32_t kw[KW], vw[4][VW];
     if (wave < tiles)
-        load_tile(wave, kw, vw);
+        load_keys(wave, kw);
     for (int tile = wave; tile < tiles; tile += kPaWaves) {
-        uint32_t kn[KW], vn[4][VW];
-        load_tile(min(tile + kPaWaves, tiles - 1), kn, vn);
+        load_values(tile, vw); // arrive while the scores are computed
         const int k0 = tile * kPaKeys;
 
         // the query is read from LDS every tile: an opaque offset keeps the
@@ -165,6 +171,9 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillAr
             s = mfma(half_at(kw, c + 2), (double) qv.z, s);
             s = mfma(half_at(kw, c + 3), (double) qv.w, s);
         }
+
+        // the next tile's keys: they arrive during the softmax and O += P V
+        load_keys(min(tile + kPaWaves, tiles - 1), kw);
 
         // row j against keys k0 + g + 4 r
         double sv[4];
@@ -212,14 +221,6 @@ __global__ __launch_bounds__(kPaThreads) void prefill_attention_kernel(PrefillAr
             for (int n = 0; n < T; ++n)
                 o[n] = mfma(p[st], half_at(vw[st], n), o[n]);
 
-#pragma unroll
-        for (int i = 0; i < KW; ++i)
-            kw[i] = kn[i];
-#pragma unroll
-        for (int st = 0; st < 4; ++st)
-#pragma unroll
-            for (int i = 0; i < VW; ++i)
-                vw[st][i] = vn[st][i];
     }
 
     // the maximum and sum of output rows g + 4 r
