@@ -361,7 +361,6 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_kernel(RowsArgs a)
     const int tile = a.geglu8 ? (wave >> 1) * upTiles + 2 * colIdx + (wave & 1)
                               : colIdx * kTiles + wave / WPT;
     const int part = wave % WPT;
-    const int n0 = tile * kRowsTile;
     const int r0 = splitIdx * range;             // the workgroup's first block
     const int rEnd = min(r0 + range, nb);
     const int b0 = r0 + part * a.per;              // this wave's blocks
