@@ -157,8 +157,11 @@ void q8_gemm_kernel(
         }
         const uint8_t *ops = sOps[0];
         // a block's four MFMAs go out together, then their double epilogue, so
-        // the later MFMAs run while the first one's results are scaled
-#pragma unroll 1
+        // the later MFMAs run while the first one's results are scaled; the
+        // blocks are unrolled (LDS offsets as immediates) with a scheduling
+        // barrier between them, so no block's loads are hoisted into another's
+        // registers
+#pragma unroll
         for (int kb = 0; kb < kChunk; ++kb) {
             long af[2], bf[2];
 #pragma unroll
@@ -190,6 +193,7 @@ void q8_gemm_kernel(
                     for (int r = 0; r < 4; ++r)
                         acc[i][j][r] += (double) d[i][j][r] * (sw[j] * sx[r]);
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 
