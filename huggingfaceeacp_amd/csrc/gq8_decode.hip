@@ -18,10 +18,10 @@
 //   (o_proj, down)       q8_matvec_kernel with the residual add;
 //   gateup_geglu_kernel  norm + Q8 prologue, the gate|up product, GeGLU and
 //                        the Q8 row for down_proj;
-//   (final norm)         rmsnorm_kernel: the final norm and its Q8 row;
-//   lmhead_argmax_kernel the tied lm_head over the whole vocabulary, each
-//                        workgroup's first maximum merged into one packed
-//                        64-bit word by atomicMax;
+//   lmhead_argmax_kernel the final norm and its Q8 row (per workgroup, in
+//                        LDS), the tied lm_head over the whole vocabulary,
+//                        each workgroup's first maximum merged into one
+//                        packed 64-bit word by atomicMax;
 //   head_finalize_kernel the id into the next sequence slot and the position
 //                        advance.
 //
@@ -879,10 +879,13 @@ void gateup_geglu_kernel(GateUpArgs a)
 }
 
 // ---- final norm + tied lm_head + argmax ----------------------------------------------
-// The final norm and its Q8 row come from a one-workgroup kernel; the lm_head
-// is then a one-shot product (every wave loads its eight rows' blocks once,
-// the activation block of its lane straight from the Q8 row) whose rows are
-// reduced together.  Each workgroup folds its rows into one 64-bit candidate
+// Every workgroup of the lm_head takes the final norm of the residual row and
+// its Q8 into LDS itself (the row's loads issued before its weight loads, the
+// norm's chain run while the weights stream in, as gate|up does; workgroup 0
+// also writes the normalised row and the Q8 row, the hiddenStates and debug
+// views); the lm_head is a one-shot product (every wave loads its eight rows'
+// blocks once, the activation block of its lane from the LDS row) whose rows
+// are reduced together.  Each workgroup folds its rows into one 64-bit candidate
 // (an order-preserving key of the logit above the complemented row index) and
 // merges it into one of kHeadSlots device words (spread over cache lines, so
 // that the atomics do not queue on one address) with one atomicMax, so the
@@ -900,7 +903,10 @@ constexpr int kHeadWaves = kHeadThreads / 64;
 
 __global__ __launch_bounds__(kHeadThreads) void lmhead_argmax_kernel(HeadArgs a)
 {
-    GQ8_ARGS_EARLY("s"(a.best), "s"(a.logits));
+    GQ8_ARGS_EARLY("s"(a.best), "s"(a.logits), "s"(a.q8), "s"(a.normalised_out));
+    static_assert(kFusedMaxWidth / 4 / 64 == kHeadWaves, "four row elements a thread");
+    __shared__ RowQ8 normRow;
+    __shared__ double sPartial[kHeadWaves];
     __shared__ unsigned long long sBest[kHeadWaves];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nb = a.width / kBlock;
@@ -908,15 +914,21 @@ __global__ __launch_bounds__(kHeadThreads) void lmhead_argmax_kernel(HeadArgs a)
     const int64_t V = a.vocab;
     const int64_t r0 = ((int64_t) blockIdx.x * kHeadWaves + wave) * kHeadRows;
 
+    const RowSlice<4> slice = load_row_slice<4>(a.hidden, nullptr, nullptr, 0, 0.f, nullptr,
+                                                a.norm_weight, a.width);
     WeightBlock w[kHeadRows];
 #pragma unroll
     for (int k = 0; k < kHeadRows; ++k)
         w[k] = load_block(a.weights, V, a.width, r0 + k, lane, valid && r0 + k < V);
-    const int ab = valid ? lane : 0; // an invalid lane's terms are zeroed by block_term
-    const int4 a0 = reinterpret_cast<const int4 *>(a.q8 + ab * kBlock)[0];
-    const int4 a1 = reinterpret_cast<const int4 *>(a.q8 + ab * kBlock)[1];
-    const double sa = (double) half_value(reinterpret_cast<const uint16_t *>(a.q8 + a.width)[ab]);
-    __builtin_amdgcn_sched_barrier(0); // every load issued before the first wait
+    __builtin_amdgcn_sched_barrier(0); // every load issued before the norm's first wait
+    norm_q8_finish(slice, a.width, a.epsilon, normRow, sPartial, a.normalised_out, a.q8);
+    int4 a0 = make_int4(0, 0, 0, 0), a1 = a0; // an invalid lane's terms are zeroed by block_term
+    double sa = 0.0;
+    if (valid) {
+        a0 = reinterpret_cast<const int4 *>(normRow.q + lane * kBlock)[0];
+        a1 = reinterpret_cast<const int4 *>(normRow.q + lane * kBlock)[1];
+        sa = normRow.scale[lane];
+    }
     double y[kHeadRows];
 #pragma unroll
     for (int k = 0; k < kHeadRows; ++k)
@@ -1143,16 +1155,6 @@ hipError_t launch_gateup_geglu(const GateUpArgs &a, hipStream_t stream)
     hipLaunchKernelGGL(gateup_geglu_kernel, dim3(a.intermediate / kBlock), dim3(kGluThreads), 0,
                        stream, a);
     return hipGetLastError();
-}
-
-// The final norm of the step's row: the row-norm kernel, whose one row takes
-// a workgroup for each element a thread holds (each sums the whole row's
-// squares and normalizes its share), so the chain after the row arrives is
-// one element long.
-hipError_t launch_final_norm(const HeadArgs &a, hipStream_t stream)
-{
-    return launch_rmsnorm(a.hidden, a.norm_weight, 1, a.width, a.epsilon, a.normalised_out, a.q8,
-                          stream);
 }
 
 hipError_t launch_lmhead_argmax(const HeadArgs &a, hipStream_t stream)

@@ -101,7 +101,7 @@ struct HeadArgs {
     float epsilon;
     const uint8_t *weights;   // the tied embedding, Int8Blocks [vocab, width]
     int vocab;
-    uint8_t *q8;              // the final-norm row's Q8 (written, then read by the lm_head)
+    uint8_t *q8;              // the final-norm row's Q8 (written by workgroup 0: the debug view)
     float *logits;            // fp32 [vocab]
     float *normalised_out;    // the final-norm row (hiddenStates)
     unsigned long long *best; // kHeadSlots packed (logit key, complemented row) maxima,
@@ -119,8 +119,7 @@ bool fused_decode_supported(int width, int heads, int kv_heads, int head_dim, in
 hipError_t launch_qkv_rope(const QkvArgs &a, hipStream_t stream);
 hipError_t launch_attention(const AttentionArgs &a, hipStream_t stream);
 hipError_t launch_gateup_geglu(const GateUpArgs &a, hipStream_t stream);
-hipError_t launch_final_norm(const HeadArgs &a, hipStream_t stream);    // one workgroup
-hipError_t launch_lmhead_argmax(const HeadArgs &a, hipStream_t stream); // logits + packed maximum
+hipError_t launch_lmhead_argmax(const HeadArgs &a, hipStream_t stream); // final norm, logits, maximum
 hipError_t launch_head_finalize(const HeadArgs &a, hipStream_t stream); // id, position, clear
 
 } // namespace gq8

@@ -1578,8 +1578,7 @@ int encode_fused_token(gq8_decoder *d, float *logits, bool sample)
     h.sequence = sample && !sampled(d) ? d->sequence : nullptr;
     h.position = d->position;
     h.advance = 1;
-    GQ8_STAGE(kStageNorm, gq8::launch_final_norm(h, st));
-    GQ8_STAGE(kStageLogits, gq8::launch_lmhead_argmax(h, st));
+    GQ8_STAGE(kStageLogits, gq8::launch_lmhead_argmax(h, st)); // the final norm included
     GQ8_STAGE(kStageArgmax, gq8::launch_head_finalize(h, st));
     // the position has advanced: the sample fills slot *position
     if (sample && sampled(d))
