@@ -16,8 +16,11 @@
 // blocks (256 bytes).  A chunk of both operands and its fp16 scales (as
 // doubles) is staged in LDS with 16-byte loads (66 KB), so two workgroups
 // share a CU and one's loads overlap the other's arithmetic.  The double
-// epilogue (a conversion, a scale product and a fused multiply-add per element
-// and block) bounds the kernel, not the MFMA.
+// epilogue (a conversion, a product with the weight scale and a fused
+// multiply-add with the activation scale per element and block) bounds the
+// kernel, not the MFMA.  The activation scales of a 16-lane row's four rows
+// reach its lanes by DPP broadcast inside that multiply-add, so a chunk reads
+// them from LDS once (four blocks a load) rather than per element.
 //
 // MFMA operand layout (checked on gfx950): for A 16 x 32 and B given as
 // B[j][k] 16 x 32, lane l supplies A[l % 16][8 (l / 16) .. + 8) and
@@ -41,6 +44,32 @@ constexpr int kStageVectors = kStageRows * kChunkBytes / 16 / kGemmThreads; // 6
 constexpr int kStageScales = kStageRows * kChunk;                           // 1536
 
 constexpr int kScalePieces = (kStageScales + kGemmThreads - 1) / kGemmThreads; // 3 a thread
+
+// acc[j][r] += part[j][r] * s', r = 0..3, where s' is the s held by lane
+// 4 Q + r of this lane's 16-lane row: v_fmac_f64 with a DPP row_newbcast
+// source operand, so the row's scales travel between lanes inside the
+// multiply-add itself (no LDS read, no extra instruction).  A fused
+// multiply-add rounds acc + part * s' once, as acc + d * (sw * sx) does: both
+// products are exact in double.  The leading s_nop 1 gives the two wait
+// states a DPP source needs after a VALU write of its register.
+template <int Q>
+__device__ inline void fmac_row_scales(double (&acc)[2][4], double s, const double (&part)[2][4])
+{
+    asm volatile("s_nop 1\n\t"
+                 "v_fmac_f64_dpp %0, %8, %9 row_newbcast:%17 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f64_dpp %1, %8, %10 row_newbcast:%18 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f64_dpp %2, %8, %11 row_newbcast:%19 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f64_dpp %3, %8, %12 row_newbcast:%20 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f64_dpp %4, %8, %13 row_newbcast:%17 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f64_dpp %5, %8, %14 row_newbcast:%18 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f64_dpp %6, %8, %15 row_newbcast:%19 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f64_dpp %7, %8, %16 row_newbcast:%20 row_mask:0xf bank_mask:0xf"
+                 : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[0][2]), "+v"(acc[0][3]),
+                   "+v"(acc[1][0]), "+v"(acc[1][1]), "+v"(acc[1][2]), "+v"(acc[1][3])
+                 : "v"(s), "v"(part[0][0]), "v"(part[0][1]), "v"(part[0][2]), "v"(part[0][3]),
+                   "v"(part[1][0]), "v"(part[1][1]), "v"(part[1][2]), "v"(part[1][3]),
+                   "n"(4 * Q), "n"(4 * Q + 1), "n"(4 * Q + 2), "n"(4 * Q + 3));
+}
 
 // kGeglu: the gate|up product of a fused [2 F, inner] weight (gate rows
 // first) with GeGLU and its Q8 folded in.  Tile column block bx stages gate
@@ -156,6 +185,17 @@ void q8_gemm_kernel(
                 sc[i] = (i < 2 ? aScales : wScales)[scaleOff[i] + c0];
         }
         const uint8_t *ops = sOps[0];
+        // the activation scales of the wave's rows, four blocks a load: lane
+        // (g, j) holds row 4 g + (j & 3)'s scale of block 4 h + (j >> 2) (the
+        // rows of MFMA tile i), and every lane of the 16-lane row g takes the
+        // one it needs by DPP
+        double sxRow[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                sxRow[i][h] = sScales[0][wm + i * 16 + (lane >> 4) * 4 + (lane & 3)]
+                                     [h * 4 + ((lane >> 2) & 3)];
         // a block's four MFMAs go out together, then their double epilogue, so
         // the later MFMAs run while the first one's results are scaled; the
         // blocks are unrolled (LDS offsets as immediates) with a scheduling
@@ -183,15 +223,18 @@ void q8_gemm_kernel(
                 }
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                double sx[4];
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    sx[r] = sScales[0][wm + i * 16 + (lane >> 4) * 4 + r][kb];
+                double part[2][4]; // d * sw: exact (a 20-bit integer times an fp16 value)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        acc[i][j][r] += (double) d[i][j][r] * (sw[j] * sx[r]);
+                        part[j][r] = (double) d[i][j][r] * sw[j];
+                switch (kb & 3) {
+                case 0: fmac_row_scales<0>(acc[i], sxRow[i][kb >> 2], part); break;
+                case 1: fmac_row_scales<1>(acc[i], sxRow[i][kb >> 2], part); break;
+                case 2: fmac_row_scales<2>(acc[i], sxRow[i][kb >> 2], part); break;
+                default: fmac_row_scales<3>(acc[i], sxRow[i][kb >> 2], part); break;
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
         }

@@ -100,8 +100,11 @@ void prefill_attention_kernel(PrefillArgs a)
     constexpr int HD = 4 * E, T = HD / 16;
     constexpr int KW = E / 2, VW = T / 2; // words of a lane's key channels / value channels
     constexpr int kBlockLanes = kBlock / T;  // lanes holding one 32-channel block of an output row
-    // one wave's state at a time for the merge: o (T x 4), then m and l of the rows g + 4 r
-    __shared__ double sState[64][T * 4 + 8 + 1];
+    constexpr int kMergeTiles = T < 2 ? T : 2;
+    // the merge: every wave's maxima and scaled sums of the rows g + 4 r, and
+    // kMergeTiles column tiles of waves 1..3's output sums at a time
+    __shared__ double sMax[kPaWaves][4][64], sSum[kPaWaves][4][64];
+    __shared__ double sPart[kPaWaves - 1][kMergeTiles * 4][64];
     __shared__ __align__(16) float sQ[kPaRows][HD + 4]; // padded: a 16-lane group's rows on distinct banks
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -231,40 +234,57 @@ void prefill_attention_kernel(PrefillArgs a)
         lO[r] = __shfl(l, g + 4 * r);
     }
 
-    // merge the waves' states into wave 0, one wave at a time (wave 0 holds
-    // tile 0, which every row attends, so its maxima are finite)
-    for (int w = 1; w < kPaWaves; ++w) {
+    // merge the waves' states into wave 0.  Every wave scales its sums to the
+    // rows' common maximum (wave 0 holds tile 0, which every row attends, so
+    // that maximum is finite; a wave whose keys a row never reached has m =
+    // -inf and weighs nothing), then waves 1..3 hand wave 0 their sums
+    // kMergeTiles column tiles at a time, so wave 0 never holds another
+    // wave's whole state in registers beside its own.
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        sMax[wave][r][lane] = mO[r];
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        double common = sMax[0][r][lane];
+#pragma unroll
+        for (int w = 1; w < kPaWaves; ++w)
+            common = fmax(common, sMax[w][r][lane]);
+        const double f = mO[r] == -INFINITY ? 0.0 : exp(mO[r] - common);
+        lO[r] *= f;
+#pragma unroll
+        for (int n = 0; n < T; ++n)
+            o[n][r] *= f;
+        sSum[wave][r][lane] = lO[r];
+    }
+#pragma unroll
+    for (int n0 = 0; n0 < T; n0 += kMergeTiles) {
         __syncthreads();
-        if (wave == w) {
+        if (wave != 0) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                sState[lane][T * 4 + r] = mO[r];
-                sState[lane][T * 4 + 4 + r] = lO[r];
-            }
-#pragma unroll
-            for (int n = 0; n < T; ++n)
+            for (int n = 0; n < kMergeTiles; ++n)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    sState[lane][n * 4 + r] = o[n][r];
+                    sPart[wave - 1][n * 4 + r][lane] = o[n0 + n][r];
         }
         __syncthreads();
         if (wave == 0) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const double om = sState[lane][T * 4 + r], ol = sState[lane][T * 4 + 4 + r];
-                const double newMax = fmax(mO[r], om);
-                const double fa = newMax == -INFINITY ? 0.0 : exp(mO[r] - newMax);
-                const double fb = om == -INFINITY ? 0.0 : exp(om - newMax);
-                lO[r] = lO[r] * fa + ol * fb;
-                mO[r] = newMax;
+            for (int w = 0; w < kPaWaves - 1; ++w)
 #pragma unroll
-                for (int n = 0; n < T; ++n)
-                    o[n][r] = o[n][r] * fa + sState[lane][n * 4 + r] * fb;
-            }
+                for (int n = 0; n < kMergeTiles; ++n)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        o[n0 + n][r] += sPart[w][n * 4 + r][lane];
         }
     }
     if (wave != 0)
         return;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int w = 1; w < kPaWaves; ++w)
+            lO[r] += sSum[w][r][lane];
 
     // rows g + 4 r, channels [j T, j T + T): fp32, then Q8 per 32-block
     // (kBlockLanes neighbouring lanes a block)
