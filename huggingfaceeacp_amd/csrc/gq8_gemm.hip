@@ -176,13 +176,29 @@ void q8_gemm_kernel(
         }
         __syncthreads();
         {
-            const int64_t c0 = (int64_t) min(c + 1, chunks - 1) * kChunk; // the last is a repeat, never stored
+            // the next chunk (the last is a repeat, never stored); its offset
+            // joins the uniform bases, so each piece's address is a 32-bit
+            // offset from a scalar base.  The chunk index and the offsets pass
+            // through empty asm statements: otherwise the loop keeps a stepped
+            // 64-bit address a piece (twelve registers) or the offsets'
+            // 64-bit extensions.
+            int next = min(c + 1, chunks - 1);
+            asm volatile("" : "+s"(next));
+            const int64_t c0 = (int64_t) next * kChunk;
+            const uint8_t *aChunk = aBase + c0 * kBlock, *wChunk = w8 + c0 * kBlock;
+            const uint16_t *aScaleChunk = aScales + c0, *wScaleChunk = wScales + c0;
 #pragma unroll
-            for (int i = 0; i < kStageVectors; ++i)
-                v[i] = *reinterpret_cast<const v4i *>((i < 4 ? aBase : w8) + srcOff[i] + c0 * kBlock);
+            for (int i = 0; i < kStageVectors; ++i) {
+                uint32_t off = srcOff[i];
+                asm volatile("" : "+v"(off));
+                v[i] = *reinterpret_cast<const v4i *>((i < 4 ? aChunk : wChunk) + off);
+            }
 #pragma unroll
-            for (int i = 0; i < kScalePieces; ++i)
-                sc[i] = (i < 2 ? aScales : wScales)[scaleOff[i] + c0];
+            for (int i = 0; i < kScalePieces; ++i) {
+                uint32_t off = scaleOff[i];
+                asm volatile("" : "+v"(off));
+                sc[i] = (i < 2 ? aScaleChunk : wScaleChunk)[off];
+            }
         }
         const uint8_t *ops = sOps[0];
         // the activation scales of the wave's rows, four blocks a load: lane
