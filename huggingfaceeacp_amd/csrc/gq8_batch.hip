@@ -737,6 +737,31 @@ __device__ inline Halves<C> load_channels(const uint16_t *p)
     return h;
 }
 
+// p[j] += q' k[j] for a lane's four keys, where q' is the query channel that
+// lane c of the lane's 16-lane row holds (c constant once the caller's loop
+// is unrolled, so the switch folds away)
+__device__ inline void row_channel_fmac(int c, double (&p)[4], double q, const double (&k)[4])
+{
+    switch (c) {
+    case 0: fmac_row_bcast4<0, 0, 0, 0>(p, q, k); break;
+    case 1: fmac_row_bcast4<1, 1, 1, 1>(p, q, k); break;
+    case 2: fmac_row_bcast4<2, 2, 2, 2>(p, q, k); break;
+    case 3: fmac_row_bcast4<3, 3, 3, 3>(p, q, k); break;
+    case 4: fmac_row_bcast4<4, 4, 4, 4>(p, q, k); break;
+    case 5: fmac_row_bcast4<5, 5, 5, 5>(p, q, k); break;
+    case 6: fmac_row_bcast4<6, 6, 6, 6>(p, q, k); break;
+    case 7: fmac_row_bcast4<7, 7, 7, 7>(p, q, k); break;
+    case 8: fmac_row_bcast4<8, 8, 8, 8>(p, q, k); break;
+    case 9: fmac_row_bcast4<9, 9, 9, 9>(p, q, k); break;
+    case 10: fmac_row_bcast4<10, 10, 10, 10>(p, q, k); break;
+    case 11: fmac_row_bcast4<11, 11, 11, 11>(p, q, k); break;
+    case 12: fmac_row_bcast4<12, 12, 12, 12>(p, q, k); break;
+    case 13: fmac_row_bcast4<13, 13, 13, 13>(p, q, k); break;
+    case 14: fmac_row_bcast4<14, 14, 14, 14>(p, q, k); break;
+    default: fmac_row_bcast4<15, 15, 15, 15>(p, q, k); break;
+    }
+}
+
 // C channels a lane (head width 64 C), H heads, G of them a workgroup
 // (blockIdx.z picks the group; the groups of one key tile share the tile's
 // rows through the L2).  Scores: wave w takes a quarter of the channels and
@@ -872,6 +897,13 @@ __global__ __launch_bounds__(kRowsThreads, 3) void attention_rows_kernel(RowsAtt
         values[(int64_t) pos * hd + t] = sVnew[t];
     }
 
+    // this lane's channel of the group's queries: lane c of a 16-lane row holds
+    // channel c of the row's slice, for every head of the group
+    double qLane[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+        qLane[h] = sQd[h][ch0 + min(kg, kSliceCh - 1)];
+
     double acc[G][C];
 #pragma unroll
     for (int h = 0; h < G; ++h)
@@ -890,12 +922,13 @@ __global__ __launch_bounds__(kRowsThreads, 3) void attention_rows_kernel(RowsAtt
                     load_key_slice(kq[j], sKnew + ch0);
         }
         // this lane's keys against every head of the group over its slice
-        double p[kLaneKeys][G];
+        double p[G][kLaneKeys];
 #pragma unroll
-        for (int j = 0; j < kLaneKeys; ++j)
+        for (int h = 0; h < G; ++h)
 #pragma unroll
-            for (int h = 0; h < G; ++h)
-                p[j][h] = 0.0;
+            for (int j = 0; j < kLaneKeys; ++j)
+                p[h][j] = 0.0;
+        // channel c of the slice takes its query from lane c of the row
 #pragma unroll
         for (int w = 0; w < kSliceWords; ++w) {
             double ka[kLaneKeys], kb[kLaneKeys];
@@ -906,12 +939,8 @@ __global__ __launch_bounds__(kRowsThreads, 3) void attention_rows_kernel(RowsAtt
             }
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                const double2 qq = *reinterpret_cast<const double2 *>(&sQd[h][ch0 + 2 * w]);
-#pragma unroll
-                for (int j = 0; j < kLaneKeys; ++j) {
-                    p[j][h] = fma(qq.x, ka[j], p[j][h]);
-                    p[j][h] = fma(qq.y, kb[j], p[j][h]);
-                }
+                row_channel_fmac(2 * w, p[h], qLane[h], ka);
+                row_channel_fmac(2 * w + 1, p[h], qLane[h], kb);
             }
         }
         const int part = wave * kSlices + (lane >> 4); // the slice's place in channel order
@@ -919,7 +948,7 @@ __global__ __launch_bounds__(kRowsThreads, 3) void attention_rows_kernel(RowsAtt
         for (int j = 0; j < kLaneKeys; ++j)
 #pragma unroll
             for (int h = 0; h < G; ++h)
-                sP[part][h][kg + 16 * j] = p[j][h];
+                sP[part][h][kg + 16 * j] = p[h][j];
         // the tile's value rows: their round trip overlaps the softmax
         load_values(t0);
         __syncthreads();

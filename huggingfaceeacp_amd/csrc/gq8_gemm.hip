@@ -27,6 +27,7 @@
 // B[l % 16][8 (l / 16) .. + 8); D[i][j] lands in lane 16 (i / 4) + j,
 // element i % 4.
 #include "gq8_kernels.hpp"
+#include "gq8_lanes.hpp"
 #include "gq8_numerics.hpp"
 
 namespace gq8 {
@@ -46,29 +47,14 @@ constexpr int kStageScales = kStageRows * kChunk;                           // 1
 constexpr int kScalePieces = (kStageScales + kGemmThreads - 1) / kGemmThreads; // 3 a thread
 
 // acc[j][r] += part[j][r] * s', r = 0..3, where s' is the s held by lane
-// 4 Q + r of this lane's 16-lane row: v_fmac_f64 with a DPP row_newbcast
-// source operand, so the row's scales travel between lanes inside the
-// multiply-add itself (no LDS read, no extra instruction).  A fused
-// multiply-add rounds acc + part * s' once, as acc + d * (sw * sx) does: both
-// products are exact in double.  The leading s_nop 1 gives the two wait
-// states a DPP source needs after a VALU write of its register.
+// 4 Q + r of this lane's 16-lane row (a DPP broadcast inside the
+// multiply-add).  It rounds acc + part * s' once, as acc + d * (sw * sx)
+// does: both products are exact in double.
 template <int Q>
 __device__ inline void fmac_row_scales(double (&acc)[2][4], double s, const double (&part)[2][4])
 {
-    asm volatile("s_nop 1\n\t"
-                 "v_fmac_f64_dpp %0, %8, %9 row_newbcast:%17 row_mask:0xf bank_mask:0xf\n\t"
-                 "v_fmac_f64_dpp %1, %8, %10 row_newbcast:%18 row_mask:0xf bank_mask:0xf\n\t"
-                 "v_fmac_f64_dpp %2, %8, %11 row_newbcast:%19 row_mask:0xf bank_mask:0xf\n\t"
-                 "v_fmac_f64_dpp %3, %8, %12 row_newbcast:%20 row_mask:0xf bank_mask:0xf\n\t"
-                 "v_fmac_f64_dpp %4, %8, %13 row_newbcast:%17 row_mask:0xf bank_mask:0xf\n\t"
-                 "v_fmac_f64_dpp %5, %8, %14 row_newbcast:%18 row_mask:0xf bank_mask:0xf\n\t"
-                 "v_fmac_f64_dpp %6, %8, %15 row_newbcast:%19 row_mask:0xf bank_mask:0xf\n\t"
-                 "v_fmac_f64_dpp %7, %8, %16 row_newbcast:%20 row_mask:0xf bank_mask:0xf"
-                 : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[0][2]), "+v"(acc[0][3]),
-                   "+v"(acc[1][0]), "+v"(acc[1][1]), "+v"(acc[1][2]), "+v"(acc[1][3])
-                 : "v"(s), "v"(part[0][0]), "v"(part[0][1]), "v"(part[0][2]), "v"(part[0][3]),
-                   "v"(part[1][0]), "v"(part[1][1]), "v"(part[1][2]), "v"(part[1][3]),
-                   "n"(4 * Q), "n"(4 * Q + 1), "n"(4 * Q + 2), "n"(4 * Q + 3));
+    fmac_row_bcast4<4 * Q, 4 * Q + 1, 4 * Q + 2, 4 * Q + 3>(acc[0], s, part[0]);
+    fmac_row_bcast4<4 * Q, 4 * Q + 1, 4 * Q + 2, 4 * Q + 3>(acc[1], s, part[1]);
 }
 
 // kGeglu: the gate|up product of a fused [2 F, inner] weight (gate rows

@@ -141,4 +141,26 @@ __device__ inline double lane_value(double v, int lane)
     return __longlong_as_double((long long) (((uint64_t) hi << 32) | lo));
 }
 
+// acc[r] += s' x part[r], r = 0..3, where s' is the s held by lane N_r of this
+// lane's row of 16: v_fmac_f64 with a DPP row_newbcast source operand, so the
+// value crosses lanes inside the multiply-add itself (no LDS read, no extra
+// instruction).  One rounding, as fma(s', part[r], acc[r]).  The leading
+// s_nop 1 gives the two wait states a DPP source needs after a VALU write of
+// its register.
+template <int N0, int N1, int N2, int N3>
+__device__ inline void fmac_row_bcast4(double (&acc)[4], double s, const double (&part)[4])
+{
+    static_assert(N0 >= 0 && N0 < 16 && N1 >= 0 && N1 < 16 && N2 >= 0 && N2 < 16 && N3 >= 0
+                      && N3 < 16,
+                  "a lane of the row");
+    asm volatile("s_nop 1\n\t"
+                 "v_fmac_f64_dpp %0, %4, %5 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f64_dpp %1, %4, %6 row_newbcast:%10 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f64_dpp %2, %4, %7 row_newbcast:%11 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f64_dpp %3, %4, %8 row_newbcast:%12 row_mask:0xf bank_mask:0xf"
+                 : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3])
+                 : "v"(s), "v"(part[0]), "v"(part[1]), "v"(part[2]), "v"(part[3]),
+                   "n"(N0), "n"(N1), "n"(N2), "n"(N3));
+}
+
 } // namespace gq8
