@@ -35,6 +35,7 @@
 #include "gq8_numerics.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace gq8 {
 namespace {
@@ -737,28 +738,38 @@ __device__ inline Halves<C> load_channels(const uint16_t *p)
     return h;
 }
 
-// p[j] += q' k[j] for a lane's four keys, where q' is the query channel that
-// lane c of the lane's 16-lane row holds (c constant once the caller's loop
-// is unrolled, so the switch folds away)
-__device__ inline void row_channel_fmac(int c, double (&p)[4], double q, const double (&k)[4])
+// f(std::integral_constant<int, i>) for i = 0 .. N - 1, in order
+template <int N, typename F>
+__device__ inline void unrolled(F &&f)
 {
-    switch (c) {
-    case 0: fmac_row_bcast4<0, 0, 0, 0>(p, q, k); break;
-    case 1: fmac_row_bcast4<1, 1, 1, 1>(p, q, k); break;
-    case 2: fmac_row_bcast4<2, 2, 2, 2>(p, q, k); break;
-    case 3: fmac_row_bcast4<3, 3, 3, 3>(p, q, k); break;
-    case 4: fmac_row_bcast4<4, 4, 4, 4>(p, q, k); break;
-    case 5: fmac_row_bcast4<5, 5, 5, 5>(p, q, k); break;
-    case 6: fmac_row_bcast4<6, 6, 6, 6>(p, q, k); break;
-    case 7: fmac_row_bcast4<7, 7, 7, 7>(p, q, k); break;
-    case 8: fmac_row_bcast4<8, 8, 8, 8>(p, q, k); break;
-    case 9: fmac_row_bcast4<9, 9, 9, 9>(p, q, k); break;
-    case 10: fmac_row_bcast4<10, 10, 10, 10>(p, q, k); break;
-    case 11: fmac_row_bcast4<11, 11, 11, 11>(p, q, k); break;
-    case 12: fmac_row_bcast4<12, 12, 12, 12>(p, q, k); break;
-    case 13: fmac_row_bcast4<13, 13, 13, 13>(p, q, k); break;
-    case 14: fmac_row_bcast4<14, 14, 14, 14>(p, q, k); break;
-    default: fmac_row_bcast4<15, 15, 15, 15>(p, q, k); break;
+    if constexpr (N > 0) {
+        unrolled<N - 1>(f);
+        f(std::integral_constant<int, N - 1>{});
+    }
+}
+
+// p[j] += s' x[j], j = 0..3, where s' is the s that lane n of the lane's
+// 16-lane row holds (n constant once the caller's loop is unrolled, so the
+// switch folds away)
+__device__ inline void row_lane_fmac(int n, double (&p)[4], double s, const double (&x)[4])
+{
+    switch (n) {
+    case 0: fmac_row_bcast4<0, 0, 0, 0>(p, s, x); break;
+    case 1: fmac_row_bcast4<1, 1, 1, 1>(p, s, x); break;
+    case 2: fmac_row_bcast4<2, 2, 2, 2>(p, s, x); break;
+    case 3: fmac_row_bcast4<3, 3, 3, 3>(p, s, x); break;
+    case 4: fmac_row_bcast4<4, 4, 4, 4>(p, s, x); break;
+    case 5: fmac_row_bcast4<5, 5, 5, 5>(p, s, x); break;
+    case 6: fmac_row_bcast4<6, 6, 6, 6>(p, s, x); break;
+    case 7: fmac_row_bcast4<7, 7, 7, 7>(p, s, x); break;
+    case 8: fmac_row_bcast4<8, 8, 8, 8>(p, s, x); break;
+    case 9: fmac_row_bcast4<9, 9, 9, 9>(p, s, x); break;
+    case 10: fmac_row_bcast4<10, 10, 10, 10>(p, s, x); break;
+    case 11: fmac_row_bcast4<11, 11, 11, 11>(p, s, x); break;
+    case 12: fmac_row_bcast4<12, 12, 12, 12>(p, s, x); break;
+    case 13: fmac_row_bcast4<13, 13, 13, 13>(p, s, x); break;
+    case 14: fmac_row_bcast4<14, 14, 14, 14>(p, s, x); break;
+    default: fmac_row_bcast4<15, 15, 15, 15>(p, s, x); break;
     }
 }
 
@@ -939,8 +950,8 @@ __global__ __launch_bounds__(kRowsThreads, 3) void attention_rows_kernel(RowsAtt
             }
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                row_channel_fmac(2 * w, p[h], qLane[h], ka);
-                row_channel_fmac(2 * w + 1, p[h], qLane[h], kb);
+                row_lane_fmac(2 * w, p[h], qLane[h], ka);
+                row_lane_fmac(2 * w + 1, p[h], qLane[h], kb);
             }
         }
         const int part = wave * kSlices + (lane >> 4); // the slice's place in channel order
@@ -989,22 +1000,36 @@ __global__ __launch_bounds__(kRowsThreads, 3) void attention_rows_kernel(RowsAtt
             for (int c = 0; c < C; ++c)
                 acc[h][c] *= f;
         }
+        // (four channels a lane: lane i of each 16-lane row holds key i's
+        // weights, which the multiply-adds take by DPP broadcast)
+        double wLane[G];
+        if constexpr (C == 4)
 #pragma unroll
-        for (int i = 0; i < kRowsWaveKeys; ++i) {
-            if (wave * kRowsWaveKeys + i >= nk) // rows past the position may hold anything
-                break;
+            for (int h = 0; h < G; ++h)
+                wLane[h] = sS[h][wave * kRowsWaveKeys + (lane & 15)];
+        // (the keys as compile-time indices: a loop with an early exit is not
+        // unrolled, and vh would be indexed from scratch memory)
+        const int keysHere = nk - wave * kRowsWaveKeys; // rows past the position may hold anything
+        unrolled<kRowsWaveKeys>([&](auto key) {
+            constexpr int i = decltype(key)::value;
+            if (i >= keysHere)
+                return;
             double v[C];
 #pragma unroll
             for (int c = 0; c < C; ++c)
                 v[c] = (double) vh[i].at(c);
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                const double wi = sS[h][wave * kRowsWaveKeys + i];
+                if constexpr (C == 4) {
+                    fmac_row_bcast4<i, i, i, i>(acc[h], wLane[h], v);
+                } else {
+                    const double wi = sS[h][wave * kRowsWaveKeys + i];
 #pragma unroll
-                for (int c = 0; c < C; ++c)
-                    acc[h][c] += wi * v[c];
+                    for (int c = 0; c < C; ++c)
+                        acc[h][c] += wi * v[c];
+                }
             }
-        }
+        });
         __syncthreads(); // the next tile rewrites the scores
     }
 
