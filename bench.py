@@ -46,7 +46,7 @@ INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 # for a 256 MiB copy, plus WRITE_SIZE); the passes, their commands and the
 # calibration are in TRAFFIC_SOURCE.
 TRAFFIC_SOURCE = "profiles/decode_kernels_gemma2b_hbm_traffic.md"
-MEASURED_TRAFFIC = {"gate_up": 71543312, "lm_head": 558244532, "down": 35967824}
+MEASURED_TRAFFIC = {"gate_up": 71542751, "lm_head": 558436311, "down": 35961103}
 METRIC = "Gemma-2B Q8_0 decode tok/s (b=1, ctx 512) + % of HBM roofline"
 STAGE_LABELS = {
     "gate_up": "gateup_geglu_kernel (post-attention norm + gate|up 2048 -> 2x16384 + GeGLU + Q8)",
