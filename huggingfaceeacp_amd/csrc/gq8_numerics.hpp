@@ -15,6 +15,21 @@
 
 #define GQ8_HD __host__ __device__ inline
 
+namespace gq8 {
+// A double constant held in a scalar register pair on the device: a VALU
+// fused multiply-add then reads it as its addend, where a literal addend is
+// rebuilt in the destination register by two v_mov_b32 before each
+// v_fmac_f64.  The value is unchanged; the host pass takes it as it is.
+__host__ __device__ inline double scalar_constant(double c)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm("" : "=s"(c) : "0"(c));
+#endif
+    return c;
+}
+} // namespace gq8
+#define GQ8_CONST(c) ::gq8::scalar_constant(c)
+
 #include "gq8_tanh.hpp"
 
 namespace gq8 {
@@ -108,8 +123,8 @@ __device__ inline float quantize_hint(float scale)
 GQ8_HD double tanh_gelu(double x)
 {
 #pragma clang fp contract(off)
-    const double rootTwoOverPi = 0.7978845608028654;
-    const double inner = rootTwoOverPi * (x + 0.044715 * x * x * x);
+    const double rootTwoOverPi = GQ8_CONST(0.7978845608028654);
+    const double inner = rootTwoOverPi * (x + GQ8_CONST(0.044715) * x * x * x);
     const double t = inner >= 10.0 ? 1.0 : (inner <= -10.0 ? -1.0 : tanh_from_exp(inner));
     return 0.5 * x * (1.0 + t);
 }

@@ -21,28 +21,34 @@
 #ifndef GQ8_HD
 #define GQ8_HD inline
 #endif
+// GQ8_CONST(c): a constant as its callers want it held (the device build
+// keeps it in scalar registers, where a fused multiply-add reads it as an
+// operand); the constant itself unchanged
+#ifndef GQ8_CONST
+#define GQ8_CONST(c) (c)
+#endif
 
 namespace gq8 {
 
 GQ8_HD double tanh_from_exp(double x)
 {
-    const double ln2Head = 0x1.62e42feep-1;           // ln2 to 32 significant bits
-    const double ln2Tail = 0x1.a39ef35793c76p-33;     // ln2 - head
-    const double invLn2 = 1.4426950408889634;
+    const double ln2Head = GQ8_CONST(0x1.62e42feep-1);       // ln2 to 32 significant bits
+    const double ln2Tail = GQ8_CONST(0x1.a39ef35793c76p-33); // ln2 - head
+    const double invLn2 = GQ8_CONST(1.4426950408889634);
     const double z = 2.0 * fabs(x);
     const double n = rint(z * invLn2);
     const double r = fma(-n, ln2Tail, fma(-n, ln2Head, z));
-    double p = 1.6059043836821613e-10;                // 1/13!
-    p = fma(p, r, 2.08767569878681e-09);              // 1/12!
-    p = fma(p, r, 2.505210838544172e-08);             // 1/11!
-    p = fma(p, r, 2.755731922398589e-07);             // 1/10!
-    p = fma(p, r, 2.7557319223985893e-06);            // 1/9!
-    p = fma(p, r, 2.48015873015873e-05);              // 1/8!
-    p = fma(p, r, 0.0001984126984126984);             // 1/7!
-    p = fma(p, r, 0.001388888888888889);              // 1/6!
-    p = fma(p, r, 0.008333333333333333);              // 1/5!
-    p = fma(p, r, 0.041666666666666664);              // 1/4!
-    p = fma(p, r, 0.16666666666666666);               // 1/3!
+    double p = GQ8_CONST(1.6059043836821613e-10);     // 1/13!
+    p = fma(p, r, GQ8_CONST(2.08767569878681e-09));   // 1/12!
+    p = fma(p, r, GQ8_CONST(2.505210838544172e-08));  // 1/11!
+    p = fma(p, r, GQ8_CONST(2.755731922398589e-07));  // 1/10!
+    p = fma(p, r, GQ8_CONST(2.7557319223985893e-06)); // 1/9!
+    p = fma(p, r, GQ8_CONST(2.48015873015873e-05));   // 1/8!
+    p = fma(p, r, GQ8_CONST(0.0001984126984126984));  // 1/7!
+    p = fma(p, r, GQ8_CONST(0.001388888888888889));   // 1/6!
+    p = fma(p, r, GQ8_CONST(0.008333333333333333));   // 1/5!
+    p = fma(p, r, GQ8_CONST(0.041666666666666664));   // 1/4!
+    p = fma(p, r, GQ8_CONST(0.16666666666666666));    // 1/3!
     p = fma(p, r, 0.5);                               // 1/2!
     p = fma(p, r, 1.0);                               // 1/1!
     p = p * r;                                        // expm1(r)
