@@ -35,7 +35,6 @@
 #include "gq8_numerics.hpp"
 
 #include <algorithm>
-#include <type_traits>
 
 namespace gq8 {
 namespace {
@@ -736,16 +735,6 @@ __device__ inline Halves<C> load_channels(const uint16_t *p)
         h.w[0] = *p;
     }
     return h;
-}
-
-// f(std::integral_constant<int, i>) for i = 0 .. N - 1, in order
-template <int N, typename F>
-__device__ inline void unrolled(F &&f)
-{
-    if constexpr (N > 0) {
-        unrolled<N - 1>(f);
-        f(std::integral_constant<int, N - 1>{});
-    }
 }
 
 // p[j] += s' x[j], j = 0..3, where s' is the s that lane n of the lane's

@@ -14,6 +14,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace gq8 {
 
 template <int D>
@@ -161,6 +163,17 @@ __device__ inline void fmac_row_bcast4(double (&acc)[4], double s, const double 
                  : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3])
                  : "v"(s), "v"(part[0]), "v"(part[1]), "v"(part[2]), "v"(part[3]),
                    "n"(N0), "n"(N1), "n"(N2), "n"(N3));
+}
+
+// f(std::integral_constant<int, i>) for i = 0 .. N - 1, in order: a loop body
+// with compile-time indices (DPP lane numbers, register arrays)
+template <int N, typename F>
+__device__ inline void unrolled(F &&f)
+{
+    if constexpr (N > 0) {
+        unrolled<N - 1>(f);
+        f(std::integral_constant<int, N - 1>{});
+    }
 }
 
 } // namespace gq8
