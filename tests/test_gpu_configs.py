@@ -11,7 +11,7 @@
 
 What is held exactly: every greedy id, and the Q8 bytes of every layer's
 product inputs (normalised, attended, activated) and of the final norm, as
-SHA-256 digests of the oracle's bytes.  Logits: the north-star bar is 1e-2
+SHA-256 digests of the oracle's bytes.  Logits: the metric's bar is 1e-2
 relative (|a - e| / (1 + |e|)); the GPU and the oracle differ only in the
 order of their double sums, so the tests also hold them to 1e-5 and print the
 bit-identical fraction.  The reference's loop tests compare the same things
@@ -31,7 +31,7 @@ from huggingfaceeacp_amd import gemma_q8 as G
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
-LOGIT_TOLERANCE = 1e-2   # the north star's relative bar
+LOGIT_TOLERANCE = 1e-2   # the metric's relative bar
 SUM_ORDER_TOLERANCE = 1e-5
 VARIED_SEED = 0x6A00
 
