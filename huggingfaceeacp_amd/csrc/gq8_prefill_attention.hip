@@ -100,12 +100,17 @@ void prefill_attention_kernel(PrefillArgs a)
     constexpr int HD = 4 * E, T = HD / 16;
     constexpr int KW = E / 2, VW = T / 2; // words of a lane's key channels / value channels
     constexpr int kBlockLanes = kBlock / T;  // lanes holding one 32-channel block of an output row
-    constexpr int kMergeTiles = T < 2 ? T : 2;
+    constexpr int kMergeTiles = T < 4 ? T : 4;
     // the merge: every wave's maxima and scaled sums of the rows g + 4 r, and
-    // kMergeTiles column tiles of waves 1..3's output sums at a time
+    // kMergeTiles column tiles of every wave's output sums at a time (over
+    // the query rows, which no wave reads once all are past their tiles)
     __shared__ double sMax[kPaWaves][4][64], sSum[kPaWaves][4][64];
-    __shared__ double sPart[kPaWaves - 1][kMergeTiles * 4][64];
-    __shared__ __align__(16) float sQ[kPaRows][HD + 4]; // padded: a 16-lane group's rows on distinct banks
+    constexpr int kQBytes = kPaRows * (HD + 4) * (int) sizeof(float);
+    constexpr int kPartBytes = kPaWaves * kMergeTiles * 4 * 64 * (int) sizeof(double);
+    __shared__ __align__(16) unsigned char sQPart[kQBytes > kPartBytes ? kQBytes : kPartBytes];
+    // padded: a 16-lane group's rows on distinct banks
+    float (*sQ)[HD + 4] = reinterpret_cast<float (*)[HD + 4]>(sQPart);
+    double (*sPart)[kMergeTiles][4][64] = reinterpret_cast<double (*)[kMergeTiles][4][64]>(sQPart);
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int g = lane >> 4, j = lane & 15;
@@ -234,16 +239,16 @@ void prefill_attention_kernel(PrefillArgs a)
         lO[r] = __shfl(l, g + 4 * r);
     }
 
-    // merge the waves' states into wave 0.  Every wave scales its sums to the
-    // rows' common maximum (wave 0 holds tile 0, which every row attends, so
-    // that maximum is finite; a wave whose keys a row never reached has m =
-    // -inf and weighs nothing), then waves 1..3 hand wave 0 their sums
-    // kMergeTiles column tiles at a time, so wave 0 never holds another
-    // wave's whole state in registers beside its own.
+    // merge the waves' states.  Every wave scales its sums to the rows'
+    // common maximum (wave 0 holds tile 0, which every row attends, so that
+    // maximum is finite; a wave whose keys a row never reached has m = -inf
+    // and weighs nothing); then the waves exchange their sums kMergeTiles
+    // column tiles at a time, and wave w adds the four waves' sums of its
+    // rows g + 4 w in wave order and finishes those rows.
 #pragma unroll
     for (int r = 0; r < 4; ++r)
         sMax[wave][r][lane] = mO[r];
-    __syncthreads();
+    __syncthreads(); // (also: every wave is past its tiles, so sQ is free)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         double common = sMax[0][r][lane];
@@ -257,47 +262,42 @@ void prefill_attention_kernel(PrefillArgs a)
             o[n][r] *= f;
         sSum[wave][r][lane] = lO[r];
     }
+    double mine[T]; // the four waves' sums of row g + 4 wave, column tile n
 #pragma unroll
     for (int n0 = 0; n0 < T; n0 += kMergeTiles) {
+        if (n0 > 0)
+            __syncthreads(); // the previous tiles have been read
+#pragma unroll
+        for (int n = 0; n < kMergeTiles; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                sPart[wave][n][r][lane] = o[n0 + n][r];
         __syncthreads();
-        if (wave != 0) {
 #pragma unroll
-            for (int n = 0; n < kMergeTiles; ++n)
+        for (int n = 0; n < kMergeTiles; ++n) {
+            double v = sPart[0][n][wave][lane];
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    sPart[wave - 1][n * 4 + r][lane] = o[n0 + n][r];
-        }
-        __syncthreads();
-        if (wave == 0) {
-#pragma unroll
-            for (int w = 0; w < kPaWaves - 1; ++w)
-#pragma unroll
-                for (int n = 0; n < kMergeTiles; ++n)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        o[n0 + n][r] += sPart[w][n * 4 + r][lane];
+            for (int w = 1; w < kPaWaves; ++w)
+                v += sPart[w][n][wave][lane];
+            mine[n0 + n] = v;
         }
     }
-    if (wave != 0)
-        return;
+    double total = sSum[0][wave][lane];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int w = 1; w < kPaWaves; ++w)
-            lO[r] += sSum[w][r][lane];
+    for (int w = 1; w < kPaWaves; ++w)
+        total += sSum[w][wave][lane];
 
-    // rows g + 4 r, channels [j T, j T + T): fp32, then Q8 per 32-block
+    // row g + 4 wave, channels [j T, j T + T): fp32, then Q8 per 32-block
     // (kBlockLanes neighbouring lanes a block)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int row = g + 4 * r;
+    {
+        const int row = g + 4 * wave;
         const bool live = row < rowsHere;
         const int64_t at = (int64_t) (r0 + min(row, rowsHere - 1)) * qWidth + h * HD + j * T;
         float v[T];
         float amax = 0.f;
 #pragma unroll
         for (int n = 0; n < T; ++n) {
-            v[n] = (float) (o[n][r] / lO[r]);
+            v[n] = (float) (mine[n] / total);
             amax = fmaxf(amax, fabsf(v[n]));
         }
         if (a.out && live) {
