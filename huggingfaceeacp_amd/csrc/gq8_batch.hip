@@ -707,8 +707,8 @@ __global__ __launch_bounds__(kRowsThreads) void tile_weights_kernel(const uint8_
 }
 
 // ---- attention of the lockstep rows ---------------------------------------------
-constexpr int kRowsTileKeys = 64;   // keys a tile (16 a key wave)
-constexpr int kRowsWaveKeys = 16;
+constexpr int kRowsTileKeys = 80;   // keys a tile (a split): five of a lane's 16-lane row
+constexpr int kRowsWaveKeys = kRowsTileKeys / kRowsWaves; // a wave's keys of the values
 constexpr int kRowsHeadGroup = 4;   // query heads a workgroup
 
 // C consecutive fp16 channels kept packed, two a register.
@@ -737,29 +737,21 @@ __device__ inline Halves<C> load_channels(const uint16_t *p)
     return h;
 }
 
-// p[j] += s' x[j], j = 0..3, where s' is the s that lane n of the lane's
-// 16-lane row holds (n constant once the caller's loop is unrolled, so the
-// switch folds away)
-__device__ inline void row_lane_fmac(int n, double (&p)[4], double s, const double (&x)[4])
+// p[j] += s' x[j], j < K, where s' is the s that lane N of the lane's
+// 16-lane row holds: four accumulators an instruction group, then the rest
+// one at a time
+template <int N, int K>
+__device__ inline void row_lane_fmac(double (&p)[K], double s, const double (&x)[K])
 {
-    switch (n) {
-    case 0: fmac_row_bcast4<0, 0, 0, 0>(p, s, x); break;
-    case 1: fmac_row_bcast4<1, 1, 1, 1>(p, s, x); break;
-    case 2: fmac_row_bcast4<2, 2, 2, 2>(p, s, x); break;
-    case 3: fmac_row_bcast4<3, 3, 3, 3>(p, s, x); break;
-    case 4: fmac_row_bcast4<4, 4, 4, 4>(p, s, x); break;
-    case 5: fmac_row_bcast4<5, 5, 5, 5>(p, s, x); break;
-    case 6: fmac_row_bcast4<6, 6, 6, 6>(p, s, x); break;
-    case 7: fmac_row_bcast4<7, 7, 7, 7>(p, s, x); break;
-    case 8: fmac_row_bcast4<8, 8, 8, 8>(p, s, x); break;
-    case 9: fmac_row_bcast4<9, 9, 9, 9>(p, s, x); break;
-    case 10: fmac_row_bcast4<10, 10, 10, 10>(p, s, x); break;
-    case 11: fmac_row_bcast4<11, 11, 11, 11>(p, s, x); break;
-    case 12: fmac_row_bcast4<12, 12, 12, 12>(p, s, x); break;
-    case 13: fmac_row_bcast4<13, 13, 13, 13>(p, s, x); break;
-    case 14: fmac_row_bcast4<14, 14, 14, 14>(p, s, x); break;
-    default: fmac_row_bcast4<15, 15, 15, 15>(p, s, x); break;
-    }
+    static_assert(K >= 4 && K < 8, "four to seven keys a lane");
+    fmac_row_bcast4<N, N, N, N>(reinterpret_cast<double (&)[4]>(p), s,
+                                reinterpret_cast<const double (&)[4]>(x));
+    if constexpr (K > 4)
+        fmac_row_bcast1<N>(p[4], s, x[4]);
+    if constexpr (K > 5)
+        fmac_row_bcast1<N>(p[5], s, x[5]);
+    if constexpr (K > 6)
+        fmac_row_bcast1<N>(p[6], s, x[6]);
 }
 
 // C channels a lane (head width 64 C), H heads, G of them a workgroup
@@ -772,7 +764,7 @@ __device__ inline void row_lane_fmac(int n, double (&p)[4], double s, const doub
 // Values: lane l takes channels C l .. C l + C - 1 and wave w keys
 // t0 + 16 w .. + 15, every head of the group.
 template <int C, int H, int G>
-__global__ __launch_bounds__(kRowsThreads, 3) void attention_rows_kernel(RowsAttentionArgs a)
+__global__ __launch_bounds__(kRowsThreads, 2) void attention_rows_kernel(RowsAttentionArgs a)
 {
     static_assert(H % G == 0, "whole head groups");
     constexpr int hd = 64 * C, half = hd / 2, qW = H * hd;
@@ -929,8 +921,8 @@ __global__ __launch_bounds__(kRowsThreads, 3) void attention_rows_kernel(RowsAtt
             for (int j = 0; j < kLaneKeys; ++j)
                 p[h][j] = 0.0;
         // channel c of the slice takes its query from lane c of the row
-#pragma unroll
-        for (int w = 0; w < kSliceWords; ++w) {
+        unrolled<kSliceWords>([&](auto word) {
+            constexpr int w = decltype(word)::value;
             double ka[kLaneKeys], kb[kLaneKeys];
 #pragma unroll
             for (int j = 0; j < kLaneKeys; ++j) {
@@ -939,10 +931,10 @@ __global__ __launch_bounds__(kRowsThreads, 3) void attention_rows_kernel(RowsAtt
             }
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                row_lane_fmac(2 * w, p[h], qLane[h], ka);
-                row_lane_fmac(2 * w + 1, p[h], qLane[h], kb);
+                row_lane_fmac<2 * w>(p[h], qLane[h], ka);
+                row_lane_fmac<2 * w + 1>(p[h], qLane[h], kb);
             }
-        }
+        });
         const int part = wave * kSlices + (lane >> 4); // the slice's place in channel order
 #pragma unroll
         for (int j = 0; j < kLaneKeys; ++j)
@@ -954,18 +946,33 @@ __global__ __launch_bounds__(kRowsThreads, 3) void attention_rows_kernel(RowsAtt
         __syncthreads();
         // the tile's softmax against the running maximum, a wave a head; the
         // slices' dots added in channel order
+        // (keys lane and, past 64, lane + 64 of the tile)
+        constexpr int kSoftKeys = (kRowsTileKeys + 63) / 64;
         for (int h = wave; h < G; h += kRowsWaves) {
-            double dot = sP[0][h][lane];
+            double sc[kSoftKeys];
+            double laneMax = -INFINITY;
 #pragma unroll
-            for (int q = 1; q < kParts; ++q)
-                dot += sP[q][h][lane];
-            const double sc = lane < nk ? (double) a.scale * dot : -INFINITY;
-            const double tileMax = wave_max_d(sc);
+            for (int k = 0; k < kSoftKeys; ++k) {
+                const int key = min(lane + 64 * k, kRowsTileKeys - 1);
+                double dot = sP[0][h][key];
+#pragma unroll
+                for (int q = 1; q < kParts; ++q)
+                    dot += sP[q][h][key];
+                sc[k] = lane + 64 * k < nk ? (double) a.scale * dot : -INFINITY;
+                laneMax = fmax(laneMax, sc[k]);
+            }
+            const double tileMax = wave_max_d(laneMax);
             const double previous = sMax[h];
             const double largest = fmax(previous, tileMax);
-            const double w = lane < nk ? exp(sc - largest) : 0.0;
-            const double total = wave_sum_d(w);
-            sS[h][lane] = w;
+            double laneSum = 0.0;
+#pragma unroll
+            for (int k = 0; k < kSoftKeys; ++k) {
+                const double w = lane + 64 * k < nk ? exp(sc[k] - largest) : 0.0;
+                laneSum += w;
+                if (lane + 64 * k < kRowsTileKeys)
+                    sS[h][lane + 64 * k] = w;
+            }
+            const double total = wave_sum_d(laneSum);
             if (lane == 0) {
                 const double factor = previous == -INFINITY ? 0.0 : exp(previous - largest);
                 sF[h] = factor;
@@ -991,11 +998,16 @@ __global__ __launch_bounds__(kRowsThreads, 3) void attention_rows_kernel(RowsAtt
         }
         // (four channels a lane: lane i of each 16-lane row holds key i's
         // weights, which the multiply-adds take by DPP broadcast)
-        double wLane[G];
+        // (keys 16 .. 19 of a wave's 20 from a second register: lane i of
+        // each row holds key 16 + i)
+        static_assert(kRowsWaveKeys <= 32, "two broadcast registers");
+        double wLane[G], wLane2[G];
         if constexpr (C == 4)
 #pragma unroll
-            for (int h = 0; h < G; ++h)
-                wLane[h] = sS[h][wave * kRowsWaveKeys + (lane & 15)];
+            for (int h = 0; h < G; ++h) {
+                wLane[h] = sS[h][wave * kRowsWaveKeys + min(lane & 15, kRowsWaveKeys - 1)];
+                wLane2[h] = sS[h][wave * kRowsWaveKeys + min(16 + (lane & 15), kRowsWaveKeys - 1)];
+            }
         // (the keys as compile-time indices: a loop with an early exit is not
         // unrolled, and vh would be indexed from scratch memory)
         const int keysHere = nk - wave * kRowsWaveKeys; // rows past the position may hold anything
@@ -1010,7 +1022,10 @@ __global__ __launch_bounds__(kRowsThreads, 3) void attention_rows_kernel(RowsAtt
 #pragma unroll
             for (int h = 0; h < G; ++h) {
                 if constexpr (C == 4) {
-                    fmac_row_bcast4<i, i, i, i>(acc[h], wLane[h], v);
+                    if constexpr (i < 16)
+                        fmac_row_bcast4<i, i, i, i>(acc[h], wLane[h], v);
+                    else
+                        fmac_row_bcast4<i - 16, i - 16, i - 16, i - 16>(acc[h], wLane2[h], v);
                 } else {
                     const double wi = sS[h][wave * kRowsWaveKeys + i];
 #pragma unroll

@@ -165,6 +165,18 @@ __device__ inline void fmac_row_bcast4(double (&acc)[4], double s, const double 
                    "n"(N0), "n"(N1), "n"(N2), "n"(N3));
 }
 
+// acc += s' x part, s' the s held by lane N of this lane's row of 16 (the
+// one-accumulator form of fmac_row_bcast4)
+template <int N>
+__device__ inline void fmac_row_bcast1(double &acc, double s, double part)
+{
+    static_assert(N >= 0 && N < 16, "a lane of the row");
+    asm volatile("s_nop 1\n\t"
+                 "v_fmac_f64_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+                 : "+v"(acc)
+                 : "v"(s), "v"(part), "n"(N));
+}
+
 // f(std::integral_constant<int, i>) for i = 0 .. N - 1, in order: a loop body
 // with compile-time indices (DPP lane numbers, register arrays)
 template <int N, typename F>
