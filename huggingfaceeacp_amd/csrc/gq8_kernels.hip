@@ -200,6 +200,50 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restri
         for (int w = 0; w < kThreads / 64; ++w)
             total += partial[w];
         const double scale = norm_scale(total, width, epsilon);
+        if constexpr (P == 1 && K == 8) {
+            // Many rows (a prefill): the normalized row goes through LDS so
+            // that a thread holds 8 consecutive elements, a 32-element
+            // block's four threads find its largest magnitude in two lane
+            // exchanges and compute its scale once, and the bytes leave in
+            // one 8-byte store.  The same values, maximum, scale and bytes
+            // as the per-element form below.
+            __shared__ __align__(16) float sRow[K * kThreads];
+#pragma unroll
+            for (int k = 0; k < K; ++k)
+                sRow[threadIdx.x + k * kThreads] = norm_value(xn[k], scale, wv[k]);
+            __syncthreads();
+            const int e0 = 8 * (int) threadIdx.x; // elements e0 .. e0 + 7, block e0 / 32
+            const float4 lo4 = *reinterpret_cast<const float4 *>(&sRow[e0]);
+            const float4 hi4 = *reinterpret_cast<const float4 *>(&sRow[e0 + 4]);
+            const float v[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
+            float amax = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                amax = fmaxf(amax, fabsf(v[i]));
+            amax = fmaxf(amax, xor_lane<1>(amax));
+            amax = fmaxf(amax, xor_lane<2>(amax));
+            const uint16_t bits = scale_bits_from_amax(amax);
+            const float sc = half_value(bits);
+            const float inv = quantize_hint(sc);
+            uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                packed[i / 4] |= (uint32_t) (uint8_t) (int8_t) quantize_in_block(v[i], bits, sc, inv)
+                                 << (8 * (i % 4));
+            if (e0 < width) { // whole 32-element blocks are live together
+                const int64_t at = (int64_t) row * width + e0;
+                if (y) {
+                    *reinterpret_cast<float4 *>(y + at) = lo4;
+                    *reinterpret_cast<float4 *>(y + at + 4) = hi4;
+                }
+                if (q8) {
+                    *reinterpret_cast<uint2 *>(q8 + at) = make_uint2(packed[0], packed[1]);
+                    if ((threadIdx.x & 3) == 0)
+                        reinterpret_cast<uint16_t *>(q8 + elements)[at / kBlock] = bits;
+                }
+            }
+            return;
+        }
         // every element's value, block scale and byte first (no branches, so
         // the K chains interleave), then the stores
         float v[KP], amax[KP];
