@@ -756,13 +756,14 @@ __device__ inline void row_lane_fmac(double (&p)[K], double s, const double (&x)
 
 // C channels a lane (head width 64 C), H heads, G of them a workgroup
 // (blockIdx.z picks the group; the groups of one key tile share the tile's
-// rows through the L2).  Scores: wave w takes a quarter of the channels and
-// its lane l keys t0 + l % 16 + 16 j (j < 4) over the quarter's slice l / 16
-// of C channels... 4 C channels, every head of the group, so each query pair
-// read from LDS serves four keys (the LDS reads, not the fp64 products, bound
-// this phase); the sixteen slices' dots are added in LDS in channel order.
+// rows through the L2), a split of per_split keys in tiles of kRowsTileKeys.
+// Scores: wave w takes a quarter of the channels and its lane l keys
+// t0 + l % 16 + 16 j (j < kLaneKeys) over the quarter's slice l / 16 of
+// 4 C channels, every head of the group; lane c of each 16-lane row holds
+// channel c of the slice's query, which the multiply-adds take by DPP
+// broadcast; the sixteen slices' dots are added in LDS in channel order.
 // Values: lane l takes channels C l .. C l + C - 1 and wave w keys
-// t0 + 16 w .. + 15, every head of the group.
+// t0 + kRowsWaveKeys w .. + kRowsWaveKeys - 1, every head of the group.
 template <int C, int H, int G>
 __global__ __launch_bounds__(kRowsThreads, 2) void attention_rows_kernel(RowsAttentionArgs a)
 {
