@@ -52,7 +52,7 @@ constexpr int kMergeBatch = 8;
 constexpr int kRowsBestSlots = 32;   // a row's greedy-pick slots (atomicMax targets)
 constexpr int kRowsBestStride = 16;  // 128 bytes between slots        // split partials a merge requests at once
 constexpr int kRowsStreamGroups = 512; // workgroups of a streamed product (two a compute unit)
-constexpr int kRowsStreamAhead = 4;    // weight chunks in flight a wave of a streamed product
+constexpr int kRowsStreamAhead = 8;    // weight chunks in flight a wave of a streamed product
 
 // A workgroup stages `range` blocks of the activation rows in LDS and its
 // waves stream weight rows against them.  Wide products (tiles >= 1024: gate
@@ -567,6 +567,9 @@ __global__ __launch_bounds__(kRowsThreads) void q8_rows_stream_kernel(RowsArgs a
 {
     constexpr int nb = NC * kChunkBlocks;
     constexpr int P = NC < kRowsStreamAhead ? NC : kRowsStreamAhead;
+    // the next group's chunk i + P - NC lands in buffer i % P and is read
+    // from buffer (i + P - NC) % P: the same one only when P divides NC
+    static_assert(NC % P == 0, "a whole number of buffer rounds a group");
     __shared__ __attribute__((aligned(16))) long sX[nb * 64];
     __shared__ __attribute__((aligned(16))) float sSx[nb * kBatchRows];
     __shared__ int sGroup[2];
