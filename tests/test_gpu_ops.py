@@ -127,7 +127,10 @@ def test_embed_bit_exact(torch_cuda):
     assert np.array_equal(out.cpu().numpy().reshape(tokens.size, width), expected)
 
 
-@pytest.mark.parametrize("width,rows", [(2048, 1), (2048, 5), (32, 3), (16384, 2)])
+# (rows past 64 take a workgroup a row; 1056 leaves part of its last 256-element
+# stretch past the row)
+@pytest.mark.parametrize("width,rows", [(2048, 1), (2048, 5), (32, 3), (16384, 2), (2048, 80),
+                                        (1056, 70)])
 def test_rmsnorm_and_q8(torch_cuda, width, rows):
     torch = torch_cuda
     x = spread(rows * width, 7 + width, 3.0)
